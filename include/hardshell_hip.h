@@ -1,0 +1,188 @@
+/*
+ * hardshell_hip.h — the C ABI of the MI355X (gfx950) HardShell backend, libhardshell_hip.so.
+ *
+ * It replaces the public API of the reference's CUDA backend crate, crates/hardshell-cuda
+ * (CudaDevice, CudaModel, CudaBatch, CudaSession and the op-level test entry points,
+ * crates/hardshell-cuda/src/lib.rs:36-43), one function per method, so that a thin FFI
+ * wrapper (a `hardshell-hip` crate) implements taco's `Lanes` trait
+ * (crates/taco/src/lanes.rs:61-113) on it exactly as `CudaLanes` does on `CudaBatch`.
+ *
+ * Rules of the ABI:
+ *  - Plain pointers and sizes; no C++ or torch types. All output arrays are caller-allocated
+ *    with the sizes documented below.
+ *  - Every function that can fail returns an hs_status. After a failure,
+ *    hs_last_error_message() and hs_last_error_code() describe it (thread-local).
+ *  - Handles are not thread-safe; the caller serialises calls on one device
+ *    (crates/hardshell-cuda/src/device.rs:8-9: CudaDevice is not Send). The device outlives its
+ *    models and a model outlives its batches; free in reverse order.
+ *  - Calls are synchronous: they return after the results are in host memory
+ *    (crates/hardshell-cuda/src/batch.rs:546-567).
+ *  - After an error, no slot position changes (crates/hardshell-cuda/src/batch.rs:444-446).
+ *  - Results are bit-identical to the CPU reference crate crates/hardshell.
+ */
+#ifndef HARDSHELL_HIP_H
+#define HARDSHELL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HS_ABI_VERSION 1
+
+typedef struct hs_device hs_device;
+typedef struct hs_model hs_model;
+typedef struct hs_batch hs_batch;
+
+/* The error variants of crates/hardshell-cuda/src/error.rs:9-51. */
+typedef enum hs_status {
+    HS_OK = 0,
+    HS_NO_DEVICE = 1,        /* Error::NoDevice: no HIP runtime or no device; use another backend */
+    HS_DEVICE_ERROR = 2,     /* Error::Cuda: a HIP runtime call failed (code: hs_last_error_code) */
+    HS_UNSUPPORTED = 3,      /* Error::Unsupported: shape, device or request not supported */
+    HS_MODEL_ERROR = 4,      /* Error::Model: model file or token error (kind: hs_last_error_code) */
+    HS_BAD_SLOT = 5,         /* Error::BadSlot */
+    HS_LENGTH_MISMATCH = 6,  /* Error::LengthMismatch */
+    HS_INVALID_ARGUMENT = 7  /* a NULL handle or pointer (no counterpart: Rust references) */
+} hs_status;
+
+/* The kind of an HS_MODEL_ERROR: the variants of crates/hardshell/src/error.rs:13-154. */
+typedef enum hs_model_error {
+    HS_MODEL_INVALID_SHAPE = 1,
+    HS_MODEL_LENGTH_MISMATCH = 2,
+    HS_MODEL_DOT_TOO_LONG = 3,
+    HS_MODEL_BAD_MAGIC = 4,
+    HS_MODEL_UNSUPPORTED_VERSION = 5,
+    HS_MODEL_TRUNCATED = 6,
+    HS_MODEL_HEADER_NOT_UTF8 = 7,
+    HS_MODEL_HEADER_JSON = 8,
+    HS_MODEL_INVALID_HEADER = 9,
+    HS_MODEL_LAYOUT = 10,
+    HS_MODEL_NON_ZERO_PADDING = 11,
+    HS_MODEL_VOCABULARY = 12,
+    HS_MODEL_MISSING_TENSOR = 13,
+    HS_MODEL_UNEXPECTED_TENSOR = 14,
+    HS_MODEL_TENSOR_MISMATCH = 15,
+    HS_MODEL_TOKEN_OUT_OF_RANGE = 16,
+    HS_MODEL_INVALID_OVERLAP = 17,
+    HS_MODEL_BAD_TRUNCATE = 18,
+    HS_MODEL_TOO_LARGE = 19,
+    HS_MODEL_UNSUPPORTED = 20
+} hs_model_error;
+
+/* The message and code of the last failure on this thread ("" and 0 if none). */
+const char *hs_last_error_message(void);
+int hs_last_error_code(void);
+/* Library version and the SHA-256 of the kernel sources it was built from
+ * (crates/hardshell-cuda/src/kernels.rs:9-22 records the PTX source hash the same way). */
+const char *hs_version(void);
+
+/* ---- Device: crates/hardshell-cuda/src/device.rs:29-74 ---------------------------------- */
+/* Opens HIP device `ordinal`. HS_NO_DEVICE if there is no runtime or no such device;
+ * HS_UNSUPPORTED if it is not a gfx950 (MI355X-class) GPU. */
+hs_status hs_device_open(int ordinal, hs_device **out);
+void hs_device_close(hs_device *dev);
+/* The device name ("AMD Instinct MI355X" ...), NUL-terminated, truncated to cap bytes. */
+hs_status hs_device_name(const hs_device *dev, char *buf, size_t cap);
+hs_status hs_device_memory(const hs_device *dev, size_t *free_bytes, size_t *total_bytes);
+
+/* ---- Model: crates/hardshell-cuda/src/model.rs:242-398 ---------------------------------- */
+/* Loads a .hsm file with exactly the accept/reject rules of hardshell::gpt2::Model::load
+ * (crates/hardshell/src/gpt2/model.rs:292-343, hsm/reader.rs:357-430) and uploads it. */
+hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t len, hs_model **out);
+void hs_model_free(hs_model *model);
+/* The SHA-256 of the model file (model.rs:353: CudaModel::hash). */
+void hs_model_hash(const hs_model *model, uint8_t out[32]);
+uint32_t hs_model_vocab(const hs_model *model);
+uint32_t hs_model_n_ctx(const hs_model *model);
+uint32_t hs_model_eot(const hs_model *model);
+/* 1 if the model uses a rule of model-file version 2 (gpt2/model.rs:379-384). */
+int hs_model_is_wide(const hs_model *model);
+uint64_t hs_model_weight_bytes(const hs_model *model);
+/* KV-cache bytes of one slot: 2 * n_layer * n_ctx * d_model (model.rs:392-398). */
+uint64_t hs_model_cache_bytes_per_slot(const hs_model *model);
+
+/* ---- Batch: crates/hardshell-cuda/src/batch.rs:237-476, batch/stream.rs:19-75 ----------- */
+typedef struct hs_input {   /* one (slot, token) input (batch.rs:447) */
+    uint32_t slot;
+    uint32_t token;
+} hs_input;
+
+typedef struct hs_query {   /* CoderQuery (batch.rs:38-43) */
+    uint32_t kind;          /* 0: Encode(token = value); 1: Decode(target = value) */
+    uint32_t value;
+} hs_query;
+
+typedef struct hs_interval {  /* CoderInterval (batch.rs:49-58); is_last is symbol + 1 == vocab */
+    uint64_t symbol;
+    uint64_t start;
+    uint64_t freq;
+} hs_interval;
+
+/* CudaBatch::new: `slots` independent sessions, passes of up to `max_rows` rows (1 becomes 2). */
+hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows, hs_batch **out);
+void hs_batch_free(hs_batch *batch);
+/* CudaBatch::set_overlap: the context overlap K (ADR 0015); HS_MODEL_ERROR
+ * (HS_MODEL_INVALID_OVERLAP) if K > n_ctx - 2. */
+hs_status hs_batch_set_overlap(hs_batch *batch, uint32_t k);
+size_t hs_batch_slots(const hs_batch *batch);
+size_t hs_batch_max_rows(const hs_batch *batch);
+uint64_t hs_batch_gpu_bytes(const hs_batch *batch);
+/* The number of tokens in the context of `slot` (0 for a slot that is not valid). */
+size_t hs_batch_position(const hs_batch *batch, size_t slot);
+/* Empties the context of `slot`. */
+void hs_batch_reset(hs_batch *batch, size_t slot);
+/* CudaBatch::run_weights: out holds n * vocab u64 values, in input order. A slot can occur many
+ * times (prefill); a full context restarts with EOT and the last K tokens. */
+hs_status hs_batch_run_weights(hs_batch *batch, const hs_input *inputs, size_t n, uint64_t *out);
+/* CudaBatch::run_coded: the interval of FreqTable::from_weights(weights, freq_bits) for each
+ * input (queries[i] belongs to inputs[i]). 1 <= freq_bits <= 32 and 2^freq_bits >= vocab. */
+hs_status hs_batch_run_coded(hs_batch *batch, const hs_input *inputs, const hs_query *queries,
+                             size_t n, uint32_t freq_bits, hs_interval *out);
+/* CudaBatch::step + weights: each listed slot at most once; keeps the weights of each slot. */
+hs_status hs_batch_step(hs_batch *batch, const hs_input *inputs, size_t n);
+/* The weights (vocab values) of the last hs_batch_step that included `slot`. */
+hs_status hs_batch_weights(const hs_batch *batch, size_t slot, uint64_t *out);
+/* batch/stream.rs: the tokens of the current stream of `slot`, the free positions before the
+ * next restart, and truncation to `len` stream tokens (ADR 0017). */
+size_t hs_batch_stream_len(const hs_batch *batch, size_t slot);
+size_t hs_batch_room(const hs_batch *batch, size_t slot);
+hs_status hs_batch_truncate(hs_batch *batch, size_t slot, size_t len);
+
+/* ---- Op-level entry points (crates/hardshell-cuda/src/ops.rs:142-335) --------------------- */
+/* out[i * n + r] = w[r] . a[i] for w [n, k] and a [m, k] i8 (host pointers), exact i32; the same
+ * values as hardshell::kernels::matvec_i8 (ops.rs:142-161 matmul_i8). */
+hs_status hs_op_gemm_i8(hs_device *dev, const int8_t *w, const int8_t *a, size_t m, size_t n,
+                        size_t k, int32_t *out);
+/* The c_attn linear of the forward pass (gpt2/ops.rs:123-130): out[i * n + r] =
+ * clamp(rescale(w[r] . a[i] + bias[r], mult[r], shift), -127, 127) as i8 (host pointers). */
+hs_status hs_op_gemm_requant_i8(hs_device *dev, const int8_t *w, const int8_t *a,
+                                const int32_t *bias, const int32_t *mult, uint8_t shift, size_t m,
+                                size_t n, size_t k, int8_t *out);
+/* The same product on device-resident operands (device pointers, `stream` a hipStream_t or
+ * NULL), with w and a padded as hs_op_gemm_layout() states. For measurements. */
+hs_status hs_op_gemm_requant_i8_dev(hs_device *dev, const int8_t *w, const int8_t *a,
+                                    const int32_t *bias, const int32_t *mult, uint8_t shift,
+                                    size_t m, size_t n, size_t k, int8_t *out, void *stream);
+/* The padded row strides that the _dev entry points expect: w is [n_pad, k_pad], a is
+ * [m_pad, k_pad] (zero padding), out is [m, n] dense. */
+void hs_op_gemm_layout(size_t m, size_t n, size_t k, size_t *m_pad, size_t *n_pad,
+                       size_t *k_pad);
+/* Integer decode attention, one query row per stream (batch rows of the decode path):
+ * q [b, h, hd] i8; k_cache, v_cache [b, h, ctx_cap, hd] i8; ctx[b] keys per stream
+ * (1 <= ctx[b] <= ctx_cap); out [b, h * hd] i8 = clamp_act_i8(rescale(sum_j p_j v_j, out_m,
+ * out_s)) with p = softmax(clamp(rescale(q . k_j, score_m, score_s), +-2^40)) over the table
+ * attn_exp (len entries), P = softmax_p (crates/hardshell/src/gpt2/reference.rs:254-283).
+ * Device pointers; `stream` a hipStream_t or NULL. */
+hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, const int8_t *k_cache,
+                                  const int8_t *v_cache, const uint32_t *ctx, size_t b, size_t h,
+                                  size_t hd, size_t ctx_cap, int32_t score_m, uint8_t score_s,
+                                  int32_t out_m, uint8_t out_s, const int32_t *attn_exp,
+                                  size_t len, uint8_t softmax_p, int8_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HARDSHELL_HIP_H */

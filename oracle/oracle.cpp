@@ -1959,3 +1959,45 @@ extern "C" size_t or_build_model(const uint32_t *dims, uint64_t seed, size_t cal
     if (b.size() <= cap) std::memcpy(out, b.data(), b.size());
     return b.size();
 }
+
+// ============================================================================================
+// 11. Op-level references for the GPU op tests.
+// ============================================================================================
+
+// The c_attn form of a linear (gpt2/reference.rs:239-245): out[i][r] =
+// clamp_act_i8(rescale(w[r] . a[i] + b[r], m[r], s)), with the scalar dot product.
+extern "C" void or_linear_act_ref(const int8_t *w, const int8_t *a, const int32_t *bias,
+                                  const int32_t *mult, uint8_t s, size_t m, size_t n, size_t k,
+                                  int8_t *out) {
+    for (size_t i = 0; i < m; i++)
+        for (size_t r = 0; r < n; r++) {
+            const int32_t acc = dot_i8(w + r * k, a + i * k, k);
+            out[i * n + r] = clamp_act_i8(rescale((int64_t)acc + bias[r], mult[r], s));
+        }
+}
+
+// One decode row of attention per stream (gpt2/reference.rs:254-283): q [b][h][hd]; caches
+// [b][h][ctx_cap][hd]; keys ctx[b]; out [b][h*hd].
+extern "C" void or_attend_decode_ref(const int8_t *q, const int8_t *kc, const int8_t *vc,
+                                     const uint32_t *ctx, size_t b, size_t h, size_t hd,
+                                     size_t ctx_cap, int32_t score_m, uint8_t score_s,
+                                     int32_t out_m, uint8_t out_s, const int32_t *table,
+                                     size_t len, uint8_t p, int8_t *out) {
+    std::vector<int32_t> t(table, table + len);
+    std::vector<int64_t> sc(ctx_cap), pr(ctx_cap), acc(hd);
+    for (size_t s = 0; s < b; s++)
+        for (size_t hh = 0; hh < h; hh++) {
+            const int8_t *qq = q + (s * h + hh) * hd;
+            const size_t base = (s * h + hh) * ctx_cap * hd;
+            const size_t n = ctx[s];
+            for (size_t j = 0; j < n; j++)
+                sc[j] = clamp_wide(rescale(dot_i8(qq, kc + base + j * hd, hd), score_m, score_s),
+                                   -SCORE_LIMIT, SCORE_LIMIT);
+            softmax_row(sc.data(), n, t, p, pr.data());
+            std::fill(acc.begin(), acc.end(), 0);
+            for (size_t j = 0; j < n; j++)
+                for (size_t c = 0; c < hd; c++) acc[c] += pr[j] * (int64_t)vc[base + j * hd + c];
+            for (size_t c = 0; c < hd; c++)
+                out[s * h * hd + hh * hd + c] = clamp_act_i8(rescale(acc[c], out_m, out_s));
+        }
+}

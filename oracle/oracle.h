@@ -123,6 +123,14 @@ long or_decode_block(const or_model *m, uint32_t overlap, const uint8_t *payload
 size_t or_build_model(const uint32_t *dims, uint64_t seed, size_t calib_len, int wide,
                       uint8_t *out, size_t cap);
 
+/* ---- op-level references for the GPU op tests ---- */
+void or_linear_act_ref(const int8_t *w, const int8_t *a, const int32_t *bias, const int32_t *mult,
+                       uint8_t s, size_t m, size_t n, size_t k, int8_t *out);
+void or_attend_decode_ref(const int8_t *q, const int8_t *kc, const int8_t *vc, const uint32_t *ctx,
+                          size_t b, size_t h, size_t hd, size_t ctx_cap, int32_t score_m,
+                          uint8_t score_s, int32_t out_m, uint8_t out_s, const int32_t *table,
+                          size_t len, uint8_t p, int8_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,11 @@ def lib():
                                    C.c_uint8, C.c_uint8, C.c_uint64, C.c_int, P]
         L.or_softmax.argtypes = [P, C.c_size_t, P, C.c_size_t, C.c_uint8, P]
         L.or_logits_to_weights.argtypes = [P, C.c_size_t, P, C.c_size_t, P]
+        L.or_linear_act_ref.argtypes = [P, P, P, P, C.c_uint8, C.c_size_t, C.c_size_t, C.c_size_t,
+                                         P]
+        L.or_attend_decode_ref.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, C.c_size_t,
+                                            C.c_size_t, C.c_int32, C.c_uint8, C.c_int32, C.c_uint8,
+                                            P, C.c_size_t, C.c_uint8, P]
         _lib = L
     return _lib
 
@@ -271,4 +276,30 @@ def matmul_i8(w, x):
     n = x.shape[0]
     out = np.zeros((n, rows), np.int32)
     lib().or_matmul_i8(ptr(w), rows, ptr(x), n, cols, ptr(out))
+    return out
+
+
+def linear_act_ref(w, a, bias, mult, shift):
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    bias = np.ascontiguousarray(bias, dtype=np.int32)
+    mult = np.ascontiguousarray(mult, dtype=np.int32)
+    n, k = w.shape
+    m = a.shape[0]
+    out = np.zeros((m, n), np.int8)
+    lib().or_linear_act_ref(ptr(w), ptr(a), ptr(bias), ptr(mult), shift, m, n, k, ptr(out))
+    return out
+
+
+def attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, p):
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    kc = np.ascontiguousarray(kc, dtype=np.int8)
+    vc = np.ascontiguousarray(vc, dtype=np.int8)
+    ctx = np.ascontiguousarray(ctx, dtype=np.uint32)
+    table = np.ascontiguousarray(table, dtype=np.int32)
+    b, h, hd = q.shape
+    cap = kc.shape[2]
+    out = np.zeros((b, h * hd), np.int8)
+    lib().or_attend_decode_ref(ptr(q), ptr(kc), ptr(vc), ptr(ctx), b, h, hd, cap, score_m,
+                               score_s, out_m, out_s, ptr(table), len(table), p, ptr(out))
     return out

@@ -1,0 +1,739 @@
+// The C ABI of libhardshell_hip.so (include/hardshell_hip.h): device, model, batch and op-level
+// entry points. Host orchestration of the kernels in kernels.hip.
+//
+// Mirrors crates/hardshell-cuda/src/{device,model,batch,ops}.rs: the same methods, argument
+// meaning and error behaviour (validation before any device work, positions committed only
+// after every pass of a call succeeded).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "common.h"
+#include "hardshell_hip.h"
+#include "hsm.h"
+#include "kernels.h"
+
+#ifndef HS_SOURCE_SHA256
+#define HS_SOURCE_SHA256 "unknown"
+#endif
+
+using hs::Epi;
+using hs::RowInfo;
+
+namespace {
+
+constexpr size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+hs_status hip_fail(const char *call, hipError_t e) {
+    return hs::fail(HS_DEVICE_ERROR, (int)e, std::string(call) + " failed: " + hipGetErrorName(e));
+}
+
+#define HIP_TRY(call)                                    \
+    do {                                                 \
+        hipError_t e_ = (call);                          \
+        if (e_ != hipSuccess) return hip_fail(#call, e_); \
+    } while (0)
+
+// Device allocations owned by a handle; freed in reverse order.
+struct DevMem {
+    std::vector<void *> ptrs;
+    uint64_t bytes = 0;
+    ~DevMem() {
+        for (auto it = ptrs.rbegin(); it != ptrs.rend(); ++it) (void)hipFree(*it);
+    }
+    template <typename T>
+    hs_status alloc(T *&p, size_t count) {
+        void *v = nullptr;
+        const size_t n = std::max<size_t>(count * sizeof(T), 256);
+        hipError_t e = hipMalloc(&v, n);
+        if (e != hipSuccess) return hip_fail("hipMalloc", e);
+        e = hipMemset(v, 0, n);
+        if (e != hipSuccess) {
+            (void)hipFree(v);
+            return hip_fail("hipMemset", e);
+        }
+        ptrs.push_back(v);
+        bytes += n;
+        p = (T *)v;
+        return HS_OK;
+    }
+    template <typename T>
+    hs_status upload(T *&p, const T *src, size_t count, size_t alloc_count = 0) {
+        hs_status st = alloc(p, std::max(count, alloc_count));
+        if (st != HS_OK) return st;
+        if (count) HIP_TRY(hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice));
+        return HS_OK;
+    }
+};
+
+}  // namespace
+
+struct hs_device {
+    int ordinal = 0;
+    std::string name;
+    hipStream_t stream = nullptr;
+};
+
+namespace {
+
+struct DevLinear {
+    int8_t *w = nullptr;  // [n_pad, k_pad]
+    int32_t *b = nullptr, *m = nullptr;
+    int s = 0, n = 0, k = 0, n_pad = 0, k_pad = 0;
+};
+
+struct DevLn {
+    int16_t *g = nullptr;
+    int32_t *b = nullptr;
+    int32_t m = 0;
+    int s = 0;
+};
+
+struct DevBlock {
+    DevLn ln1, ln2;
+    DevLinear c_attn, c_proj, c_fc, mlp_proj;
+    int32_t score_m = 0, out_m = 0;
+    int score_s = 0, out_s = 0;
+    int8_t *gelu = nullptr;
+    int gelu_off = 0;
+};
+
+}  // namespace
+
+struct hs_model {
+    hs_device *dev = nullptr;
+    hs::HostModel host;
+    DevMem mem;
+    int d = 0, f = 0, V = 0, C = 0, H = 0, hd = 0, L = 0;
+    int d_pad = 0, f_pad = 0, V_pad = 0;
+    int8_t *wte = nullptr;  // [V_pad, d_pad]: the LM head operand; the embedding reads row tok
+    int8_t *wpe = nullptr;  // [C, d]
+    int32_t *embed_m = nullptr, *logit_m = nullptr, *pos_m = nullptr;
+    std::vector<DevBlock> blocks;
+    DevLn ln_f;
+    int32_t *attn_exp = nullptr;
+    uint64_t *logits_exp = nullptr;
+    uint64_t weight_bytes = 0;
+};
+
+namespace {
+
+hs_status upload_linear(DevMem &mem, const hs::HostLinear &l, DevLinear &o) {
+    o.n = (int)l.rows;
+    o.k = (int)l.cols;
+    o.n_pad = (int)round_up(l.rows, hs::GEMM_BN);
+    o.k_pad = (int)round_up(l.cols, hs::GEMM_BK);
+    std::vector<int8_t> w((size_t)o.n_pad * o.k_pad, 0);
+    for (uint32_t r = 0; r < l.rows; r++) std::memcpy(&w[(size_t)r * o.k_pad], l.w + (size_t)r * l.cols, l.cols);
+    hs_status st = mem.upload(o.w, w.data(), w.size());
+    if (st == HS_OK) st = mem.upload(o.b, l.b.data(), l.b.size(), o.n_pad);
+    if (st == HS_OK) st = mem.upload(o.m, l.m.data(), l.m.size(), o.n_pad);
+    o.s = l.s;
+    return st;
+}
+
+hs_status upload_ln(DevMem &mem, const hs::HostLayerNorm &l, DevLn &o) {
+    hs_status st = mem.upload(o.g, l.g.data(), l.g.size());
+    if (st == HS_OK) st = mem.upload(o.b, l.b.data(), l.b.size());
+    o.m = l.m;
+    o.s = l.s;
+    return st;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------
+// Device
+// ---------------------------------------------------------------------------------------------
+
+extern "C" const char *hs_version(void) {
+    return "hardshell-hip " "0.1.0" " gfx950 kernels sha256:" HS_SOURCE_SHA256;
+}
+
+extern "C" hs_status hs_device_open(int ordinal, hs_device **out) {
+    hs::clear_error();
+    if (!out) return hs::fail(HS_INVALID_ARGUMENT, 0, "out is NULL");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return hs::fail(HS_NO_DEVICE, (int)e, "no HIP device: " + std::string(hipGetErrorName(e)));
+    if (ordinal < 0 || ordinal >= count)
+        return hs::fail(HS_NO_DEVICE, 0, "no HIP device with ordinal " + std::to_string(ordinal));
+    HIP_TRY(hipSetDevice(ordinal));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, ordinal));
+    const std::string arch = prop.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0)
+        return hs::fail(HS_UNSUPPORTED, 0, "the kernels are built for gfx950 only; this device is " + arch);
+    auto dev = std::make_unique<hs_device>();
+    dev->ordinal = ordinal;
+    dev->name = prop.name;
+    HIP_TRY(hipStreamCreate(&dev->stream));
+    *out = dev.release();
+    return HS_OK;
+}
+
+extern "C" void hs_device_close(hs_device *dev) {
+    if (!dev) return;
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
+    delete dev;
+}
+
+extern "C" hs_status hs_device_name(const hs_device *dev, char *buf, size_t cap) {
+    if (!dev || !buf || cap == 0) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    std::strncpy(buf, dev->name.c_str(), cap - 1);
+    buf[cap - 1] = 0;
+    return HS_OK;
+}
+
+extern "C" hs_status hs_device_memory(const hs_device *dev, size_t *free_bytes, size_t *total_bytes) {
+    if (!dev || !free_bytes || !total_bytes) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    HIP_TRY(hipMemGetInfo(free_bytes, total_bytes));
+    return HS_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Model: crates/hardshell-cuda/src/model.rs:242-349
+// ---------------------------------------------------------------------------------------------
+
+extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t len, hs_model **out) {
+    hs::clear_error();
+    if (!dev || !bytes || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    *out = nullptr;
+    auto m = std::make_unique<hs_model>();
+    hs::ModelError err{};
+    if (!hs::load_host_model(bytes, len, m->host, err)) return hs::fail(HS_MODEL_ERROR, err.kind, err.msg);
+    const hs::HostModel &h = m->host;
+    if (h.is_wide())
+        return hs::fail(HS_UNSUPPORTED, 0, "model-file version 2 rules (i16 activations, ln_beta_frac) are not implemented by the gfx950 backend yet");
+    if (h.head_dim % 4 != 0 || h.head_dim > 256)
+        return hs::fail(HS_UNSUPPORTED, 0, "head_dim must be a multiple of 4 and at most 256");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    m->dev = dev;
+    m->d = (int)h.d_model; m->f = (int)h.d_ff; m->V = (int)h.vocab; m->C = (int)h.n_ctx;
+    m->H = (int)h.n_head; m->hd = (int)h.head_dim; m->L = (int)h.n_layer;
+    m->d_pad = (int)round_up(h.d_model, hs::GEMM_BK);
+    m->f_pad = (int)round_up(h.d_ff, hs::GEMM_BK);
+    m->V_pad = (int)round_up(h.vocab, hs::GEMM_BN);
+    DevMem &mem = m->mem;
+    hs_status st;
+    {
+        std::vector<int8_t> w((size_t)m->V_pad * m->d_pad, 0);
+        for (int v = 0; v < m->V; v++) std::memcpy(&w[(size_t)v * m->d_pad], h.wte + (size_t)v * m->d, m->d);
+        if ((st = mem.upload(m->wte, w.data(), w.size())) != HS_OK) return st;
+    }
+    if ((st = mem.upload(m->wpe, h.wpe, (size_t)m->C * m->d)) != HS_OK) return st;
+    if ((st = mem.upload(m->embed_m, h.embed_m.data(), h.embed_m.size())) != HS_OK) return st;
+    if ((st = mem.upload(m->logit_m, h.logit_m.data(), h.logit_m.size(), m->V_pad)) != HS_OK) return st;
+    if ((st = mem.upload(m->pos_m, h.pos_m.data(), h.pos_m.size())) != HS_OK) return st;
+    m->blocks.resize(m->L);
+    for (int l = 0; l < m->L; l++) {
+        const hs::HostBlock &hb = h.blocks[l];
+        DevBlock &b = m->blocks[l];
+        if ((st = upload_ln(mem, hb.ln1, b.ln1)) != HS_OK) return st;
+        if ((st = upload_ln(mem, hb.ln2, b.ln2)) != HS_OK) return st;
+        if ((st = upload_linear(mem, hb.c_attn, b.c_attn)) != HS_OK) return st;
+        if ((st = upload_linear(mem, hb.c_proj, b.c_proj)) != HS_OK) return st;
+        if ((st = upload_linear(mem, hb.c_fc, b.c_fc)) != HS_OK) return st;
+        if ((st = upload_linear(mem, hb.mlp_proj, b.mlp_proj)) != HS_OK) return st;
+        b.score_m = hb.score_m; b.score_s = hb.score_s;
+        b.out_m = hb.out_m; b.out_s = hb.out_s;
+        if ((st = mem.upload(b.gelu, hb.gelu8.data(), hb.gelu8.size())) != HS_OK) return st;
+        b.gelu_off = (int)hb.gelu_len / 2;
+    }
+    if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
+    if ((st = mem.upload(m->attn_exp, h.attn_exp.data(), h.attn_exp.size())) != HS_OK) return st;
+    if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size())) != HS_OK) return st;
+    m->weight_bytes = mem.bytes;
+    *out = m.release();
+    return HS_OK;
+}
+
+extern "C" void hs_model_free(hs_model *model) { delete model; }
+extern "C" void hs_model_hash(const hs_model *m, uint8_t out[32]) {
+    if (m && out) std::memcpy(out, m->host.hash, 32);
+}
+extern "C" uint32_t hs_model_vocab(const hs_model *m) { return m ? m->host.vocab : 0; }
+extern "C" uint32_t hs_model_n_ctx(const hs_model *m) { return m ? m->host.n_ctx : 0; }
+extern "C" uint32_t hs_model_eot(const hs_model *m) { return m ? m->host.eot : 0; }
+extern "C" int hs_model_is_wide(const hs_model *m) { return m && m->host.is_wide() ? 1 : 0; }
+extern "C" uint64_t hs_model_weight_bytes(const hs_model *m) { return m ? m->weight_bytes : 0; }
+extern "C" uint64_t hs_model_cache_bytes_per_slot(const hs_model *m) {
+    return m ? 2ull * m->host.n_layer * m->host.n_ctx * m->host.d_model : 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Batch: crates/hardshell-cuda/src/batch.rs, batch/plan.rs
+// ---------------------------------------------------------------------------------------------
+
+namespace {
+
+struct PassRow {
+    uint32_t slot, token, pos;
+    int64_t input;  // index of the input it answers, -1 for a restart row
+};
+
+}  // namespace
+
+struct hs_batch {
+    hs_model *model = nullptr;
+    size_t slots = 0, max_rows = 0, rows_pad = 0;
+    uint32_t overlap = 0;
+    std::vector<size_t> pos;
+    std::vector<uint32_t> hist;    // [slots, n_ctx]: the token at each position
+    std::vector<size_t> stream;    // tokens of the current stream of each slot (ADR 0017)
+    std::vector<uint64_t> host_w;  // [slots, vocab]: weights of the last step
+    hipStream_t st = nullptr;
+    DevMem mem;
+    RowInfo *d_rows = nullptr;
+    int32_t *d_x = nullptr, *d_src = nullptr;
+    int8_t *d_a = nullptr, *d_qkv = nullptr, *d_att = nullptr, *d_g = nullptr, *d_af = nullptr;
+    int64_t *d_logits = nullptr;
+    uint32_t *d_queries = nullptr;
+    uint64_t *d_intervals = nullptr, *d_weights = nullptr;
+    size_t chunk_rows = 0;
+    std::vector<int8_t *> kc, vc;  // per layer: [slots][H][n_ctx][hd]
+    ~hs_batch() {
+        if (st) (void)hipStreamDestroy(st);
+    }
+};
+
+extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows, hs_batch **out) {
+    hs::clear_error();
+    if (!model || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    *out = nullptr;
+    if (slots == 0 || max_rows == 0)
+        return hs::fail(HS_UNSUPPORTED, 0, "a batch needs at least one slot and one row");
+    HIP_TRY(hipSetDevice(model->dev->ordinal));
+    auto b = std::make_unique<hs_batch>();
+    const hs_model &m = *model;
+    b->model = model;
+    b->slots = slots;
+    b->max_rows = std::max<size_t>(max_rows, 2);  // a restart needs two rows
+    b->rows_pad = round_up(b->max_rows, hs::GEMM_BM);
+    b->pos.assign(slots, 0);
+    b->hist.assign(slots * m.C, 0);
+    b->stream.assign(slots, 0);
+    // The LM head runs on chunks of output rows so that the i64 logits stay near 1 GiB.
+    b->chunk_rows = std::max<size_t>(hs::GEMM_BM, round_up(std::min<size_t>(b->rows_pad, (size_t)((1ull << 30) / (8ull * m.V_pad))), hs::GEMM_BM));
+    b->chunk_rows = std::min(b->chunk_rows, b->rows_pad);
+    const size_t R = b->max_rows, RP = b->rows_pad;
+    DevMem &mem = b->mem;
+    hs_status s;
+    if ((s = mem.alloc(b->d_rows, R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_src, R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_x, R * m.d)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_a, RP * m.d_pad)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_af, RP * m.d_pad)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_qkv, R * 3 * m.d)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_att, RP * m.d_pad)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_g, RP * m.f_pad)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_logits, b->chunk_rows * m.V)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_queries, 2 * R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_intervals, 3 * R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_weights, b->chunk_rows * m.V)) != HS_OK) return s;
+    const size_t cache = slots * (size_t)m.C * m.d;
+    b->kc.resize(m.L);
+    b->vc.resize(m.L);
+    for (int l = 0; l < m.L; l++) {
+        if ((s = mem.alloc(b->kc[l], cache)) != HS_OK) return s;
+        if ((s = mem.alloc(b->vc[l], cache)) != HS_OK) return s;
+    }
+    HIP_TRY(hipStreamCreate(&b->st));
+    *out = b.release();
+    return HS_OK;
+}
+
+extern "C" void hs_batch_free(hs_batch *b) { delete b; }
+
+extern "C" hs_status hs_batch_set_overlap(hs_batch *b, uint32_t k) {
+    hs::clear_error();
+    if (!b) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL batch");
+    const uint32_t n_ctx = b->model->host.n_ctx;
+    if ((uint64_t)k + 2 > n_ctx)
+        return hs::fail(HS_MODEL_ERROR, HS_MODEL_INVALID_OVERLAP,
+                        "the overlap " + std::to_string(k) + " does not fit a context of " + std::to_string(n_ctx));
+    b->overlap = k;
+    return HS_OK;
+}
+
+extern "C" size_t hs_batch_slots(const hs_batch *b) { return b ? b->slots : 0; }
+extern "C" size_t hs_batch_max_rows(const hs_batch *b) { return b ? b->max_rows : 0; }
+extern "C" uint64_t hs_batch_gpu_bytes(const hs_batch *b) { return b ? b->mem.bytes : 0; }
+extern "C" size_t hs_batch_position(const hs_batch *b, size_t slot) {
+    return (b && slot < b->slots) ? b->pos[slot] : 0;
+}
+extern "C" void hs_batch_reset(hs_batch *b, size_t slot) {
+    if (b && slot < b->slots) {
+        b->pos[slot] = 0;
+        b->stream[slot] = 0;
+    }
+}
+
+namespace {
+
+// The plan of a call (batch/plan.rs:60-117): inputs -> rows -> passes of <= max_rows rows; a
+// restart of a slot that already has rows in the current pass starts a new pass.
+struct Plan {
+    std::vector<std::vector<PassRow>> passes;
+    std::vector<size_t> pos;
+    std::unordered_map<size_t, std::vector<uint32_t>> hist;
+    std::vector<size_t> stream;
+};
+
+Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
+    Plan p;
+    const size_t C = b.model->host.n_ctx;
+    const size_t k = std::min<size_t>(b.overlap, C - 2);
+    const uint32_t eot = b.model->host.eot;
+    p.pos = b.pos;
+    p.stream = b.stream;
+    std::vector<PassRow> cur;
+    std::vector<char> in_pass(b.slots, 0);
+    auto flush = [&]() {
+        if (!cur.empty()) p.passes.push_back(std::move(cur));
+        cur.clear();
+        std::fill(in_pass.begin(), in_pass.end(), 0);
+    };
+    auto push = [&](PassRow r) {
+        if (cur.size() >= b.max_rows) flush();
+        in_pass[r.slot] = 1;
+        cur.push_back(r);
+    };
+    for (size_t i = 0; i < n; i++) {
+        const size_t slot = in[i].slot;
+        auto it = p.hist.find(slot);
+        if (it == p.hist.end())
+            it = p.hist.emplace(slot, std::vector<uint32_t>(b.hist.begin() + slot * C, b.hist.begin() + (slot + 1) * C)).first;
+        std::vector<uint32_t> &h = it->second;
+        size_t at = p.pos[slot];
+        if (at >= C) {
+            if (in_pass[slot]) flush();
+            if (k > 0) std::memmove(&h[1], &h[C - k], k * sizeof(uint32_t));
+            h[0] = eot;
+            for (size_t q = 0; q <= k; q++) push(PassRow{(uint32_t)slot, h[q], (uint32_t)q, -1});
+            at = k + 1;
+            p.stream[slot] = k;  // the stream keeps its last k tokens
+        }
+        h[at] = in[i].token;
+        p.stream[slot] += 1;
+        push(PassRow{(uint32_t)slot, in[i].token, (uint32_t)at, (int64_t)i});
+        p.pos[slot] = at + 1;
+    }
+    flush();
+    return p;
+}
+
+void commit(hs_batch &b, Plan &p) {
+    const size_t C = b.model->host.n_ctx;
+    b.pos = p.pos;
+    b.stream = p.stream;
+    for (auto &kv : p.hist) std::memcpy(&b.hist[kv.first * C], kv.second.data(), C * sizeof(uint32_t));
+}
+
+enum class Out { Weights, Intervals };
+
+// One forward pass over `rows`, then the LM head and the coder op for the rows with an input.
+hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const uint32_t *queries,
+                   uint32_t bits, uint64_t *sink) {
+    const hs_model &m = *b.model;
+    hipStream_t st = b.st;
+    const int n = (int)rows.size();
+    std::vector<RowInfo> info(n);
+    std::vector<int32_t> src;
+    std::vector<uint32_t> q;
+    std::vector<int64_t> owner;
+    for (int r = 0; r < n; r++) {
+        info[r] = RowInfo{(int32_t)rows[r].slot, (int32_t)rows[r].token, (int32_t)rows[r].pos, -1};
+        if (rows[r].input >= 0) {
+            info[r].out = (int32_t)src.size();
+            src.push_back(r);
+            owner.push_back(rows[r].input);
+            if (out == Out::Intervals) {
+                q.push_back(queries[2 * rows[r].input]);
+                q.push_back(queries[2 * rows[r].input + 1]);
+            }
+        }
+    }
+    HIP_TRY(hipMemcpyAsync(b.d_rows, info.data(), n * sizeof(RowInfo), hipMemcpyHostToDevice, st));
+    const int n_out = (int)src.size();
+    if (n_out) HIP_TRY(hipMemcpyAsync(b.d_src, src.data(), n_out * sizeof(int32_t), hipMemcpyHostToDevice, st));
+    if (!q.empty()) HIP_TRY(hipMemcpyAsync(b.d_queries, q.data(), q.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+
+    HIP_TRY(hs::launch_embed(b.d_rows, n, m.wte, m.d_pad, m.wpe, m.embed_m, m.host.embed_s, m.pos_m,
+                             m.host.pos_s, m.d, b.d_x, st));
+    auto ln = [&](const DevLn &l, const int32_t *src_rows, int rows_n, int8_t *dst) {
+        hs::LnArgs a;
+        a.x = b.d_x; a.d = m.d; a.gamma = l.g; a.beta = l.b; a.m = l.m; a.s = l.s;
+        a.beta_frac = m.host.ln_beta_frac; a.k = m.host.ln_k; a.j = m.host.ln_j; a.eps = m.host.ln_eps;
+        a.out = dst; a.ldo = m.d_pad; a.src = src_rows;
+        return hs::launch_layernorm(a, rows_n, st);
+    };
+    auto gemm = [&](Epi epi, const DevLinear &lin, const int8_t *a, int rows_n, void *o, int ldo,
+                    const int8_t *gelu = nullptr, int gelu_off = 0) {
+        hs::GemmArgs g;
+        g.a = a; g.w = lin.w; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
+        g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
+        g.gelu = gelu; g.gelu_off = gelu_off;
+        return hs::launch_gemm(epi, g, st);
+    };
+    for (int l = 0; l < m.L; l++) {
+        const DevBlock &blk = m.blocks[l];
+        HIP_TRY(ln(blk.ln1, nullptr, n, b.d_a));
+        HIP_TRY(gemm(Epi::Act, blk.c_attn, b.d_a, n, b.d_qkv, 3 * m.d));
+        HIP_TRY(hs::launch_kv_store(b.d_rows, n, b.d_qkv, m.d, m.H, m.hd, m.C, b.kc[l], b.vc[l], st));
+        hs::AttnArgs at;
+        at.rows = b.d_rows; at.q = b.d_qkv; at.ldq = 3 * m.d; at.kc = b.kc[l]; at.vc = b.vc[l];
+        at.n_head = m.H; at.hd = m.hd; at.ctx_cap = m.C; at.score_m = blk.score_m; at.score_s = blk.score_s;
+        at.out_m = blk.out_m; at.out_s = blk.out_s; at.exp_table = m.attn_exp;
+        at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
+        at.out = b.d_att; at.ldo = m.d_pad;
+        HIP_TRY(hs::launch_attend(at, n, st));
+        HIP_TRY(gemm(Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
+        HIP_TRY(ln(blk.ln2, nullptr, n, b.d_a));
+        HIP_TRY(gemm(Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
+        HIP_TRY(gemm(Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
+    }
+    if (n_out == 0) return HS_OK;
+    HIP_TRY(ln(m.ln_f, b.d_src, n_out, b.d_af));
+    DevLinear head;
+    head.w = m.wte; head.m = m.logit_m; head.s = m.host.logit_s; head.n = m.V; head.k = m.d;
+    head.n_pad = m.V_pad; head.k_pad = m.d_pad;
+    const size_t per_row = out == Out::Weights ? (size_t)m.V : 3;
+    std::vector<uint64_t> host((size_t)n_out * per_row);
+    for (int c0 = 0; c0 < n_out; c0 += (int)b.chunk_rows) {
+        const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
+        HIP_TRY(gemm(Epi::Logits, head, b.d_af + (size_t)c0 * m.d_pad, cn, b.d_logits, m.V));
+        hs::CoderArgs ca;
+        ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
+        ca.table_len = (int)m.host.logits_exp.size();
+        ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
+        ca.bits = (int)bits;
+        ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
+        ca.weights = out == Out::Weights ? b.d_weights : nullptr;
+        HIP_TRY(hs::launch_coder(ca, cn, st));
+        if (out == Out::Weights)
+            HIP_TRY(hipMemcpyAsync(host.data() + (size_t)c0 * m.V, b.d_weights, (size_t)cn * m.V * 8,
+                                   hipMemcpyDeviceToHost, st));
+    }
+    if (out == Out::Intervals)
+        HIP_TRY(hipMemcpyAsync(host.data(), b.d_intervals, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    for (int i = 0; i < n_out; i++)
+        std::memcpy(sink + (size_t)owner[i] * per_row, host.data() + (size_t)i * per_row, per_row * 8);
+    return HS_OK;
+}
+
+hs_status check_inputs(const hs_batch *b, const hs_input *in, size_t n) {
+    if (!b || (n && !in)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    const uint32_t V = b->model->host.vocab;
+    for (size_t i = 0; i < n; i++) {
+        if (in[i].slot >= b->slots)
+            return hs::fail(HS_BAD_SLOT, (int)in[i].slot, "slot " + std::to_string(in[i].slot) +
+                            " is not valid in a batch of " + std::to_string(b->slots) + " slots");
+        if (in[i].token >= V)
+            return hs::fail(HS_MODEL_ERROR, HS_MODEL_TOKEN_OUT_OF_RANGE,
+                            "token " + std::to_string(in[i].token) + " is not in the vocabulary of " +
+                                std::to_string(V) + " tokens");
+    }
+    return HS_OK;
+}
+
+hs_status run(hs_batch *b, const hs_input *in, size_t n, Out out, const uint32_t *queries,
+              uint32_t bits, uint64_t *sink) {
+    HIP_TRY(hipSetDevice(b->model->dev->ordinal));
+    Plan plan = make_plan(*b, in, n);
+    for (auto &pass : plan.passes) {
+        hs_status s = run_pass(*b, pass, out, queries, bits, sink);
+        if (s != HS_OK) return s;  // no position changes after an error
+    }
+    commit(*b, plan);
+    return HS_OK;
+}
+
+}  // namespace
+
+extern "C" hs_status hs_batch_run_weights(hs_batch *b, const hs_input *in, size_t n, uint64_t *out) {
+    hs::clear_error();
+    hs_status s = check_inputs(b, in, n);
+    if (s != HS_OK) return s;
+    if (n && !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "out is NULL");
+    return run(b, in, n, Out::Weights, nullptr, 0, out);
+}
+
+extern "C" hs_status hs_batch_run_coded(hs_batch *b, const hs_input *in, const hs_query *queries,
+                                        size_t n, uint32_t freq_bits, hs_interval *out) {
+    hs::clear_error();
+    hs_status s = check_inputs(b, in, n);
+    if (s != HS_OK) return s;
+    if (n && (!queries || !out)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    const uint32_t V = b->model->host.vocab;
+    // coder_words (batch.rs:647-666)
+    if (freq_bits == 0 || freq_bits > 32 || (uint64_t)V > (1ull << freq_bits))
+        return hs::fail(HS_UNSUPPORTED, 0, "freq_bits must be in 1..=32 and 2^freq_bits >= vocab");
+    std::vector<uint32_t> words(2 * n);
+    for (size_t i = 0; i < n; i++) {
+        const bool ok = (queries[i].kind == 0 && queries[i].value < V) ||
+                        (queries[i].kind == 1 && (uint64_t)queries[i].value < (1ull << freq_bits));
+        if (!ok) return hs::fail(HS_UNSUPPORTED, 0, "a coder token or target is out of range");
+        words[2 * i] = queries[i].kind;
+        words[2 * i + 1] = queries[i].value;
+    }
+    return run(b, in, n, Out::Intervals, words.data(), freq_bits, (uint64_t *)out);
+}
+
+extern "C" hs_status hs_batch_step(hs_batch *b, const hs_input *in, size_t n) {
+    hs::clear_error();
+    hs_status s = check_inputs(b, in, n);
+    if (s != HS_OK) return s;
+    std::vector<char> seen(b->slots, 0);
+    for (size_t i = 0; i < n; i++) {
+        if (seen[in[i].slot]) return hs::fail(HS_BAD_SLOT, (int)in[i].slot, "a slot occurs two times in one step");
+        seen[in[i].slot] = 1;
+    }
+    const size_t V = b->model->host.vocab;
+    std::vector<uint64_t> w(n * V);
+    if ((s = run(b, in, n, Out::Weights, nullptr, 0, w.data())) != HS_OK) return s;
+    if (b->host_w.empty()) b->host_w.assign(b->slots * V, 0);
+    for (size_t i = 0; i < n; i++) std::memcpy(&b->host_w[in[i].slot * V], &w[i * V], V * 8);
+    return HS_OK;
+}
+
+extern "C" hs_status hs_batch_weights(const hs_batch *b, size_t slot, uint64_t *out) {
+    if (!b || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (slot >= b->slots) return hs::fail(HS_BAD_SLOT, (int)slot, "slot is not valid");
+    const size_t V = b->model->host.vocab;
+    if (b->host_w.empty()) std::memset(out, 0, V * 8);
+    else std::memcpy(out, &b->host_w[slot * V], V * 8);
+    return HS_OK;
+}
+
+// The stream of a slot (crates/hardshell/src/gpt2/stream.rs, hardshell-cuda batch/stream.rs):
+// the tokens since the block start that the current context still holds, the free positions
+// before the next restart, and truncation back to `len` stream tokens.
+extern "C" size_t hs_batch_stream_len(const hs_batch *b, size_t slot) {
+    return (b && slot < b->slots) ? b->stream[slot] : 0;
+}
+extern "C" size_t hs_batch_room(const hs_batch *b, size_t slot) {
+    if (!b || slot >= b->slots) return 0;
+    const size_t C = b->model->host.n_ctx;
+    return b->pos[slot] >= C ? 0 : C - b->pos[slot];
+}
+extern "C" hs_status hs_batch_truncate(hs_batch *b, size_t slot, size_t len) {
+    hs::clear_error();
+    if (!b) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL batch");
+    if (slot >= b->slots) return hs::fail(HS_BAD_SLOT, (int)slot, "slot is not valid");
+    const size_t cur = b->stream[slot];
+    const size_t drop = cur >= len ? cur - len : 0;
+    if (len > cur || drop > b->pos[slot] - (b->pos[slot] > cur ? b->pos[slot] - cur : 0))
+        return hs::fail(HS_MODEL_ERROR, HS_MODEL_BAD_TRUNCATE, "the truncation is outside the current context");
+    b->pos[slot] -= drop;
+    b->stream[slot] = len;
+    return HS_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Op-level entry points: crates/hardshell-cuda/src/ops.rs:142-335
+// ---------------------------------------------------------------------------------------------
+
+extern "C" void hs_op_gemm_layout(size_t m, size_t n, size_t k, size_t *m_pad, size_t *n_pad, size_t *k_pad) {
+    if (m_pad) *m_pad = round_up(std::max<size_t>(m, 1), hs::GEMM_BM);
+    if (n_pad) *n_pad = round_up(std::max<size_t>(n, 1), hs::GEMM_BN);
+    if (k_pad) *k_pad = round_up(std::max<size_t>(k, 1), hs::GEMM_BK);
+}
+
+namespace {
+
+hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, const int32_t *bias,
+                    const int32_t *mult, uint8_t shift, size_t m, size_t n, size_t k, void *out) {
+    hs::clear_error();
+    if (!dev || !w || !a || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (m == 0 || n == 0 || k == 0) return HS_OK;
+    if (k > 65536) return hs::fail(HS_MODEL_ERROR, HS_MODEL_DOT_TOO_LONG, "a dot product is longer than 2^16");
+    if (m > (1u << 30) || n > (1u << 30)) return hs::fail(HS_UNSUPPORTED, 0, "the product is too large");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    size_t mp, np, kp;
+    hs_op_gemm_layout(m, n, k, &mp, &np, &kp);
+    std::vector<int8_t> wp(np * kp, 0), ap(mp * kp, 0);
+    for (size_t r = 0; r < n; r++) std::memcpy(&wp[r * kp], w + r * k, k);
+    for (size_t r = 0; r < m; r++) std::memcpy(&ap[r * kp], a + r * k, k);
+    DevMem mem;
+    int8_t *dw, *da;
+    int32_t *db = nullptr, *dm = nullptr;
+    void *dout;
+    hs_status s;
+    if ((s = mem.upload(dw, wp.data(), wp.size())) != HS_OK) return s;
+    if ((s = mem.upload(da, ap.data(), ap.size())) != HS_OK) return s;
+    if (bias && (s = mem.upload(db, bias, n)) != HS_OK) return s;
+    if (mult && (s = mem.upload(dm, mult, n)) != HS_OK) return s;
+    const size_t esz = epi == Epi::Raw ? 4 : 1;
+    int8_t *o8;
+    if ((s = mem.alloc(o8, m * n * esz)) != HS_OK) return s;
+    dout = o8;
+    hs::GemmArgs g;
+    g.a = da; g.w = dw; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
+    g.bias = db; g.mult = dm; g.shift = shift; g.out = dout; g.ldo = (int)n;
+    HIP_TRY(hs::launch_gemm(epi, g, dev->stream));
+    HIP_TRY(hipMemcpyAsync(out, dout, m * n * esz, hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
+}
+
+}  // namespace
+
+extern "C" hs_status hs_op_gemm_i8(hs_device *dev, const int8_t *w, const int8_t *a, size_t m, size_t n,
+                                   size_t k, int32_t *out) {
+    return gemm_host(dev, Epi::Raw, w, a, nullptr, nullptr, 0, m, n, k, out);
+}
+
+extern "C" hs_status hs_op_gemm_requant_i8(hs_device *dev, const int8_t *w, const int8_t *a,
+                                           const int32_t *bias, const int32_t *mult, uint8_t shift,
+                                           size_t m, size_t n, size_t k, int8_t *out) {
+    if (!bias || !mult) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    return gemm_host(dev, Epi::Act, w, a, bias, mult, shift, m, n, k, out);
+}
+
+extern "C" hs_status hs_op_gemm_requant_i8_dev(hs_device *dev, const int8_t *w, const int8_t *a,
+                                               const int32_t *bias, const int32_t *mult, uint8_t shift,
+                                               size_t m, size_t n, size_t k, int8_t *out, void *stream) {
+    hs::clear_error();
+    if (!dev || !w || !a || !bias || !mult || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (m == 0 || n == 0 || k == 0) return HS_OK;
+    if (k > 65536) return hs::fail(HS_MODEL_ERROR, HS_MODEL_DOT_TOO_LONG, "a dot product is longer than 2^16");
+    size_t kp;
+    hs_op_gemm_layout(m, n, k, nullptr, nullptr, &kp);
+    hs::GemmArgs g;
+    g.a = a; g.w = w; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
+    g.bias = bias; g.mult = mult; g.shift = shift; g.out = out; g.ldo = (int)n;
+    HIP_TRY(hs::launch_gemm(Epi::Act, g, stream ? (hipStream_t)stream : dev->stream));
+    return HS_OK;
+}
+
+extern "C" hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, const int8_t *k_cache,
+                                             const int8_t *v_cache, const uint32_t *ctx, size_t b,
+                                             size_t h, size_t hd, size_t ctx_cap, int32_t score_m,
+                                             uint8_t score_s, int32_t out_m, uint8_t out_s,
+                                             const int32_t *attn_exp, size_t len, uint8_t softmax_p,
+                                             int8_t *out, void *stream) {
+    hs::clear_error();
+    if (!dev || !q || !k_cache || !v_cache || !ctx || !attn_exp || !out)
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (hd == 0 || hd % 4 != 0 || hd > 256 || h == 0 || len == 0 || softmax_p > 30 || ctx_cap == 0)
+        return hs::fail(HS_UNSUPPORTED, 0, "head_dim must be a multiple of 4 in 4..=256; h, len and ctx_cap >= 1; P <= 30");
+    if (b == 0) return HS_OK;
+    hs::AttnArgs at;
+    at.rows = nullptr; at.keys = ctx; at.q = q; at.ldq = (int)(h * hd); at.kc = k_cache; at.vc = v_cache;
+    at.n_head = (int)h; at.hd = (int)hd; at.ctx_cap = (int)ctx_cap; at.score_m = score_m;
+    at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
+    at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
+    HIP_TRY(hs::launch_attend(at, (int)b, stream ? (hipStream_t)stream : dev->stream));
+    return HS_OK;
+}

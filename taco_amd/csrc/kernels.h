@@ -1,0 +1,93 @@
+// Launch wrappers of the gfx950 kernels (kernels.hip). All pointers are device pointers; every
+// launch goes on `stream`. The host checks shapes before it calls these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace hs {
+
+// One row of a pass: slot, token, position, and the packed output index (-1: no output).
+struct RowInfo {
+    int32_t slot, token, pos, out;
+};
+
+enum class Epi : int { Raw = 0, Act = 1, Residual = 2, Gelu = 3, Logits = 4 };
+
+struct GemmArgs {
+    const int8_t *a = nullptr;  // [m_pad, k_pad]
+    const int8_t *w = nullptr;  // [n_pad, k_pad]
+    int m = 0, n = 0, k_pad = 0;
+    const int32_t *bias = nullptr;  // [n] (Act, Residual, Gelu)
+    const int32_t *mult = nullptr;  // [n]
+    int shift = 0;
+    void *out = nullptr;  // Raw: i32; Act/Gelu: i8; Residual: i32 x (read-modify-write); Logits: i64
+    int ldo = 0;          // elements per output row
+    const int8_t *gelu = nullptr;  // Gelu table, i8 entries
+    int gelu_off = 0;              // 128 or 32768
+};
+
+// Tile sizes of the MFMA GEMM: w and a rows are padded to these multiples, k to 64.
+constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 64;
+
+hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream);
+
+hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_ld,
+                        const int8_t *wpe, const int32_t *embed_m, int embed_s,
+                        const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream);
+
+struct LnArgs {
+    const int32_t *x = nullptr;  // [rows, d]
+    int d = 0;
+    const int16_t *gamma = nullptr;
+    const int32_t *beta = nullptr;
+    int32_t m = 0;
+    int s = 0;
+    int beta_frac = 0;
+    int k = 0, j = 0;
+    uint64_t eps = 1;
+    int8_t *out = nullptr;  // [rows, ldo]
+    int ldo = 0;
+    const int32_t *src = nullptr;  // optional: output row i reads x row src[i]
+};
+hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream);
+
+// K and V of each row into the caches [L][slots][H][n_ctx][hd] (layer base pointers given).
+hipError_t launch_kv_store(const RowInfo *rows, int n_rows, const int8_t *qkv, int d, int n_head,
+                           int hd, int n_ctx, int8_t *kc, int8_t *vc, hipStream_t stream);
+
+struct AttnArgs {
+    const RowInfo *rows = nullptr;
+    const int8_t *q = nullptr;  // row r, head h at q[r * ldq + h * hd]
+    int ldq = 0;
+    const int8_t *kc = nullptr, *vc = nullptr;  // [slots][H][ctx_cap][hd] (one layer)
+    int n_head = 0, hd = 0, ctx_cap = 0;
+    const uint32_t *keys = nullptr;  // optional: keys of row r (default rows[r].pos + 1)
+    int32_t score_m = 0;
+    int score_s = 0;
+    int32_t out_m = 0;
+    int out_s = 0;
+    const int32_t *exp_table = nullptr;
+    int exp_len = 0;
+    int softmax_p = 0;
+    int8_t *out = nullptr;  // row r, head h at out[r * ldo + h * hd]
+    int ldo = 0;
+};
+hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream);
+
+struct CoderArgs {
+    const int64_t *logits = nullptr;  // [rows, ld]
+    int ld = 0;
+    int vocab = 0;
+    const uint64_t *table = nullptr;  // logits_exp
+    int table_len = 0;
+    const uint32_t *queries = nullptr;  // [rows][2]: kind, value
+    int bits = 32;
+    uint64_t *intervals = nullptr;  // [rows][3]
+    uint64_t *weights = nullptr;    // optional [rows, vocab]: the weights themselves
+};
+hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream);
+
+}  // namespace hs

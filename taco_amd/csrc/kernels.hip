@@ -1,0 +1,593 @@
+// gfx950 (CDNA4, MI355X) kernels of the HardShell forward pass. Integer only; every result is
+// the exact value of the reference CPU rule it cites (crates/hardshell/src/...). No atomics: all
+// reductions are fixed-order wave/LDS trees, so results do not depend on scheduling.
+#include <hip/hip_runtime.h>
+
+#include "kernels.h"
+
+namespace hs {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+constexpr int32_t RES = (1 << 30) - 1;             // gpt2/mod.rs:116
+constexpr int64_t SCORE_LIMIT = (int64_t)1 << 40;  // gpt2/mod.rs:119
+
+// ---- integer rules (crates/hardshell/src/int.rs) ------------------------------------------
+
+// floor((p + 2^(s-1)) / 2^s) for |p| < 2^63 (int.rs:110-124 with max shift >= 63: for s >= 64
+// the exact result is 0). Never overflows: the low s bits round separately.
+__device__ __forceinline__ int64_t shift_round64(int64_t p, uint32_t s) {
+    if (s == 0) return p;
+    if (s >= 64) return 0;
+    const uint64_t r = (uint64_t)p & (((uint64_t)1 << s) - 1);
+    const uint64_t up = (r + ((uint64_t)1 << (s - 1))) >> s;
+    return (p >> s) + (int64_t)up;
+}
+
+// rescale(x, m, s) for |x| < 2^32: the product is exact in i64.
+__device__ __forceinline__ int64_t rescale_small(int64_t x, int32_t m, uint32_t s) {
+    return shift_round64(x * (int64_t)m, s);
+}
+
+__device__ __forceinline__ i128 shift_round128(i128 p, uint32_t s, uint32_t max_shift) {
+    if (s == 0) return p;
+    if (s > max_shift) return 0;
+    const u128 half = (u128)1 << (s - 1);
+    return (i128)((u128)p + half) >> s;
+}
+
+// rescale (int.rs:63-67) for any i64 x.
+__device__ __forceinline__ i128 rescale_full(int64_t x, int32_t m, uint32_t s) {
+    return shift_round128((i128)x * (i128)m, s, 95);
+}
+
+__device__ __forceinline__ int64_t clamp64(int64_t x, int64_t lo, int64_t hi) {
+    int64_t u = x < hi ? x : hi;
+    return u > lo ? u : lo;
+}
+
+__device__ __forceinline__ int64_t clamp128(i128 x, int64_t lo, int64_t hi) {
+    i128 u = x < (i128)hi ? x : (i128)hi;
+    return (int64_t)(u > (i128)lo ? u : (i128)lo);
+}
+
+__device__ __forceinline__ int64_t floor_div64(int64_t a, int64_t b) {
+    int64_t q = a / b, r = a % b;
+    return (r != 0 && r < 0) ? q - 1 : q;
+}
+
+// isqrt_u128 (int.rs:213-233): exact floor square root, bitwise.
+__device__ u128 isqrt128(u128 x) {
+    u128 bit = (u128)1 << 126;
+    while (bit > x) bit >>= 2;
+    u128 rem = x, res = 0;
+    while (bit != 0) {
+        if (rem >= res + bit) {
+            rem -= res + bit;
+            res = (res >> 1) + bit;
+        } else {
+            res >>= 1;
+        }
+        bit >>= 2;
+    }
+    return res;
+}
+
+// ---- wave reductions (wave64) -------------------------------------------------------------
+
+__device__ __forceinline__ int64_t wave_max64(int64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        int64_t u = __shfl_xor(v, o, 64);
+        v = u > v ? u : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// =============================================================================================
+// Int8 GEMM on MFMA: C[m][n] = sum_k A[m][k] * W[n][k] (both operands K-contiguous, "NT"),
+// exact int32 (|C| <= 2^30 for K <= 2^16, crates/hardshell/src/kernels.rs:24-29), with the
+// requantize epilogue of the op fused (crates/hardshell/src/gpt2/ops.rs:107-176).
+//
+// Tile 128 x 128 x 64, 256 threads = 4 waves in 2 x 2; each wave owns 64 x 64 = 4 x 4 tiles of
+// v_mfma_i32_16x16x64_i8. Operands go global -> registers -> LDS (double buffered, one
+// barrier per k-step); the next k-tile's global loads are in flight during the MFMAs.
+// =============================================================================================
+
+constexpr int LDS_STRIDE = GEMM_BK + 16;  // bytes per LDS row: 64 data + 16 pad (bank spread)
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][GEMM_BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) int8_t sW[2][GEMM_BN * LDS_STRIDE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * GEMM_BN;
+    const int K = g.k_pad, nk = K / GEMM_BK;
+    const int8_t *A = g.a + (size_t)m0 * K;
+    const int8_t *W = g.w + (size_t)n0 * K;
+
+    // Each thread moves two 16-byte chunks of each 128 x 64 tile: chunk c -> row c / 4,
+    // column 16 * (c % 4).
+    const int c0 = tid, c1 = tid + 256;
+    const int r0 = c0 >> 2, q0 = (c0 & 3) * 16, r1 = c1 >> 2, q1 = (c1 & 3) * 16;
+    v4i ra0, ra1, rw0, rw1;
+    auto gload = [&](int kt) {
+        const int kk = kt * GEMM_BK;
+        ra0 = *(const v4i *)(A + (size_t)r0 * K + kk + q0);
+        ra1 = *(const v4i *)(A + (size_t)r1 * K + kk + q1);
+        rw0 = *(const v4i *)(W + (size_t)r0 * K + kk + q0);
+        rw1 = *(const v4i *)(W + (size_t)r1 * K + kk + q1);
+    };
+    auto sstore = [&](int st) {
+        *(v4i *)(&sA[st][r0 * LDS_STRIDE + q0]) = ra0;
+        *(v4i *)(&sA[st][r1 * LDS_STRIDE + q1]) = ra1;
+        *(v4i *)(&sW[st][r0 * LDS_STRIDE + q0]) = rw0;
+        *(v4i *)(&sW[st][r1 * LDS_STRIDE + q1]) = rw1;
+    };
+
+    v4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    const int frow = lane & 15, fk = (lane >> 4) * 16;
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        v4i af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            af[i] = *(const v4i *)(&sA[cur][(wm * 64 + i * 16 + frow) * LDS_STRIDE + fk]);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            bf[j] = *(const v4i *)(&sW[cur][(wn * 64 + j * 16 + frow) * LDS_STRIDE + fk]);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        if (kt + 1 < nk) sstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds C[4 * (lane / 16) + e][lane % 16] of each 16 x 16 tile.
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + wn * 64 + j * 16 + (lane & 15);
+        if (n >= g.n) continue;
+        int32_t bias = 0, mult = 0;
+        if (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu) bias = g.bias[n];
+        if (EPI != (int)Epi::Raw) mult = g.mult[n];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + e;
+                if (m >= g.m) continue;
+                const int32_t a = acc[i][j][e];
+                const size_t o = (size_t)m * g.ldo + n;
+                if (EPI == (int)Epi::Raw) {
+                    ((int32_t *)g.out)[o] = a;
+                } else if (EPI == (int)Epi::Act) {  // ops.rs:123-130
+                    const int64_t y = rescale_small((int64_t)a + bias, mult, g.shift);
+                    ((int8_t *)g.out)[o] = (int8_t)clamp64(y, -127, 127);
+                } else if (EPI == (int)Epi::Residual) {  // ops.rs:131-145
+                    const int64_t y = clamp64(rescale_small((int64_t)a + bias, mult, g.shift),
+                                              -SCORE_LIMIT, SCORE_LIMIT);
+                    int32_t *x = (int32_t *)g.out + o;
+                    *x = (int32_t)clamp64((int64_t)*x + y, -RES, RES);
+                } else if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62
+                    const int64_t y = clamp64(rescale_small((int64_t)a + bias, mult, g.shift),
+                                              -g.gelu_off, g.gelu_off - 1);
+                    ((int8_t *)g.out)[o] = g.gelu[y + g.gelu_off];
+                } else {  // Logits: ops.rs:229-234
+                    ((int64_t *)g.out)[o] =
+                        clamp64(rescale_small(a, mult, g.shift), -SCORE_LIMIT, SCORE_LIMIT);
+                }
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream) {
+    dim3 grid((g.n + GEMM_BN - 1) / GEMM_BN, (g.m + GEMM_BM - 1) / GEMM_BM);
+    switch (epi) {
+        case Epi::Raw: hipLaunchKernelGGL(k_gemm<0>, grid, dim3(256), 0, stream, g); break;
+        case Epi::Act: hipLaunchKernelGGL(k_gemm<1>, grid, dim3(256), 0, stream, g); break;
+        case Epi::Residual: hipLaunchKernelGGL(k_gemm<2>, grid, dim3(256), 0, stream, g); break;
+        case Epi::Gelu: hipLaunchKernelGGL(k_gemm<3>, grid, dim3(256), 0, stream, g); break;
+        case Epi::Logits: hipLaunchKernelGGL(k_gemm<4>, grid, dim3(256), 0, stream, g); break;
+    }
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// Embedding (reference.rs:208-221): x = clamp(rescale(wte[tok]) + rescale(wpe[pos]), -R, R).
+// =============================================================================================
+
+__global__ void k_embed(const RowInfo *rows, const int8_t *wte, int wte_ld, const int8_t *wpe,
+                        const int32_t *embed_m, int embed_s, const int32_t *pos_m, int pos_s,
+                        int d, int32_t *x) {
+    const int r = blockIdx.y, j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= d) return;
+    const RowInfo ri = rows[r];
+    const int64_t v = rescale_small(wte[(size_t)ri.token * wte_ld + j], embed_m[ri.token], embed_s) +
+                      rescale_small(wpe[(size_t)ri.pos * d + j], pos_m[ri.pos], pos_s);
+    x[(size_t)r * d + j] = (int32_t)clamp64(v, -RES, RES);
+}
+
+hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_ld,
+                        const int8_t *wpe, const int32_t *embed_m, int embed_s,
+                        const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream) {
+    dim3 grid((d + 255) / 256, n_rows);
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_ld, wpe, embed_m,
+                       embed_s, pos_m, pos_s, d, x);
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// Integer LayerNorm (crates/hardshell/src/layernorm.rs:201-256), one workgroup per row:
+// mean = floor(sum / n); var = floor(sum (x - mean)^2 / n) in u128; inv = 2^K / isqrt(var *
+// 2^2J + eps); y = rescale_wide((x - mean) * inv * gamma, m, s) + beta (or the one-rounding form
+// with beta_frac); out = clamp(y, -127, 127).
+// =============================================================================================
+
+__global__ __launch_bounds__(256) void k_layernorm(LnArgs a) {
+    __shared__ int64_t s_sum[256];
+    __shared__ u128 s_sq[256];
+    __shared__ int64_t s_mean;
+    __shared__ uint64_t s_inv;
+    const int row = blockIdx.x, tid = threadIdx.x, d = a.d;
+    const int src = a.src ? a.src[row] : row;
+    const int32_t *x = a.x + (size_t)src * d;
+    int64_t sum = 0;
+    for (int j = tid; j < d; j += 256) sum += x[j];
+    s_sum[tid] = sum;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) s_sum[tid] += s_sum[tid + o];
+        __syncthreads();
+    }
+    const int64_t mean = floor_div64(s_sum[0], d);
+    u128 sq = 0;
+    for (int j = tid; j < d; j += 256) {
+        const int64_t c = (int64_t)x[j] - mean;
+        const uint64_t u = c < 0 ? (uint64_t)(-c) : (uint64_t)c;
+        sq += (u128)u * u;
+    }
+    s_sq[tid] = sq;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) s_sq[tid] += s_sq[tid + o];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const u128 var = s_sq[0] / (u128)(uint32_t)d;
+        const u128 root = isqrt128((var << (2 * a.j)) + (u128)a.eps);
+        const u128 inv = ((u128)1 << a.k) / (root > 0 ? root : 1);
+        s_mean = mean;
+        s_inv = (uint64_t)inv;
+    }
+    __syncthreads();
+    const i128 inv = (i128)(u128)s_inv;
+    const int64_t mn = s_mean;
+    for (int j = tid; j < d; j += 256) {
+        const i128 t = (i128)((int64_t)x[j] - mn) * inv * (i128)a.gamma[j];
+        const i128 p = (i128)((u128)t * (u128)(i128)a.m);  // wrapping, as rescale_wide
+        i128 y;
+        if (a.beta_frac == 0) {
+            y = shift_round128(p, a.s, 126) + (i128)a.beta[j];
+        } else {
+            const i128 c = (i128)a.beta[j] << (a.s - a.beta_frac);
+            y = shift_round128((i128)((u128)p + (u128)c), a.s, 126);
+        }
+        a.out[(size_t)row * a.ldo + j] = (int8_t)clamp128(y, -127, 127);
+    }
+}
+
+hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
+    if (n_rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_layernorm, dim3(n_rows), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// K and V of each row into the cache at the row's position (reference.rs:246-252).
+// Cache layout of one layer: [slot][head][position][hd].
+// =============================================================================================
+
+__global__ void k_kv_store(const RowInfo *rows, const int8_t *qkv, int d, int n_head, int hd,
+                           int n_ctx, int8_t *kc, int8_t *vc) {
+    const int r = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= d) return;
+    const RowInfo ri = rows[r];
+    const int h = c / hd, cc = c - h * hd;
+    const size_t o = (((size_t)ri.slot * n_head + h) * n_ctx + ri.pos) * hd + cc;
+    kc[o] = qkv[(size_t)r * 3 * d + d + c];
+    vc[o] = qkv[(size_t)r * 3 * d + 2 * d + c];
+}
+
+hipError_t launch_kv_store(const RowInfo *rows, int n_rows, const int8_t *qkv, int d, int n_head,
+                           int hd, int n_ctx, int8_t *kc, int8_t *vc, hipStream_t stream) {
+    dim3 grid((d + 255) / 256, n_rows);
+    hipLaunchKernelGGL(k_kv_store, grid, dim3(256), 0, stream, rows, qkv, d, n_head, hd, n_ctx,
+                       kc, vc);
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// Causal integer attention (reference.rs:254-283, softmax.rs:78-104): one wave per (row, head)
+// over the keys 0..pos of the row's slot. Three passes over the keys: the max score, the sum of
+// the table entries, then p = floor(e * 2^P / S) and sum p * v in i64. Dots with v_dot4_i32_i8.
+// =============================================================================================
+
+__device__ __forceinline__ int32_t dot_key(const int *q4, const int8_t *k, int hd) {
+    int32_t s = 0;
+    const int *k4 = (const int *)k;
+    for (int c = 0; c < hd / 4; c++) s = __builtin_amdgcn_sdot4(q4[c], k4[c], s, false);
+    return s;
+}
+
+__global__ __launch_bounds__(256) void k_attend(AttnArgs a, int n_tasks) {
+    __shared__ __attribute__((aligned(16))) int s_q[4][64];  // hd <= 256 bytes per wave
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int task = blockIdx.x * 4 + wave;
+    const bool valid = task < n_tasks;
+    const int r = valid ? task / a.n_head : 0, h = valid ? task % a.n_head : 0;
+    const int hd = a.hd;
+    int slot, keys;
+    if (a.rows) {
+        slot = a.rows[r].slot;
+        keys = a.keys ? (int)a.keys[r] : a.rows[r].pos + 1;
+    } else {
+        slot = r;
+        keys = (int)a.keys[r];
+    }
+    keys = keys < 1 ? 1 : (keys > a.ctx_cap ? a.ctx_cap : keys);  // never read past the cache
+    if (valid && lane < hd / 4) s_q[wave][lane] = ((const int *)(a.q + (size_t)r * a.ldq + h * hd))[lane];
+    __syncthreads();
+    if (!valid) return;
+    const int *q4 = s_q[wave];
+    const size_t base = ((size_t)slot * a.n_head + h) * a.ctx_cap * hd;
+    const int8_t *K = a.kc + base, *V = a.vc + base;
+    const int last = a.exp_len - 1;
+
+    // pass 1: M = max score
+    int64_t mx = INT64_MIN;
+    for (int j = lane; j < keys; j += 64) {
+        const int64_t s = clamp64(rescale_small(dot_key(q4, K + (size_t)j * hd, hd), a.score_m,
+                                                a.score_s), -SCORE_LIMIT, SCORE_LIMIT);
+        mx = s > mx ? s : mx;
+    }
+    mx = wave_max64(mx);
+    // pass 2: S = sum e_j
+    int64_t sum = 0;
+    for (int j = lane; j < keys; j += 64) {
+        const int64_t s = clamp64(rescale_small(dot_key(q4, K + (size_t)j * hd, hd), a.score_m,
+                                                a.score_s), -SCORE_LIMIT, SCORE_LIMIT);
+        const int64_t dd = mx - s;
+        sum += a.exp_table[dd < last ? dd : last];
+    }
+    sum = wave_sum64(sum);
+    // pass 3: p_j and the weighted sum of the values (c = lane + 64 t)
+    int64_t acc[4] = {0, 0, 0, 0};
+    for (int j0 = 0; j0 < keys; j0 += 64) {
+        const int j = j0 + lane;
+        uint64_t p = 0;
+        if (j < keys) {
+            const int64_t s = clamp64(rescale_small(dot_key(q4, K + (size_t)j * hd, hd), a.score_m,
+                                                    a.score_s), -SCORE_LIMIT, SCORE_LIMIT);
+            const int64_t dd = mx - s;
+            const uint64_t e = (uint64_t)a.exp_table[dd < last ? dd : last];
+            p = (e << a.softmax_p) / (uint64_t)sum;
+        }
+        const int cnt = keys - j0 < 64 ? keys - j0 : 64;
+        for (int jj = 0; jj < cnt; jj++) {
+            const int64_t pj = (int64_t)__shfl(p, jj, 64);
+            const int8_t *v = V + (size_t)(j0 + jj) * hd;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int c = lane + 64 * t;
+                if (c < hd) acc[t] += pj * (int64_t)v[c];
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int c = lane + 64 * t;
+        if (c < hd)
+            a.out[(size_t)r * a.ldo + h * hd + c] =
+                (int8_t)clamp128(rescale_full(acc[t], a.out_m, a.out_s), -127, 127);
+    }
+}
+
+hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
+    const int tasks = n_rows * a.n_head;
+    if (tasks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_attend, dim3((tasks + 3) / 4), dim3(256), 0, stream, a, tasks);
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// The coder op: logits -> weights (logits.rs:62-72) -> the interval of FreqTable::from_weights
+// (crates/taco-coder/src/freq.rs:103-149) for an Encode(token) or Decode(target) query.
+// One workgroup per row; thread t owns the symbols [t * chunk, (t + 1) * chunk).
+// f_i = 1 + floor(w_i * spare / W) with an exact quotient: a 64-bit reciprocal of W and one
+// correction step (W >= 2^32), or a plain u64 division (W < 2^32).
+// =============================================================================================
+
+__device__ __forceinline__ uint64_t quotient(uint64_t w, uint64_t spare, uint64_t W, uint64_t frac) {
+    if (W < ((uint64_t)1 << 32)) return (w * spare) / W;  // w <= W < 2^32: no overflow
+    uint64_t est = __umul64hi(w, frac);                   // floor(w * frac / 2^64) <= q
+    const u128 num = (u128)w * spare;
+    if (num - (u128)est * W >= W) est++;  // q - est is 0 or 1
+    return est;
+}
+
+__global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
+    __shared__ int64_t s_i64[256];
+    __shared__ uint64_t s_u64[256];
+    __shared__ uint32_t s_idx[256];
+    __shared__ uint64_t s_W, s_frac;
+    __shared__ uint32_t s_largest;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int V = a.vocab;
+    const int chunk = (V + 255) / 256;
+    const int j0 = tid * chunk, j1 = min(V, j0 + chunk);
+    const int64_t *l = a.logits + (size_t)row * a.ld;
+    const int last = a.table_len - 1;
+
+    // pass 1: the largest logit
+    int64_t mx = INT64_MIN;
+    for (int j = j0; j < j1; j++) mx = l[j] > mx ? l[j] : mx;
+    s_i64[tid] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) s_i64[tid] = s_i64[tid + o] > s_i64[tid] ? s_i64[tid + o] : s_i64[tid];
+        __syncthreads();
+    }
+    const int64_t M = s_i64[0];
+    __syncthreads();
+    // pass 2: W = sum w and the largest weight (the lowest id on a tie)
+    uint64_t W = 0, best = 0;
+    uint32_t bidx = 0xFFFFFFFFu;
+    for (int j = j0; j < j1; j++) {
+        const int64_t dd = M - l[j];
+        const uint64_t w = a.table[dd < last ? dd : last];
+        if (a.weights) a.weights[(size_t)row * V + j] = w;
+        W += w;
+        if (bidx == 0xFFFFFFFFu || w > best) {
+            best = w;
+            bidx = j;
+        }
+    }
+    s_u64[tid] = W;
+    s_i64[tid] = (int64_t)best;
+    s_idx[tid] = bidx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) {
+            s_u64[tid] += s_u64[tid + o];
+            const uint64_t b0 = (uint64_t)s_i64[tid], b1 = (uint64_t)s_i64[tid + o];
+            const uint32_t i0 = s_idx[tid], i1 = s_idx[tid + o];
+            // the larger weight wins; on a tie the lower index (i1 > i0 whenever both valid)
+            if (i0 == 0xFFFFFFFFu || (i1 != 0xFFFFFFFFu && b1 > b0)) {
+                s_i64[tid] = (int64_t)b1;
+                s_idx[tid] = i1;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        uint64_t Wt = s_u64[0];
+        uint32_t largest = s_idx[0];
+        if (Wt == 0) {  // every weight 0: every weight is 1 (freq.rs:119-123)
+            Wt = (uint64_t)V;
+            largest = 0;
+        }
+        const uint64_t total = (uint64_t)1 << a.bits;
+        const uint64_t spare = total - (uint64_t)V;
+        s_W = Wt;
+        s_largest = largest;
+        s_frac = Wt >= ((uint64_t)1 << 32) ? (uint64_t)(((u128)spare << 64) / Wt) : 0;
+    }
+    __syncthreads();
+    const uint64_t Wt = s_W, frac = s_frac;
+    const bool all_zero = s_u64[0] == 0;
+    const uint32_t largest = s_largest;
+    const uint64_t total = (uint64_t)1 << a.bits, spare = total - (uint64_t)V;
+    const uint32_t kind = a.queries ? a.queries[2 * row] : 0;
+    const uint32_t value = a.queries ? a.queries[2 * row + 1] : 0;
+    // pass 3: the sum of f over the chunk, and over the symbols below the encode token
+    uint64_t F = 0, Fbelow = 0, ftok = 0;
+    for (int j = j0; j < j1; j++) {
+        const int64_t dd = M - l[j];
+        const uint64_t w = all_zero ? 1 : a.table[dd < last ? dd : last];
+        const uint64_t f = 1 + quotient(w, spare, Wt, frac);
+        F += f;
+        if (kind == 0 && (uint32_t)j < value) Fbelow += f;
+        if (kind == 0 && (uint32_t)j == value) ftok = f;
+    }
+    __syncthreads();
+    s_u64[tid] = F;
+    __syncthreads();
+    if (tid == 0) {  // exclusive scan of the chunk sums, in order
+        uint64_t run = 0;
+        for (int t = 0; t < 256; t++) {
+            const uint64_t v = s_u64[t];
+            s_u64[t] = run;
+            run += v;
+        }
+        s_W = run;  // sum of all f
+    }
+    __syncthreads();
+    const uint64_t base = s_u64[tid];
+    const uint64_t Q = s_W;
+    const uint64_t rem = total - Q;
+    uint64_t *out = a.intervals ? a.intervals + 3 * (size_t)row : nullptr;
+    if (!out) return;
+    if (kind == 0) {
+        // start = sum_{j < tok} f_j (+ rem if the largest is below tok); the owner writes it
+        const uint32_t tok = value;
+        if ((int)tok >= j0 && (int)tok < j1) {
+            const uint64_t start = base + Fbelow + (largest < tok ? rem : 0);
+            const uint64_t freq = ftok + (largest == tok ? rem : 0);
+            out[0] = tok;
+            out[1] = start;
+            out[2] = freq;
+        }
+        return;
+    }
+    // Decode: the largest i with start_i <= target; starts increase with i.
+    const uint64_t target = value;
+    uint64_t run = base;
+    int cand = -1;
+    uint64_t cstart = 0, cfreq = 0;
+    for (int j = j0; j < j1; j++) {
+        const int64_t dd = M - l[j];
+        const uint64_t w = all_zero ? 1 : a.table[dd < last ? dd : last];
+        const uint64_t f = 1 + quotient(w, spare, Wt, frac);
+        const uint64_t start = run + ((uint32_t)j > largest ? rem : 0);
+        run += f;
+        if (start <= target) {
+            cand = j;
+            cstart = start;
+            cfreq = f + ((uint32_t)j == largest ? rem : 0);
+        } else {
+            break;
+        }
+    }
+    __syncthreads();
+    s_i64[tid] = cand;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) s_i64[tid] = s_i64[tid + o] > s_i64[tid] ? s_i64[tid + o] : s_i64[tid];
+        __syncthreads();
+    }
+    if (cand >= 0 && cand == s_i64[0]) {
+        out[0] = (uint64_t)cand;
+        out[1] = cstart;
+        out[2] = cfreq;
+    }
+}
+
+hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream) {
+    if (n_rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_coder, dim3(n_rows), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace hs

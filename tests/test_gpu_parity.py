@@ -1,0 +1,295 @@
+"""GPU parity: the HIP path through the C ABI against the oracle and the reference's golden
+vectors. Every comparison is bit-exact."""
+
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.conftest import GOLDEN, splitmix_tokens
+from tests.test_oracle import (GOLDEN_MODEL, GOLDEN_OUTPUT, GOLDEN_OVERLAP_OUTPUT, read_container,
+                               vocab_of, weights_hash)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from taco_amd import hip
+    return hip.HipDevice.open(0)
+
+
+@pytest.fixture(scope="module")
+def golden(dev):
+    from taco_amd import hip
+    b = O.build_model(O.tiny_dims(), 0x7AC0_0001, 64)
+    assert hashlib.sha256(b).hexdigest() == GOLDEN_MODEL
+    return b, hip.HipModel.load(dev, b), O.Model(b)
+
+
+# The CUDA matmul test shapes (crates/hardshell-cuda/tests/ops.rs:29-60): (rows, cols, inputs).
+GEMM_SHAPES = [(1, 1, 1), (3, 5, 2), (64, 64, 1), (65, 63, 7), (128, 128, 128), (300, 64, 17),
+               (768, 768, 9), (2304, 768, 256), (1000, 64, 513), (50, 3072, 33)]
+
+
+@pytest.mark.parametrize("n,k,m", GEMM_SHAPES)
+def test_gemm_i8_is_the_exact_product(dev, n, k, m):
+    from taco_amd import hip
+    print(f"gemm n={n} k={k} m={m}", flush=True)
+    r = np.random.default_rng(n * 7919 + k * 31 + m)
+    w = r.integers(-128, 128, (n, k)).astype(np.int8)
+    a = r.integers(-128, 128, (m, k)).astype(np.int8)
+    got = hip.matmul_i8(dev, w, a)
+    want = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(got, want)
+
+
+def test_gemm_i8_worst_case_at_the_bound(dev):
+    # kernels.rs:112-119: 2^16 products of (-128) * (-128) sum to exactly 2^30.
+    from taco_amd import hip
+    k = 1 << 16
+    w = np.full((3, k), -128, np.int8)
+    a = np.full((2, k), -128, np.int8)
+    a[1, ::2] = 127
+    got = hip.matmul_i8(dev, w, a)
+    assert got[0].tolist() == [1 << 30] * 3
+    assert got[1].tolist() == [(k // 2) * (-128 * 127) + (k // 2) * (1 << 14)] * 3
+
+
+def test_gemm_requant_c1_shape(dev):
+    # The c_attn linear at GPT-2-small shape: A [256, 768], W [2304, 768], per-channel m, one s.
+    from taco_amd import hip
+    r = np.random.default_rng(1)
+    a = r.integers(-127, 128, (256, 768)).astype(np.int8)
+    w = r.integers(-127, 128, (2304, 768)).astype(np.int8)
+    bias = r.integers(-(1 << 16), 1 << 16, 2304).astype(np.int32)
+    mult = r.integers(1 << 30, 1 << 31, 2304).astype(np.int64).astype(np.int32)
+    for shift in (42, 0, 1, 62, 63, 64, 95, 96):
+        got = hip.gemm_requant_i8(dev, w, a, bias, mult, shift)
+        want = O.linear_act_ref(w, a, bias, mult, shift)
+        assert np.array_equal(got, want), shift
+    # negative multipliers and extremes
+    mult2 = r.integers(-(1 << 31), 1 << 31, 2304).astype(np.int64).astype(np.int32)
+    mult2[:4] = [-(1 << 31), (1 << 31) - 1, 0, -1]
+    got = hip.gemm_requant_i8(dev, w, a, bias, mult2, 40)
+    assert np.array_equal(got, O.linear_act_ref(w, a, bias, mult2, 40))
+
+
+def test_golden_output_hash_on_gpu(golden):
+    # crates/hardshell/tests/gpt2.rs:203-226 through the GPU step path (150 tokens, 1 restart).
+    from taco_amd import hip
+    _, hm, _ = golden
+    s = hip.HipSession(hm)
+    rows = [s.start_block()] + [s.step(t) for t in splitmix_tokens(0x7AC0_0002, 150, 300)]
+    assert weights_hash(rows) == GOLDEN_OUTPUT
+
+
+def test_golden_overlap_hash_on_gpu(golden):
+    # crates/hardshell/tests/context.rs:321-353: overlap 32, 300 tokens, 8 restarts.
+    from taco_amd import hip
+    _, hm, _ = golden
+    s = hip.HipSession(hm, overlap=32)
+    rows = [s.start_block()] + [s.step(t) for t in splitmix_tokens(0x7AC0_0002, 300, 300)]
+    assert weights_hash(rows) == GOLDEN_OVERLAP_OUTPUT
+
+
+@pytest.mark.parametrize("max_rows", [2, 5, 40, 64, 200])
+def test_prefill_passes_equal_the_reference(golden, max_rows):
+    # Prefill of 151 rows in passes of max_rows (crates/hardshell-cuda/tests/gpt2.rs:33-112).
+    from taco_amd import hip
+    _, hm, om = golden
+    toks = splitmix_tokens(0x7AC0_0002, 150, 300)
+    s = O.Session(om)
+    want = np.array([s.start_block()] + [s.step(t) for t in toks])
+    b = hip.HipBatch(hm, 1, max_rows)
+    got = b.run_weights([(0, 299)] + [(0, t) for t in toks])
+    assert np.array_equal(got, want)
+    assert b.position(0) == s.position()  # two restarts at n_ctx 64
+
+
+def test_batch_of_slots_equals_independent_sessions(golden):
+    from taco_amd import hip
+    _, hm, om = golden
+    slots = 5
+    seqs = [splitmix_tokens(100 + s, 40 + 7 * s, 299) for s in range(slots)]
+    want = []
+    for seq in seqs:
+        s = O.Session(om)
+        want.append([s.start_block()] + [s.step(t) for t in seq[:-1]])
+    b = hip.HipBatch(hm, slots, 97)
+    # interleave: each call gives every slot a run of its next tokens
+    got = [[] for _ in range(slots)]
+    done = [0] * slots
+    while any(done[s] < len(seqs[s]) for s in range(slots)):
+        inputs, owner = [], []
+        for s in range(slots):
+            take = min(len(seqs[s]) - done[s], 3 + s)
+            for i in range(done[s], done[s] + take):
+                tok = 299 if i == 0 else seqs[s][i - 1]
+                inputs.append((s, tok))
+                owner.append(s)
+            done[s] += take
+        w = b.run_weights(inputs)
+        for o, row in zip(owner, w):
+            got[o].append(row)
+    for s in range(slots):
+        assert np.array_equal(np.array(got[s]), np.array(want[s])), s
+
+
+def test_coded_intervals_equal_from_weights(golden):
+    from taco_amd import hip
+    _, hm, om = golden
+    toks = splitmix_tokens(0x5EED, 63, 300)
+    s = O.Session(om)
+    weights = [s.start_block()] + [s.step(t) for t in toks[:-1]]
+    b = hip.HipBatch(hm, 1, 64)
+    inputs = [(0, 299)] + [(0, t) for t in toks[:-1]]
+    enc = b.run_coded(inputs, [(0, t) for t in toks], 32)
+    for i, (w, iv) in enumerate(zip(weights, enc)):
+        st, fr = O.freq_interval(w, 32, toks[i])
+        assert (iv.symbol, iv.start, iv.freq) == (toks[i], st, fr), i
+        assert iv.is_last == (st + fr == 1 << 32)
+    # decode queries: targets 0, T/3, T-1 and random ones, and a smaller total (freq_bits 20)
+    r = np.random.default_rng(2)
+    for bits in (32, 20, 9):
+        targets = [0, (1 << bits) // 3, (1 << bits) - 1] + [int(x) for x in r.integers(0, 1 << bits, 60)]
+        b.reset(0)
+        dec = b.run_coded(inputs, [(1, targets[i % len(targets)]) for i in range(len(inputs))], bits)
+        for i, (w, iv) in enumerate(zip(weights, dec)):
+            t = targets[i % len(targets)]
+            assert (iv.symbol, iv.start, iv.freq) == O.freq_find(w, bits, t), (bits, i)
+
+
+def test_refusals_keep_positions(golden):
+    from taco_amd import hip
+    _, hm, _ = golden
+    b = hip.HipBatch(hm, 2, 8)
+    b.run_weights([(0, 299), (0, 5)])
+    with pytest.raises(hip.BadSlot):
+        b.run_weights([(0, 1), (2, 1)])
+    with pytest.raises(hip.ModelError) as e:
+        b.run_weights([(0, 1), (1, 300)])
+    assert e.value.kind == "TokenOutOfRange"
+    with pytest.raises(hip.Unsupported):
+        b.run_coded([(0, 1)], [(0, 300)], 32)
+    with pytest.raises(hip.Unsupported):
+        b.run_coded([(0, 1)], [(0, 1)], 8)  # 2^8 < vocab
+    with pytest.raises(hip.ModelError):
+        b.set_overlap(63)
+    assert b.position(0) == 2 and b.position(1) == 0
+
+
+@pytest.mark.parametrize("name", ["predicted_text_k0", "predicted_text_k32", "all_kinds_text"])
+def test_conformance_blocks_through_the_gpu_coder(dev, name):
+    """The coded blocks of conformance/v2 decode on the GPU (Decode queries, one row per step,
+    as gpu_unfold.rs:143-160) and re-encode on the GPU to the same payload bytes."""
+    from taco_amd import hip
+    hsm = open(os.path.join(GOLDEN, "tiny.hsm"), "rb").read()
+    om = O.Model(hsm)
+    hm = hip.HipModel.load(dev, hsm)
+    vocab = vocab_of(hsm)
+    data = open(os.path.join(GOLDEN, name + ".taco"), "rb").read()
+    original = open(os.path.join(GOLDEN, name + ".in"), "rb").read()
+    c = read_container(data)
+    coded = [(i, p) for i, (k, p) in enumerate(c["blocks"]) if k == 1]
+    b = hip.HipBatch(hm, len(coded), 64)
+    b.set_overlap(c["overlap"])
+    # decode all coded blocks in lockstep, one slot each
+    decs, counts, toks = [], [], []
+    for _, payload in coded:
+        n, used = 0, 0
+        shift = 0
+        while True:
+            byte = payload[used]
+            n |= (byte & 0x7F) << shift
+            used += 1
+            shift += 7
+            if byte < 0x80:
+                break
+        decs.append(O.Decoder(payload[used:]))
+        counts.append(n)
+        toks.append([])
+    nxt = [299] * len(coded)
+    while any(len(toks[s]) < counts[s] for s in range(len(coded))):
+        live = [s for s in range(len(coded)) if len(toks[s]) < counts[s]]
+        ans = b.run_coded([(s, nxt[s]) for s in live], [(1, decs[s].target(32)) for s in live], 32)
+        for s, iv in zip(live, ans):
+            decs[s].decode_interval(iv.start, iv.freq, 32)
+            toks[s].append(iv.symbol)
+            nxt[s] = iv.symbol
+    for s, (i, payload) in enumerate(coded):
+        piece = original[i * c["block_size"]:(i + 1) * c["block_size"]]
+        assert b"".join(vocab[t] for t in toks[s]) == piece
+        assert O.encode_block(om, toks[s], overlap=c["overlap"]) == payload
+    # encode on the GPU: Encode queries over the whole block in one call (prefill)
+    b2 = hip.HipBatch(hm, len(coded), 512)
+    b2.set_overlap(c["overlap"])
+    inputs, queries = [], []
+    for s in range(len(coded)):
+        seq = toks[s]
+        inputs += [(s, 299)] + [(s, t) for t in seq[:-1]]
+        queries += [(0, t) for t in seq]
+    got = b2.run_coded_raw(inputs, queries, 32)
+    pos = 0
+    for s, (i, payload) in enumerate(coded):
+        n = len(toks[s])
+        ops = [[0, int(st), int(fr), 32] for _, st, fr in got[pos:pos + n]]
+        pos += n
+        body = O.encode_script(ops)
+        head = bytearray()
+        v = n
+        while True:
+            lo = v & 0x7F
+            v >>= 7
+            head.append(lo | (0x80 if v else 0))
+            if not v:
+                break
+        assert bytes(head) + body == payload
+
+
+@pytest.mark.parametrize("dims", [(1, 3, 60, 100, 300, 40), (1, 2, 40, 64, 260, 30),
+                                  (3, 2, 128, 200, 1000, 48)])
+def test_odd_dims_equal_the_reference(dev, dims):
+    from taco_amd import hip
+    b = O.build_model(dims, 9, 16)
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    toks = splitmix_tokens(12, dims[5] + 5, dims[4])
+    s = O.Session(om)
+    want = np.array([s.start_block()] + [s.step(t) for t in toks])
+    hb = hip.HipBatch(hm, 1, 13)
+    got = hb.run_weights([(0, om.eot)] + [(0, t) for t in toks])
+    assert np.array_equal(got, want)
+
+
+def test_head_dim_not_multiple_of_4_is_unsupported(dev):
+    from taco_amd import hip
+    b = O.build_model((1, 1, 33, 47, 270, 20), 9, 8)
+    with pytest.raises(hip.Unsupported):
+        hip.HipModel.load(dev, b)
+
+
+def test_attend_decode_op(dev):
+    """Config 3 shape, small: 8 streams x 12 heads x 64, ctx up to 300, against the oracle."""
+    import torch
+    from taco_amd import hip
+    r = np.random.default_rng(3)
+    B, H, hd, cap = 8, 12, 64, 320
+    q = r.integers(-127, 128, (B, H, hd)).astype(np.int8)
+    kc = r.integers(-127, 128, (B, H, cap, hd)).astype(np.int8)
+    vc = r.integers(-127, 128, (B, H, cap, hd)).astype(np.int8)
+    ctx = np.array([1, 2, 63, 64, 65, 128, 300, 320], np.uint32)
+    table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
+    score_m, score_s, out_m, out_s = 1_400_000_000, 33, 1_300_000_000, 53
+    want = O.attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, 30)
+    dq, dk, dv = (torch.from_numpy(x).cuda() for x in (q, kc, vc))
+    dctx, dt = torch.from_numpy(ctx.view(np.int32)).cuda(), torch.from_numpy(table).cuda()
+    out = torch.zeros((B, H * hd), dtype=torch.int8, device="cuda")
+    torch.cuda.synchronize()
+    hip._check(hip.lib().hs_op_attend_decode_dev(
+        dev.h, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dctx.data_ptr(), B, H, hd, cap,
+        score_m, score_s, out_m, out_s, dt.data_ptr(), len(table), 30, out.data_ptr(),
+        torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
