@@ -93,6 +93,9 @@ hs_status hs_device_memory(const hs_device *dev, size_t *free_bytes, size_t *tot
  * (crates/hardshell/src/gpt2/model.rs:292-343, hsm/reader.rs:357-430) and uploads it. */
 hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t len, hs_model **out);
 void hs_model_free(hs_model *model);
+/* Model::load on the host alone (gpt2/model.rs:292-343): validates the file with the same
+ * rules as hs_model_load and gives its SHA-256, without a device. HS_OK or HS_MODEL_ERROR. */
+hs_status hs_model_validate(const uint8_t *bytes, size_t len, uint8_t hash[32]);
 /* The SHA-256 of the model file (model.rs:353: CudaModel::hash). */
 void hs_model_hash(const hs_model *model, uint8_t out[32]);
 uint32_t hs_model_vocab(const hs_model *model);
@@ -128,6 +131,8 @@ void hs_batch_free(hs_batch *batch);
  * (HS_MODEL_INVALID_OVERLAP) if K > n_ctx - 2. */
 hs_status hs_batch_set_overlap(hs_batch *batch, uint32_t k);
 size_t hs_batch_slots(const hs_batch *batch);
+/* The model of the batch (CudaBatch<'m> holds &'m CudaModel). */
+const hs_model *hs_batch_model(const hs_batch *batch);
 size_t hs_batch_max_rows(const hs_batch *batch);
 uint64_t hs_batch_gpu_bytes(const hs_batch *batch);
 /* The number of tokens in the context of `slot` (0 for a slot that is not valid). */
@@ -181,6 +186,48 @@ hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, const int8_t 
                                   size_t hd, size_t ctx_cap, int32_t score_m, uint8_t score_s,
                                   int32_t out_m, uint8_t out_s, const int32_t *attn_exp,
                                   size_t len, uint8_t softmax_p, int8_t *out, void *stream);
+
+/* The coder op alone (the logits_weights + coder_interval kernels of
+ * crates/hardshell-cuda/kernels/hardshell.cu:1393-1611, no public counterpart; for tests): for
+ * each of `rows` rows of i64 logits [rows, vocab] (host pointers, each within +-2^40), the
+ * weights table[min(max - l, len - 1)] (crates/hardshell/src/logits.rs:62-72) and the interval
+ * of FreqTable::from_weights(weights, freq_bits) for queries[r] (Encode or Decode). */
+hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t rows, size_t vocab,
+                      const uint64_t *table, size_t len, const hs_query *queries,
+                      uint32_t freq_bits, hs_interval *out);
+
+/* The GPU time of `reps` launches of the requant GEMM on device operands (hipEvents on the
+ * device stream), as matmul_gpu_ns (crates/hardshell-cuda/src/ops.rs:284-335). */
+hs_status hs_op_gemm_requant_gpu_ns(hs_device *dev, const int8_t *w, const int8_t *a,
+                                    const int32_t *bias, const int32_t *mult, uint8_t shift,
+                                    size_t m, size_t n, size_t k, int8_t *out, size_t reps,
+                                    uint64_t *ns);
+/* The GPU time of `reps` launches of hs_op_attend_decode_dev (hipEvents on the device stream). */
+hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8_t *k_cache,
+                                     const int8_t *v_cache, const uint32_t *ctx, size_t b,
+                                     size_t h, size_t hd, size_t ctx_cap, int32_t score_m,
+                                     uint8_t score_s, int32_t out_m, uint8_t out_s,
+                                     const int32_t *attn_exp, size_t len, uint8_t softmax_p,
+                                     int8_t *out, size_t reps, uint64_t *ns);
+
+/* ---- Batch profiling: CudaBatch::profile (crates/hardshell-cuda/src/batch.rs:493-498) ----- */
+/* With profiling on, every kernel launch of the batch is bracketed by hipEvents on the batch's
+ * stream; hs_batch_profile gives, for each op label, the summed GPU nanoseconds, the launch
+ * count and the algorithmic int8 operations (2 per multiply-accumulate of the GEMMs). */
+hs_status hs_batch_set_profiling(hs_batch *batch, int on);
+/* Writes up to cap entries (labels are NUL-terminated in 32-byte slots); returns the number of
+ * labels. Clears the counters when `clear` is nonzero. */
+size_t hs_batch_profile(hs_batch *batch, char *labels, uint64_t *ns, uint64_t *launches,
+                        uint64_t *ops, size_t cap, int clear);
+
+/* ---- Device memory (test and measurement plumbing; the reference's device buffers,
+ * crates/hardshell-cuda/src/driver.rs:229-265, are crate-private, so these have no public
+ * counterpart). All copies are synchronous on the device stream. ---------------------------- */
+hs_status hs_device_alloc(hs_device *dev, size_t bytes, void **out);
+void hs_device_free(hs_device *dev, void *ptr);
+hs_status hs_device_upload(hs_device *dev, void *dst, const void *src, size_t bytes);
+hs_status hs_device_download(hs_device *dev, void *dst, const void *src, size_t bytes);
+hs_status hs_device_synchronize(hs_device *dev);
 
 #ifdef __cplusplus
 }

@@ -174,7 +174,7 @@ extern "C" hs_status hs_device_open(int ordinal, hs_device **out) {
         return hs::fail(HS_UNSUPPORTED, 0, "the kernels are built for gfx950 only; this device is " + arch);
     auto dev = std::make_unique<hs_device>();
     dev->ordinal = ordinal;
-    dev->name = prop.name;
+    dev->name = prop.name[0] ? std::string(prop.name) : "AMD " + arch;
     HIP_TRY(hipStreamCreate(&dev->stream));
     *out = dev.release();
     return HS_OK;
@@ -258,6 +258,17 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
 }
 
 extern "C" void hs_model_free(hs_model *model) { delete model; }
+
+extern "C" hs_status hs_model_validate(const uint8_t *bytes, size_t len, uint8_t hash[32]) {
+    hs::clear_error();
+    if (!bytes && len) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    hs::HostModel h;
+    hs::ModelError err{};
+    if (!hs::load_host_model(bytes ? bytes : (const uint8_t *)"", len, h, err))
+        return hs::fail(HS_MODEL_ERROR, err.kind, err.msg);
+    if (hash) std::memcpy(hash, h.hash, 32);
+    return HS_OK;
+}
 extern "C" void hs_model_hash(const hs_model *m, uint8_t out[32]) {
     if (m && out) std::memcpy(out, m->host.hash, 32);
 }
@@ -301,8 +312,70 @@ struct hs_batch {
     uint64_t *d_intervals = nullptr, *d_weights = nullptr;
     size_t chunk_rows = 0;
     std::vector<int8_t *> kc, vc;  // per layer: [slots][H][n_ctx][hd]
+    // Profiling (CudaBatch::profile): per-label GPU time from hipEvents around each launch.
+    struct ProfEntry {
+        std::string label;
+        uint64_t ns = 0, launches = 0, ops = 0;
+    };
+    struct Pending {
+        size_t entry;
+        hipEvent_t e0, e1;
+        uint64_t ops;
+    };
+    bool profiling = false;
+    std::vector<ProfEntry> prof;
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> event_pool;
     ~hs_batch() {
+        for (auto &p : pending) {
+            event_pool.push_back(p.e0);
+            event_pool.push_back(p.e1);
+        }
+        for (auto e : event_pool) (void)hipEventDestroy(e);
         if (st) (void)hipStreamDestroy(st);
+    }
+    hipError_t event(hipEvent_t &e) {
+        if (!event_pool.empty()) {
+            e = event_pool.back();
+            event_pool.pop_back();
+            return hipSuccess;
+        }
+        return hipEventCreate(&e);
+    }
+    size_t entry(const char *label) {
+        for (size_t i = 0; i < prof.size(); i++)
+            if (prof[i].label == label) return i;
+        prof.push_back(ProfEntry{label});
+        return prof.size() - 1;
+    }
+    // Runs `fn` (a launch on the batch stream), bracketed by events when profiling.
+    template <typename F>
+    hipError_t launch(const char *label, uint64_t ops, F &&fn) {
+        if (!profiling) return fn();
+        hipEvent_t e0, e1;
+        hipError_t e = event(e0);
+        if (e == hipSuccess) e = event(e1);
+        if (e != hipSuccess) return e;
+        if ((e = hipEventRecord(e0, st)) != hipSuccess) return e;
+        if ((e = fn()) != hipSuccess) return e;
+        if ((e = hipEventRecord(e1, st)) != hipSuccess) return e;
+        pending.push_back(Pending{entry(label), e0, e1, ops});
+        return hipSuccess;
+    }
+    // After a stream synchronisation: adds the event times of the finished launches.
+    hipError_t collect() {
+        for (auto &p : pending) {
+            float ms = 0;
+            hipError_t e = hipEventElapsedTime(&ms, p.e0, p.e1);
+            if (e != hipSuccess) return e;
+            prof[p.entry].ns += (uint64_t)((double)ms * 1e6);
+            prof[p.entry].launches += 1;
+            prof[p.entry].ops += p.ops;
+            event_pool.push_back(p.e0);
+            event_pool.push_back(p.e1);
+        }
+        pending.clear();
+        return hipSuccess;
     }
 };
 
@@ -366,6 +439,7 @@ extern "C" hs_status hs_batch_set_overlap(hs_batch *b, uint32_t k) {
 }
 
 extern "C" size_t hs_batch_slots(const hs_batch *b) { return b ? b->slots : 0; }
+extern "C" const hs_model *hs_batch_model(const hs_batch *b) { return b ? b->model : nullptr; }
 extern "C" size_t hs_batch_max_rows(const hs_batch *b) { return b ? b->max_rows : 0; }
 extern "C" uint64_t hs_batch_gpu_bytes(const hs_batch *b) { return b ? b->mem.bytes : 0; }
 extern "C" size_t hs_batch_position(const hs_batch *b, size_t slot) {
@@ -468,41 +542,55 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     if (n_out) HIP_TRY(hipMemcpyAsync(b.d_src, src.data(), n_out * sizeof(int32_t), hipMemcpyHostToDevice, st));
     if (!q.empty()) HIP_TRY(hipMemcpyAsync(b.d_queries, q.data(), q.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
 
-    HIP_TRY(hs::launch_embed(b.d_rows, n, m.wte, m.d_pad, m.wpe, m.embed_m, m.host.embed_s, m.pos_m,
-                             m.host.pos_s, m.d, b.d_x, st));
+    uint64_t attn_keys = 0;  // sum over rows of the keys each row reads
+    for (int r = 0; r < n; r++) attn_keys += (uint64_t)rows[r].pos + 1;
+    HIP_TRY(b.launch("embed", 0, [&] {
+        return hs::launch_embed(b.d_rows, n, m.wte, m.d_pad, m.wpe, m.embed_m, m.host.embed_s,
+                                m.pos_m, m.host.pos_s, m.d, b.d_x, st);
+    }));
     auto ln = [&](const DevLn &l, const int32_t *src_rows, int rows_n, int8_t *dst) {
         hs::LnArgs a;
         a.x = b.d_x; a.d = m.d; a.gamma = l.g; a.beta = l.b; a.m = l.m; a.s = l.s;
         a.beta_frac = m.host.ln_beta_frac; a.k = m.host.ln_k; a.j = m.host.ln_j; a.eps = m.host.ln_eps;
         a.out = dst; a.ldo = m.d_pad; a.src = src_rows;
-        return hs::launch_layernorm(a, rows_n, st);
+        return b.launch("layer_norm", 0, [&] { return hs::launch_layernorm(a, rows_n, st); });
     };
-    auto gemm = [&](Epi epi, const DevLinear &lin, const int8_t *a, int rows_n, void *o, int ldo,
-                    const int8_t *gelu = nullptr, int gelu_off = 0) {
+    auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int rows_n,
+                    void *o, int ldo, const int8_t *gelu = nullptr, int gelu_off = 0) {
         hs::GemmArgs g;
         g.a = a; g.w = lin.w; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
         g.gelu = gelu; g.gelu_off = gelu_off;
-        return hs::launch_gemm(epi, g, st);
+        const uint64_t ops = 2ull * (uint64_t)rows_n * (uint64_t)lin.n * (uint64_t)lin.k;
+        return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
     };
     for (int l = 0; l < m.L; l++) {
         const DevBlock &blk = m.blocks[l];
         HIP_TRY(ln(blk.ln1, nullptr, n, b.d_a));
-        HIP_TRY(gemm(Epi::Act, blk.c_attn, b.d_a, n, b.d_qkv, 3 * m.d));
-        HIP_TRY(hs::launch_kv_store(b.d_rows, n, b.d_qkv, m.d, m.H, m.hd, m.C, b.kc[l], b.vc[l], st));
+        HIP_TRY(gemm("gemm_qkv", Epi::Act, blk.c_attn, b.d_a, n, b.d_qkv, 3 * m.d));
+        HIP_TRY(b.launch("kv_store", 0, [&] {
+            return hs::launch_kv_store(b.d_rows, n, b.d_qkv, m.d, m.H, m.hd, m.C, b.kc[l], b.vc[l], st);
+        }));
         hs::AttnArgs at;
         at.rows = b.d_rows; at.q = b.d_qkv; at.ldq = 3 * m.d; at.kc = b.kc[l]; at.vc = b.vc[l];
         at.n_head = m.H; at.hd = m.hd; at.ctx_cap = m.C; at.score_m = blk.score_m; at.score_s = blk.score_s;
         at.out_m = blk.out_m; at.out_s = blk.out_s; at.exp_table = m.attn_exp;
         at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
         at.out = b.d_att; at.ldo = m.d_pad;
-        HIP_TRY(hs::launch_attend(at, n, st));
-        HIP_TRY(gemm(Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
+        HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d,
+                         [&] { return hs::launch_attend(at, n, st); }));
+        HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
         HIP_TRY(ln(blk.ln2, nullptr, n, b.d_a));
-        HIP_TRY(gemm(Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
-        HIP_TRY(gemm(Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
+        HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
+        HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
     }
-    if (n_out == 0) return HS_OK;
+    if (n_out == 0) {
+        if (b.profiling) {
+            HIP_TRY(hipStreamSynchronize(st));
+            HIP_TRY(b.collect());
+        }
+        return HS_OK;
+    }
     HIP_TRY(ln(m.ln_f, b.d_src, n_out, b.d_af));
     DevLinear head;
     head.w = m.wte; head.m = m.logit_m; head.s = m.host.logit_s; head.n = m.V; head.k = m.d;
@@ -511,7 +599,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     std::vector<uint64_t> host((size_t)n_out * per_row);
     for (int c0 = 0; c0 < n_out; c0 += (int)b.chunk_rows) {
         const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
-        HIP_TRY(gemm(Epi::Logits, head, b.d_af + (size_t)c0 * m.d_pad, cn, b.d_logits, m.V));
+        HIP_TRY(gemm("gemm_logits", Epi::Logits, head, b.d_af + (size_t)c0 * m.d_pad, cn, b.d_logits, m.V));
         hs::CoderArgs ca;
         ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
         ca.table_len = (int)m.host.logits_exp.size();
@@ -519,7 +607,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         ca.bits = (int)bits;
         ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
         ca.weights = out == Out::Weights ? b.d_weights : nullptr;
-        HIP_TRY(hs::launch_coder(ca, cn, st));
+        HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder(ca, cn, st); }));
         if (out == Out::Weights)
             HIP_TRY(hipMemcpyAsync(host.data() + (size_t)c0 * m.V, b.d_weights, (size_t)cn * m.V * 8,
                                    hipMemcpyDeviceToHost, st));
@@ -527,6 +615,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     if (out == Out::Intervals)
         HIP_TRY(hipMemcpyAsync(host.data(), b.d_intervals, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
+    if (b.profiling) HIP_TRY(b.collect());
     for (int i = 0; i < n_out; i++)
         std::memcpy(sink + (size_t)owner[i] * per_row, host.data() + (size_t)i * per_row, per_row * 8);
     return HS_OK;
@@ -735,5 +824,164 @@ extern "C" hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, co
     at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
     at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
     HIP_TRY(hs::launch_attend(at, (int)b, stream ? (hipStream_t)stream : dev->stream));
+    return HS_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Profiling, GPU timers and device memory
+// ---------------------------------------------------------------------------------------------
+
+extern "C" hs_status hs_batch_set_profiling(hs_batch *b, int on) {
+    if (!b) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL batch");
+    b->profiling = on != 0;
+    return HS_OK;
+}
+
+extern "C" size_t hs_batch_profile(hs_batch *b, char *labels, uint64_t *ns, uint64_t *launches,
+                                   uint64_t *ops, size_t cap, int clear) {
+    if (!b) return 0;
+    const size_t n = b->prof.size();
+    for (size_t i = 0; i < n && i < cap; i++) {
+        if (labels) {
+            std::memset(labels + 32 * i, 0, 32);
+            std::strncpy(labels + 32 * i, b->prof[i].label.c_str(), 31);
+        }
+        if (ns) ns[i] = b->prof[i].ns;
+        if (launches) launches[i] = b->prof[i].launches;
+        if (ops) ops[i] = b->prof[i].ops;
+    }
+    if (clear) b->prof.clear();
+    return n;
+}
+
+namespace {
+
+template <typename F>
+hs_status time_reps(hs_device *dev, size_t reps, uint64_t *ns, F &&fn) {
+    if (!ns) return hs::fail(HS_INVALID_ARGUMENT, 0, "ns is NULL");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    hs_status s = HS_OK;
+    hipError_t e = hipEventRecord(e0, dev->stream);
+    for (size_t i = 0; e == hipSuccess && i < reps; i++) e = fn();
+    if (e == hipSuccess) e = hipEventRecord(e1, dev->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e != hipSuccess) s = hip_fail("timed launches", e);
+    *ns = (uint64_t)((double)ms * 1e6);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return s;
+}
+
+}  // namespace
+
+extern "C" hs_status hs_op_gemm_requant_gpu_ns(hs_device *dev, const int8_t *w, const int8_t *a,
+                                               const int32_t *bias, const int32_t *mult, uint8_t shift,
+                                               size_t m, size_t n, size_t k, int8_t *out, size_t reps,
+                                               uint64_t *ns) {
+    hs::clear_error();
+    if (!dev || !w || !a || !bias || !mult || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (m == 0 || n == 0 || k == 0 || k > 65536) return hs::fail(HS_UNSUPPORTED, 0, "bad GEMM shape");
+    size_t kp;
+    hs_op_gemm_layout(m, n, k, nullptr, nullptr, &kp);
+    hs::GemmArgs g;
+    g.a = a; g.w = w; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
+    g.bias = bias; g.mult = mult; g.shift = shift; g.out = out; g.ldo = (int)n;
+    return time_reps(dev, reps, ns, [&] { return hs::launch_gemm(Epi::Act, g, dev->stream); });
+}
+
+extern "C" hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8_t *k_cache,
+                                                const int8_t *v_cache, const uint32_t *ctx, size_t b,
+                                                size_t h, size_t hd, size_t ctx_cap, int32_t score_m,
+                                                uint8_t score_s, int32_t out_m, uint8_t out_s,
+                                                const int32_t *attn_exp, size_t len, uint8_t softmax_p,
+                                                int8_t *out, size_t reps, uint64_t *ns) {
+    hs::clear_error();
+    if (!dev || !q || !k_cache || !v_cache || !ctx || !attn_exp || !out)
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (hd == 0 || hd % 4 != 0 || hd > 256 || h == 0 || len == 0 || softmax_p > 30 || ctx_cap == 0 || b == 0)
+        return hs::fail(HS_UNSUPPORTED, 0, "bad attention shape");
+    hs::AttnArgs at;
+    at.rows = nullptr; at.keys = ctx; at.q = q; at.ldq = (int)(h * hd); at.kc = k_cache; at.vc = v_cache;
+    at.n_head = (int)h; at.hd = (int)hd; at.ctx_cap = (int)ctx_cap; at.score_m = score_m;
+    at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
+    at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
+    return time_reps(dev, reps, ns, [&] { return hs::launch_attend(at, (int)b, dev->stream); });
+}
+
+extern "C" hs_status hs_device_alloc(hs_device *dev, size_t bytes, void **out) {
+    hs::clear_error();
+    if (!dev || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    HIP_TRY(hipMalloc(out, std::max<size_t>(bytes, 256)));
+    HIP_TRY(hipMemset(*out, 0, std::max<size_t>(bytes, 256)));
+    return HS_OK;
+}
+
+extern "C" void hs_device_free(hs_device *dev, void *ptr) {
+    if (dev && ptr) {
+        (void)hipSetDevice(dev->ordinal);
+        (void)hipFree(ptr);
+    }
+}
+
+extern "C" hs_status hs_device_upload(hs_device *dev, void *dst, const void *src, size_t bytes) {
+    if (!dev || (bytes && (!dst || !src))) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
+}
+
+extern "C" hs_status hs_device_download(hs_device *dev, void *dst, const void *src, size_t bytes) {
+    if (!dev || (bytes && (!dst || !src))) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
+}
+
+extern "C" hs_status hs_device_synchronize(hs_device *dev) {
+    if (!dev) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL device");
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
+}
+
+extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t rows, size_t vocab,
+                                 const uint64_t *table, size_t len, const hs_query *queries,
+                                 uint32_t freq_bits, hs_interval *out) {
+    hs::clear_error();
+    if (!dev || !logits || !table || !queries || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (rows == 0) return HS_OK;
+    if (vocab == 0 || vocab > (1u << 20) || len == 0 || freq_bits == 0 || freq_bits > 32 ||
+        (uint64_t)vocab > (1ull << freq_bits))
+        return hs::fail(HS_UNSUPPORTED, 0, "vocab in 1..=2^20, len >= 1, freq_bits in 1..=32 with 2^freq_bits >= vocab");
+    std::vector<uint32_t> q(2 * rows);
+    for (size_t r = 0; r < rows; r++) {
+        const bool ok = (queries[r].kind == 0 && queries[r].value < vocab) ||
+                        (queries[r].kind == 1 && (uint64_t)queries[r].value < (1ull << freq_bits));
+        if (!ok) return hs::fail(HS_UNSUPPORTED, 0, "a coder token or target is out of range");
+        q[2 * r] = queries[r].kind;
+        q[2 * r + 1] = queries[r].value;
+    }
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    DevMem mem;
+    int64_t *dl;
+    uint64_t *dt, *di;
+    uint32_t *dq;
+    hs_status s;
+    if ((s = mem.upload(dl, logits, rows * vocab)) != HS_OK) return s;
+    if ((s = mem.upload(dt, table, len)) != HS_OK) return s;
+    if ((s = mem.upload(dq, q.data(), q.size())) != HS_OK) return s;
+    if ((s = mem.alloc(di, 3 * rows)) != HS_OK) return s;
+    hs::CoderArgs ca;
+    ca.logits = dl; ca.ld = (int)vocab; ca.vocab = (int)vocab; ca.table = dt; ca.table_len = (int)len;
+    ca.queries = dq; ca.bits = (int)freq_bits; ca.intervals = di;
+    HIP_TRY(hs::launch_coder(ca, (int)rows, dev->stream));
+    HIP_TRY(hipMemcpyAsync(out, di, rows * 24, hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
     return HS_OK;
 }

@@ -221,7 +221,7 @@ hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream) {
 __global__ void k_embed(const RowInfo *rows, const int8_t *wte, int wte_ld, const int8_t *wpe,
                         const int32_t *embed_m, int embed_s, const int32_t *pos_m, int pos_s,
                         int d, int32_t *x) {
-    const int r = blockIdx.y, j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = blockIdx.x, j = blockIdx.y * blockDim.x + threadIdx.x;
     if (j >= d) return;
     const RowInfo ri = rows[r];
     const int64_t v = rescale_small(wte[(size_t)ri.token * wte_ld + j], embed_m[ri.token], embed_s) +
@@ -232,7 +232,7 @@ __global__ void k_embed(const RowInfo *rows, const int8_t *wte, int wte_ld, cons
 hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_ld,
                         const int8_t *wpe, const int32_t *embed_m, int embed_s,
                         const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream) {
-    dim3 grid((d + 255) / 256, n_rows);
+    dim3 grid(n_rows, (d + 255) / 256);
     hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_ld, wpe, embed_m,
                        embed_s, pos_m, pos_s, d, x);
     return hipGetLastError();
@@ -311,7 +311,7 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
 
 __global__ void k_kv_store(const RowInfo *rows, const int8_t *qkv, int d, int n_head, int hd,
                            int n_ctx, int8_t *kc, int8_t *vc) {
-    const int r = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = blockIdx.x, c = blockIdx.y * blockDim.x + threadIdx.x;
     if (c >= d) return;
     const RowInfo ri = rows[r];
     const int h = c / hd, cc = c - h * hd;
@@ -322,7 +322,7 @@ __global__ void k_kv_store(const RowInfo *rows, const int8_t *qkv, int d, int n_
 
 hipError_t launch_kv_store(const RowInfo *rows, int n_rows, const int8_t *qkv, int d, int n_head,
                            int hd, int n_ctx, int8_t *kc, int8_t *vc, hipStream_t stream) {
-    dim3 grid((d + 255) / 256, n_rows);
+    dim3 grid(n_rows, (d + 255) / 256);
     hipLaunchKernelGGL(k_kv_store, grid, dim3(256), 0, stream, rows, qkv, d, n_head, hd, n_ctx,
                        kc, vc);
     return hipGetLastError();
@@ -483,8 +483,9 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
             s_u64[tid] += s_u64[tid + o];
             const uint64_t b0 = (uint64_t)s_i64[tid], b1 = (uint64_t)s_i64[tid + o];
             const uint32_t i0 = s_idx[tid], i1 = s_idx[tid + o];
-            // the larger weight wins; on a tie the lower index (i1 > i0 whenever both valid)
-            if (i0 == 0xFFFFFFFFu || (i1 != 0xFFFFFFFFu && b1 > b0)) {
+            // the larger weight wins; on a tie the lower index (a strided tree does not keep
+            // the lower slot on the lower indices, so compare them)
+            if (i0 == 0xFFFFFFFFu || (i1 != 0xFFFFFFFFu && (b1 > b0 || (b1 == b0 && i1 < i0)))) {
                 s_i64[tid] = (int64_t)b1;
                 s_idx[tid] = i1;
             }

@@ -1,0 +1,367 @@
+// The host harness above the HardShell C ABI (include/taco_hip.h): the role of the reference's
+// `taco` crate on the fold/unfold path. Restates crates/taco/src/gpu_fold.rs:128-306 (windows
+// and their rows), crates/taco/src/codec.rs:72-310 (the block encoder and its stop rule),
+// crates/taco/src/payload.rs:20-60 (LEB128), crates/taco-coder/src/{encoder,decoder}.rs (the
+// range coder) and crates/taco-format/src/writer.rs:245-288 (the container).
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../common.h"
+#include "hardshell_hip.h"
+#include "taco_hip.h"
+
+namespace {
+
+typedef unsigned __int128 u128;
+constexpr uint64_t TOP = (uint64_t)1 << 56;
+constexpr uint64_t TOTAL = (uint64_t)1 << TC_FREQ_BITS;
+
+// The range encoder (crates/taco-coder/src/encoder.rs:13-212): a 65-bit `low`, the LZMA carry
+// rule with a 64-bit window, and a flush that strips trailing zero bytes.
+struct Encoder {
+    u128 low = 0;
+    uint64_t range = UINT64_MAX;
+    uint8_t cache = 0;
+    size_t pending = 0;
+    std::vector<uint8_t> out;
+    size_t nonzero_len = 0;  // the lower bound of the final length (encoder.rs:159-167)
+
+    void shift_low() {
+        const uint8_t carry = (uint8_t)((low >> 64) & 1);
+        const uint64_t window = (uint64_t)low;
+        if (pending == 0 || window < 0xFF00000000000000ull || carry) {
+            if (pending > 0) {
+                const uint8_t first = (uint8_t)(cache + carry);
+                out.push_back(first);
+                if (first) nonzero_len = out.size();
+                const uint8_t fill = (uint8_t)(0xFF + carry);
+                out.insert(out.end(), pending - 1, fill);
+                if (fill && pending > 1) nonzero_len = out.size();
+            }
+            cache = (uint8_t)(window >> 56);
+            pending = 0;
+        }
+        pending++;
+        low = (u128)(window << 8);
+    }
+    void encode(uint64_t start, uint64_t freq) {  // encode_interval with T = 2^32
+        const uint64_t r = range >> TC_FREQ_BITS;
+        const uint64_t off = r * start;
+        low += off;
+        range = (start + freq == TOTAL) ? range - off : r * freq;
+        while (range < TOP) {
+            range <<= 8;
+            shift_low();
+        }
+    }
+    std::vector<uint8_t> finish() {
+        const u128 end = low + range;
+        for (unsigned k : {64u, 56u}) {
+            const u128 mask = ((u128)1 << k) - 1;
+            const u128 v = (low + mask) & ~mask;
+            if (v < end) {
+                low = v;
+                break;
+            }
+        }
+        shift_low();
+        shift_low();
+        while (!out.empty() && out.back() == 0) out.pop_back();
+        return out;
+    }
+};
+
+// The range decoder (crates/taco-coder/src/decoder.rs:27-135), target/decode_interval form.
+struct Decoder {
+    const uint8_t *in = nullptr;
+    size_t len = 0, pos = 0;
+    uint64_t code = 0, range = UINT64_MAX;
+    uint8_t next() { return pos < len ? in[pos++] : (pos++, (uint8_t)0); }
+    void init(const uint8_t *p, size_t n) {
+        in = p;
+        len = n;
+        for (int i = 0; i < 8; i++) code = (code << 8) | next();
+    }
+    uint64_t target() const {
+        const uint64_t t = code / (range >> TC_FREQ_BITS);
+        return t < TOTAL - 1 ? t : TOTAL - 1;
+    }
+    bool decode(uint64_t start, uint64_t freq) {
+        const uint64_t t = target();
+        if (!(t >= start && t - start < freq)) return false;
+        const uint64_t r = range >> TC_FREQ_BITS;
+        const uint64_t off = r * start;
+        code -= off;
+        range = (start + freq == TOTAL) ? range - off : r * freq;
+        while (range < TOP) {
+            range <<= 8;
+            code = (code << 8) | next();
+        }
+        return true;
+    }
+};
+
+void write_varint(uint64_t v, std::vector<uint8_t> &out) {  // payload.rs:20-31
+    for (;;) {
+        const uint8_t low = (uint8_t)(v & 0x7F);
+        v >>= 7;
+        if (!v) {
+            out.push_back(low);
+            return;
+        }
+        out.push_back(low | 0x80);
+    }
+}
+
+size_t varint_len(uint64_t v) {
+    size_t n = 1;
+    while (v > 0x7F) {
+        v >>= 7;
+        n++;
+    }
+    return n;
+}
+
+bool read_varint(const uint8_t *b, size_t len, uint64_t &value, size_t &used) {  // payload.rs:40-60
+    value = 0;
+    unsigned shift = 0;
+    for (size_t i = 0; i < len && i < 10; i++) {
+        const uint64_t group = b[i] & 0x7F;
+        if (i == 9 && group > 1) return false;
+        value |= group << shift;
+        shift += 7;
+        if (!(b[i] & 0x80)) {
+            if (b[i] == 0 && i > 0) return false;
+            used = i + 1;
+            return true;
+        }
+    }
+    return false;
+}
+
+// A context window of a block (gpu_fold.rs:128-134).
+struct Window {
+    size_t block, first, len;
+};
+
+// The block encoder with its stop (codec.rs:72-126, 132-252): the candidate dies when the varint
+// and the lower bound of the coder output reach the stop length.
+struct BlockEnc {
+    Encoder enc;
+    uint64_t count = 0;
+    size_t prefix = 0, stop = SIZE_MAX;
+    bool live = true;
+    bool stopped() const { return prefix >= stop || !live; }
+    void push(uint64_t start, uint64_t freq) {
+        if (!live) return;
+        enc.encode(start, freq);
+        if (prefix + enc.nonzero_len >= stop) live = false;
+    }
+};
+
+}  // namespace
+
+extern "C" hs_status tc_fold_blocks(hs_batch *batch, uint32_t overlap, const uint32_t *tokens,
+                                    const size_t *offsets, size_t count, const size_t *stop,
+                                    uint8_t *out, size_t cap, size_t *lens) {
+    if (!batch || (count && (!tokens || !offsets || !out || !lens)))
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    // The model constants come through the batch's model (the caller made the batch for it).
+    const size_t slots = hs_batch_slots(batch);
+    std::vector<BlockEnc> enc(count);
+    for (size_t b = 0; b < count; b++) {
+        enc[b].count = offsets[b + 1] - offsets[b];
+        enc[b].prefix = varint_len(enc[b].count);
+        enc[b].stop = stop ? stop[b] : SIZE_MAX;
+    }
+    // windows_of (gpu_fold.rs:167-186)
+    const size_t n_ctx = hs_model_n_ctx(hs_batch_model(batch));
+    const uint32_t eot = hs_model_eot(hs_batch_model(batch));
+    const size_t k = overlap;
+    if (k + 2 > n_ctx) return hs::fail(HS_MODEL_ERROR, HS_MODEL_INVALID_OVERLAP, "the overlap does not fit the context");
+    std::vector<Window> windows;
+    for (size_t b = 0; b < count; b++) {
+        const size_t n = enc[b].count;
+        if (n == 0 || enc[b].stopped()) continue;
+        size_t first = 0, size = std::max<size_t>(n_ctx, 2);
+        while (first < n) {
+            const size_t len = std::min(size, n - first);
+            windows.push_back(Window{b, first, len});
+            first += len;
+            size = std::max<size_t>(1, std::max<size_t>(n_ctx, 2) - std::min(std::max<size_t>(n_ctx, 2), 1 + k));
+        }
+    }
+    std::vector<hs_input> inputs;
+    std::vector<hs_query> queries;
+    std::vector<int64_t> owner;  // the block of each coded row, -1 for a row that codes nothing
+    std::vector<hs_interval> answers;
+    for (size_t w0 = 0; w0 < windows.size(); w0 += slots) {
+        const size_t w1 = std::min(windows.size(), w0 + slots);
+        inputs.clear();
+        queries.clear();
+        owner.clear();
+        for (size_t wi = w0; wi < w1; wi++) {
+            const Window &w = windows[wi];
+            if (enc[w.block].stopped()) continue;
+            const uint32_t slot = (uint32_t)(wi - w0);
+            hs_batch_reset(batch, slot);
+            const uint32_t *t = tokens + offsets[w.block];
+            // Window::rows (gpu_fold.rs:145-160)
+            auto row = [&](uint32_t in, int64_t code) {
+                inputs.push_back(hs_input{slot, in});
+                queries.push_back(hs_query{0, code >= 0 ? (uint32_t)code : eot});
+                owner.push_back(code >= 0 ? (int64_t)w.block : -1);
+            };
+            if (w.first == 0) {
+                row(eot, t[0]);
+            } else {
+                row(eot, -1);
+                const size_t kept0 = w.first >= 1 + k ? w.first - 1 - k : 0;
+                for (size_t i = kept0; i < w.first - 1; i++) row(t[i], -1);
+                row(t[w.first - 1], t[w.first]);
+            }
+            for (size_t i = w.first + 1; i < w.first + w.len; i++) row(t[i - 1], t[i]);
+        }
+        if (inputs.empty()) continue;
+        answers.resize(inputs.size());
+        hs_status s = hs_batch_run_coded(batch, inputs.data(), queries.data(), inputs.size(),
+                                         TC_FREQ_BITS, answers.data());
+        if (s != HS_OK) return s;
+        // The rows are in window order, so each block's tokens reach its encoder in order.
+        for (size_t i = 0; i < inputs.size(); i++) {
+            if (owner[i] < 0) continue;
+            const hs_interval &a = answers[i];
+            // lanes.rs:121-128: a bad interval or last-symbol flag is a fault of the device
+            if (a.freq == 0 || a.start > TOTAL || a.freq > TOTAL - a.start || a.symbol != queries[i].value)
+                return hs::fail(HS_DEVICE_ERROR, 0, "the coder op gave a bad interval");
+            enc[(size_t)owner[i]].push(a.start, a.freq);
+        }
+    }
+    for (size_t b = 0; b < count; b++) {
+        BlockEnc &e = enc[b];
+        if (e.stopped()) {
+            lens[b] = SIZE_MAX;
+            continue;
+        }
+        std::vector<uint8_t> p;
+        write_varint(e.count, p);
+        if (e.count > 0) {
+            std::vector<uint8_t> body = e.enc.finish();
+            p.insert(p.end(), body.begin(), body.end());
+        }
+        lens[b] = p.size();
+        if (p.size() <= cap) std::memcpy(out + b * cap, p.data(), p.size());
+    }
+    return HS_OK;
+}
+
+extern "C" hs_status tc_unfold_blocks(hs_batch *batch, uint32_t overlap, const uint8_t *payloads,
+                                      const size_t *offsets, size_t count, uint32_t *tokens,
+                                      size_t cap, size_t *counts) {
+    if (!batch || (count && (!payloads || !offsets || !tokens || !counts)))
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    (void)overlap;  // the batch applies its own overlap at each restart
+    const size_t slots = hs_batch_slots(batch);
+    const uint32_t eot = hs_model_eot(hs_batch_model(batch));
+    std::vector<Decoder> dec(count);
+    std::vector<uint64_t> total(count, 0), done(count, 0);
+    for (size_t b = 0; b < count; b++) {
+        const uint8_t *p = payloads + offsets[b];
+        const size_t n = offsets[b + 1] - offsets[b];
+        size_t used = 0;
+        if (!read_varint(p, n, total[b], used) || total[b] > cap)
+            return hs::fail(HS_LENGTH_MISMATCH, (int)b, "block " + std::to_string(b) + ": the token count is not valid");
+        dec[b].init(p + used, n - used);
+        counts[b] = (size_t)total[b];
+    }
+    std::vector<hs_input> inputs;
+    std::vector<hs_query> queries;
+    std::vector<size_t> live;
+    std::vector<hs_interval> answers;
+    for (size_t b0 = 0; b0 < count; b0 += slots) {
+        const size_t b1 = std::min(count, b0 + slots);
+        for (size_t b = b0; b < b1; b++) hs_batch_reset(batch, b - b0);
+        for (;;) {
+            inputs.clear();
+            queries.clear();
+            live.clear();
+            for (size_t b = b0; b < b1; b++) {
+                if (done[b] >= total[b]) continue;
+                const uint32_t prev = done[b] == 0 ? eot : tokens[b * cap + done[b] - 1];
+                inputs.push_back(hs_input{(uint32_t)(b - b0), prev});
+                queries.push_back(hs_query{1, (uint32_t)dec[b].target()});
+                live.push_back(b);
+            }
+            if (live.empty()) break;
+            answers.resize(inputs.size());
+            hs_status s = hs_batch_run_coded(batch, inputs.data(), queries.data(), inputs.size(),
+                                             TC_FREQ_BITS, answers.data());
+            if (s != HS_OK) return s;
+            for (size_t i = 0; i < live.size(); i++) {
+                const size_t b = live[i];
+                const hs_interval &a = answers[i];
+                if (!dec[b].decode(a.start, a.freq))
+                    return hs::fail(HS_DEVICE_ERROR, (int)b, "the coder op gave an interval that does not hold the target");
+                tokens[b * cap + done[b]] = (uint32_t)a.symbol;
+                done[b]++;
+            }
+        }
+    }
+    return HS_OK;
+}
+
+extern "C" size_t tc_container_build(const uint8_t model_hash[32], const uint8_t *original, size_t len,
+                                     uint32_t block_size, uint32_t overlap, const uint8_t *kinds,
+                                     const uint8_t *blocks, const size_t *block_offsets, uint8_t *out,
+                                     size_t cap) {
+    if (block_size == 0 || !model_hash) return 0;
+    const uint64_t count = (len + block_size - 1) / block_size;
+    std::vector<uint8_t> o;
+    auto put = [&](uint64_t v, int bytes) {
+        for (int i = 0; i < bytes; i++) o.push_back((uint8_t)(v >> (8 * i)));
+    };
+    // Header (taco-format/src/header.rs:200-215, lib.rs:14-36): 104 bytes in version 2.
+    o.insert(o.end(), {'T', 'A', 'C', 'O'});
+    put(2, 2);
+    put(0, 2);
+    o.insert(o.end(), model_hash, model_hash + 32);
+    put(len, 8);
+    uint8_t digest[32];
+    hs::sha256(original, len, digest);
+    o.insert(o.end(), digest, digest + 32);
+    put(block_size, 4);
+    put(count, 4);
+    o.push_back(0);                 // profile: text
+    o.push_back(0);                 // reserved
+    put(overlap ? 2 : 0, 2);        // coding parts: bit 1 = the context overlap
+    uint8_t params[12] = {0};
+    if (overlap) {
+        params[2] = (uint8_t)(overlap & 0xFF);
+        params[3] = (uint8_t)(overlap >> 8);
+    }
+    o.insert(o.end(), params, params + 12);
+    std::vector<size_t> stored(count);
+    for (uint64_t b = 0; b < count; b++) {
+        const size_t orig = std::min<size_t>(block_size, len - b * block_size);
+        size_t sl = orig;
+        if (kinds[b] == 1) {
+            sl = block_offsets[b + 1] - block_offsets[b];
+            if (sl >= orig) return 0;  // a coded block must be smaller (writer.rs:71-104)
+        } else if (kinds[b] != 0) {
+            return 0;
+        }
+        stored[b] = sl;
+        o.push_back(kinds[b]);
+        put(sl, 4);
+    }
+    for (uint64_t b = 0; b < count; b++) {
+        if (kinds[b] == 1)
+            o.insert(o.end(), blocks + block_offsets[b], blocks + block_offsets[b + 1]);
+        else
+            o.insert(o.end(), original + b * block_size, original + b * block_size + stored[b]);
+    }
+    if (o.size() <= cap && out) std::memcpy(out, o.data(), o.size());
+    return o.size();
+}

@@ -132,6 +132,23 @@ def lib() -> C.CDLL:
         L.hs_op_gemm_layout.restype = None
         L.hs_op_attend_decode_dev.argtypes = [P, P, P, P, P, S, S, S, S, C.c_int32, C.c_uint8,
                                               C.c_int32, C.c_uint8, P, S, C.c_uint8, P, P]
+        L.hs_device_alloc.argtypes = [P, S, C.POINTER(P)]
+        L.hs_device_free.argtypes = [P, P]
+        L.hs_device_upload.argtypes = [P, P, P, S]
+        L.hs_device_download.argtypes = [P, P, P, S]
+        L.hs_device_synchronize.argtypes = [P]
+        L.hs_op_gemm_requant_gpu_ns.argtypes = [P, P, P, P, P, C.c_uint8, S, S, S, P, S,
+                                                C.POINTER(U64)]
+        L.hs_op_attend_decode_gpu_ns.argtypes = [P, P, P, P, P, S, S, S, S, C.c_int32,
+                                                 C.c_uint8, C.c_int32, C.c_uint8, P, S,
+                                                 C.c_uint8, P, S, C.POINTER(U64)]
+        L.hs_batch_set_profiling.argtypes = [P, C.c_int]
+        L.hs_batch_profile.restype = S
+        L.hs_batch_profile.argtypes = [P, P, P, P, P, S, C.c_int]
+        L.hs_batch_model.restype = P
+        L.hs_batch_model.argtypes = [P]
+        L.hs_model_validate.argtypes = [P, S, P]
+        L.hs_op_coder.argtypes = [P, P, S, S, P, S, P, U32, P]
         _lib = L
     return _lib
 
@@ -373,3 +390,16 @@ def gemm_layout(m: int, n: int, k: int) -> Tuple[int, int, int]:
     a, b, c = C.c_size_t(), C.c_size_t(), C.c_size_t()
     lib().hs_op_gemm_layout(m, n, k, C.byref(a), C.byref(b), C.byref(c))
     return a.value, b.value, c.value
+
+
+def coder(dev: HipDevice, logits: np.ndarray, table: np.ndarray, queries, freq_bits: int = 32
+          ) -> np.ndarray:
+    """The coder op on given i64 logits [rows, vocab]: (symbol, start, freq) per row."""
+    logits = np.ascontiguousarray(logits, dtype=np.int64)
+    table = np.ascontiguousarray(table, dtype=np.uint64)
+    q = np.ascontiguousarray(np.asarray(queries, dtype=np.uint32).reshape(-1, 2))
+    rows, vocab = logits.shape
+    out = np.zeros((rows, 3), np.uint64)
+    _check(lib().hs_op_coder(dev.h, _ptr(logits), rows, vocab, _ptr(table), len(table), _ptr(q),
+                             freq_bits, _ptr(out)))
+    return out

@@ -270,26 +270,89 @@ def test_head_dim_not_multiple_of_4_is_unsupported(dev):
         hip.HipModel.load(dev, b)
 
 
-def test_attend_decode_op(dev):
-    """Config 3 shape, small: 8 streams x 12 heads x 64, ctx up to 300, against the oracle."""
-    import torch
+def _dev_buf(dev, arr):
+    from taco_amd import hip
+    import ctypes as C
+    p = C.c_void_p()
+    hip._check(hip.lib().hs_device_alloc(dev.h, arr.nbytes, C.byref(p)))
+    hip._check(hip.lib().hs_device_upload(dev.h, p, arr.ctypes.data_as(C.c_void_p), arr.nbytes))
+    return p
+
+
+@pytest.mark.parametrize("ctx_cap", [320, 1024])
+def test_attend_decode_op(dev, ctx_cap):
+    """Config 3's op, smaller: 8 streams x 12 heads x 64 over caches of ctx_cap positions."""
+    import ctypes as C
     from taco_amd import hip
     r = np.random.default_rng(3)
-    B, H, hd, cap = 8, 12, 64, 320
+    B, H, hd = 8, 12, 64
     q = r.integers(-127, 128, (B, H, hd)).astype(np.int8)
-    kc = r.integers(-127, 128, (B, H, cap, hd)).astype(np.int8)
-    vc = r.integers(-127, 128, (B, H, cap, hd)).astype(np.int8)
-    ctx = np.array([1, 2, 63, 64, 65, 128, 300, 320], np.uint32)
+    kc = r.integers(-127, 128, (B, H, ctx_cap, hd)).astype(np.int8)
+    vc = r.integers(-127, 128, (B, H, ctx_cap, hd)).astype(np.int8)
+    ctx = np.array([1, 2, 63, 64, 65, 128, ctx_cap - 20, ctx_cap], np.uint32)
     table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
     score_m, score_s, out_m, out_s = 1_400_000_000, 33, 1_300_000_000, 53
     want = O.attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, 30)
-    dq, dk, dv = (torch.from_numpy(x).cuda() for x in (q, kc, vc))
-    dctx, dt = torch.from_numpy(ctx.view(np.int32)).cuda(), torch.from_numpy(table).cuda()
-    out = torch.zeros((B, H * hd), dtype=torch.int8, device="cuda")
-    torch.cuda.synchronize()
-    hip._check(hip.lib().hs_op_attend_decode_dev(
-        dev.h, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dctx.data_ptr(), B, H, hd, cap,
-        score_m, score_s, out_m, out_s, dt.data_ptr(), len(table), 30, out.data_ptr(),
-        torch.cuda.current_stream().cuda_stream))
-    torch.cuda.synchronize()
-    assert np.array_equal(out.cpu().numpy(), want)
+    bufs = [_dev_buf(dev, a) for a in (q, kc, vc, ctx, table)]
+    out = np.zeros((B, H * hd), np.int8)
+    dout = _dev_buf(dev, out)
+    try:
+        hip._check(hip.lib().hs_op_attend_decode_dev(
+            dev.h, bufs[0], bufs[1], bufs[2], bufs[3], B, H, hd, ctx_cap, score_m, score_s,
+            out_m, out_s, bufs[4], len(table), 30, dout, None))
+        hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                out.nbytes))
+    finally:
+        for p in bufs + [dout]:
+            hip.lib().hs_device_free(dev.h, p)
+    assert np.array_equal(out, want)
+
+
+def _coder_cases():
+    r = np.random.default_rng(11)
+    cases = []
+    table = np.array([round(2 ** 40 * np.exp(-i / 256)) for i in range(8192)], np.uint64)
+    for vocab in (300, 50257, 1000, 257, 1):
+        rows = []
+        for kind in range(6):
+            l = r.integers(-3000, 3000, vocab).astype(np.int64)
+            if kind == 1:  # ties at the maximum, far apart (different threads of the op)
+                l[r.choice(vocab, size=min(vocab, 5), replace=False)] = 5000
+            if kind == 2:  # every logit equal
+                l[:] = 7
+            if kind == 3:  # the maximum at the last id, a tie at the first
+                l[-1] = 9000
+                l[0] = 9000
+            if kind == 4:  # extremes of the clamped range
+                l = r.choice([-(1 << 40), 1 << 40, 0], vocab).astype(np.int64)
+            rows.append(l)
+        cases.append((vocab, np.array(rows), table))
+    # a short table and a table with a flat start (ties among weights for different logits)
+    t2 = np.array([1 << 40, 1 << 40, 1 << 39, 5, 1], np.uint64)
+    cases.append((700, r.integers(-8, 8, (4, 700)).astype(np.int64), t2))
+    return cases
+
+
+def test_coder_op_equals_from_weights(dev):
+    from taco_amd import hip
+    r = np.random.default_rng(12)
+    for vocab, logits, table in _coder_cases():
+        rows = len(logits)
+        weights = []
+        for l in logits:
+            w = np.zeros(vocab, np.uint64)
+            assert O.lib().or_logits_to_weights(O.ptr(l), vocab, O.ptr(table), len(table),
+                                                O.ptr(w)) == 0
+            weights.append(w)
+        for bits in sorted({32, 24, max(1, (vocab - 1).bit_length())}):
+            if vocab > 1 << bits:
+                continue
+            toks = r.integers(0, vocab, rows)
+            enc = hip.coder(dev, logits, table, [(0, int(t)) for t in toks], bits)
+            for i in range(rows):
+                assert tuple(enc[i]) == (toks[i],) + O.freq_interval(weights[i], bits, int(toks[i])), \
+                    (vocab, bits, i)
+            targets = [0, (1 << bits) - 1] + [int(x) for x in r.integers(0, 1 << bits, rows - 2)]
+            dec = hip.coder(dev, logits, table, [(1, t) for t in targets[:rows]], bits)
+            for i in range(rows):
+                assert tuple(dec[i]) == O.freq_find(weights[i], bits, targets[i]), (vocab, bits, i)
