@@ -90,6 +90,7 @@ struct DevLinear {
 
 struct DevLn {
     int16_t *g = nullptr;
+    int64_t *gm = nullptr;  // g[j] * m
     int32_t *b = nullptr;
     int32_t m = 0;
     int s = 0;
@@ -120,6 +121,9 @@ struct hs_model {
     int32_t *attn_exp = nullptr;
     uint64_t *logits_exp = nullptr;
     uint64_t weight_bytes = 0;
+    bool compact = false;  // the LM head writes compact logits (table_len <= CODER_MAX_TABLE)
+    int d0 = 0;            // the largest d with logits_exp[d] == logits_exp[0]
+    int ntiles = 0, ld16 = 0;
 };
 
 namespace {
@@ -139,7 +143,10 @@ hs_status upload_linear(DevMem &mem, const hs::HostLinear &l, DevLinear &o) {
 }
 
 hs_status upload_ln(DevMem &mem, const hs::HostLayerNorm &l, DevLn &o) {
+    std::vector<int64_t> gm(l.g.size());
+    for (size_t j = 0; j < gm.size(); j++) gm[j] = (int64_t)l.g[j] * (int64_t)l.m;
     hs_status st = mem.upload(o.g, l.g.data(), l.g.size());
+    if (st == HS_OK) st = mem.upload(o.gm, gm.data(), gm.size());
     if (st == HS_OK) st = mem.upload(o.b, l.b.data(), l.b.size());
     o.m = l.m;
     o.s = l.s;
@@ -252,6 +259,10 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
     if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
     if ((st = mem.upload(m->attn_exp, h.attn_exp.data(), h.attn_exp.size())) != HS_OK) return st;
     if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size())) != HS_OK) return st;
+    m->compact = h.logits_exp.size() <= (size_t)hs::CODER_MAX_TABLE;
+    while ((size_t)m->d0 + 1 < h.logits_exp.size() && h.logits_exp[m->d0 + 1] == h.logits_exp[0]) m->d0++;
+    m->ntiles = (m->V + 63) / 64;
+    m->ld16 = (int)round_up(m->V, 64);
     m->weight_bytes = mem.bytes;
     *out = m.release();
     return HS_OK;
@@ -306,8 +317,11 @@ struct hs_batch {
     DevMem mem;
     RowInfo *d_rows = nullptr;
     int32_t *d_x = nullptr, *d_src = nullptr;
+    hs::AttnGroup *d_groups = nullptr;
     int8_t *d_a = nullptr, *d_qkv = nullptr, *d_att = nullptr, *d_g = nullptr, *d_af = nullptr;
     int64_t *d_logits = nullptr;
+    uint16_t *d_d16 = nullptr;
+    int64_t *d_tmax = nullptr;
     uint32_t *d_queries = nullptr;
     uint64_t *d_intervals = nullptr, *d_weights = nullptr;
     size_t chunk_rows = 0;
@@ -395,21 +409,30 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     b->pos.assign(slots, 0);
     b->hist.assign(slots * m.C, 0);
     b->stream.assign(slots, 0);
-    // The LM head runs on chunks of output rows so that the i64 logits stay near 1 GiB.
-    b->chunk_rows = std::max<size_t>(hs::GEMM_BM, round_up(std::min<size_t>(b->rows_pad, (size_t)((1ull << 30) / (8ull * m.V_pad))), hs::GEMM_BM));
+    // The LM head runs on chunks of output rows: compact logits (2 B per logit) up to 4 GiB a
+    // chunk, i64 logits up to 1 GiB.
+    const size_t per_row = m.compact ? 2ull * m.ld16 : 8ull * m.V_pad;
+    const size_t budget = m.compact ? (4ull << 30) : (1ull << 30);
+    b->chunk_rows = std::max<size_t>(hs::GEMM_BM, round_up(std::min<size_t>(b->rows_pad, budget / per_row), hs::GEMM_BM));
     b->chunk_rows = std::min(b->chunk_rows, b->rows_pad);
     const size_t R = b->max_rows, RP = b->rows_pad;
     DevMem &mem = b->mem;
     hs_status s;
     if ((s = mem.alloc(b->d_rows, R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_src, R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_groups, R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_x, R * m.d)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_a, RP * m.d_pad)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_af, RP * m.d_pad)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_qkv, R * 3 * m.d)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_att, RP * m.d_pad)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_g, RP * m.f_pad)) != HS_OK) return s;
-    if ((s = mem.alloc(b->d_logits, b->chunk_rows * m.V)) != HS_OK) return s;
+    if (m.compact) {
+        if ((s = mem.alloc(b->d_d16, b->chunk_rows * m.ld16)) != HS_OK) return s;
+        if ((s = mem.alloc(b->d_tmax, b->chunk_rows * m.ntiles)) != HS_OK) return s;
+    } else if ((s = mem.alloc(b->d_logits, b->chunk_rows * m.V)) != HS_OK) {
+        return s;
+    }
     if ((s = mem.alloc(b->d_queries, 2 * R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_intervals, 3 * R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_weights, b->chunk_rows * m.V)) != HS_OK) return s;
@@ -538,6 +561,19 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         }
     }
     HIP_TRY(hipMemcpyAsync(b.d_rows, info.data(), n * sizeof(RowInfo), hipMemcpyHostToDevice, st));
+    // Attention groups (runs of one slot at consecutive positions, at most 64 rows each) for
+    // the MFMA prefill kernel; decode-shaped passes (short runs) use the row kernel.
+    std::vector<hs::AttnGroup> groups;
+    for (int r = 0; r < n;) {
+        int c = 1;
+        while (r + c < n && c < 64 && rows[r + c].slot == rows[r].slot && rows[r + c].pos == rows[r].pos + (uint32_t)c) c++;
+        groups.push_back(hs::AttnGroup{r, c, (int32_t)rows[r].slot, (int32_t)rows[r].pos});
+        r += c;
+    }
+    const bool mfma_attn = m.hd == 64 && (size_t)n >= 16 * groups.size();
+    if (mfma_attn)
+        HIP_TRY(hipMemcpyAsync(b.d_groups, groups.data(), groups.size() * sizeof(hs::AttnGroup),
+                               hipMemcpyHostToDevice, st));
     const int n_out = (int)src.size();
     if (n_out) HIP_TRY(hipMemcpyAsync(b.d_src, src.data(), n_out * sizeof(int32_t), hipMemcpyHostToDevice, st));
     if (!q.empty()) HIP_TRY(hipMemcpyAsync(b.d_queries, q.data(), q.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
@@ -552,7 +588,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         hs::LnArgs a;
         a.x = b.d_x; a.d = m.d; a.gamma = l.g; a.beta = l.b; a.m = l.m; a.s = l.s;
         a.beta_frac = m.host.ln_beta_frac; a.k = m.host.ln_k; a.j = m.host.ln_j; a.eps = m.host.ln_eps;
-        a.out = dst; a.ldo = m.d_pad; a.src = src_rows;
+        a.out = dst; a.ldo = m.d_pad; a.src = src_rows; a.gm = l.gm;
         return b.launch("layer_norm", 0, [&] { return hs::launch_layernorm(a, rows_n, st); });
     };
     auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int rows_n,
@@ -577,8 +613,10 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         at.out_m = blk.out_m; at.out_s = blk.out_s; at.exp_table = m.attn_exp;
         at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
         at.out = b.d_att; at.ldo = m.d_pad;
-        HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d,
-                         [&] { return hs::launch_attend(at, n, st); }));
+        HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d, [&] {
+            return mfma_attn ? hs::launch_attend_groups(at, b.d_groups, (int)groups.size(), st)
+                             : hs::launch_attend(at, n, st);
+        }));
         HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
         HIP_TRY(ln(blk.ln2, nullptr, n, b.d_a));
         HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
@@ -599,15 +637,32 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     std::vector<uint64_t> host((size_t)n_out * per_row);
     for (int c0 = 0; c0 < n_out; c0 += (int)b.chunk_rows) {
         const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
-        HIP_TRY(gemm("gemm_logits", Epi::Logits, head, b.d_af + (size_t)c0 * m.d_pad, cn, b.d_logits, m.V));
-        hs::CoderArgs ca;
-        ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
-        ca.table_len = (int)m.host.logits_exp.size();
-        ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
-        ca.bits = (int)bits;
-        ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
-        ca.weights = out == Out::Weights ? b.d_weights : nullptr;
-        HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder(ca, cn, st); }));
+        if (m.compact) {
+            hs::GemmArgs g;
+            g.a = b.d_af + (size_t)c0 * m.d_pad; g.w = m.wte; g.m = cn; g.n = m.V; g.k_pad = m.d_pad;
+            g.mult = m.logit_m; g.shift = m.host.logit_s; g.out = b.d_d16; g.ldo = m.ld16;
+            g.tmax = b.d_tmax; g.tmax_ld = m.ntiles; g.cap16 = (int)m.host.logits_exp.size() - 1;
+            const uint64_t ops = 2ull * (uint64_t)cn * (uint64_t)m.V * (uint64_t)m.d;
+            HIP_TRY(b.launch("gemm_logits", ops, [&] { return hs::launch_gemm(Epi::LogitsCompact, g, st); }));
+            hs::CompactCoderArgs ca;
+            ca.d16 = b.d_d16; ca.ld16 = m.ld16; ca.tmax = b.d_tmax; ca.ntiles = m.ntiles; ca.vocab = m.V;
+            ca.table = m.logits_exp; ca.table_len = (int)m.host.logits_exp.size(); ca.d0 = m.d0;
+            ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
+            ca.bits = (int)bits;
+            ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
+            ca.weights = out == Out::Weights ? b.d_weights : nullptr;
+            HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder_compact(ca, cn, st); }));
+        } else {
+            HIP_TRY(gemm("gemm_logits", Epi::Logits, head, b.d_af + (size_t)c0 * m.d_pad, cn, b.d_logits, m.V));
+            hs::CoderArgs ca;
+            ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
+            ca.table_len = (int)m.host.logits_exp.size();
+            ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
+            ca.bits = (int)bits;
+            ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
+            ca.weights = out == Out::Weights ? b.d_weights : nullptr;
+            HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder(ca, cn, st); }));
+        }
         if (out == Out::Weights)
             HIP_TRY(hipMemcpyAsync(host.data() + (size_t)c0 * m.V, b.d_weights, (size_t)cn * m.V * 8,
                                    hipMemcpyDeviceToHost, st));
@@ -969,18 +1024,45 @@ extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t r
     }
     HIP_TRY(hipSetDevice(dev->ordinal));
     DevMem mem;
-    int64_t *dl;
     uint64_t *dt, *di;
     uint32_t *dq;
     hs_status s;
-    if ((s = mem.upload(dl, logits, rows * vocab)) != HS_OK) return s;
     if ((s = mem.upload(dt, table, len)) != HS_OK) return s;
     if ((s = mem.upload(dq, q.data(), q.size())) != HS_OK) return s;
     if ((s = mem.alloc(di, 3 * rows)) != HS_OK) return s;
-    hs::CoderArgs ca;
-    ca.logits = dl; ca.ld = (int)vocab; ca.vocab = (int)vocab; ca.table = dt; ca.table_len = (int)len;
-    ca.queries = dq; ca.bits = (int)freq_bits; ca.intervals = di;
-    HIP_TRY(hs::launch_coder(ca, (int)rows, dev->stream));
+    if (len <= (size_t)hs::CODER_MAX_TABLE) {
+        // the compact form the LM head writes: the max of each 64-column tile and
+        // min(tilemax - l, len - 1) as u16
+        const size_t nt = (vocab + 63) / 64, ld16 = round_up(vocab, 64);
+        std::vector<int64_t> tm(rows * nt, INT64_MIN);
+        std::vector<uint16_t> dd(rows * ld16, 0);
+        for (size_t r = 0; r < rows; r++)
+            for (size_t j = 0; j < vocab; j++)
+                tm[r * nt + j / 64] = std::max(tm[r * nt + j / 64], logits[r * vocab + j]);
+        for (size_t r = 0; r < rows; r++)
+            for (size_t j = 0; j < vocab; j++) {
+                const int64_t d = tm[r * nt + j / 64] - logits[r * vocab + j];
+                dd[r * ld16 + j] = (uint16_t)std::min<int64_t>(d, (int64_t)len - 1);
+            }
+        uint16_t *d16;
+        int64_t *dtm;
+        if ((s = mem.upload(d16, dd.data(), dd.size())) != HS_OK) return s;
+        if ((s = mem.upload(dtm, tm.data(), tm.size())) != HS_OK) return s;
+        int d0 = 0;
+        while ((size_t)d0 + 1 < len && table[d0 + 1] == table[0]) d0++;
+        hs::CompactCoderArgs ca;
+        ca.d16 = d16; ca.ld16 = (int)ld16; ca.tmax = dtm; ca.ntiles = (int)nt; ca.vocab = (int)vocab;
+        ca.table = dt; ca.table_len = (int)len; ca.d0 = d0; ca.queries = dq; ca.bits = (int)freq_bits;
+        ca.intervals = di;
+        HIP_TRY(hs::launch_coder_compact(ca, (int)rows, dev->stream));
+    } else {
+        int64_t *dl;
+        if ((s = mem.upload(dl, logits, rows * vocab)) != HS_OK) return s;
+        hs::CoderArgs ca;
+        ca.logits = dl; ca.ld = (int)vocab; ca.vocab = (int)vocab; ca.table = dt; ca.table_len = (int)len;
+        ca.queries = dq; ca.bits = (int)freq_bits; ca.intervals = di;
+        HIP_TRY(hs::launch_coder(ca, (int)rows, dev->stream));
+    }
     HIP_TRY(hipMemcpyAsync(out, di, rows * 24, hipMemcpyDeviceToHost, dev->stream));
     HIP_TRY(hipStreamSynchronize(dev->stream));
     return HS_OK;

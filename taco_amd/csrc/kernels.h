@@ -14,7 +14,7 @@ struct RowInfo {
     int32_t slot, token, pos, out;
 };
 
-enum class Epi : int { Raw = 0, Act = 1, Residual = 2, Gelu = 3, Logits = 4 };
+enum class Epi : int { Raw = 0, Act = 1, Residual = 2, Gelu = 3, Logits = 4, LogitsCompact = 5 };
 
 struct GemmArgs {
     const int8_t *a = nullptr;  // [m_pad, k_pad]
@@ -27,6 +27,11 @@ struct GemmArgs {
     int ldo = 0;          // elements per output row
     const int8_t *gelu = nullptr;  // Gelu table, i8 entries
     int gelu_off = 0;              // 128 or 32768
+    // LogitsCompact: out is u16 [m, ldo] = min(tilemax - logit, cap16) and tmax [m, tmax_ld] is
+    // the largest logit of each 64-column tile.
+    int64_t *tmax = nullptr;
+    int tmax_ld = 0;
+    int cap16 = 0;
 };
 
 // Tile sizes of the MFMA GEMM: w and a rows are padded to these multiples, k to 64.
@@ -51,6 +56,7 @@ struct LnArgs {
     int8_t *out = nullptr;  // [rows, ldo]
     int ldo = 0;
     const int32_t *src = nullptr;  // optional: output row i reads x row src[i]
+    const int64_t *gm = nullptr;   // gamma[j] * m, exact in i64 (|gamma m| < 2^46)
 };
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream);
 
@@ -77,6 +83,14 @@ struct AttnArgs {
 };
 hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream);
 
+// Prefill attention on MFMA for head_dim 64: a group is up to 64 consecutive rows of one slot
+// at consecutive positions (rows first .. first + count - 1 at positions pos0 ..).
+struct AttnGroup {
+    int32_t first, count, slot, pos0;
+};
+hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups,
+                                hipStream_t stream);
+
 struct CoderArgs {
     const int64_t *logits = nullptr;  // [rows, ld]
     int ld = 0;
@@ -89,5 +103,24 @@ struct CoderArgs {
     uint64_t *weights = nullptr;    // optional [rows, vocab]: the weights themselves
 };
 hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream);
+
+// The coder op over compact logits (the LogitsCompact GEMM epilogue): d16 [rows, ld16] u16 and
+// tmax [rows, ntiles] i64, with table_len <= CODER_MAX_TABLE.
+constexpr int CODER_MAX_TABLE = 16384;
+struct CompactCoderArgs {
+    const uint16_t *d16 = nullptr;
+    int ld16 = 0;
+    const int64_t *tmax = nullptr;
+    int ntiles = 0;
+    int vocab = 0;
+    const uint64_t *table = nullptr;
+    int table_len = 0;
+    int d0 = 0;  // the largest d with table[d] == table[0]
+    const uint32_t *queries = nullptr;
+    int bits = 32;
+    uint64_t *intervals = nullptr;
+    uint64_t *weights = nullptr;
+};
+hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream);
 
 }  // namespace hs

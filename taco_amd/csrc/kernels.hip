@@ -164,6 +164,52 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
 
     // Epilogue: lane holds C[4 * (lane / 16) + e][lane % 16] of each 16 x 16 tile.
+    if (EPI == (int)Epi::LogitsCompact) {
+        // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the largest
+        // logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16) per logit.
+        // The table index min(max - l, len - 1) is recovered exactly from them, because
+        // max - l = (max - tilemax) + (tilemax - l) and cap16 >= len - 1.
+        const int tile_n0 = n0 + wn * 64;
+        int32_t mlt[4];
+        bool okn[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = tile_n0 + j * 16 + (lane & 15);
+            okn[j] = n < g.n;
+            mlt[j] = okn[j] ? g.mult[n] : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + e;
+                int64_t l[4], mx = INT64_MIN;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    l[j] = okn[j] ? clamp64(rescale_small(acc[i][j][e], mlt[j], g.shift), -SCORE_LIMIT,
+                                            SCORE_LIMIT)
+                                  : INT64_MIN;
+                    mx = l[j] > mx ? l[j] : mx;
+                }
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes that hold this row
+                    const int64_t u = __shfl_xor(mx, o, 64);
+                    mx = u > mx ? u : mx;
+                }
+                if (m < g.m) {
+                    if ((lane & 15) == 0 && tile_n0 < g.n) g.tmax[(size_t)m * g.tmax_ld + tile_n0 / 64] = mx;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (!okn[j]) continue;
+                        const int64_t dd = mx - l[j];
+                        ((uint16_t *)g.out)[(size_t)m * g.ldo + tile_n0 + j * 16 + (lane & 15)] =
+                            (uint16_t)(dd < g.cap16 ? dd : g.cap16);
+                    }
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int n = n0 + wn * 64 + j * 16 + (lane & 15);
@@ -210,6 +256,7 @@ hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream) {
         case Epi::Residual: hipLaunchKernelGGL(k_gemm<2>, grid, dim3(256), 0, stream, g); break;
         case Epi::Gelu: hipLaunchKernelGGL(k_gemm<3>, grid, dim3(256), 0, stream, g); break;
         case Epi::Logits: hipLaunchKernelGGL(k_gemm<4>, grid, dim3(256), 0, stream, g); break;
+        case Epi::LogitsCompact: hipLaunchKernelGGL(k_gemm<5>, grid, dim3(256), 0, stream, g); break;
     }
     return hipGetLastError();
 }
@@ -245,62 +292,65 @@ hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int 
 // with beta_frac); out = clamp(y, -127, 127).
 // =============================================================================================
 
-__global__ __launch_bounds__(256) void k_layernorm(LnArgs a) {
-    __shared__ int64_t s_sum[256];
-    __shared__ u128 s_sq[256];
-    __shared__ int64_t s_mean;
-    __shared__ uint64_t s_inv;
-    const int row = blockIdx.x, tid = threadIdx.x, d = a.d;
+__device__ __forceinline__ u128 wave_sum128(u128 v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t lo = __shfl_xor((uint64_t)v, o, 64);
+        const uint64_t hi = __shfl_xor((uint64_t)(v >> 64), o, 64);
+        v += ((u128)hi << 64) | lo;
+    }
+    return v;
+}
+
+// One wave per row, four rows per workgroup: no LDS and no barriers. The per-row constants
+// (mean, inv) come from lane 0 through a readlane; every lane then rescales its elements.
+// (x - mean) * inv * gamma * m is formed as ((x - mean) * inv) * (gamma * m): the reference's
+// bounds (|t| < 2^95, |m| < 2^31, layernorm.rs:31-39) keep it below 2^126, so its wrapping
+// product never wraps and the two forms are the same integer.
+__global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;
+    const int d = a.d;
     const int src = a.src ? a.src[row] : row;
     const int32_t *x = a.x + (size_t)src * d;
     int64_t sum = 0;
-    for (int j = tid; j < d; j += 256) sum += x[j];
-    s_sum[tid] = sum;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) s_sum[tid] += s_sum[tid + o];
-        __syncthreads();
-    }
-    const int64_t mean = floor_div64(s_sum[0], d);
+    for (int j = lane; j < d; j += 64) sum += x[j];
+    sum = wave_sum64(sum);
+    const int64_t mean = floor_div64(sum, d);
     u128 sq = 0;
-    for (int j = tid; j < d; j += 256) {
+    for (int j = lane; j < d; j += 64) {
         const int64_t c = (int64_t)x[j] - mean;
         const uint64_t u = c < 0 ? (uint64_t)(-c) : (uint64_t)c;
         sq += (u128)u * u;
     }
-    s_sq[tid] = sq;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) s_sq[tid] += s_sq[tid + o];
-        __syncthreads();
-    }
-    if (tid == 0) {
-        const u128 var = s_sq[0] / (u128)(uint32_t)d;
+    sq = wave_sum128(sq);
+    uint64_t inv = 0;
+    if (lane == 0) {
+        const u128 var = sq / (u128)(uint32_t)d;
         const u128 root = isqrt128((var << (2 * a.j)) + (u128)a.eps);
-        const u128 inv = ((u128)1 << a.k) / (root > 0 ? root : 1);
-        s_mean = mean;
-        s_inv = (uint64_t)inv;
+        inv = (uint64_t)(((u128)1 << a.k) / (root > 0 ? root : 1));
     }
-    __syncthreads();
-    const i128 inv = (i128)(u128)s_inv;
-    const int64_t mn = s_mean;
-    for (int j = tid; j < d; j += 256) {
-        const i128 t = (i128)((int64_t)x[j] - mn) * inv * (i128)a.gamma[j];
-        const i128 p = (i128)((u128)t * (u128)(i128)a.m);  // wrapping, as rescale_wide
+    inv = __shfl(inv, 0, 64);
+    const i128 inv128 = (i128)(u128)inv;
+    int8_t *out = a.out + (size_t)row * a.ldo;
+    for (int j = lane; j < d; j += 64) {
+        const i128 cinv = (i128)((int64_t)x[j] - mean) * inv128;
+        const i128 p = cinv * (i128)a.gm[j];
         i128 y;
         if (a.beta_frac == 0) {
             y = shift_round128(p, a.s, 126) + (i128)a.beta[j];
         } else {
             const i128 c = (i128)a.beta[j] << (a.s - a.beta_frac);
-            y = shift_round128((i128)((u128)p + (u128)c), a.s, 126);
+            y = shift_round128(p + c, a.s, 126);
         }
-        a.out[(size_t)row * a.ldo + j] = (int8_t)clamp128(y, -127, 127);
+        out[j] = (int8_t)clamp128(y, -127, 127);
     }
 }
 
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_layernorm, dim3(n_rows), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(k_layernorm, dim3((n_rows + 3) / 4), dim3(256), 0, stream, a, n_rows);
     return hipGetLastError();
 }
 
@@ -418,6 +468,190 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
     const int tasks = n_rows * a.n_head;
     if (tasks <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_attend, dim3((tasks + 3) / 4), dim3(256), 0, stream, a, tasks);
+    return hipGetLastError();
+}
+
+// =============================================================================================
+// Prefill attention on MFMA (head_dim 64). One workgroup = one group of <= 64 rows x one head;
+// wave w owns rows 16w .. 16w + 15. Three passes over the keys in blocks of 64, recomputing
+// S = Q K^T with v_mfma_i32_16x16x64_i8 (exact i32): (1) the row max of the scores, (2) the sum
+// of the table entries, (3) p = floor(e 2^P / S) and sum_j p_j v_j. The PV product splits p into
+// four balanced signed base-256 digits (crates/hardshell/src/gpt2/attention.rs:36-46), so it is
+// four exact i8 MFMA products: |sum_j d_j v_j| <= 2^16 * 128 * 127 < 2^31.
+// =============================================================================================
+
+constexpr int AT_ST = 80;  // LDS row stride in bytes (64 + 16)
+
+__global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup *groups) {
+    __shared__ __attribute__((aligned(16))) int8_t sQ[64 * AT_ST];
+    __shared__ __attribute__((aligned(16))) int8_t sK[64 * AT_ST];
+    __shared__ __attribute__((aligned(16))) int8_t sVt[64 * AT_ST];
+    __shared__ __attribute__((aligned(16))) int8_t sP[4][64 * AT_ST];
+    const AttnGroup G = groups[blockIdx.x];
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int nk = G.pos0 + G.count;  // keys 0 .. nk - 1, never past the cache
+    nk = nk > a.ctx_cap ? a.ctx_cap : nk;
+    const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
+    const int last = a.exp_len - 1;
+    {
+        const int r = tid >> 2, c = (tid & 3) * 16;
+        v4i v = {0, 0, 0, 0};
+        if (r < G.count) v = *(const v4i *)(a.q + (size_t)(G.first + r) * a.ldq + h * 64 + c);
+        *(v4i *)&sQ[r * AT_ST + c] = v;
+    }
+    __syncthreads();
+    const v4i qf = *(const v4i *)&sQ[(16 * w + (lane & 15)) * AT_ST + (lane >> 4) * 16];
+    // this lane's rows (e = 0..3) and their positions
+    int row[4], posr[4];
+    bool valid[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        row[e] = 16 * w + 4 * (lane >> 4) + e;
+        valid[e] = row[e] < G.count;
+        posr[e] = G.pos0 + row[e];
+    }
+    auto load_k = [&](int kb) {
+        const int key = kb * 64 + (tid >> 2), c = (tid & 3) * 16;
+        v4i v = {0, 0, 0, 0};
+        if (key < nk) v = *(const v4i *)(a.kc + base + (size_t)key * 64 + c);
+        *(v4i *)&sK[(tid >> 2) * AT_ST + c] = v;
+    };
+    auto load_vt = [&](int kb) {
+        const int kl = tid >> 2, key = kb * 64 + kl, c = (tid & 3) * 16;
+        v4i v = {0, 0, 0, 0};
+        if (key < nk) v = *(const v4i *)(a.vc + base + (size_t)key * 64 + c);
+        const int8_t *b = (const int8_t *)&v;
+#pragma unroll
+        for (int i = 0; i < 16; i++) sVt[(c + i) * AT_ST + kl] = b[i];
+    };
+    auto qk = [&](v4i s[4]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const v4i kf = *(const v4i *)&sK[(t * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
+            s[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qf, kf, v4i{0, 0, 0, 0}, 0, 0, 0);
+        }
+    };
+    auto score = [&](int32_t dot) {
+        return clamp64(rescale_small(dot, a.score_m, a.score_s), -SCORE_LIMIT, SCORE_LIMIT);
+    };
+    const int nkb = (nk + 63) / 64;
+    int64_t mx[4] = {INT64_MIN, INT64_MIN, INT64_MIN, INT64_MIN};
+    for (int kb = 0; kb < nkb; kb++) {  // pass 1: the row max
+        load_k(kb);
+        __syncthreads();
+        v4i s[4];
+        qk(s);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int key = kb * 64 + t * 16 + (lane & 15);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (valid[e] && key <= posr[e]) {
+                    const int64_t sc = score(s[t][e]);
+                    mx[e] = sc > mx[e] ? sc : mx[e];
+                }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const int64_t u = __shfl_xor(mx[e], o, 64);
+            mx[e] = u > mx[e] ? u : mx[e];
+        }
+    int64_t sum[4] = {0, 0, 0, 0};
+    for (int kb = 0; kb < nkb; kb++) {  // pass 2: the sum of the table entries
+        load_k(kb);
+        __syncthreads();
+        v4i s[4];
+        qk(s);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int key = kb * 64 + t * 16 + (lane & 15);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (valid[e] && key <= posr[e]) {
+                    const int64_t dd = mx[e] - score(s[t][e]);
+                    sum[e] += a.exp_table[dd < last ? dd : last];
+                }
+        }
+        __syncthreads();
+    }
+    uint64_t frac[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sum[e] += __shfl_xor(sum[e], o, 64);
+        // floor(2^64 / S) for S >= 2; S = 1 divides exactly
+        frac[e] = sum[e] >= 2 ? (uint64_t)(((u128)1 << 64) / (uint64_t)sum[e]) : 0;
+    }
+    v4i acc[4][4];  // [digit plane][channel tile]
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[k][c] = v4i{0, 0, 0, 0};
+    for (int kb = 0; kb < nkb; kb++) {  // pass 3: p and the digit-plane PV products
+        load_k(kb);
+        load_vt(kb);
+        __syncthreads();
+        v4i s[4];
+        qk(s);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int key = kb * 64 + t * 16 + (lane & 15);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int64_t p = 0;
+                if (valid[e] && key <= posr[e]) {
+                    const int64_t dd = mx[e] - score(s[t][e]);
+                    const uint64_t num = (uint64_t)a.exp_table[dd < last ? dd : last] << a.softmax_p;
+                    const uint64_t S = (uint64_t)sum[e];
+                    uint64_t q = num;
+                    if (S >= 2) {
+                        q = __umul64hi(num, frac[e]);  // q <= floor(num / S) <= q + 1
+                        if (num - q * S >= S) q++;
+                    }
+                    p = (int64_t)q;
+                }
+                int64_t rest = p;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int64_t dg = ((rest + 128) & 255) - 128;
+                    sP[k][row[e] * AT_ST + t * 16 + (lane & 15)] = (int8_t)dg;
+                    rest = (rest - dg) >> 8;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const v4i af = *(const v4i *)&sP[k][(16 * w + (lane & 15)) * AT_ST + (lane >> 4) * 16];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const v4i bf = *(const v4i *)&sVt[(c * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
+                acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, acc[k][c], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (!valid[e]) continue;
+            const int64_t o = (int64_t)acc[0][c][e] + ((int64_t)acc[1][c][e] << 8) +
+                              ((int64_t)acc[2][c][e] << 16) + ((int64_t)acc[3][c][e] << 24);
+            a.out[(size_t)(G.first + row[e]) * a.ldo + h * 64 + c * 16 + (lane & 15)] =
+                (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
+        }
+}
+
+hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups,
+                                hipStream_t stream) {
+    if (n_groups <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_attend_mfma, dim3(n_groups, a.n_head), dim3(256), 0, stream, a, groups);
     return hipGetLastError();
 }
 
@@ -588,6 +822,189 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
 hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_coder, dim3(n_rows), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+
+// =============================================================================================
+// The coder op over compact logits. One workgroup per row, one coalesced pass over the row: the
+// table index d_j = min(M - l_j, len - 1) of every symbol goes into a histogram in LDS (and a
+// second one for the symbols below an Encode token), so the quotients floor(table[d] * spare /
+// W) are computed once per table entry, not once per symbol:
+//   W = sum_d cnt[d] table[d];  sum f = V + sum_d cnt[d] q[d];  sum_{j<tok} f = tok + sum_d
+//   cnt_lo[d] q[d].  largest = the first symbol whose weight is table[0] (d <= d0).
+// A Decode query needs the starts in symbol order: an ordered block scan over the row.
+// =============================================================================================
+
+__device__ __forceinline__ int64_t block_max64(int64_t v, int64_t *s, int tid) {
+    s[tid] = v;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) s[tid] = s[tid + o] > s[tid] ? s[tid + o] : s[tid];
+        __syncthreads();
+    }
+    v = s[0];
+    __syncthreads();
+    return v;
+}
+
+__device__ __forceinline__ uint64_t block_sum64(uint64_t v, uint64_t *s, int tid) {
+    s[tid] = v;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) s[tid] += s[tid + o];
+        __syncthreads();
+    }
+    v = s[0];
+    __syncthreads();
+    return v;
+}
+
+__global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
+    extern __shared__ uint32_t hist[];  // cnt[len], cnt_lo[len]
+    __shared__ int64_t s_i[256];
+    __shared__ uint64_t s_u[256];
+    __shared__ uint32_t s_dtok;
+    __shared__ uint64_t s_frac;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int V = a.vocab, len = a.table_len, last = len - 1;
+    uint32_t *cnt = hist, *cnt_lo = hist + len;
+    const uint16_t *d16 = a.d16 + (size_t)row * a.ld16;
+    const int64_t *tm = a.tmax + (size_t)row * a.ntiles;
+    const uint32_t kind = a.queries ? a.queries[2 * row] : 0;
+    const uint32_t value = a.queries ? a.queries[2 * row + 1] : 0;
+    const uint32_t tok = kind == 0 ? value : 0;  // Encode token (0: no symbol below)
+
+    int64_t mx = INT64_MIN;
+    for (int t = tid; t < a.ntiles; t += 256) mx = tm[t] > mx ? tm[t] : mx;
+    const int64_t M = block_max64(mx, s_i, tid);
+    for (int d = tid; d < 2 * len; d += 256) hist[d] = 0;
+    __syncthreads();
+
+    // One pass: 8 consecutive symbols per thread and step (one 16-byte load).
+    int64_t first = INT64_MAX;  // the first symbol with weight table[0]
+    for (int g0 = tid * 8; g0 < V; g0 += 256 * 8) {
+        const uint4 raw = *(const uint4 *)(d16 + g0);
+        const uint16_t *dv = (const uint16_t *)&raw;
+        const int64_t base = M - tm[g0 >> 6];  // the 8 symbols share a 64-column tile
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = g0 + q;
+            if (j >= V) break;
+            const int64_t dd = base + dv[q];
+            const int d = (int)(dd < last ? dd : last);
+            atomicAdd(&cnt[d], 1u);
+            if ((uint32_t)j < tok) atomicAdd(&cnt_lo[d], 1u);
+            if ((uint32_t)j == value && kind == 0) s_dtok = (uint32_t)d;
+            if (d <= a.d0 && j < first) first = j;
+            if (a.weights) a.weights[(size_t)row * V + j] = a.table[d];
+        }
+    }
+    __syncthreads();
+    const int64_t largest = -block_max64(-first, s_i, tid);
+
+    uint64_t W = 0;
+    for (int d = tid; d < len; d += 256) W += (uint64_t)cnt[d] * a.table[d];
+    W = block_sum64(W, s_u, tid);
+    const uint64_t total = (uint64_t)1 << a.bits, spare = total - (uint64_t)V;
+    if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? (uint64_t)(((u128)spare << 64) / W) : 0;
+    __syncthreads();
+    const uint64_t frac = s_frac;
+    uint64_t S = 0, Slo = 0;
+    for (int d = tid; d < len; d += 256) {
+        if (!cnt[d]) continue;
+        const uint64_t q = quotient(a.table[d], spare, W, frac);
+        S += (uint64_t)cnt[d] * q;
+        Slo += (uint64_t)cnt_lo[d] * q;
+    }
+    S = block_sum64(S, s_u, tid);
+    Slo = block_sum64(Slo, s_u, tid);
+    const uint64_t rem = total - ((uint64_t)V + S);
+    uint64_t *out = a.intervals ? a.intervals + 3 * (size_t)row : nullptr;
+    if (!out) return;
+    if (kind == 0) {
+        if (tid == 0) {
+            const uint64_t f = 1 + quotient(a.table[s_dtok], spare, W, frac);
+            out[0] = tok;
+            out[1] = (uint64_t)tok + Slo + ((int64_t)tok > largest ? rem : 0);
+            out[2] = f + ((int64_t)tok == largest ? rem : 0);
+        }
+        return;
+    }
+    // Decode: the largest i with start_i <= target, in symbol order, 2048 symbols per step.
+    const uint64_t target = value;
+    uint64_t run = 0;
+    int64_t cand = -1;
+    uint64_t cstart = 0, cfreq = 0;
+    for (int b = 0; b < V; b += 2048) {
+        uint64_t f[8];
+        uint64_t local = 0;
+        const int j0 = b + tid * 8;
+        if (j0 < V) {
+            const uint4 raw = *(const uint4 *)(d16 + j0);
+            const uint16_t *dv = (const uint16_t *)&raw;
+            const int64_t base = M - tm[j0 >> 6];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = j0 + q;
+                f[q] = 0;
+                if (j < V) {
+                    const int64_t dd = base + dv[q];
+                    const int d = (int)(dd < last ? dd : last);
+                    f[q] = 1 + quotient(a.table[d], spare, W, frac) + (j == largest ? rem : 0);
+                    local += f[q];
+                }
+            }
+        }
+        s_u[tid] = local;
+        __syncthreads();
+        if (tid == 0) {  // exclusive scan of the 256 partial sums, in order
+            uint64_t acc = run;
+            for (int t = 0; t < 256; t++) {
+                const uint64_t v = s_u[t];
+                s_u[t] = acc;
+                acc += v;
+            }
+            s_i[0] = (int64_t)acc;
+        }
+        __syncthreads();
+        uint64_t start = s_u[tid];
+        const uint64_t next_run = (uint64_t)s_i[0];
+        __syncthreads();
+        if (j0 < V) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = j0 + q;
+                if (j >= V) break;
+                if (start <= target) {
+                    cand = j;
+                    cstart = start;
+                    cfreq = f[q];
+                }
+                start += f[q];
+            }
+        }
+        run = next_run;
+    }
+    const int64_t best = block_max64(cand, s_i, tid);
+    if (cand >= 0 && cand == best) {
+        out[0] = (uint64_t)cand;
+        out[1] = cstart;
+        out[2] = cfreq;
+    }
+}
+
+hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
+    if (n_rows <= 0) return hipSuccess;
+    const size_t lds = 2 * sizeof(uint32_t) * (size_t)a.table_len;
+    static size_t allowed = 0;  // raise the dynamic LDS limit once per size
+    if (lds > allowed) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_coder_compact,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        allowed = lds;
+    }
+    hipLaunchKernelGGL(k_coder_compact, dim3(n_rows), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 

@@ -330,6 +330,11 @@ def _coder_cases():
     # a short table and a table with a flat start (ties among weights for different logits)
     t2 = np.array([1 << 40, 1 << 40, 1 << 39, 5, 1], np.uint64)
     cases.append((700, r.integers(-8, 8, (4, 700)).astype(np.int64), t2))
+    # a table longer than the compact form allows (the i64 logits kernel)
+    t3 = np.array([round(2 ** 40 * np.exp(-i / 2048)) for i in range(20000)], np.uint64)
+    l3 = r.integers(-30000, 30000, (6, 3000)).astype(np.int64)
+    l3[1, [5, 2999]] = 40000
+    cases.append((3000, l3, t3))
     return cases
 
 
@@ -356,3 +361,21 @@ def test_coder_op_equals_from_weights(dev):
             dec = hip.coder(dev, logits, table, [(1, t) for t in targets[:rows]], bits)
             for i in range(rows):
                 assert tuple(dec[i]) == O.freq_find(weights[i], bits, targets[i]), (vocab, bits, i)
+
+
+@pytest.mark.parametrize("overlap", [0, 32])
+def test_head_dim_64_prefill_equals_the_reference(dev, overlap):
+    """head_dim 64 takes the MFMA prefill attention (groups of up to 64 rows of one slot):
+    windows shorter and longer than a group, and longer than n_ctx (context restarts)."""
+    from taco_amd import fold, hip
+    b = O.build_model((2, 2, 128, 256, 500, 160), 21, 16)
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    lens = [1, 17, 64, 65, 130, 200, 333]
+    blocks = [np.array(splitmix_tokens(40 + i, n, 499), np.uint32) for i, n in enumerate(lens)]
+    batch = hip.HipBatch(hm, 4, 512)
+    batch.set_overlap(overlap)
+    from taco_amd import fold
+    got = fold.fold_blocks(batch, blocks, overlap)
+    for i, blk in enumerate(blocks):
+        print(f"block {i} ({len(blk)} tokens, K {overlap})", flush=True)
+        assert got[i] == O.encode_block(om, blk, overlap=overlap), i
