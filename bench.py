@@ -48,6 +48,9 @@ def main():
                     help="windows in the CPU-baseline sample (0: one per thread)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first copy this many MiB device to device (the known-size copy that "
+                         "scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): the fold shards by windows "
@@ -70,6 +73,16 @@ def main():
         f"{synth.sha256_tokens(tokens)[:16]}")
 
     dev = hip.HipDevice.open(0)
+    if args.calib_copy_mib:
+        import ctypes as C
+        nb = args.calib_copy_mib << 20
+        src, dst = C.c_void_p(), C.c_void_p()
+        hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(src)))
+        hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(dst)))
+        hip._check(hip.lib().hs_device_copy(dev.h, dst, src, nb))
+        hip.lib().hs_device_free(dev.h, src)
+        hip.lib().hs_device_free(dev.h, dst)
+        log(f"calibration copy: {args.calib_copy_mib} MiB device to device")
     model = hip.HipModel.load(dev, model_bytes)
     batch = hip.HipBatch(model, W, W * n)
     log(f"device {dev.name()}, model {model.weight_bytes() / 1e6:.1f} MB, batch "

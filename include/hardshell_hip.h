@@ -228,6 +228,8 @@ void hs_device_free(hs_device *dev, void *ptr);
 hs_status hs_device_upload(hs_device *dev, void *dst, const void *src, size_t bytes);
 hs_status hs_device_download(hs_device *dev, void *dst, const void *src, size_t bytes);
 hs_status hs_device_synchronize(hs_device *dev);
+/* Device-to-device copy; also the known-size copy that calibrates HBM traffic counters. */
+hs_status hs_device_copy(hs_device *dev, void *dst, const void *src, size_t bytes);
 
 #ifdef __cplusplus
 }

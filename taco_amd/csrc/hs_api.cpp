@@ -123,6 +123,7 @@ struct hs_model {
     uint64_t weight_bytes = 0;
     bool compact = false;  // the LM head writes compact logits (table_len <= CODER_MAX_TABLE)
     int d0 = 0;            // the largest d with logits_exp[d] == logits_exp[0]
+    int zcut = 0;          // logits_exp[d] == 0 for every d >= zcut
     int ntiles = 0, ld16 = 0;
 };
 
@@ -261,6 +262,8 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
     if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size())) != HS_OK) return st;
     m->compact = h.logits_exp.size() <= (size_t)hs::CODER_MAX_TABLE;
     while ((size_t)m->d0 + 1 < h.logits_exp.size() && h.logits_exp[m->d0 + 1] == h.logits_exp[0]) m->d0++;
+    m->zcut = (int)h.logits_exp.size();
+    while (m->zcut > 1 && h.logits_exp[m->zcut - 1] == 0) m->zcut--;
     m->ntiles = (m->V + 63) / 64;
     m->ld16 = (int)round_up(m->V, 64);
     m->weight_bytes = mem.bytes;
@@ -303,6 +306,65 @@ struct PassRow {
     int64_t input;  // index of the input it answers, -1 for a restart row
 };
 
+// The bookkeeping of the inputs of one slot for a truncation (crates/hardshell/src/gpt2/
+// stream.rs:43-204): the inputs since the last reset, the first position of the current context
+// that holds an input, one more than the highest position written, and `first` of the context
+// before the last restart.
+struct StreamState {
+    size_t len = 0, first = 0, written = 0;
+    bool has_prev = false;
+    size_t prev_first = 0;
+
+    // stream.rs:119-121: the inputs a slot at `pos` takes before its next restart.
+    static size_t room(size_t pos, size_t n_ctx, size_t k) {
+        if (pos >= n_ctx) return n_ctx > k + 1 ? n_ctx - (k + 1) : 0;
+        return n_ctx - pos;
+    }
+    void input(size_t pos) {
+        len += 1;
+        written = std::max(written, pos + 1);
+    }
+    void restart(size_t k) {
+        prev_first = first;
+        has_prev = true;
+        first = k + 1;
+        written = k + 1;
+    }
+};
+
+struct Truncation {
+    size_t len = 0, pos = 0;
+    bool restore = false;
+    size_t rebuild_end = 0;  // positions 0 .. rebuild_end run again with the kept history
+};
+
+// stream.rs:155-172. Returns false for a truncation the rules refuse (BadTruncate).
+bool plan_truncate(const StreamState &st, size_t len, size_t pos, size_t n_ctx, Truncation &t) {
+    if (len > st.len) return false;
+    const size_t drop = st.len - len;
+    const size_t here = pos > st.first ? pos - st.first : 0;
+    if (drop <= here) {
+        t = Truncation{len, pos - drop, false, 0};
+        return true;
+    }
+    if (!st.has_prev) return false;
+    const size_t before = drop - here;
+    if (before > (n_ctx > st.prev_first ? n_ctx - st.prev_first : 0)) return false;
+    const size_t target = n_ctx - before;  // the old context was full: its position was n_ctx
+    t = Truncation{len, target, true, std::min(target, st.written)};
+    return true;
+}
+
+// stream.rs:176-188.
+void commit_truncate(StreamState &st, const Truncation &t, size_t n_ctx) {
+    st.len = t.len;
+    if (t.restore && st.has_prev) {
+        st.first = st.prev_first;
+        st.has_prev = false;
+        st.written = n_ctx;
+    }
+}
+
 }  // namespace
 
 struct hs_batch {
@@ -311,7 +373,8 @@ struct hs_batch {
     uint32_t overlap = 0;
     std::vector<size_t> pos;
     std::vector<uint32_t> hist;    // [slots, n_ctx]: the token at each position
-    std::vector<size_t> stream;    // tokens of the current stream of each slot (ADR 0017)
+    std::vector<StreamState> streams;
+    std::vector<std::vector<uint32_t>> prev;  // [slot]: the full context before its last restart
     std::vector<uint64_t> host_w;  // [slots, vocab]: weights of the last step
     hipStream_t st = nullptr;
     DevMem mem;
@@ -408,7 +471,8 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     b->rows_pad = round_up(b->max_rows, hs::GEMM_BM);
     b->pos.assign(slots, 0);
     b->hist.assign(slots * m.C, 0);
-    b->stream.assign(slots, 0);
+    b->streams.assign(slots, StreamState{});
+    b->prev.assign(slots, {});
     // The LM head runs on chunks of output rows: compact logits (2 B per logit) up to 4 GiB a
     // chunk, i64 logits up to 1 GiB.
     const size_t per_row = m.compact ? 2ull * m.ld16 : 8ull * m.V_pad;
@@ -471,7 +535,7 @@ extern "C" size_t hs_batch_position(const hs_batch *b, size_t slot) {
 extern "C" void hs_batch_reset(hs_batch *b, size_t slot) {
     if (b && slot < b->slots) {
         b->pos[slot] = 0;
-        b->stream[slot] = 0;
+        b->streams[slot] = StreamState{};
     }
 }
 
@@ -483,7 +547,8 @@ struct Plan {
     std::vector<std::vector<PassRow>> passes;
     std::vector<size_t> pos;
     std::unordered_map<size_t, std::vector<uint32_t>> hist;
-    std::vector<size_t> stream;
+    std::vector<StreamState> streams;
+    std::unordered_map<size_t, std::vector<uint32_t>> prev;
 };
 
 Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
@@ -492,7 +557,7 @@ Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
     const size_t k = std::min<size_t>(b.overlap, C - 2);
     const uint32_t eot = b.model->host.eot;
     p.pos = b.pos;
-    p.stream = b.stream;
+    p.streams = b.streams;
     std::vector<PassRow> cur;
     std::vector<char> in_pass(b.slots, 0);
     auto flush = [&]() {
@@ -514,14 +579,15 @@ Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
         size_t at = p.pos[slot];
         if (at >= C) {
             if (in_pass[slot]) flush();
+            p.prev[slot] = h;  // the full context before the restart, for a truncation
+            p.streams[slot].restart(k);
             if (k > 0) std::memmove(&h[1], &h[C - k], k * sizeof(uint32_t));
             h[0] = eot;
             for (size_t q = 0; q <= k; q++) push(PassRow{(uint32_t)slot, h[q], (uint32_t)q, -1});
             at = k + 1;
-            p.stream[slot] = k;  // the stream keeps its last k tokens
         }
         h[at] = in[i].token;
-        p.stream[slot] += 1;
+        p.streams[slot].input(at);
         push(PassRow{(uint32_t)slot, in[i].token, (uint32_t)at, (int64_t)i});
         p.pos[slot] = at + 1;
     }
@@ -532,8 +598,9 @@ Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
 void commit(hs_batch &b, Plan &p) {
     const size_t C = b.model->host.n_ctx;
     b.pos = p.pos;
-    b.stream = p.stream;
+    b.streams = p.streams;
     for (auto &kv : p.hist) std::memcpy(&b.hist[kv.first * C], kv.second.data(), C * sizeof(uint32_t));
+    for (auto &kv : p.prev) b.prev[kv.first] = std::move(kv.second);
 }
 
 enum class Out { Weights, Intervals };
@@ -647,6 +714,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             hs::CompactCoderArgs ca;
             ca.d16 = b.d_d16; ca.ld16 = m.ld16; ca.tmax = b.d_tmax; ca.ntiles = m.ntiles; ca.vocab = m.V;
             ca.table = m.logits_exp; ca.table_len = (int)m.host.logits_exp.size(); ca.d0 = m.d0;
+            ca.zcut = m.zcut;
             ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
             ca.bits = (int)bits;
             ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
@@ -760,27 +828,45 @@ extern "C" hs_status hs_batch_weights(const hs_batch *b, size_t slot, uint64_t *
     return HS_OK;
 }
 
-// The stream of a slot (crates/hardshell/src/gpt2/stream.rs, hardshell-cuda batch/stream.rs):
-// the tokens since the block start that the current context still holds, the free positions
-// before the next restart, and truncation back to `len` stream tokens.
+// The stream of a slot (crates/hardshell-cuda/src/batch/stream.rs:15-75): the inputs since the
+// last reset, the room before the next restart, and the truncation of speculative decoding.
 extern "C" size_t hs_batch_stream_len(const hs_batch *b, size_t slot) {
-    return (b && slot < b->slots) ? b->stream[slot] : 0;
+    return (b && slot < b->slots) ? b->streams[slot].len : 0;
 }
 extern "C" size_t hs_batch_room(const hs_batch *b, size_t slot) {
     if (!b || slot >= b->slots) return 0;
-    const size_t C = b->model->host.n_ctx;
-    return b->pos[slot] >= C ? 0 : C - b->pos[slot];
+    return StreamState::room(b->pos[slot], b->model->host.n_ctx, b->overlap);
 }
 extern "C" hs_status hs_batch_truncate(hs_batch *b, size_t slot, size_t len) {
     hs::clear_error();
     if (!b) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL batch");
-    if (slot >= b->slots) return hs::fail(HS_BAD_SLOT, (int)slot, "slot is not valid");
-    const size_t cur = b->stream[slot];
-    const size_t drop = cur >= len ? cur - len : 0;
-    if (len > cur || drop > b->pos[slot] - (b->pos[slot] > cur ? b->pos[slot] - cur : 0))
-        return hs::fail(HS_MODEL_ERROR, HS_MODEL_BAD_TRUNCATE, "the truncation is outside the current context");
-    b->pos[slot] -= drop;
-    b->stream[slot] = len;
+    if (slot >= b->slots)
+        return hs::fail(HS_BAD_SLOT, (int)slot, "slot " + std::to_string(slot) + " is not valid in a batch of " +
+                                                     std::to_string(b->slots) + " slots");
+    const size_t C = b->model->host.n_ctx;
+    Truncation t;
+    if (!plan_truncate(b->streams[slot], len, b->pos[slot], C, t))
+        return hs::fail(HS_MODEL_ERROR, HS_MODEL_BAD_TRUNCATE,
+                        "cannot truncate a stream of " + std::to_string(b->streams[slot].len) + " inputs to " +
+                            std::to_string(len));
+    if (t.restore) {
+        // The rows of the old context that the new context wrote again, with the kept history
+        // (no weights); positions the new context did not write keep their old cache entries.
+        HIP_TRY(hipSetDevice(b->model->dev->ordinal));
+        const std::vector<uint32_t> &prev = b->prev[slot];
+        std::vector<PassRow> rows;
+        for (size_t q = 0; q < t.rebuild_end && q < prev.size(); q++)
+            rows.push_back(PassRow{(uint32_t)slot, prev[q], (uint32_t)q, -1});
+        for (size_t r0 = 0; r0 < rows.size(); r0 += b->max_rows) {
+            std::vector<PassRow> pass(rows.begin() + r0, rows.begin() + std::min(rows.size(), r0 + b->max_rows));
+            hs_status s = run_pass(*b, pass, Out::Weights, nullptr, 0, nullptr);
+            if (s != HS_OK) return s;
+        }
+        HIP_TRY(hipStreamSynchronize(b->st));
+        if (prev.size() == C) std::memcpy(&b->hist[slot * C], prev.data(), C * sizeof(uint32_t));
+    }
+    commit_truncate(b->streams[slot], t, C);
+    b->pos[slot] = t.pos;
     return HS_OK;
 }
 
@@ -1005,6 +1091,13 @@ extern "C" hs_status hs_device_synchronize(hs_device *dev) {
     return HS_OK;
 }
 
+extern "C" hs_status hs_device_copy(hs_device *dev, void *dst, const void *src, size_t bytes) {
+    if (!dev || (bytes && (!dst || !src))) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
+}
+
 extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t rows, size_t vocab,
                                  const uint64_t *table, size_t len, const hs_query *queries,
                                  uint32_t freq_bits, hs_interval *out) {
@@ -1014,6 +1107,12 @@ extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t r
     if (vocab == 0 || vocab > (1u << 20) || len == 0 || freq_bits == 0 || freq_bits > 32 ||
         (uint64_t)vocab > (1ull << freq_bits))
         return hs::fail(HS_UNSUPPORTED, 0, "vocab in 1..=2^20, len >= 1, freq_bits in 1..=32 with 2^freq_bits >= vocab");
+    // The table rule of the model loader's logits table (crates/hardshell/src/logits.rs:38-49):
+    // non-increasing, first entry >= 1, entries <= 2^40.
+    if (table[0] < 1 || table[0] > (1ull << 40))
+        return hs::fail(HS_UNSUPPORTED, 0, "the table must start in 1..=2^40");
+    for (size_t i = 1; i < len; i++)
+        if (table[i] > table[i - 1]) return hs::fail(HS_UNSUPPORTED, 0, "the table must be non-increasing");
     std::vector<uint32_t> q(2 * rows);
     for (size_t r = 0; r < rows; r++) {
         const bool ok = (queries[r].kind == 0 && queries[r].value < vocab) ||
@@ -1050,9 +1149,12 @@ extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t r
         if ((s = mem.upload(dtm, tm.data(), tm.size())) != HS_OK) return s;
         int d0 = 0;
         while ((size_t)d0 + 1 < len && table[d0 + 1] == table[0]) d0++;
+        int zcut = (int)len;
+        while (zcut > 1 && table[zcut - 1] == 0) zcut--;
         hs::CompactCoderArgs ca;
         ca.d16 = d16; ca.ld16 = (int)ld16; ca.tmax = dtm; ca.ntiles = (int)nt; ca.vocab = (int)vocab;
-        ca.table = dt; ca.table_len = (int)len; ca.d0 = d0; ca.queries = dq; ca.bits = (int)freq_bits;
+        ca.table = dt; ca.table_len = (int)len; ca.d0 = d0; ca.zcut = zcut; ca.queries = dq;
+        ca.bits = (int)freq_bits;
         ca.intervals = di;
         HIP_TRY(hs::launch_coder_compact(ca, (int)rows, dev->stream));
     } else {

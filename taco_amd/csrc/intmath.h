@@ -1,0 +1,170 @@
+// Exact integer helpers shared by the gfx950 kernels and a host test build (g++). Every function
+// is the exact value of the integer rule it names (crates/hardshell/src/int.rs); the divisions
+// avoid generic 128-bit division, which the GPU compiler expands into a bit-serial loop.
+#pragma once
+
+#include <cstdint>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define HS_HD __host__ __device__ __forceinline__
+#else
+#define HS_HD inline
+#endif
+
+namespace hs {
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+HS_HD int clz64(uint64_t x) { return x ? __builtin_clzll(x) : 64; }
+
+HS_HD int clz128(u128 x) {
+    const uint64_t hi = (uint64_t)(x >> 64);
+    return hi ? __builtin_clzll(hi) : 64 + clz64((uint64_t)x);
+}
+
+// floor((p + 2^(s-1)) / 2^s) for |p| < 2^63 (int.rs:110-124; for s >= 64 the exact result is
+// 0). Never overflows: the low s bits round separately.
+HS_HD int64_t shift_round64(int64_t p, uint32_t s) {
+    if (s == 0) return p;
+    if (s >= 64) return 0;
+    const uint64_t r = (uint64_t)p & (((uint64_t)1 << s) - 1);
+    const uint64_t up = (r + ((uint64_t)1 << (s - 1))) >> s;
+    return (p >> s) + (int64_t)up;
+}
+
+// rescale(x, m, s) for |x| < 2^32: the product is exact in i64.
+HS_HD int64_t rescale_small(int64_t x, int32_t m, uint32_t s) { return shift_round64(x * (int64_t)m, s); }
+
+// shift_round (int.rs:110-124) of an i128 with the rule's largest shift: s = 0 keeps p, a
+// shift above max_shift gives 0.
+HS_HD i128 shift_round128(i128 p, uint32_t s, uint32_t max_shift) {
+    if (s == 0) return p;
+    if (s > max_shift) return 0;
+    const u128 half = (u128)1 << (s - 1);
+    return (i128)((u128)p + half) >> s;
+}
+
+// rescale (int.rs:63-67) for any i64 x.
+HS_HD i128 rescale_full(int64_t x, int32_t m, uint32_t s) { return shift_round128((i128)x * (i128)m, s, 95); }
+
+HS_HD int64_t clamp64(int64_t x, int64_t lo, int64_t hi) {
+    int64_t u = x < hi ? x : hi;
+    return u > lo ? u : lo;
+}
+
+HS_HD int64_t clamp128(i128 x, int64_t lo, int64_t hi) {
+    i128 u = x < (i128)hi ? x : (i128)hi;
+    return (int64_t)(u > (i128)lo ? u : (i128)lo);
+}
+
+// floor_div (int.rs) for b > 0.
+HS_HD int64_t floor_div64(int64_t a, int64_t b) {
+    int64_t q = a / b, r = a % b;
+    return (r != 0 && r < 0) ? q - 1 : q;
+}
+
+// isqrt_u128 (int.rs:213-233): the exact floor square root, digit by digit from the highest
+// even bit at or below the top bit of x.
+HS_HD u128 isqrt128(u128 x) {
+    if (x == 0) return 0;
+    u128 bit = (u128)1 << ((127 - clz128(x)) & ~1);
+    u128 rem = x, res = 0;
+    while (bit != 0) {
+        if (rem >= res + bit) {
+            rem -= res + bit;
+            res = (res >> 1) + bit;
+        } else {
+            res >>= 1;
+        }
+        bit >>= 2;
+    }
+    return res;
+}
+
+// isqrt128 for x < 2^100 from a double-precision estimate, then corrected exactly: the result
+// is the floor square root whatever the estimate (the loops step to it), and the estimate is
+// within one of it (correctly rounded conversion and square root, root < 2^50).
+HS_HD uint64_t isqrt_est(u128 x) {
+    if (x >> 100) return (uint64_t)isqrt128(x);
+    const double dx = (double)(uint64_t)(x >> 64) * 18446744073709551616.0 + (double)(uint64_t)x;
+    uint64_t r = (uint64_t)__builtin_sqrt(dx);
+    while ((u128)r * r > x) r--;
+    while ((u128)(r + 1) * (r + 1) <= x) r++;
+    return r;
+}
+
+// floor(2^64 / s) for s >= 2: 2^64 - 1 = q s + r, so 2^64 = q s + r + 1.
+HS_HD uint64_t div_2p64(uint64_t s) {
+    const uint64_t q = ~(uint64_t)0 / s;
+    const uint64_t r = ~(uint64_t)0 - q * s;
+    return r + 1 == s ? q + 1 : q;
+}
+
+// floor(x / d) for d >= 1: long division over the four 32-bit limbs (each step divides a
+// value below d * 2^32 <= 2^64).
+HS_HD u128 div_u128_u32(u128 x, uint32_t d) {
+    u128 q = 0;
+    uint64_t rem = 0;
+    for (int i = 3; i >= 0; i--) {
+        const uint64_t cur = (rem << 32) | (uint64_t)(uint32_t)(x >> (32 * i));
+        const uint64_t qi = cur / d;
+        rem = cur - qi * d;
+        q |= (u128)qi << (32 * i);
+    }
+    return q;
+}
+
+// floor((u1 * 2^64 + u0) / v) for u1 < v (the quotient fits 64 bits): the two-digit long
+// division with normalized 32-bit digits of H. S. Warren, Hacker's Delight, 2nd ed., 9-4
+// ("divlu"), with 64-bit words.
+HS_HD uint64_t div_u128_u64(uint64_t u1, uint64_t u0, uint64_t v) {
+    const uint64_t b = (uint64_t)1 << 32;
+    const int s = clz64(v);
+    v <<= s;
+    const uint64_t vn1 = v >> 32, vn0 = v & 0xffffffffu;
+    const uint64_t un32 = s ? (u1 << s) | (u0 >> (64 - s)) : u1;
+    const uint64_t un10 = u0 << s;
+    const uint64_t un1 = un10 >> 32, un0 = un10 & 0xffffffffu;
+    uint64_t q1 = un32 / vn1, rhat = un32 - q1 * vn1;
+    while (q1 >= b || q1 * vn0 > b * rhat + un1) {
+        q1--;
+        rhat += vn1;
+        if (rhat >= b) break;
+    }
+    const uint64_t un21 = un32 * b + un1 - q1 * v;
+    uint64_t q0 = un21 / vn1;
+    rhat = un21 - q0 * vn1;
+    while (q0 >= b || q0 * vn0 > b * rhat + un0) {
+        q0--;
+        rhat += vn1;
+        if (rhat >= b) break;
+    }
+    return q1 * b + q0;
+}
+
+// The reciprocal of FreqTable::from_weights' quotient: floor(spare * 2^64 / W) for
+// spare < W (W >= 2^32 > spare in the coder).
+HS_HD uint64_t coder_frac(uint64_t spare, uint64_t W) { return div_u128_u64(spare, 0, W); }
+
+// floor(w * spare / W) for w <= W (freq.rs:103-149): a plain u64 division when W < 2^32 (then
+// w * spare < 2^64), else the 64-bit reciprocal frac = floor(spare 2^64 / W) and one correction
+// (the estimate is at most one below the quotient).
+HS_HD uint64_t quotient(uint64_t w, uint64_t spare, uint64_t W, uint64_t frac) {
+    if (W < ((uint64_t)1 << 32)) return (w * spare) / W;
+    uint64_t est = (uint64_t)(((u128)w * frac) >> 64);
+    const u128 num = (u128)w * spare;
+    if (num - (u128)est * W >= W) est++;
+    return est;
+}
+
+// The LayerNorm scale of a row (layernorm.rs:188-256): inv = floor(2^k / isqrt(var 2^(2j) + eps))
+// with var = floor(sq / n). k <= 48 and the root is below 2^64, so the division is in u64.
+HS_HD uint64_t ln_inv(u128 sq, uint32_t n, uint32_t k, uint32_t j, uint64_t eps) {
+    const u128 var = div_u128_u32(sq, n);
+    const uint64_t r = isqrt_est((var << (2 * j)) + (u128)eps);
+    return ((uint64_t)1 << k) / (r > 0 ? r : 1);
+}
+
+}  // namespace hs

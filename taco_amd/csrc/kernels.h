@@ -32,10 +32,18 @@ struct GemmArgs {
     int64_t *tmax = nullptr;
     int tmax_ld = 0;
     int cap16 = 0;
+    int group = 0;  // M-tiles per group of the tile order (0: gemm_group(m))
 };
+
 
 // Tile sizes of the MFMA GEMM: w and a rows are padded to these multiples, k to 64.
 constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 64;
+
+// The group size of the XCD-aware tile order: one band of M-tiles per XCD.
+inline int gemm_group(int m) {
+    const int gm = (m + GEMM_BM - 1) / GEMM_BM;
+    return gm < 8 ? 1 : (gm + 7) / 8;
+}
 
 hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream);
 
@@ -105,7 +113,7 @@ struct CoderArgs {
 hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream);
 
 // The coder op over compact logits (the LogitsCompact GEMM epilogue): d16 [rows, ld16] u16 and
-// tmax [rows, ntiles] i64, with table_len <= CODER_MAX_TABLE.
+// tmax [rows, ntiles] i64, with a non-increasing table of table_len <= CODER_MAX_TABLE entries.
 constexpr int CODER_MAX_TABLE = 16384;
 struct CompactCoderArgs {
     const uint16_t *d16 = nullptr;
@@ -115,7 +123,8 @@ struct CompactCoderArgs {
     int vocab = 0;
     const uint64_t *table = nullptr;
     int table_len = 0;
-    int d0 = 0;  // the largest d with table[d] == table[0]
+    int d0 = 0;    // the largest d with table[d] == table[0]
+    int zcut = 0;  // every table[d] with d >= zcut is 0 (1 <= zcut <= table_len)
     const uint32_t *queries = nullptr;
     int bits = 32;
     uint64_t *intervals = nullptr;

@@ -3,77 +3,14 @@
 // reductions are fixed-order wave/LDS trees, so results do not depend on scheduling.
 #include <hip/hip_runtime.h>
 
+#include "intmath.h"
 #include "kernels.h"
 
 namespace hs {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef __int128 i128;
-typedef unsigned __int128 u128;
-
 constexpr int32_t RES = (1 << 30) - 1;             // gpt2/mod.rs:116
 constexpr int64_t SCORE_LIMIT = (int64_t)1 << 40;  // gpt2/mod.rs:119
-
-// ---- integer rules (crates/hardshell/src/int.rs) ------------------------------------------
-
-// floor((p + 2^(s-1)) / 2^s) for |p| < 2^63 (int.rs:110-124 with max shift >= 63: for s >= 64
-// the exact result is 0). Never overflows: the low s bits round separately.
-__device__ __forceinline__ int64_t shift_round64(int64_t p, uint32_t s) {
-    if (s == 0) return p;
-    if (s >= 64) return 0;
-    const uint64_t r = (uint64_t)p & (((uint64_t)1 << s) - 1);
-    const uint64_t up = (r + ((uint64_t)1 << (s - 1))) >> s;
-    return (p >> s) + (int64_t)up;
-}
-
-// rescale(x, m, s) for |x| < 2^32: the product is exact in i64.
-__device__ __forceinline__ int64_t rescale_small(int64_t x, int32_t m, uint32_t s) {
-    return shift_round64(x * (int64_t)m, s);
-}
-
-__device__ __forceinline__ i128 shift_round128(i128 p, uint32_t s, uint32_t max_shift) {
-    if (s == 0) return p;
-    if (s > max_shift) return 0;
-    const u128 half = (u128)1 << (s - 1);
-    return (i128)((u128)p + half) >> s;
-}
-
-// rescale (int.rs:63-67) for any i64 x.
-__device__ __forceinline__ i128 rescale_full(int64_t x, int32_t m, uint32_t s) {
-    return shift_round128((i128)x * (i128)m, s, 95);
-}
-
-__device__ __forceinline__ int64_t clamp64(int64_t x, int64_t lo, int64_t hi) {
-    int64_t u = x < hi ? x : hi;
-    return u > lo ? u : lo;
-}
-
-__device__ __forceinline__ int64_t clamp128(i128 x, int64_t lo, int64_t hi) {
-    i128 u = x < (i128)hi ? x : (i128)hi;
-    return (int64_t)(u > (i128)lo ? u : (i128)lo);
-}
-
-__device__ __forceinline__ int64_t floor_div64(int64_t a, int64_t b) {
-    int64_t q = a / b, r = a % b;
-    return (r != 0 && r < 0) ? q - 1 : q;
-}
-
-// isqrt_u128 (int.rs:213-233): exact floor square root, bitwise.
-__device__ u128 isqrt128(u128 x) {
-    u128 bit = (u128)1 << 126;
-    while (bit > x) bit >>= 2;
-    u128 rem = x, res = 0;
-    while (bit != 0) {
-        if (rem >= res + bit) {
-            rem -= res + bit;
-            res = (res >> 1) + bit;
-        } else {
-            res >>= 1;
-        }
-        bit >>= 2;
-    }
-    return res;
-}
 
 // ---- wave reductions (wave64) -------------------------------------------------------------
 
@@ -110,7 +47,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) int8_t sW[2][GEMM_BN * LDS_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * GEMM_BN;
+    // XCD-aware tile order: workgroup L runs on XCD L % 8, and XCD x takes the x-th contiguous
+    // chunk of a grouped order (groups of `group` M-tiles, N outermost inside a group), so an
+    // A row-tile stays in one XCD's L2 while the W tiles stream past it.
+    int mt, nt;
+    {
+        const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + GEMM_BN - 1) / GEMM_BN;
+        const int T = gm * gn, L = blockIdx.x, x = L & 7, k = L >> 3;
+        const int q = T >> 3, r = T & 7;
+        const int p = x * q + (x < r ? x : r) + k;
+        const int G = g.group, grp = p / (G * gn), in = p - grp * G * gn;
+        const int gs = gm - grp * G < G ? gm - grp * G : G;
+        nt = in / gs;
+        mt = grp * G + in % gs;
+    }
+    const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
     const int K = g.k_pad, nk = K / GEMM_BK;
     const int8_t *A = g.a + (size_t)m0 * K;
     const int8_t *W = g.w + (size_t)n0 * K;
@@ -248,8 +199,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
 }
 
-hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream) {
-    dim3 grid((g.n + GEMM_BN - 1) / GEMM_BN, (g.m + GEMM_BM - 1) / GEMM_BM);
+hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
+    GemmArgs g = ga;
+    if (g.m <= 0 || g.n <= 0) return hipSuccess;
+    const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + GEMM_BN - 1) / GEMM_BN;
+    if (g.group == 0) g.group = gemm_group(g.m);
+    if (g.group < 1 || g.group > gm) return hipErrorInvalidValue;
+    dim3 grid(gm * gn);
     switch (epi) {
         case Epi::Raw: hipLaunchKernelGGL(k_gemm<0>, grid, dim3(256), 0, stream, g); break;
         case Epi::Act: hipLaunchKernelGGL(k_gemm<1>, grid, dim3(256), 0, stream, g); break;
@@ -302,11 +258,12 @@ __device__ __forceinline__ u128 wave_sum128(u128 v) {
     return v;
 }
 
-// One wave per row, four rows per workgroup: no LDS and no barriers. The per-row constants
-// (mean, inv) come from lane 0 through a readlane; every lane then rescales its elements.
-// (x - mean) * inv * gamma * m is formed as ((x - mean) * inv) * (gamma * m): the reference's
-// bounds (|t| < 2^95, |m| < 2^31, layernorm.rs:31-39) keep it below 2^126, so its wrapping
-// product never wraps and the two forms are the same integer.
+// One wave per row, four rows per workgroup, no LDS and no barriers: the row sum, then the sum
+// of squares of c = x - mean (|c| < 2^32, so a square fits u64 and each lane carries into a
+// high word), and the per-row inv of ln_inv (no 128-bit division). The product c * inv * gamma
+// * m is formed as (c * inv) * (gamma * m): the reference's bounds (|t| < 2^95, |m| < 2^31,
+// layernorm.rs:31-39) keep it below 2^126, so its wrapping product never wraps and the two
+// forms are the same integer. When max|c| * inv < 2^63 (exact test), c * inv is an i64.
 __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -318,31 +275,30 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     for (int j = lane; j < d; j += 64) sum += x[j];
     sum = wave_sum64(sum);
     const int64_t mean = floor_div64(sum, d);
-    u128 sq = 0;
+    uint64_t lo = 0, hi = 0, cmax = 0;
     for (int j = lane; j < d; j += 64) {
         const int64_t c = (int64_t)x[j] - mean;
         const uint64_t u = c < 0 ? (uint64_t)(-c) : (uint64_t)c;
-        sq += (u128)u * u;
+        const uint64_t v = u * u;
+        lo += v;
+        hi += lo < v;
+        cmax = u > cmax ? u : cmax;
     }
-    sq = wave_sum128(sq);
-    uint64_t inv = 0;
-    if (lane == 0) {
-        const u128 var = sq / (u128)(uint32_t)d;
-        const u128 root = isqrt128((var << (2 * a.j)) + (u128)a.eps);
-        inv = (uint64_t)(((u128)1 << a.k) / (root > 0 ? root : 1));
-    }
-    inv = __shfl(inv, 0, 64);
-    const i128 inv128 = (i128)(u128)inv;
+    const u128 sq = wave_sum128(((u128)hi << 64) | lo);
+    cmax = (uint64_t)wave_max64((int64_t)cmax);
+    const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
+    const bool small = (u128)cmax * inv < ((u128)1 << 63);
     int8_t *out = a.out + (size_t)row * a.ldo;
     for (int j = lane; j < d; j += 64) {
-        const i128 cinv = (i128)((int64_t)x[j] - mean) * inv128;
+        const int64_t c = (int64_t)x[j] - mean;
+        const i128 cinv = small ? (i128)(c * (int64_t)inv) : (i128)c * (i128)(u128)inv;
         const i128 p = cinv * (i128)a.gm[j];
         i128 y;
         if (a.beta_frac == 0) {
             y = shift_round128(p, a.s, 126) + (i128)a.beta[j];
         } else {
-            const i128 c = (i128)a.beta[j] << (a.s - a.beta_frac);
-            y = shift_round128(p + c, a.s, 126);
+            const i128 cb = (i128)a.beta[j] << (a.s - a.beta_frac);
+            y = shift_round128(p + cb, a.s, 126);
         }
         out[j] = (int8_t)clamp128(y, -127, 127);
     }
@@ -536,8 +492,12 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
         return clamp64(rescale_small(dot, a.score_m, a.score_s), -SCORE_LIMIT, SCORE_LIMIT);
     };
     const int nkb = (nk + 63) / 64;
-    int64_t mx[4] = {INT64_MIN, INT64_MIN, INT64_MIN, INT64_MIN};
-    for (int kb = 0; kb < nkb; kb++) {  // pass 1: the row max
+    // pass 1: the row max. The score clamp(rescale(dot)) is monotone in the dot (its direction
+    // is the sign of score_m), so the largest score is the score of the largest or of the
+    // smallest dot.
+    int32_t dmax[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
+    int32_t dmin[4] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX};
+    for (int kb = 0; kb < nkb; kb++) {
         load_k(kb);
         __syncthreads();
         v4i s[4];
@@ -547,20 +507,25 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
             const int key = kb * 64 + t * 16 + (lane & 15);
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                if (valid[e] && key <= posr[e]) {
-                    const int64_t sc = score(s[t][e]);
-                    mx[e] = sc > mx[e] ? sc : mx[e];
+                if (key <= posr[e]) {
+                    dmax[e] = s[t][e] > dmax[e] ? s[t][e] : dmax[e];
+                    dmin[e] = s[t][e] < dmin[e] ? s[t][e] : dmin[e];
                 }
         }
         __syncthreads();
     }
+    int64_t mx[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
+    for (int e = 0; e < 4; e++) {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
-            const int64_t u = __shfl_xor(mx[e], o, 64);
-            mx[e] = u > mx[e] ? u : mx[e];
+            const int32_t u = __shfl_xor(dmax[e], o, 64), v = __shfl_xor(dmin[e], o, 64);
+            dmax[e] = u > dmax[e] ? u : dmax[e];
+            dmin[e] = v < dmin[e] ? v : dmin[e];
         }
+        const int64_t a0 = score(dmax[e]), a1 = score(dmin[e]);
+        mx[e] = a0 > a1 ? a0 : a1;  // rows past the group's count: unused
+    }
     int64_t sum[4] = {0, 0, 0, 0};
     for (int kb = 0; kb < nkb; kb++) {  // pass 2: the sum of the table entries
         load_k(kb);
@@ -585,7 +550,7 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) sum[e] += __shfl_xor(sum[e], o, 64);
         // floor(2^64 / S) for S >= 2; S = 1 divides exactly
-        frac[e] = sum[e] >= 2 ? (uint64_t)(((u128)1 << 64) / (uint64_t)sum[e]) : 0;
+        frac[e] = sum[e] >= 2 ? div_2p64((uint64_t)sum[e]) : 0;
     }
     v4i acc[4][4];  // [digit plane][channel tile]
 #pragma unroll
@@ -663,13 +628,6 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
 // correction step (W >= 2^32), or a plain u64 division (W < 2^32).
 // =============================================================================================
 
-__device__ __forceinline__ uint64_t quotient(uint64_t w, uint64_t spare, uint64_t W, uint64_t frac) {
-    if (W < ((uint64_t)1 << 32)) return (w * spare) / W;  // w <= W < 2^32: no overflow
-    uint64_t est = __umul64hi(w, frac);                   // floor(w * frac / 2^64) <= q
-    const u128 num = (u128)w * spare;
-    if (num - (u128)est * W >= W) est++;  // q - est is 0 or 1
-    return est;
-}
 
 __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
     __shared__ int64_t s_i64[256];
@@ -737,7 +695,7 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
         const uint64_t spare = total - (uint64_t)V;
         s_W = Wt;
         s_largest = largest;
-        s_frac = Wt >= ((uint64_t)1 << 32) ? (uint64_t)(((u128)spare << 64) / Wt) : 0;
+        s_frac = Wt >= ((uint64_t)1 << 32) ? coder_frac(spare, Wt) : 0;
     }
     __syncthreads();
     const uint64_t Wt = s_W, frac = s_frac;
@@ -860,15 +818,40 @@ __device__ __forceinline__ uint64_t block_sum64(uint64_t v, uint64_t *s, int tid
     return v;
 }
 
+// Reductions over a 256-thread block through wave shuffles and one LDS slot per wave.
+__device__ __forceinline__ int64_t block_max64w(int64_t v, int64_t *s4, int tid) {
+    v = wave_max64(v);
+    if ((tid & 63) == 0) s4[tid >> 6] = v;
+    __syncthreads();
+    int64_t r = s4[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) r = s4[w] > r ? s4[w] : r;
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint64_t block_sum64w(uint64_t v, uint64_t *s4, int tid) {
+    v = (uint64_t)wave_sum64((int64_t)v);
+    if ((tid & 63) == 0) s4[tid >> 6] = v;
+    __syncthreads();
+    const uint64_t r = s4[0] + s4[1] + s4[2] + s4[3];
+    __syncthreads();
+    return r;
+}
+
+// One row per workgroup. The histogram counts the symbols of each table index d < zcut (the
+// bins with a nonzero weight); with V < 2^16 the count and the count below the Encode token
+// share one u32 (low and high half), else they are two arrays. Symbols with d >= zcut have
+// weight 0, f = 1 and no share of the spare, and need no count.
 __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
-    extern __shared__ uint32_t hist[];  // cnt[len], cnt_lo[len]
+    extern __shared__ uint32_t hist[];
     __shared__ int64_t s_i[256];
     __shared__ uint64_t s_u[256];
-    __shared__ uint32_t s_dtok;
     __shared__ uint64_t s_frac;
     const int row = blockIdx.x, tid = threadIdx.x;
     const int V = a.vocab, len = a.table_len, last = len - 1;
-    uint32_t *cnt = hist, *cnt_lo = hist + len;
+    const int zc = a.zcut;
+    const bool packed = V < 65536;
     const uint16_t *d16 = a.d16 + (size_t)row * a.ld16;
     const int64_t *tm = a.tmax + (size_t)row * a.ntiles;
     const uint32_t kind = a.queries ? a.queries[2 * row] : 0;
@@ -877,54 +860,71 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
 
     int64_t mx = INT64_MIN;
     for (int t = tid; t < a.ntiles; t += 256) mx = tm[t] > mx ? tm[t] : mx;
-    const int64_t M = block_max64(mx, s_i, tid);
-    for (int d = tid; d < 2 * len; d += 256) hist[d] = 0;
-    __syncthreads();
-
-    // One pass: 8 consecutive symbols per thread and step (one 16-byte load).
-    int64_t first = INT64_MAX;  // the first symbol with weight table[0]
-    for (int g0 = tid * 8; g0 < V; g0 += 256 * 8) {
-        const uint4 raw = *(const uint4 *)(d16 + g0);
-        const uint16_t *dv = (const uint16_t *)&raw;
-        const int64_t base = M - tm[g0 >> 6];  // the 8 symbols share a 64-column tile
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int j = g0 + q;
-            if (j >= V) break;
-            const int64_t dd = base + dv[q];
-            const int d = (int)(dd < last ? dd : last);
-            atomicAdd(&cnt[d], 1u);
-            if ((uint32_t)j < tok) atomicAdd(&cnt_lo[d], 1u);
-            if ((uint32_t)j == value && kind == 0) s_dtok = (uint32_t)d;
-            if (d <= a.d0 && j < first) first = j;
-            if (a.weights) a.weights[(size_t)row * V + j] = a.table[d];
+    const int64_t M = block_max64w(mx, s_i, tid);
+    for (int d = tid; d < (packed ? zc : 2 * zc); d += 256) hist[d] = 0;
+    if (a.weights) {  // the weights themselves (run_weights)
+        for (int j = tid; j < V; j += 256) {
+            const int64_t dd = M - tm[j >> 6] + d16[j];
+            a.weights[(size_t)row * V + j] = a.table[dd < last ? dd : last];
         }
     }
     __syncthreads();
-    const int64_t largest = -block_max64(-first, s_i, tid);
+
+    // One pass: 8 consecutive symbols per thread and step (one 16-byte load; the 8 share a
+    // 64-column tile). A group whose tile max is zcut or more below M has only weight-0 symbols.
+    int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0 < zcut)
+    for (int g0 = tid * 8; g0 < V; g0 += 256 * 8) {
+        const int64_t base64 = M - tm[g0 >> 6];
+        if (base64 >= zc) continue;
+        const uint4 raw = *(const uint4 *)(d16 + g0);
+        const uint16_t *dv = (const uint16_t *)&raw;
+        const int base = (int)base64;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int j = g0 + q;
+            const int dd = base + (int)dv[q];
+            if (j < V && dd < zc) {  // then dd <= last: d = dd
+                if (packed) {
+                    atomicAdd(&hist[dd], (uint32_t)j < tok ? 0x10001u : 1u);
+                } else {
+                    atomicAdd(&hist[dd], 1u);
+                    if ((uint32_t)j < tok) atomicAdd(&hist[zc + dd], 1u);
+                }
+                if (dd <= a.d0 && j < first) first = j;
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t largest = -block_max64w(-first, s_i, tid);
 
     uint64_t W = 0;
-    for (int d = tid; d < len; d += 256) W += (uint64_t)cnt[d] * a.table[d];
-    W = block_sum64(W, s_u, tid);
+    for (int d = tid; d < zc; d += 256) {
+        const uint32_t c = packed ? (hist[d] & 0xffffu) : hist[d];
+        W += (uint64_t)c * a.table[d];
+    }
+    W = block_sum64w(W, s_u, tid);
     const uint64_t total = (uint64_t)1 << a.bits, spare = total - (uint64_t)V;
-    if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? (uint64_t)(((u128)spare << 64) / W) : 0;
+    if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0;
     __syncthreads();
     const uint64_t frac = s_frac;
     uint64_t S = 0, Slo = 0;
-    for (int d = tid; d < len; d += 256) {
-        if (!cnt[d]) continue;
+    for (int d = tid; d < zc; d += 256) {
+        const uint32_t h = hist[d];
+        const uint32_t c = packed ? (h & 0xffffu) : h, clo = packed ? (h >> 16) : hist[zc + d];
+        if (!c) continue;
         const uint64_t q = quotient(a.table[d], spare, W, frac);
-        S += (uint64_t)cnt[d] * q;
-        Slo += (uint64_t)cnt_lo[d] * q;
+        S += (uint64_t)c * q;
+        Slo += (uint64_t)clo * q;
     }
-    S = block_sum64(S, s_u, tid);
-    Slo = block_sum64(Slo, s_u, tid);
+    S = block_sum64w(S, s_u, tid);
+    Slo = block_sum64w(Slo, s_u + 8, tid);
     const uint64_t rem = total - ((uint64_t)V + S);
     uint64_t *out = a.intervals ? a.intervals + 3 * (size_t)row : nullptr;
     if (!out) return;
     if (kind == 0) {
         if (tid == 0) {
-            const uint64_t f = 1 + quotient(a.table[s_dtok], spare, W, frac);
+            const int64_t dt = M - tm[tok >> 6] + d16[tok];
+            const uint64_t f = 1 + quotient(a.table[dt < last ? dt : last], spare, W, frac);
             out[0] = tok;
             out[1] = (uint64_t)tok + Slo + ((int64_t)tok > largest ? rem : 0);
             out[2] = f + ((int64_t)tok == largest ? rem : 0);
@@ -996,7 +996,7 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
 
 hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
-    const size_t lds = 2 * sizeof(uint32_t) * (size_t)a.table_len;
+    const size_t lds = (a.vocab < 65536 ? 1 : 2) * sizeof(uint32_t) * (size_t)a.zcut;
     static size_t allowed = 0;  // raise the dynamic LDS limit once per size
     if (lds > allowed) {
         hipError_t e = hipFuncSetAttribute((const void *)k_coder_compact,

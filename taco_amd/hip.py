@@ -137,6 +137,7 @@ def lib() -> C.CDLL:
         L.hs_device_upload.argtypes = [P, P, P, S]
         L.hs_device_download.argtypes = [P, P, P, S]
         L.hs_device_synchronize.argtypes = [P]
+        L.hs_device_copy.argtypes = [P, P, P, S]
         L.hs_op_gemm_requant_gpu_ns.argtypes = [P, P, P, P, P, C.c_uint8, S, S, S, P, S,
                                                 C.POINTER(U64)]
         L.hs_op_attend_decode_gpu_ns.argtypes = [P, P, P, P, P, S, S, S, S, C.c_int32,

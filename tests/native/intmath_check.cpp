@@ -1,0 +1,149 @@
+// Host build of taco_amd/csrc/intmath.h against plain unsigned __int128 arithmetic (libgcc's
+// exact division) and the digit-by-digit square root of the rule: edge cases and seeded
+// random cases. Prints "ok <n>" or the first mismatch and exits 1.
+#include <cstdio>
+#include <cstdlib>
+#include <initializer_list>
+
+#include "../../taco_amd/csrc/intmath.h"
+
+using hs::i128;
+using hs::u128;
+
+static uint64_t sm_state = 0x1234567;
+static uint64_t next() {  // splitmix64
+    uint64_t z = (sm_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+static uint64_t rnd_bits() {  // random value with a random bit length
+    const int b = (int)(next() % 65);
+    return b == 0 ? 0 : (b == 64 ? next() : next() & ((1ull << b) - 1));
+}
+
+static u128 isqrt_ref(u128 x) {  // bitwise from 2^126 as int.rs
+    u128 bit = (u128)1 << 126;
+    while (bit > x) bit >>= 2;
+    u128 rem = x, res = 0;
+    while (bit != 0) {
+        if (rem >= res + bit) {
+            rem -= res + bit;
+            res = (res >> 1) + bit;
+        } else {
+            res >>= 1;
+        }
+        bit >>= 2;
+    }
+    return res;
+}
+
+#define CHECK(cond, ...)                   \
+    do {                                   \
+        if (!(cond)) {                     \
+            std::printf(__VA_ARGS__);      \
+            std::printf("\n");             \
+            return 1;                      \
+        }                                  \
+    } while (0)
+
+int main(int argc, char **argv) {
+    const long n = argc > 1 ? std::atol(argv[1]) : 200000;
+    long count = 0;
+    // div_2p64
+    const uint64_t edge[] = {2, 3, 4, 5, 7, 1ull << 32, (1ull << 32) + 1, (1ull << 63), (1ull << 63) + 1,
+                             ~0ull, ~0ull - 1, 1000000007ull, 1ull << 40};
+    for (uint64_t s : edge) {
+        CHECK(hs::div_2p64(s) == (uint64_t)(((u128)1 << 64) / s), "div_2p64 %llu", (unsigned long long)s);
+        count++;
+    }
+    for (long i = 0; i < n; i++) {
+        uint64_t s = rnd_bits();
+        if (s < 2) s = 2;
+        CHECK(hs::div_2p64(s) == (uint64_t)(((u128)1 << 64) / s), "div_2p64 %llu", (unsigned long long)s);
+        count++;
+    }
+    // div_u128_u32
+    for (long i = 0; i < n; i++) {
+        const u128 x = ((u128)rnd_bits() << 64) | rnd_bits();
+        uint32_t d = (uint32_t)rnd_bits();
+        if (d == 0) d = 1 + (uint32_t)(next() % 1000);
+        CHECK(hs::div_u128_u32(x, d) == x / d, "div_u128_u32");
+        count++;
+    }
+    // div_u128_u64 (u1 < v)
+    for (long i = 0; i < n; i++) {
+        uint64_t v = rnd_bits();
+        if (v == 0) v = 1;
+        const uint64_t u1 = v == 1 ? 0 : next() % v, u0 = (i & 1) ? next() : rnd_bits();
+        const u128 want = (((u128)u1 << 64) | u0) / v;
+        CHECK(hs::div_u128_u64(u1, u0, v) == (uint64_t)want, "div_u128_u64 %llu %llu %llu",
+              (unsigned long long)u1, (unsigned long long)u0, (unsigned long long)v);
+        count++;
+    }
+    for (uint64_t v : edge) {
+        for (uint64_t u1 : {(uint64_t)0, (uint64_t)1, v - 1, v / 2}) {
+            if (u1 >= v) continue;
+            for (uint64_t u0 : {(uint64_t)0, ~(uint64_t)0, (uint64_t)1 << 63}) {
+                const u128 want = (((u128)u1 << 64) | u0) / v;
+                CHECK(hs::div_u128_u64(u1, u0, v) == (uint64_t)want, "div_u128_u64 edge");
+                count++;
+            }
+        }
+    }
+    // coder_frac and quotient against the exact floor(w * spare / W)
+    for (long i = 0; i < n; i++) {
+        const uint64_t spare = next() >> 32;
+        uint64_t W = rnd_bits();
+        if (W <= spare) W = spare + 1 + (next() >> 8);
+        const uint64_t w = W == 0 ? 0 : next() % (W + 1);
+        const uint64_t frac = W >= (1ull << 32) ? hs::coder_frac(spare, W) : 0;
+        if (W >= (1ull << 32))
+            CHECK(frac == (uint64_t)((((u128)spare) << 64) / W), "coder_frac");
+        CHECK(hs::quotient(w, spare, W, frac) == (uint64_t)(((u128)w * spare) / W), "quotient");
+        count++;
+    }
+    // isqrt128
+    for (long i = 0; i < n; i++) {
+        const int sh = (int)(next() % 128);
+        const u128 x = (((u128)next() << 64) | next()) >> sh;
+        const u128 r = hs::isqrt128(x);
+        CHECK(r == isqrt_ref(x), "isqrt128");
+        CHECK(r * r <= x && (r + 1) * (r + 1) > x, "isqrt128 bound");
+        count++;
+    }
+    for (u128 x : {(u128)0, (u128)1, (u128)2, (u128)3, (u128)4, ~(u128)0, (u128)1 << 126, ((u128)1 << 126) - 1}) {
+        CHECK(hs::isqrt128(x) == isqrt_ref(x), "isqrt128 edge");
+        count++;
+    }
+    // isqrt_est (double estimate + exact correction) against the bitwise root
+    for (long i = 0; i < n; i++) {
+        const int sh = (int)(next() % 128);
+        const u128 x = (((u128)next() << 64) | next()) >> sh;
+        CHECK((u128)hs::isqrt_est(x) == isqrt_ref(x), "isqrt_est");
+        count++;
+    }
+    for (int b = 0; b < 127; b++)
+        for (int dlt = -2; dlt <= 2; dlt++) {
+            const u128 base = (u128)1 << b;
+            const u128 r = isqrt_ref(base);
+            const u128 x = (dlt < 0 && base < (u128)(-dlt)) ? 0 : base + dlt;
+            const u128 sqv = r * r + dlt;  // around perfect squares too
+            CHECK((u128)hs::isqrt_est(x) == isqrt_ref(x), "isqrt_est pow2");
+            if (dlt >= -1 || r * r >= 2) CHECK((u128)hs::isqrt_est(sqv) == isqrt_ref(sqv), "isqrt_est square");
+            count += 2;
+        }
+    // ln_inv against the u128 form
+    for (long i = 0; i < n / 4; i++) {
+        const u128 sq = ((u128)(next() >> (next() % 64)) << (next() % 12)) * (1 + next() % 3);
+        const uint32_t nn = 1 + (uint32_t)(next() % 4096), k = (uint32_t)(next() % 49), j = (uint32_t)(next() % 17);
+        const uint64_t eps = 1 + (next() >> (2 + next() % 62));
+        const u128 var = sq / nn;
+        const u128 root = isqrt_ref((var << (2 * j)) + eps);
+        const uint64_t want = (uint64_t)(((u128)1 << k) / root);
+        CHECK(hs::ln_inv(sq, nn, k, j, eps) == want, "ln_inv");
+        count++;
+    }
+    std::printf("ok %ld\n", count);
+    return 0;
+}
