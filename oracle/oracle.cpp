@@ -564,12 +564,12 @@ struct or_session {
     void attention(const Block &b, size_t layer, size_t t) {
         const size_t d = m->d, hd = m->hd, C = m->n_ctx;
         layernorm_apply(b.ln1, m->lnc, m->ln_beta_frac, x.data(), a.data());
-        if (probing) p_ln1 = a;
+        if (probing && layer == 0) p_ln1 = a;
         matvec_i8(b.c_attn, a.data(), acc.data());
         for (size_t r = 0; r < 3 * d; r++)
             qkv[r] = clamp_act_i8(rescale((int64_t)acc[r] + b.c_attn.b[r], b.c_attn.r.m[r],
                                           b.c_attn.r.s));
-        if (probing) p_qkv = qkv;
+        if (probing && layer == 0) p_qkv = qkv;
         const size_t base = layer * C * d;
         std::memcpy(&kc[base + t * d], &qkv[d], d);
         std::memcpy(&vc[base + t * d], &qkv[2 * d], d);
@@ -589,7 +589,7 @@ struct or_session {
             for (size_t c = 0; c < hd; c++)
                 att[off + c] = clamp_act_i8(rescale(head[c], b.out_m, b.out_s));
         }
-        if (probing) p_att = att;
+        if (probing && layer == 0) p_att = att;
         add_to_residual(b.c_proj, att.data());
     }
 

@@ -421,3 +421,62 @@ def test_fold_payloads_equal_encode_block(golden_model):
     got = O.fold_payloads(m, toks, 3, 40, chunk=32, threads=2)
     for w in range(3):
         assert got[w] == O.encode_block(m, toks[w * 40:(w + 1) * 40])
+
+
+def read_hsm(data: bytes):
+    """The header and the tensors of a .hsm file (layout of crates/hardshell/src/hsm/mod.rs):
+    8-byte magic, u32 version, u32 header length, the JSON header, aligned sections."""
+    import json
+    hl = int.from_bytes(data[12:16], "little")
+    hdr = json.loads(data[16:16 + hl])
+    dts = {"i8": np.int8, "i16": np.int16, "i32": np.int32, "u64": np.uint64}
+    tensors = {}
+    for t in hdr["tensors"]:
+        dt = np.dtype(dts[t["dtype"]])
+        a = np.frombuffer(data, dt, count=t["length"] // dt.itemsize, offset=t["offset"])
+        tensors[t["name"]] = (a.reshape(t["shape"]), t.get("shift"))
+    return hdr, tensors
+
+
+def test_linear_act_ref_equals_the_session(golden_model):
+    """The op-level reference of the C1 GEMM (i8 x i8 -> i32, bias, per-channel rescale, clamp
+    to +-127) against block 0's c_attn in the golden-hash-pinned reference session: its input is
+    the session's ln_1 output and its output the session's q, k, v."""
+    b, om = golden_model
+    _, ts = read_hsm(b)
+    w, _ = ts["h.0.attn.c_attn.w"]
+    bias, _ = ts["h.0.attn.c_attn.b"]
+    mult, shift = ts["h.0.attn.c_attn.rescale"]
+    s = O.Session(om)
+    for i, tok in enumerate([om.eot] + splitmix_tokens(5, 20, om.vocab)):
+        pr = s.probe(tok)
+        got = O.linear_act_ref(w, pr["ln1"][None, :], bias, mult, shift)[0]
+        assert np.array_equal(got, pr["qkv"]), i
+
+
+def test_attend_decode_ref_equals_the_session(golden_model):
+    """The op-level reference of decode attention (config 3) against block 0's attention in the
+    reference session: q, k, v of every position from the session's own c_attn output, the
+    cache of positions 0..t, the block's score and output rescales and attn_exp."""
+    b, om = golden_model
+    hdr, ts = read_hsm(b)
+    H, d = hdr["model"]["n_head"], hdr["model"]["d_model"]
+    hd = d // H
+    p = hdr["model"]["constants"]["softmax_p"]
+    sm, ss = ts["h.0.attn.score.rescale"]
+    omul, osh = ts["h.0.attn.out.rescale"]
+    table, _ = ts["attn_exp"]
+    toks = [om.eot] + splitmix_tokens(6, 40, om.vocab)
+    cap = 48
+    kc = np.zeros((1, H, cap, hd), np.int8)
+    vc = np.zeros((1, H, cap, hd), np.int8)
+    s = O.Session(om)
+    for t, tok in enumerate(toks):
+        pr = s.probe(tok)
+        qkv = pr["qkv"]
+        kc[0, :, t, :] = qkv[d:2 * d].reshape(H, hd)
+        vc[0, :, t, :] = qkv[2 * d:].reshape(H, hd)
+        q = qkv[:d].reshape(1, H, hd)
+        got = O.attend_decode_ref(q, kc, vc, np.array([t + 1], np.uint32), int(sm[0]), ss,
+                                  int(omul[0]), osh, table, p)[0]
+        assert np.array_equal(got, pr["att"]), t
