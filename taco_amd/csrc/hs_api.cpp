@@ -86,7 +86,15 @@ struct DevLinear {
     int8_t *w = nullptr;  // [n_pad, k_pad]
     int32_t *b = nullptr, *m = nullptr;
     int s = 0, n = 0, k = 0, n_pad = 0, k_pad = 0;
+    int fast32 = 0;  // k * 2^14 + max|b| < 2^31: every acc + b fits i32
 };
+
+// |acc| <= k * 128 * 128 for i8 operands, so acc + b fits i32 when k * 2^14 + max|b| < 2^31.
+int fits_i32(size_t k, const int32_t *b, size_t n) {
+    int64_t mb = 0;
+    for (size_t i = 0; b && i < n; i++) mb = std::max<int64_t>(mb, b[i] < 0 ? -(int64_t)b[i] : b[i]);
+    return (int64_t)k * 16384 + mb < ((int64_t)1 << 31) ? 1 : 0;
+}
 
 struct DevLn {
     int16_t *g = nullptr;
@@ -140,6 +148,7 @@ hs_status upload_linear(DevMem &mem, const hs::HostLinear &l, DevLinear &o) {
     if (st == HS_OK) st = mem.upload(o.b, l.b.data(), l.b.size(), o.n_pad);
     if (st == HS_OK) st = mem.upload(o.m, l.m.data(), l.m.size(), o.n_pad);
     o.s = l.s;
+    o.fast32 = fits_i32(l.cols, l.b.data(), l.b.size());
     return st;
 }
 
@@ -663,6 +672,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         hs::GemmArgs g;
         g.a = a; g.w = lin.w; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
+        g.fast32 = lin.fast32;
         g.gelu = gelu; g.gelu_off = gelu_off;
         const uint64_t ops = 2ull * (uint64_t)rows_n * (uint64_t)lin.n * (uint64_t)lin.k;
         return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
@@ -911,6 +921,7 @@ hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, c
     hs::GemmArgs g;
     g.a = da; g.w = dw; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
     g.bias = db; g.mult = dm; g.shift = shift; g.out = dout; g.ldo = (int)n;
+    g.fast32 = fits_i32(k, bias, bias ? n : 0);
     HIP_TRY(hs::launch_gemm(epi, g, dev->stream));
     HIP_TRY(hipMemcpyAsync(out, dout, m * n * esz, hipMemcpyDeviceToHost, dev->stream));
     HIP_TRY(hipStreamSynchronize(dev->stream));

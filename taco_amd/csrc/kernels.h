@@ -33,11 +33,14 @@ struct GemmArgs {
     int tmax_ld = 0;
     int cap16 = 0;
     int group = 0;  // M-tiles per group of the tile order (0: gemm_group(m))
+    // 1 if the caller has shown |acc + bias| < 2^31 for every output (K * 2^14 + max|bias|
+    // < 2^31: |a|, |w| <= 128); the epilogue then rescales with one i64 multiply-add.
+    int fast32 = 0;
 };
 
 
-// Tile sizes of the MFMA GEMM: w and a rows are padded to these multiples, k to 64.
-constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_BK = 64;
+// Tile sizes of the MFMA GEMM: a rows are padded to GEMM_BM, w rows to GEMM_BN, k to 64.
+constexpr int GEMM_BM = 256, GEMM_BN = 128, GEMM_BK = 64;
 
 // The group size of the XCD-aware tile order: one band of M-tiles per XCD.
 inline int gemm_group(int m) {

@@ -12,6 +12,10 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int32_t RES = (1 << 30) - 1;             // gpt2/mod.rs:116
 constexpr int64_t SCORE_LIMIT = (int64_t)1 << 40;  // gpt2/mod.rs:119
 
+__device__ __forceinline__ int32_t med3_i32(int32_t x, int32_t lo, int32_t hi) {
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+
 // ---- wave reductions (wave64) -------------------------------------------------------------
 
 __device__ __forceinline__ int64_t wave_max64(int64_t v) {
@@ -34,18 +38,36 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 // exact int32 (|C| <= 2^30 for K <= 2^16, crates/hardshell/src/kernels.rs:24-29), with the
 // requantize epilogue of the op fused (crates/hardshell/src/gpt2/ops.rs:107-176).
 //
-// Tile 128 x 128 x 64, 256 threads = 4 waves in 2 x 2; each wave owns 64 x 64 = 4 x 4 tiles of
-// v_mfma_i32_16x16x64_i8. Operands go global -> registers -> LDS (double buffered, one
-// barrier per k-step); the next k-tile's global loads are in flight during the MFMAs.
+// Block tile 256 x 128 x 64, 256 threads = 4 waves in 2 x 2; each wave owns 128 x 64 = 8 x 4
+// tiles of v_mfma_i32_16x16x64_i8. Operands go straight from global memory to LDS
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l) in MFMA fragment order: a
+// fragment is 16 rows x 64 k, lane l holding row l % 16, k 16 (l / 16) .. +16, so the LDS image
+// of a fragment is exactly what one ds_read_b128 per lane reads back, without bank conflicts.
+// A stage is the 16 A and 8 W fragments of one k-step (24 KiB); GEMM_STAGES stages form a ring,
+// loads run GEMM_STAGES - 1 k-steps ahead, and each k-step has one barrier after each wave's
+// own loads of that stage have landed (vmcnt).
 // =============================================================================================
 
-constexpr int LDS_STRIDE = GEMM_BK + 16;  // bytes per LDS row: 64 data + 16 pad (bank spread)
+constexpr int GEMM_STAGES = 3;
+constexpr int GEMM_FRAGS = GEMM_BM / 16 + GEMM_BN / 16;  // 24 fragments of 1 KiB per stage
+constexpr int GEMM_LOADS = GEMM_FRAGS / 4;                // per wave and stage
+static_assert(GEMM_BM == 256 && GEMM_BN == 128 && GEMM_BK == 64, "tile shape of k_gemm");
 
-template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][GEMM_BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) int8_t sW[2][GEMM_BN * LDS_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(N) with the other counters left at their maximum (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// NARROW: g.fast32 holds and the shift is at least 32, so every rescaled value fits i32.
+template <int EPI, bool NARROW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
+    extern __shared__ __attribute__((aligned(1024))) int8_t gemm_lds[];  // [stages][24][1024]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     // XCD-aware tile order: workgroup L runs on XCD L % 8, and XCD x takes the x-th contiguous
     // chunk of a grouped order (groups of `group` M-tiles, N outermost inside a group), so an
@@ -63,58 +85,230 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
     const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
     const int K = g.k_pad, nk = K / GEMM_BK;
-    const int8_t *A = g.a + (size_t)m0 * K;
-    const int8_t *W = g.w + (size_t)n0 * K;
 
-    // Each thread moves two 16-byte chunks of each 128 x 64 tile: chunk c -> row c / 4,
-    // column 16 * (c % 4).
-    const int c0 = tid, c1 = tid + 256;
-    const int r0 = c0 >> 2, q0 = (c0 & 3) * 16, r1 = c1 >> 2, q1 = (c1 & 3) * 16;
-    v4i ra0, ra1, rw0, rw1;
-    auto gload = [&](int kt) {
-        const int kk = kt * GEMM_BK;
-        ra0 = *(const v4i *)(A + (size_t)r0 * K + kk + q0);
-        ra1 = *(const v4i *)(A + (size_t)r1 * K + kk + q1);
-        rw0 = *(const v4i *)(W + (size_t)r0 * K + kk + q0);
-        rw1 = *(const v4i *)(W + (size_t)r1 * K + kk + q1);
-    };
-    auto sstore = [&](int st) {
-        *(v4i *)(&sA[st][r0 * LDS_STRIDE + q0]) = ra0;
-        *(v4i *)(&sA[st][r1 * LDS_STRIDE + q1]) = ra1;
-        *(v4i *)(&sW[st][r0 * LDS_STRIDE + q0]) = rw0;
-        *(v4i *)(&sW[st][r1 * LDS_STRIDE + q1]) = rw1;
-    };
-
-    v4i acc[4][4];
+    // This wave loads fragments GEMM_LOADS * wave .. +GEMM_LOADS of each stage (0..15: A row
+    // blocks, 16..23: W row blocks); lane l reads row l % 16 of the block at k 16 (l / 16).
+    const int8_t *src[GEMM_LOADS];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < GEMM_LOADS; i++) {
+        const int f = wave * GEMM_LOADS + i;
+        const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + (lane & 15);
+        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) +
+                 (lane >> 4) * 16;
+    }
+    auto issue = [&](int kt, int stage) {
+        int8_t *base = gemm_lds + stage * (GEMM_FRAGS * 1024) + wave * GEMM_LOADS * 1024;
+#pragma unroll
+        for (int i = 0; i < GEMM_LOADS; i++)
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + kt * GEMM_BK),
+                                             (lds_void *)(base + i * 1024), 16, 0, 0);
+    };
+
+    v4i acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    const int frow = lane & 15, fk = (lane >> 4) * 16;
+#pragma unroll
+    for (int s = 0; s < GEMM_STAGES - 1; s++)
+        if (s < nk) issue(s, s);
     for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-        v4i af[4], bf[4];
+        // this wave's loads of stage kt have landed once at most (stages issued after it)
+        // x GEMM_LOADS loads are outstanding
+        const int after = nk - 1 - kt < GEMM_STAGES - 2 ? nk - 1 - kt : GEMM_STAGES - 2;
+        if (after >= 2) wait_vmcnt<2 * GEMM_LOADS>();
+        else if (after == 1) wait_vmcnt<GEMM_LOADS>();
+        else wait_vmcnt<0>();
+        // Every wave's loads of stage kt landed; every wave finished reading stage kt - 1. A bare
+        // s_barrier (a compiler memory barrier, no fence): a fence would also wait for the
+        // stages still in flight.
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + GEMM_STAGES - 1 < nk) issue(kt + GEMM_STAGES - 1, (kt + GEMM_STAGES - 1) % GEMM_STAGES);
+        const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (GEMM_FRAGS * 1024) + lane * 16;
+        v4i af[8], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            af[i] = *(const v4i *)(&sA[cur][(wm * 64 + i * 16 + frow) * LDS_STRIDE + fk]);
+        for (int i = 0; i < 8; i++) af[i] = *(const v4i *)(st + (wm * 8 + i) * 1024);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            bf[j] = *(const v4i *)(&sW[cur][(wn * 64 + j * 16 + frow) * LDS_STRIDE + fk]);
+        for (int j = 0; j < 4; j++) bf[j] = *(const v4i *)(st + (GEMM_BM / 16 + wn * 4 + j) * 1024);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 8; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-        if (kt + 1 < nk) sstore(cur ^ 1);
-        __syncthreads();
     }
 
     // Epilogue: lane holds C[4 * (lane / 16) + e][lane % 16] of each 16 x 16 tile.
+    // rescale(a + bias, mult, shift) (int.rs:63-67). With the host's bound |a + bias| < 2^31
+    // (fast32; the logits have no bias and |a| <= 2^30), |(a + bias) mult| < 2^62: one i64
+    // multiply-add and an arithmetic shift are exact, and a shift of 63 or more gives 0 as
+    // the rule does.
+    const bool fast = EPI == (int)Epi::Logits || EPI == (int)Epi::LogitsCompact || g.fast32;
+    const int s_eff = g.shift < 63 ? g.shift : 63;
+    const int64_t half = s_eff ? (int64_t)1 << (s_eff - 1) : 0;
+    auto rq = [&](int32_t a, int32_t bias, int32_t mult) -> int64_t {
+        if (NARROW || fast) return ((int64_t)(a + bias) * mult + half) >> s_eff;
+        return rescale_small((int64_t)a + bias, mult, g.shift);
+    };
+    // Staged epilogue: each wave writes its 128 x 64 results into its own LDS region (the
+    // stages are free after the barrier below) and stores them back as 16-byte row pieces, 8-32
+    // stores per wave instead of one per element. Needs 16-byte aligned output rows.
+    constexpr int ES = EPI == (int)Epi::Residual ? 4 : (EPI == (int)Epi::LogitsCompact ? 2 : 1);
+    constexpr bool STAGEABLE = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu ||
+                               EPI == (int)Epi::Residual || EPI == (int)Epi::LogitsCompact;
+    if (STAGEABLE && ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0) {
+        __syncthreads();  // every wave finished reading the stages
+        int8_t *wr = gemm_lds + wave * 18432;  // this wave's region (4 x 18 KiB = the stages)
+        const int rw = m0 + wm * 128, cw = n0 + wn * 64;  // the wave's sub-tile origin
+        const int g4 = (lane >> 4) * 4, c16 = lane & 15;
+        int32_t bias[4], mult[4];
+        bool okn[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = cw + j * 16 + c16;
+            okn[j] = n < g.n;
+            bias[j] = (okn[j] && EPI != (int)Epi::LogitsCompact) ? g.bias[n] : 0;
+            mult[j] = okn[j] ? g.mult[n] : 0;
+        }
+        if (EPI == (int)Epi::Act || EPI == (int)Epi::Gelu) {
+            if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62: table[clamp(r) + off]
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
+                            acc[i][j][e] = (NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
+                                                   : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1)) +
+                                           g.gelu_off;
+                        }
+                const int T = 2 * g.gelu_off;  // 256 or 65,536 entries, copied into LDS
+                for (int c = threadIdx.x; c < T / 16; c += 256)
+                    *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[i][j][e] = gemm_lds[acc[i][j][e]];
+                __syncthreads();  // the table reads are done before the regions are written
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        int32_t v;
+                        if (EPI == (int)Epi::Act) {  // ops.rs:123-130
+                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
+                            v = NARROW ? med3_i32((int32_t)r, -127, 127) : (int32_t)clamp64(r, -127, 127);
+                        } else {
+                            v = acc[i][j][e];
+                        }
+                        wr[(i * 16 + g4 + e) * 80 + j * 16 + c16] = (int8_t)v;
+                    }
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int rl = q * 16 + (lane >> 2), cl = (lane & 3) * 16;
+                const v4i v = *(const v4i *)(wr + rl * 80 + cl);
+                const int m = rw + rl, n = cw + cl;
+                if (m >= g.m) continue;
+                int8_t *o = (int8_t *)g.out + (size_t)m * g.ldo + n;
+                if (n + 16 <= g.n) {
+                    *(v4i *)o = v;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 16; t++)
+                        if (n + t < g.n) o[t] = (int8_t)(v[t >> 2] >> (8 * (t & 3)));
+                }
+            }
+            return;
+        }
+        if (EPI == (int)Epi::Residual) {  // ops.rs:131-145, in two halves of 64 rows
+            // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+#pragma unroll
+                for (int i = 4 * h; i < 4 * h + 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
+                            *(int32_t *)(wr + ((i - 4 * h) * 16 + g4 + e) * 272 + (j * 16 + c16) * 4) =
+                                NARROW ? (int32_t)r : (int32_t)clamp64(r, INT32_MIN, INT32_MAX);
+                        }
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int rl = q * 4 + (lane >> 4), cl = (lane & 15) * 4;
+                    const v4i v = *(const v4i *)(wr + rl * 272 + cl * 4);
+                    const int m = rw + 64 * h + rl, n = cw + cl;
+                    if (m >= g.m) continue;
+                    int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n;
+                    if (n + 4 <= g.n) {
+                        v4i xv = *(const v4i *)x;
+#pragma unroll
+                        for (int t = 0; t < 4; t++) xv[t] = (int32_t)clamp64((int64_t)xv[t] + v[t], -RES, RES);
+                        *(v4i *)x = xv;
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 4; t++)
+                            if (n + t < g.n) x[t] = (int32_t)clamp64((int64_t)x[t] + v[t], -RES, RES);
+                    }
+                }
+            }
+            return;
+        }
+        if (EPI == (int)Epi::LogitsCompact) {
+            // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the
+            // largest logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16)
+            // per logit; the table index min(max - l, len - 1) follows exactly from them.
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    int64_t l[4], mx = INT64_MIN;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int64_t r = rq(acc[i][j][e], 0, mult[j]);
+                        l[j] = okn[j] ? (NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : INT64_MIN;
+                        mx = l[j] > mx ? l[j] : mx;
+                    }
+#pragma unroll
+                    for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes that hold this row
+                        const int64_t u = __shfl_xor(mx, o, 64);
+                        mx = u > mx ? u : mx;
+                    }
+                    const int rl = i * 16 + g4 + e, m = rw + rl;
+                    if (m < g.m && c16 == 0 && cw < g.n) g.tmax[(size_t)m * g.tmax_ld + cw / 64] = mx;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int64_t dd = mx - l[j];
+                        *(uint16_t *)(wr + rl * 144 + (j * 16 + c16) * 2) = (uint16_t)(dd < g.cap16 ? dd : g.cap16);
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int rl = q * 8 + (lane >> 3), cl = (lane & 7) * 8;
+                const v4i v = *(const v4i *)(wr + rl * 144 + cl * 2);
+                const int m = rw + rl, n = cw + cl;
+                if (m >= g.m) continue;
+                uint16_t *o = (uint16_t *)g.out + (size_t)m * g.ldo + n;
+                if (n + 8 <= g.n) {
+                    *(v4i *)o = v;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; t++)
+                        if (n + t < g.n) o[t] = (uint16_t)((uint32_t)v[t >> 1] >> (16 * (t & 1)));
+                }
+            }
+            return;
+        }
+    }
     if (EPI == (int)Epi::LogitsCompact) {
         // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the largest
         // logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16) per logit.
@@ -130,16 +324,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             mlt[j] = okn[j] ? g.mult[n] : 0;
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 8; i++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + e;
+                const int m = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + e;
                 int64_t l[4], mx = INT64_MIN;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    l[j] = okn[j] ? clamp64(rescale_small(acc[i][j][e], mlt[j], g.shift), -SCORE_LIMIT,
-                                            SCORE_LIMIT)
-                                  : INT64_MIN;
+                    const int64_t r = rq(acc[i][j][e], 0, mlt[j]);
+                    l[j] = okn[j] ? (NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : INT64_MIN;
                     mx = l[j] > mx ? l[j] : mx;
                 }
 #pragma unroll
@@ -169,52 +362,75 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         if (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu) bias = g.bias[n];
         if (EPI != (int)Epi::Raw) mult = g.mult[n];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 8; i++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + e;
+                const int m = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + e;
                 if (m >= g.m) continue;
                 const int32_t a = acc[i][j][e];
                 const size_t o = (size_t)m * g.ldo + n;
                 if (EPI == (int)Epi::Raw) {
                     ((int32_t *)g.out)[o] = a;
-                } else if (EPI == (int)Epi::Act) {  // ops.rs:123-130
-                    const int64_t y = rescale_small((int64_t)a + bias, mult, g.shift);
-                    ((int8_t *)g.out)[o] = (int8_t)clamp64(y, -127, 127);
+                    continue;
+                }
+                const int64_t r = rq(a, bias, mult);
+                if (EPI == (int)Epi::Act) {  // ops.rs:123-130
+                    ((int8_t *)g.out)[o] = (int8_t)(NARROW ? med3_i32((int32_t)r, -127, 127) : clamp64(r, -127, 127));
                 } else if (EPI == (int)Epi::Residual) {  // ops.rs:131-145
-                    const int64_t y = clamp64(rescale_small((int64_t)a + bias, mult, g.shift),
-                                              -SCORE_LIMIT, SCORE_LIMIT);
+                    // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R
                     int32_t *x = (int32_t *)g.out + o;
-                    *x = (int32_t)clamp64((int64_t)*x + y, -RES, RES);
+                    const int64_t rs = NARROW ? (int64_t)(int32_t)r : clamp64(r, INT32_MIN, INT32_MAX);
+                    *x = (int32_t)clamp64((int64_t)*x + rs, -RES, RES);
                 } else if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62
-                    const int64_t y = clamp64(rescale_small((int64_t)a + bias, mult, g.shift),
-                                              -g.gelu_off, g.gelu_off - 1);
+                    const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
+                                             : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
                     ((int8_t *)g.out)[o] = g.gelu[y + g.gelu_off];
                 } else {  // Logits: ops.rs:229-234
-                    ((int64_t *)g.out)[o] =
-                        clamp64(rescale_small(a, mult, g.shift), -SCORE_LIMIT, SCORE_LIMIT);
+                    ((int64_t *)g.out)[o] = NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
                 }
             }
         }
     }
 }
 
+template <int EPI, bool NARROW>
+static hipError_t launch_gemm_t(const GemmArgs &g, dim3 grid, hipStream_t stream) {
+    constexpr size_t lds = (size_t)GEMM_STAGES * GEMM_FRAGS * 1024;
+    static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
+    if (!ready) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        ready = true;
+    }
+    hipLaunchKernelGGL((k_gemm<EPI, NARROW>), grid, dim3(256), lds, stream, g);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_gemm_e(const GemmArgs &g, dim3 grid, hipStream_t stream) {
+    const bool fast = EPI == (int)Epi::Logits || EPI == (int)Epi::LogitsCompact || g.fast32;
+    if (fast && g.shift >= 32) return launch_gemm_t<EPI, true>(g, grid, stream);
+    return launch_gemm_t<EPI, false>(g, grid, stream);
+}
+
 hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
     GemmArgs g = ga;
     if (g.m <= 0 || g.n <= 0) return hipSuccess;
+    if (g.k_pad % GEMM_BK != 0) return hipErrorInvalidValue;
     const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + GEMM_BN - 1) / GEMM_BN;
     if (g.group == 0) g.group = gemm_group(g.m);
     if (g.group < 1 || g.group > gm) return hipErrorInvalidValue;
-    dim3 grid(gm * gn);
+    const dim3 grid(gm * gn);
     switch (epi) {
-        case Epi::Raw: hipLaunchKernelGGL(k_gemm<0>, grid, dim3(256), 0, stream, g); break;
-        case Epi::Act: hipLaunchKernelGGL(k_gemm<1>, grid, dim3(256), 0, stream, g); break;
-        case Epi::Residual: hipLaunchKernelGGL(k_gemm<2>, grid, dim3(256), 0, stream, g); break;
-        case Epi::Gelu: hipLaunchKernelGGL(k_gemm<3>, grid, dim3(256), 0, stream, g); break;
-        case Epi::Logits: hipLaunchKernelGGL(k_gemm<4>, grid, dim3(256), 0, stream, g); break;
-        case Epi::LogitsCompact: hipLaunchKernelGGL(k_gemm<5>, grid, dim3(256), 0, stream, g); break;
+        case Epi::Raw: return launch_gemm_t<0, false>(g, grid, stream);
+        case Epi::Act: return launch_gemm_e<1>(g, grid, stream);
+        case Epi::Residual: return launch_gemm_e<2>(g, grid, stream);
+        case Epi::Gelu: return launch_gemm_e<3>(g, grid, stream);
+        case Epi::Logits: return launch_gemm_e<4>(g, grid, stream);
+        case Epi::LogitsCompact: return launch_gemm_e<5>(g, grid, stream);
     }
-    return hipGetLastError();
+    return hipErrorInvalidValue;
 }
 
 // =============================================================================================
