@@ -677,13 +677,25 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         const uint64_t ops = 2ull * (uint64_t)rows_n * (uint64_t)lin.n * (uint64_t)lin.k;
         return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
     };
+    const bool kv_fused = m.hd % 16 == 0 && m.d % 16 == 0;
     for (int l = 0; l < m.L; l++) {
         const DevBlock &blk = m.blocks[l];
         HIP_TRY(ln(blk.ln1, nullptr, n, b.d_a));
-        HIP_TRY(gemm("gemm_qkv", Epi::Act, blk.c_attn, b.d_a, n, b.d_qkv, 3 * m.d));
-        HIP_TRY(b.launch("kv_store", 0, [&] {
-            return hs::launch_kv_store(b.d_rows, n, b.d_qkv, m.d, m.H, m.hd, m.C, b.kc[l], b.vc[l], st);
-        }));
+        if (kv_fused) {  // K and V go from the c_attn epilogue straight into the caches
+            hs::GemmArgs g;
+            g.a = b.d_a; g.w = blk.c_attn.w; g.m = n; g.n = blk.c_attn.n; g.k_pad = blk.c_attn.k_pad;
+            g.bias = blk.c_attn.b; g.mult = blk.c_attn.m; g.shift = blk.c_attn.s; g.out = b.d_qkv;
+            g.ldo = 3 * m.d; g.fast32 = blk.c_attn.fast32;
+            g.kv_rows = b.d_rows; g.kc = b.kc[l]; g.vc = b.vc[l];
+            g.kv_d = m.d; g.kv_hd = m.hd; g.kv_h = m.H; g.kv_ctx = m.C;
+            const uint64_t ops = 2ull * (uint64_t)n * (uint64_t)blk.c_attn.n * (uint64_t)blk.c_attn.k;
+            HIP_TRY(b.launch("gemm_qkv", ops, [&] { return hs::launch_gemm(Epi::Act, g, st); }));
+        } else {
+            HIP_TRY(gemm("gemm_qkv", Epi::Act, blk.c_attn, b.d_a, n, b.d_qkv, 3 * m.d));
+            HIP_TRY(b.launch("kv_store", 0, [&] {
+                return hs::launch_kv_store(b.d_rows, n, b.d_qkv, m.d, m.H, m.hd, m.C, b.kc[l], b.vc[l], st);
+            }));
+        }
         hs::AttnArgs at;
         at.rows = b.d_rows; at.q = b.d_qkv; at.ldq = 3 * m.d; at.kc = b.kc[l]; at.vc = b.vc[l];
         at.n_head = m.H; at.hd = m.hd; at.ctx_cap = m.C; at.score_m = blk.score_m; at.score_s = blk.score_s;

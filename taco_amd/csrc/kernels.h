@@ -36,6 +36,12 @@ struct GemmArgs {
     // 1 if the caller has shown |acc + bias| < 2^31 for every output (K * 2^14 + max|bias|
     // < 2^31: |a|, |w| <= 128); the epilogue then rescales with one i64 multiply-add.
     int fast32 = 0;
+    // Act only: when kv_rows is set, columns kv_d .. 3 kv_d (K and V of a c_attn output) go to
+    // the caches kc, vc [slot][kv_h][kv_ctx][kv_hd] at the row's slot and position instead of
+    // `out` (kv_d and kv_hd multiples of 16).
+    const struct RowInfo *kv_rows = nullptr;
+    int8_t *kc = nullptr, *vc = nullptr;
+    int kv_d = 0, kv_hd = 0, kv_h = 0, kv_ctx = 0;
 };
 
 

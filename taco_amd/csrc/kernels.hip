@@ -216,6 +216,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 const v4i v = *(const v4i *)(wr + rl * 80 + cl);
                 const int m = rw + rl, n = cw + cl;
                 if (m >= g.m) continue;
+                if (EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
+                    // K or V of the row straight into the cache (kv_d, kv_hd multiples of 16);
+                    // the columns past N = 3 kv_d are padding and go nowhere
+                    if (n + 16 > g.n) continue;
+                    const RowInfo ri = g.kv_rows[m];
+                    const int part = n >= 2 * g.kv_d, c = n - (part + 1) * g.kv_d;
+                    const int hh = c / g.kv_hd, cc = c - hh * g.kv_hd;
+                    *(v4i *)((part ? g.vc : g.kc) +
+                             (((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc) = v;
+                    continue;
+                }
                 int8_t *o = (int8_t *)g.out + (size_t)m * g.ldo + n;
                 if (n + 16 <= g.n) {
                     *(v4i *)o = v;
@@ -375,7 +386,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 }
                 const int64_t r = rq(a, bias, mult);
                 if (EPI == (int)Epi::Act) {  // ops.rs:123-130
-                    ((int8_t *)g.out)[o] = (int8_t)(NARROW ? med3_i32((int32_t)r, -127, 127) : clamp64(r, -127, 127));
+                    const int8_t v = (int8_t)(NARROW ? med3_i32((int32_t)r, -127, 127) : clamp64(r, -127, 127));
+                    if (g.kv_rows && n >= g.kv_d) {
+                        const RowInfo ri = g.kv_rows[m];
+                        const int part = n >= 2 * g.kv_d, c = n - (part + 1) * g.kv_d;
+                        const int hh = c / g.kv_hd, cc = c - hh * g.kv_hd;
+                        (part ? g.vc : g.kc)[(((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc] = v;
+                    } else {
+                        ((int8_t *)g.out)[o] = v;
+                    }
                 } else if (EPI == (int)Epi::Residual) {  // ops.rs:131-145
                     // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R
                     int32_t *x = (int32_t *)g.out + o;
@@ -653,12 +672,14 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
 // =============================================================================================
 
 constexpr int AT_ST = 80;  // LDS row stride in bytes (64 + 16)
+constexpr int ATTN_LDS_TABLE = 16384;  // attn_exp entries kept in LDS (64 KiB)
 
 __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup *groups) {
     __shared__ __attribute__((aligned(16))) int8_t sQ[64 * AT_ST];
     __shared__ __attribute__((aligned(16))) int8_t sK[64 * AT_ST];
     __shared__ __attribute__((aligned(16))) int8_t sVt[64 * AT_ST];
     __shared__ __attribute__((aligned(16))) int8_t sP[4][64 * AT_ST];
+    extern __shared__ __attribute__((aligned(16))) int32_t s_exp[];  // attn_exp when it fits
     const AttnGroup G = groups[blockIdx.x];
     const int h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -666,6 +687,12 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
     nk = nk > a.ctx_cap ? a.ctx_cap : nk;
     const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
     const int last = a.exp_len - 1;
+    // attn_exp into LDS (every score of passes 2 and 3 reads it); the launch gives the dynamic
+    // LDS only when the table fits (exp_len <= ATTN_LDS_TABLE).
+    const bool lds_table = a.exp_len <= ATTN_LDS_TABLE;
+    if (lds_table)
+        for (int i = tid; i < a.exp_len; i += 256) s_exp[i] = a.exp_table[i];
+    const int32_t *etab = lds_table ? (const int32_t *)s_exp : a.exp_table;
     {
         const int r = tid >> 2, c = (tid & 3) * 16;
         v4i v = {0, 0, 0, 0};
@@ -704,8 +731,12 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
             s[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qf, kf, v4i{0, 0, 0, 0}, 0, 0, 0);
         }
     };
+    // score = clamp(rescale(dot, m, s), +-2^40): |dot| <= hd 2^14 <= 2^22, so |dot m| < 2^53 and
+    // one multiply-add and an arithmetic shift are exact (a shift of 63 or more gives 0).
+    const int s_eff = a.score_s < 63 ? a.score_s : 63;
+    const int64_t s_half = s_eff ? (int64_t)1 << (s_eff - 1) : 0;
     auto score = [&](int32_t dot) {
-        return clamp64(rescale_small(dot, a.score_m, a.score_s), -SCORE_LIMIT, SCORE_LIMIT);
+        return clamp64(((int64_t)dot * a.score_m + s_half) >> s_eff, -SCORE_LIMIT, SCORE_LIMIT);
     };
     const int nkb = (nk + 63) / 64;
     // pass 1: the row max. The score clamp(rescale(dot)) is monotone in the dot (its direction
@@ -755,7 +786,7 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
             for (int e = 0; e < 4; e++)
                 if (valid[e] && key <= posr[e]) {
                     const int64_t dd = mx[e] - score(s[t][e]);
-                    sum[e] += a.exp_table[dd < last ? dd : last];
+                    sum[e] += etab[dd < last ? dd : last];
                 }
         }
         __syncthreads();
@@ -787,7 +818,7 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
                 int64_t p = 0;
                 if (valid[e] && key <= posr[e]) {
                     const int64_t dd = mx[e] - score(s[t][e]);
-                    const uint64_t num = (uint64_t)a.exp_table[dd < last ? dd : last] << a.softmax_p;
+                    const uint64_t num = (uint64_t)etab[dd < last ? dd : last] << a.softmax_p;
                     const uint64_t S = (uint64_t)sum[e];
                     uint64_t q = num;
                     if (S >= 2) {
@@ -832,7 +863,14 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
 hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups,
                                 hipStream_t stream) {
     if (n_groups <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_attend_mfma, dim3(n_groups, a.n_head), dim3(256), 0, stream, a, groups);
+    const size_t lds = a.exp_len <= ATTN_LDS_TABLE ? sizeof(int32_t) * (size_t)a.exp_len : 0;
+    static size_t allowed = 0;  // the dynamic LDS limit, raised once
+    if (lds > allowed) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_attend_mfma, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        allowed = lds;
+    }
+    hipLaunchKernelGGL(k_attend_mfma, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
     return hipGetLastError();
 }
 
