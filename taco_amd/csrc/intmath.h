@@ -159,6 +159,17 @@ HS_HD uint64_t quotient(uint64_t w, uint64_t spare, uint64_t W, uint64_t frac) {
     return est;
 }
 
+// shift_round(t * g, s) for 64 <= s <= 126 from the high word of the product only:
+// floor((P + 2^(s-1)) / 2^s) = floor((P_hi + 2^(s-65)) / 2^(s-64)) for s >= 65 (the low word
+// cannot carry the floor across an integer), and P_hi + [P_lo >= 2^63] for s = 64. |t g| < 2^126.
+HS_HD int64_t shift_round_hi(int64_t t, int64_t g, uint32_t s) {
+    const i128 p = (i128)t * (i128)g;
+    const int64_t hi = (int64_t)(p >> 64);
+    if (s == 64) return hi + (int64_t)((uint64_t)p >> 63);
+    const uint32_t u = s - 64;
+    return (hi + ((int64_t)1 << (u - 1))) >> u;
+}
+
 // The LayerNorm scale of a row (layernorm.rs:188-256): inv = floor(2^k / isqrt(var 2^(2j) + eps))
 // with var = floor(sq / n). k <= 48 and the root is below 2^64, so the division is in u64.
 HS_HD uint64_t ln_inv(u128 sq, uint32_t n, uint32_t k, uint32_t j, uint64_t eps) {

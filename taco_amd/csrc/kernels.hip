@@ -524,6 +524,15 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
     int8_t *out = a.out + (size_t)row * a.ldo;
+    if (small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126) {
+        // the rounding shift from the high word of (c inv) (gamma m) alone (shift_round_hi)
+        for (int j = lane; j < d; j += 64) {
+            const int64_t c = (int64_t)x[j] - mean;
+            const int64_t y = shift_round_hi(c * (int64_t)inv, a.gm[j], (uint32_t)a.s) + a.beta[j];
+            out[j] = (int8_t)clamp64(y, -127, 127);
+        }
+        return;
+    }
     for (int j = lane; j < d; j += 64) {
         const int64_t c = (int64_t)x[j] - mean;
         const i128 cinv = small ? (i128)(c * (int64_t)inv) : (i128)c * (i128)(u128)inv;
@@ -664,21 +673,43 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
 
 // =============================================================================================
 // Prefill attention on MFMA (head_dim 64). One workgroup = one group of <= 64 rows x one head;
-// wave w owns rows 16w .. 16w + 15. Three passes over the keys in blocks of 64, recomputing
-// S = Q K^T with v_mfma_i32_16x16x64_i8 (exact i32): (1) the row max of the scores, (2) the sum
-// of the table entries, (3) p = floor(e 2^P / S) and sum_j p_j v_j. The PV product splits p into
-// four balanced signed base-256 digits (crates/hardshell/src/gpt2/attention.rs:36-46), so it is
-// four exact i8 MFMA products: |sum_j d_j v_j| <= 2^16 * 128 * 127 < 2^31.
+// wave w owns rows 16w .. 16w + 15. S = Q K^T comes from v_mfma_i32_16x16x64_i8 (exact i32) for
+// a super-block of up to AT_SB key blocks of 64, held in registers: with n_ctx <= 256 keys the
+// product runs once, else once per pass. Pass 1 takes the row max (from the extreme dots: the
+// score is monotone in the dot), pass 2 turns the dots into table indices min(M - s, last) in
+// place and sums the table entries, pass 3 forms p = floor(e 2^P / S) (a 64-bit reciprocal of S
+// and one correction) and sum_j p_j v_j. The PV product splits p into four balanced signed
+// base-256 digits (crates/hardshell/src/gpt2/attention.rs:36-46): for p < 2^31 the bytes of
+// (p + 0x80808080) ^ 0x80808080 are those digits, so one word per score goes to LDS and a 4 x 4
+// byte transpose (8 v_perm_b32) gives the four digit-plane MFMA operands. Each plane is an exact
+// i8 product: |sum_j d_j v_j| <= 2^16 * 128 * 127 < 2^31.
 // =============================================================================================
 
-constexpr int AT_ST = 80;  // LDS row stride in bytes (64 + 16)
-constexpr int ATTN_LDS_TABLE = 16384;  // attn_exp entries kept in LDS (64 KiB)
+constexpr int AT_ST = 80;               // LDS row stride in bytes (64 + 16)
+constexpr int AT_PP = 68;               // words per row of the packed-digit tile (64 + 4)
+constexpr int AT_SB = 4;                // key blocks of 64 held in registers
+constexpr int ATTN_LDS_TABLE = 16384;   // attn_exp entries kept in LDS (64 KiB)
 
-__global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup *groups) {
+// 4 x 4 byte transpose: out[k] holds byte k of w0, w1, w2, w3 (in that order).
+__device__ __forceinline__ void byte_transpose(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                               uint32_t out[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    out[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    out[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+// NOCLAMP: score_s >= 13, so |dot m| < 2^53 keeps every score within +-2^40 (the clamp is a no-op).
+template <bool NOCLAMP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_mfma(AttnArgs a, const AttnGroup *groups) {
     __shared__ __attribute__((aligned(16))) int8_t sQ[64 * AT_ST];
     __shared__ __attribute__((aligned(16))) int8_t sK[64 * AT_ST];
     __shared__ __attribute__((aligned(16))) int8_t sVt[64 * AT_ST];
-    __shared__ __attribute__((aligned(16))) int8_t sP[4][64 * AT_ST];
+    __shared__ __attribute__((aligned(16))) uint32_t sP[64 * AT_PP];
     extern __shared__ __attribute__((aligned(16))) int32_t s_exp[];  // attn_exp when it fits
     const AttnGroup G = groups[blockIdx.x];
     const int h = blockIdx.y;
@@ -703,63 +734,59 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
     const v4i qf = *(const v4i *)&sQ[(16 * w + (lane & 15)) * AT_ST + (lane >> 4) * 16];
     // this lane's rows (e = 0..3) and their positions
     int row[4], posr[4];
-    bool valid[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         row[e] = 16 * w + 4 * (lane >> 4) + e;
-        valid[e] = row[e] < G.count;
         posr[e] = G.pos0 + row[e];
     }
-    auto load_k = [&](int kb) {
-        const int key = kb * 64 + (tid >> 2), c = (tid & 3) * 16;
-        v4i v = {0, 0, 0, 0};
-        if (key < nk) v = *(const v4i *)(a.kc + base + (size_t)key * 64 + c);
-        *(v4i *)&sK[(tid >> 2) * AT_ST + c] = v;
-    };
-    auto load_vt = [&](int kb) {
-        const int kl = tid >> 2, key = kb * 64 + kl, c = (tid & 3) * 16;
-        v4i v = {0, 0, 0, 0};
-        if (key < nk) v = *(const v4i *)(a.vc + base + (size_t)key * 64 + c);
-        const int8_t *b = (const int8_t *)&v;
-#pragma unroll
-        for (int i = 0; i < 16; i++) sVt[(c + i) * AT_ST + kl] = b[i];
-    };
-    auto qk = [&](v4i s[4]) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const v4i kf = *(const v4i *)&sK[(t * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
-            s[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qf, kf, v4i{0, 0, 0, 0}, 0, 0, 0);
-        }
-    };
+    const int nkb = (nk + 63) / 64, nsb = (nkb + AT_SB - 1) / AT_SB;
     // score = clamp(rescale(dot, m, s), +-2^40): |dot| <= hd 2^14 <= 2^22, so |dot m| < 2^53 and
     // one multiply-add and an arithmetic shift are exact (a shift of 63 or more gives 0).
     const int s_eff = a.score_s < 63 ? a.score_s : 63;
     const int64_t s_half = s_eff ? (int64_t)1 << (s_eff - 1) : 0;
-    auto score = [&](int32_t dot) {
-        return clamp64(((int64_t)dot * a.score_m + s_half) >> s_eff, -SCORE_LIMIT, SCORE_LIMIT);
+    auto score = [&](int32_t dot) -> int64_t {
+        const int64_t r = ((int64_t)dot * a.score_m + s_half) >> s_eff;
+        return NOCLAMP ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
     };
-    const int nkb = (nk + 63) / 64;
-    // pass 1: the row max. The score clamp(rescale(dot)) is monotone in the dot (its direction
-    // is the sign of score_m), so the largest score is the score of the largest or of the
-    // smallest dot.
+    v4i S[AT_SB][4];  // the dots (then the table indices) of one super-block
+    auto qk_super = [&](int sb) {
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++) {
+            const int kb = sb * AT_SB + b;
+            if (kb >= nkb) break;
+            {
+                const int key = kb * 64 + (tid >> 2), c = (tid & 3) * 16;
+                v4i v = {0, 0, 0, 0};
+                if (key < nk) v = *(const v4i *)(a.kc + base + (size_t)key * 64 + c);
+                *(v4i *)&sK[(tid >> 2) * AT_ST + c] = v;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const v4i kf = *(const v4i *)&sK[(t * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
+                S[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qf, kf, v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+            __syncthreads();
+        }
+    };
+
+    // pass 1: the row max, from the largest and the smallest dot
     int32_t dmax[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
     int32_t dmin[4] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX};
-    for (int kb = 0; kb < nkb; kb++) {
-        load_k(kb);
-        __syncthreads();
-        v4i s[4];
-        qk(s);
+    for (int sb = 0; sb < nsb; sb++) {
+        qk_super(sb);
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int key = kb * 64 + t * 16 + (lane & 15);
+        for (int b = 0; b < AT_SB; b++)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (key <= posr[e]) {
-                    dmax[e] = s[t][e] > dmax[e] ? s[t][e] : dmax[e];
-                    dmin[e] = s[t][e] < dmin[e] ? s[t][e] : dmin[e];
-                }
-        }
-        __syncthreads();
+            for (int t = 0; t < 4; t++) {
+                const int key = (sb * AT_SB + b) * 64 + t * 16 + (lane & 15);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (key <= posr[e] && key < nk) {
+                        dmax[e] = S[b][t][e] > dmax[e] ? S[b][t][e] : dmax[e];
+                        dmin[e] = S[b][t][e] < dmin[e] ? S[b][t][e] : dmin[e];
+                    }
+            }
     }
     int64_t mx[4];
 #pragma unroll
@@ -773,86 +800,109 @@ __global__ __launch_bounds__(256) void k_attend_mfma(AttnArgs a, const AttnGroup
         const int64_t a0 = score(dmax[e]), a1 = score(dmin[e]);
         mx[e] = a0 > a1 ? a0 : a1;  // rows past the group's count: unused
     }
-    int64_t sum[4] = {0, 0, 0, 0};
-    for (int kb = 0; kb < nkb; kb++) {  // pass 2: the sum of the table entries
-        load_k(kb);
-        __syncthreads();
-        v4i s[4];
-        qk(s);
+    // the dots of super-block sb -> table indices min(M - s, last), -1 for a masked key
+    auto to_index = [&](int sb) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int key = kb * 64 + t * 16 + (lane & 15);
+        for (int b = 0; b < AT_SB; b++)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (valid[e] && key <= posr[e]) {
-                    const int64_t dd = mx[e] - score(s[t][e]);
-                    sum[e] += etab[dd < last ? dd : last];
+            for (int t = 0; t < 4; t++) {
+                const int key = (sb * AT_SB + b) * 64 + t * 16 + (lane & 15);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int64_t dd = mx[e] - score(S[b][t][e]);
+                    S[b][t][e] = (key <= posr[e] && key < nk) ? (int32_t)(dd < last ? dd : last) : -1;
                 }
-        }
-        __syncthreads();
+            }
+    };
+    // pass 2: the sum of the table entries
+    int64_t sum[4] = {0, 0, 0, 0};
+    for (int sb = 0; sb < nsb; sb++) {
+        if (nsb > 1) qk_super(sb);
+        to_index(sb);
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (S[b][t][e] >= 0) sum[e] += etab[S[b][t][e]];
     }
     uint64_t frac[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) sum[e] += __shfl_xor(sum[e], o, 64);
-        // floor(2^64 / S) for S >= 2; S = 1 divides exactly
-        frac[e] = sum[e] >= 2 ? div_2p64((uint64_t)sum[e]) : 0;
+        frac[e] = sum[e] >= 2 ? div_2p64((uint64_t)sum[e]) : 0;  // S = 1 divides exactly
     }
+    // pass 3: p, its packed digits, and the digit-plane PV products
     v4i acc[4][4];  // [digit plane][channel tile]
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[k][c] = v4i{0, 0, 0, 0};
-    for (int kb = 0; kb < nkb; kb++) {  // pass 3: p and the digit-plane PV products
-        load_k(kb);
-        load_vt(kb);
-        __syncthreads();
-        v4i s[4];
-        qk(s);
+    for (int sb = 0; sb < nsb; sb++) {
+        if (nsb > 1) {
+            qk_super(sb);
+            to_index(sb);
+        }
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int key = kb * 64 + t * 16 + (lane & 15);
+        for (int b = 0; b < AT_SB; b++) {
+            const int kb = sb * AT_SB + b;
+            if (kb >= nkb) break;
+            {  // V^T of the block into LDS
+                const int kl = tid >> 2, key = kb * 64 + kl, c = (tid & 3) * 16;
+                v4i v = {0, 0, 0, 0};
+                if (key < nk) v = *(const v4i *)(a.vc + base + (size_t)key * 64 + c);
+                const int8_t *bv = (const int8_t *)&v;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                int64_t p = 0;
-                if (valid[e] && key <= posr[e]) {
-                    const int64_t dd = mx[e] - score(s[t][e]);
-                    const uint64_t num = (uint64_t)etab[dd < last ? dd : last] << a.softmax_p;
-                    const uint64_t S = (uint64_t)sum[e];
-                    uint64_t q = num;
-                    if (S >= 2) {
-                        q = __umul64hi(num, frac[e]);  // q <= floor(num / S) <= q + 1
-                        if (num - q * S >= S) q++;
+                for (int i = 0; i < 16; i++) sVt[(c + i) * AT_ST + kl] = bv[i];
+            }
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int32_t idx = S[b][t][e];
+                    uint32_t p = 0;
+                    if (idx >= 0) {
+                        const uint64_t num = (uint64_t)etab[idx] << a.softmax_p;
+                        const uint64_t Sv = (uint64_t)sum[e];
+                        uint64_t q = num;
+                        if (Sv >= 2) {
+                            q = __umul64hi(num, frac[e]);  // q <= floor(num / S) <= q + 1
+                            if (num - q * Sv >= Sv) q++;
+                        }
+                        p = (uint32_t)q;  // <= 2^P <= 2^30
                     }
-                    p = (int64_t)q;
+                    sP[row[e] * AT_PP + t * 16 + (lane & 15)] = (p + 0x80808080u) ^ 0x80808080u;
                 }
-                int64_t rest = p;
+            __syncthreads();
+            v4i af[4];
+            {
+                const uint32_t *pr = &sP[(16 * w + (lane & 15)) * AT_PP + (lane >> 4) * 16];
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int64_t dg = ((rest + 128) & 255) - 128;
-                    sP[k][row[e] * AT_ST + t * 16 + (lane & 15)] = (int8_t)dg;
-                    rest = (rest - dg) >> 8;
+                for (int gq = 0; gq < 4; gq++) {
+                    const v4i wv = *(const v4i *)(pr + 4 * gq);
+                    uint32_t pl[4];
+                    byte_transpose((uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3], pl);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) af[k][gq] = (int32_t)pl[k];
                 }
             }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const v4i af = *(const v4i *)&sP[k][(16 * w + (lane & 15)) * AT_ST + (lane >> 4) * 16];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const v4i bf = *(const v4i *)&sVt[(c * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
-                acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, acc[k][c], 0, 0, 0);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[k], bf, acc[k][c], 0, 0, 0);
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 #pragma unroll
     for (int c = 0; c < 4; c++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            if (!valid[e]) continue;
+            if (row[e] >= G.count) continue;
             const int64_t o = (int64_t)acc[0][c][e] + ((int64_t)acc[1][c][e] << 8) +
                               ((int64_t)acc[2][c][e] << 16) + ((int64_t)acc[3][c][e] << 24);
             a.out[(size_t)(G.first + row[e]) * a.ldo + h * 64 + c * 16 + (lane & 15)] =
@@ -864,13 +914,18 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
                                 hipStream_t stream) {
     if (n_groups <= 0) return hipSuccess;
     const size_t lds = a.exp_len <= ATTN_LDS_TABLE ? sizeof(int32_t) * (size_t)a.exp_len : 0;
-    static size_t allowed = 0;  // the dynamic LDS limit, raised once
-    if (lds > allowed) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_attend_mfma, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    static size_t allowed[2] = {0, 0};  // the dynamic LDS limit, raised once per variant
+    const bool noclamp = a.score_s >= 13;
+    if (lds > allowed[noclamp]) {
+        hipError_t e = hipFuncSetAttribute(noclamp ? (const void *)k_attend_mfma<true> : (const void *)k_attend_mfma<false>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        allowed = lds;
+        allowed[noclamp] = lds;
     }
-    hipLaunchKernelGGL(k_attend_mfma, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+    if (noclamp)
+        hipLaunchKernelGGL(k_attend_mfma<true>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+    else
+        hipLaunchKernelGGL(k_attend_mfma<false>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
     return hipGetLastError();
 }
 

@@ -133,6 +133,17 @@ int main(int argc, char **argv) {
             if (dlt >= -1 || r * r >= 2) CHECK((u128)hs::isqrt_est(sqv) == isqrt_ref(sqv), "isqrt_est square");
             count += 2;
         }
+    // shift_round_hi against the i128 rule (|t g| < 2^126, 64 <= s <= 126)
+    for (long i = 0; i < n; i++) {
+        const int tb = (int)(next() % 63), gb = (int)(next() % 63);
+        int64_t t = (int64_t)(next() >> (64 - tb)), gg = (int64_t)(next() >> (64 - gb));
+        if (next() & 1) t = -t;
+        if (next() & 1) gg = -gg;
+        const uint32_t sh = 64 + (uint32_t)(next() % 63);
+        const i128 want = hs::shift_round128((i128)t * (i128)gg, sh, 126);
+        CHECK((i128)hs::shift_round_hi(t, gg, sh) == want, "shift_round_hi %lld %lld %u", (long long)t, (long long)gg, sh);
+        count++;
+    }
     // ln_inv against the u128 form
     for (long i = 0; i < n / 4; i++) {
         const u128 sq = ((u128)(next() >> (next() % 64)) << (next() % 12)) * (1 + next() % 3);

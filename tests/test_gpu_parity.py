@@ -379,3 +379,20 @@ def test_head_dim_64_prefill_equals_the_reference(dev, overlap):
     for i, blk in enumerate(blocks):
         print(f"block {i} ({len(blk)} tokens, K {overlap})", flush=True)
         assert got[i] == O.encode_block(om, blk, overlap=overlap), i
+
+
+@pytest.mark.parametrize("overlap", [0, 100])
+def test_head_dim_64_long_contexts_equal_the_reference(dev, overlap):
+    """More than 256 keys per row (the MFMA prefill kernel recomputes Q K^T per pass for
+    contexts past four key blocks), windows longer than n_ctx = 600 (restarts)."""
+    from taco_amd import fold, hip
+    b = O.build_model((1, 2, 128, 128, 400, 600), 33, 16)
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    lens = [257, 320, 599, 600, 900]
+    blocks = [np.array(splitmix_tokens(70 + i, n, 399), np.uint32) for i, n in enumerate(lens)]
+    batch = hip.HipBatch(hm, 3, 1200)
+    batch.set_overlap(overlap)
+    got = fold.fold_blocks(batch, blocks, overlap)
+    for i, blk in enumerate(blocks):
+        print(f"block {i} ({len(blk)} tokens, K {overlap})", flush=True)
+        assert got[i] == O.encode_block(om, blk, overlap=overlap), i
