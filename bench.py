@@ -88,9 +88,16 @@ def main():
     log(f"device {dev.name()}, model {model.weight_bytes() / 1e6:.1f} MB, batch "
         f"{batch.gpu_bytes() / 1e9:.2f} GB")
 
+    phase = {"fold": 0.0, "container": 0.0}
+
     def step():
+        t0 = time.perf_counter()
         payloads = fold.fold_blocks(batch, blocks, 0)  # every row runs (no early stop)
-        return payloads, fold.container(model.hash(), original, block_size, 0, payloads)
+        t1 = time.perf_counter()
+        cont = fold.container(model.hash(), original, block_size, 0, payloads)
+        phase["fold"] += t1 - t0
+        phase["container"] += time.perf_counter() - t1
+        return payloads, cont
 
     for i in range(args.warmup):
         ts = time.time()
@@ -98,6 +105,7 @@ def main():
         log(f"warmup {i}: {time.time() - ts:.3f}s, container {len(cont)} B")
     hip._check(hip.lib().hs_batch_set_profiling(batch.h, 1))
     hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
+    phase.update(fold=0.0, container=0.0)
     ts = time.perf_counter()
     for i in range(args.steps):
         payloads, cont = step()
@@ -126,6 +134,9 @@ def main():
     coded = sum(1 for p in payloads if p is not None and len(p) < block_size)
     log(f"timed: {args.steps} steps in {elapsed:.3f}s -> {value:.0f} tokens/s; container "
         f"{len(cont)} B sha256 {cont_sha[:16]}, {coded}/{W} blocks coded")
+    gpu_ms = sum(v["ns"] for v in prof.values()) / 1e6 / args.steps
+    log(f"  per step: fold call {1e3 * phase['fold'] / args.steps:.3f} ms (kernels {gpu_ms:.3f} ms), "
+        f"container {1e3 * phase['container'] / args.steps:.3f} ms")
     for kk, v in sorted(prof.items(), key=lambda x: -x[1]["ns"]):
         log(f"  {kk:12s} {v['ns'] / 1e6 / args.steps:8.3f} ms/step  {v['launches'] // args.steps:5d} "
             f"launches/step" + (f"  {v['ops'] / v['ns'] / 1e3:7.1f} TOPS" if v["ops"] and v["ns"] else ""))

@@ -216,7 +216,8 @@ hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8
  * count and the algorithmic int8 operations (2 per multiply-accumulate of the GEMMs). */
 hs_status hs_batch_set_profiling(hs_batch *batch, int on);
 /* Writes up to cap entries (labels are NUL-terminated in 32-byte slots); returns the number of
- * labels. Clears the counters when `clear` is nonzero. */
+ * labels. Clears the counters when `clear` is nonzero. The event times of the calls since the
+ * last read are gathered here (the calls themselves only record the events). */
 size_t hs_batch_profile(hs_batch *batch, char *labels, uint64_t *ns, uint64_t *launches,
                         uint64_t *ops, size_t cap, int clear);
 

@@ -11,6 +11,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(ROOT, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+# Host-only sources go through the host compiler; the HIP runtime calls and kernels through hipcc.
+HOST_SOURCES = {"common.cpp", "hsm.cpp", "taco/harness.cpp"}
 
 BACKEND_SOURCES = ["common.cpp", "hsm.cpp", "hs_api.cpp", "kernels.hip"]
 HARNESS_SOURCES = ["taco/harness.cpp", "common.cpp"]
@@ -30,6 +33,16 @@ def source_sha256() -> str:
 
 
 def _compile(src: str, obj: str, sha: str, verbose: bool):
+    rel = os.path.relpath(src, CSRC).replace(os.sep, "/")
+    if rel in HOST_SOURCES:
+        cmd = [CXX, "-O3", "-std=c++17", "-fPIC", "-pthread", "-I", os.path.join(ROOT, "include"),
+               "-I", CSRC, f'-DHS_SOURCE_SHA256="{sha[:16]}"', "-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{CXX} failed for {src}:\n{r.stdout}\n{r.stderr}")
+        return
     cmd = [
         HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
         # packed FP32 ops stay off (no float arithmetic here; the flag keeps hipcc from emitting
@@ -68,7 +81,7 @@ def build(verbose: bool = False, jobs: int = 8):
     harness = [s for s in HARNESS_SOURCES if s in objs]
     if "taco/harness.cpp" in objs:
         _link([objs[s] for s in harness], LIB_HARNESS,
-              ["-L", HERE, "-lhardshell_hip", "-Wl,-rpath,$ORIGIN"], verbose)
+              ["-L", HERE, "-lhardshell_hip", "-Wl,-rpath,$ORIGIN", "-pthread"], verbose)
     return LIB_BACKEND
 
 

@@ -1,6 +1,11 @@
 #include "common.h"
 
+#include <cstdlib>
 #include <cstring>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
 
 namespace hs {
 
@@ -57,11 +62,68 @@ void clear_error() {
     g_code = 0;
 }
 
+namespace {
+
+#if defined(__x86_64__)
+// The same compression with the x86 SHA extensions (sha256rnds2 runs two rounds on the state
+// split as ABEF / CDGH; sha256msg1 / sha256msg2 extend the message schedule four words at a time).
+__attribute__((target("sha,sse4.1,ssse3"))) void compress_ni(uint32_t h[8], const uint8_t *data, size_t nblk) {
+    const __m128i bswap = _mm_set_epi64x(0x0c0d0e0f08090a0bULL, 0x0405060700010203ULL);
+    __m128i t = _mm_shuffle_epi32(_mm_loadu_si128((const __m128i *)&h[0]), 0xB1);  // C D A B
+    __m128i s1 = _mm_shuffle_epi32(_mm_loadu_si128((const __m128i *)&h[4]), 0x1B);  // E F G H
+    __m128i s0 = _mm_alignr_epi8(t, s1, 8);                                         // A B E F
+    s1 = _mm_blend_epi16(s1, t, 0xF0);                                              // C D G H
+    for (size_t b = 0; b < nblk; b++, data += 64) {
+        const __m128i save0 = s0, save1 = s1;
+        __m128i w[4];
+        for (int q = 0; q < 16; q++) {
+            if (q < 4) {
+                w[q] = _mm_shuffle_epi8(_mm_loadu_si128((const __m128i *)(data + 16 * q)), bswap);
+            } else {
+                __m128i x = _mm_sha256msg1_epu32(w[(q - 4) & 3], w[(q - 3) & 3]);
+                x = _mm_add_epi32(x, _mm_alignr_epi8(w[(q - 1) & 3], w[(q - 2) & 3], 4));
+                w[q & 3] = _mm_sha256msg2_epu32(x, w[(q - 1) & 3]);
+            }
+            const __m128i wk = _mm_add_epi32(w[q & 3], _mm_loadu_si128((const __m128i *)&K256[4 * q]));
+            s1 = _mm_sha256rnds2_epu32(s1, s0, wk);
+            s0 = _mm_sha256rnds2_epu32(s0, s1, _mm_shuffle_epi32(wk, 0x0E));
+        }
+        s0 = _mm_add_epi32(s0, save0);
+        s1 = _mm_add_epi32(s1, save1);
+    }
+    t = _mm_shuffle_epi32(s0, 0x1B);             // F E B A
+    s1 = _mm_shuffle_epi32(s1, 0xB1);            // D C H G
+    s0 = _mm_blend_epi16(t, s1, 0xF0);           // D C B A
+    s1 = _mm_alignr_epi8(s1, t, 8);              // H G F E
+    _mm_storeu_si128((__m128i *)&h[0], s0);
+    _mm_storeu_si128((__m128i *)&h[4], s1);
+}
+
+// HS_SHA256_PORTABLE=1 selects the portable compression (for tests of both forms).
+bool have_sha_ni() {
+    static const bool yes = !std::getenv("HS_SHA256_PORTABLE") && __builtin_cpu_supports("sha") &&
+                            __builtin_cpu_supports("sse4.1") && __builtin_cpu_supports("ssse3");
+    return yes;
+}
+#endif
+
+void compress_blocks(uint32_t h[8], const uint8_t *data, size_t nblk) {
+#if defined(__x86_64__)
+    if (have_sha_ni()) {
+        compress_ni(h, data, nblk);
+        return;
+    }
+#endif
+    for (size_t b = 0; b < nblk; b++) compress(h, data + 64 * b);
+}
+
+}  // namespace
+
 void sha256(const uint8_t *data, size_t len, uint8_t out[32]) {
     uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
                      0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
-    size_t i = 0;
-    for (; i + 64 <= len; i += 64) compress(h, data + i);
+    size_t i = len / 64 * 64;
+    compress_blocks(h, data, len / 64);
     uint8_t tail[128] = {0};
     const size_t rest = len - i;
     std::memcpy(tail, data + i, rest);
@@ -69,8 +131,7 @@ void sha256(const uint8_t *data, size_t len, uint8_t out[32]) {
     const size_t tl = rest + 9 <= 64 ? 64 : 128;
     const uint64_t bits = (uint64_t)len * 8;
     for (int b = 0; b < 8; b++) tail[tl - 1 - b] = (uint8_t)(bits >> (8 * b));
-    compress(h, tail);
-    if (tl == 128) compress(h, tail + 64);
+    compress_blocks(h, tail, tl / 64);
     for (int k = 0; k < 8; k++)
         for (int b = 0; b < 4; b++) out[4 * k + b] = (uint8_t)(h[k] >> (24 - 8 * b));
 }

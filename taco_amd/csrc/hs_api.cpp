@@ -390,6 +390,14 @@ struct hs_batch {
     RowInfo *d_rows = nullptr;
     int32_t *d_x = nullptr, *d_src = nullptr;
     hs::AttnGroup *d_groups = nullptr;
+    // Pinned host staging of each pass's rows, groups, output rows, queries and intervals, so
+    // the copies run asynchronously on the batch stream.
+    RowInfo *h_rows = nullptr;
+    hs::AttnGroup *h_groups = nullptr;
+    int32_t *h_src = nullptr;
+    uint32_t *h_queries = nullptr;
+    uint64_t *h_intervals = nullptr;
+    bool inflight = false;  // a pass returned with copies or kernels still queued on `st`
     int8_t *d_a = nullptr, *d_qkv = nullptr, *d_att = nullptr, *d_g = nullptr, *d_af = nullptr;
     int64_t *d_logits = nullptr;
     uint16_t *d_d16 = nullptr;
@@ -418,6 +426,9 @@ struct hs_batch {
             event_pool.push_back(p.e1);
         }
         for (auto e : event_pool) (void)hipEventDestroy(e);
+        if (st) (void)hipStreamSynchronize(st);
+        for (void *p : {(void *)h_rows, (void *)h_groups, (void *)h_src, (void *)h_queries, (void *)h_intervals})
+            if (p) (void)hipHostFree(p);
         if (st) (void)hipStreamDestroy(st);
     }
     hipError_t event(hipEvent_t &e) {
@@ -516,6 +527,11 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
         if ((s = mem.alloc(b->kc[l], cache)) != HS_OK) return s;
         if ((s = mem.alloc(b->vc[l], cache)) != HS_OK) return s;
     }
+    HIP_TRY(hipHostMalloc((void **)&b->h_rows, R * sizeof(RowInfo), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_groups, R * sizeof(hs::AttnGroup), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_src, R * sizeof(int32_t), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_queries, 2 * R * sizeof(uint32_t), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_intervals, 3 * R * sizeof(uint64_t), hipHostMallocDefault));
     HIP_TRY(hipStreamCreate(&b->st));
     *out = b.release();
     return HS_OK;
@@ -555,7 +571,8 @@ namespace {
 struct Plan {
     std::vector<std::vector<PassRow>> passes;
     std::vector<size_t> pos;
-    std::unordered_map<size_t, std::vector<uint32_t>> hist;
+    std::vector<size_t> touched;               // the slots of the call, in first-use order
+    std::vector<std::vector<uint32_t>> hist;   // their token histories after the call
     std::vector<StreamState> streams;
     std::unordered_map<size_t, std::vector<uint32_t>> prev;
 };
@@ -579,12 +596,15 @@ Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
         in_pass[r.slot] = 1;
         cur.push_back(r);
     };
+    std::vector<int32_t> index(b.slots, -1);  // slot -> its entry in p.touched / p.hist
     for (size_t i = 0; i < n; i++) {
         const size_t slot = in[i].slot;
-        auto it = p.hist.find(slot);
-        if (it == p.hist.end())
-            it = p.hist.emplace(slot, std::vector<uint32_t>(b.hist.begin() + slot * C, b.hist.begin() + (slot + 1) * C)).first;
-        std::vector<uint32_t> &h = it->second;
+        if (index[slot] < 0) {
+            index[slot] = (int32_t)p.touched.size();
+            p.touched.push_back(slot);
+            p.hist.emplace_back(b.hist.begin() + slot * C, b.hist.begin() + (slot + 1) * C);
+        }
+        std::vector<uint32_t> &h = p.hist[index[slot]];
         size_t at = p.pos[slot];
         if (at >= C) {
             if (in_pass[slot]) flush();
@@ -608,7 +628,8 @@ void commit(hs_batch &b, Plan &p) {
     const size_t C = b.model->host.n_ctx;
     b.pos = p.pos;
     b.streams = p.streams;
-    for (auto &kv : p.hist) std::memcpy(&b.hist[kv.first * C], kv.second.data(), C * sizeof(uint32_t));
+    for (size_t t = 0; t < p.touched.size(); t++)
+        std::memcpy(&b.hist[p.touched[t] * C], p.hist[t].data(), C * sizeof(uint32_t));
     for (auto &kv : p.prev) b.prev[kv.first] = std::move(kv.second);
 }
 
@@ -620,39 +641,45 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     const hs_model &m = *b.model;
     hipStream_t st = b.st;
     const int n = (int)rows.size();
-    std::vector<RowInfo> info(n);
-    std::vector<int32_t> src;
-    std::vector<uint32_t> q;
+    if (b.inflight) {  // the staging buffers may still feed the previous pass's copies
+        HIP_TRY(hipStreamSynchronize(st));
+        b.inflight = false;
+    }
+    RowInfo *info = b.h_rows;
+    int32_t *src = b.h_src;
+    uint32_t *q = b.h_queries;
     std::vector<int64_t> owner;
+    owner.reserve(n);
+    int n_out = 0;
     for (int r = 0; r < n; r++) {
         info[r] = RowInfo{(int32_t)rows[r].slot, (int32_t)rows[r].token, (int32_t)rows[r].pos, -1};
         if (rows[r].input >= 0) {
-            info[r].out = (int32_t)src.size();
-            src.push_back(r);
+            info[r].out = n_out;
+            src[n_out] = r;
             owner.push_back(rows[r].input);
             if (out == Out::Intervals) {
-                q.push_back(queries[2 * rows[r].input]);
-                q.push_back(queries[2 * rows[r].input + 1]);
+                q[2 * n_out] = queries[2 * rows[r].input];
+                q[2 * n_out + 1] = queries[2 * rows[r].input + 1];
             }
+            n_out++;
         }
     }
-    HIP_TRY(hipMemcpyAsync(b.d_rows, info.data(), n * sizeof(RowInfo), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(b.d_rows, info, n * sizeof(RowInfo), hipMemcpyHostToDevice, st));
     // Attention groups (runs of one slot at consecutive positions, at most 64 rows each) for
     // the MFMA prefill kernel; decode-shaped passes (short runs) use the row kernel.
-    std::vector<hs::AttnGroup> groups;
+    int n_groups = 0;
     for (int r = 0; r < n;) {
         int c = 1;
         while (r + c < n && c < 64 && rows[r + c].slot == rows[r].slot && rows[r + c].pos == rows[r].pos + (uint32_t)c) c++;
-        groups.push_back(hs::AttnGroup{r, c, (int32_t)rows[r].slot, (int32_t)rows[r].pos});
+        b.h_groups[n_groups++] = hs::AttnGroup{r, c, (int32_t)rows[r].slot, (int32_t)rows[r].pos};
         r += c;
     }
-    const bool mfma_attn = m.hd == 64 && (size_t)n >= 16 * groups.size();
+    const bool mfma_attn = m.hd == 64 && n >= 16 * n_groups;
     if (mfma_attn)
-        HIP_TRY(hipMemcpyAsync(b.d_groups, groups.data(), groups.size() * sizeof(hs::AttnGroup),
-                               hipMemcpyHostToDevice, st));
-    const int n_out = (int)src.size();
-    if (n_out) HIP_TRY(hipMemcpyAsync(b.d_src, src.data(), n_out * sizeof(int32_t), hipMemcpyHostToDevice, st));
-    if (!q.empty()) HIP_TRY(hipMemcpyAsync(b.d_queries, q.data(), q.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(b.d_groups, b.h_groups, n_groups * sizeof(hs::AttnGroup), hipMemcpyHostToDevice, st));
+    if (n_out) HIP_TRY(hipMemcpyAsync(b.d_src, src, n_out * sizeof(int32_t), hipMemcpyHostToDevice, st));
+    if (out == Out::Intervals && n_out)
+        HIP_TRY(hipMemcpyAsync(b.d_queries, q, 2 * (size_t)n_out * sizeof(uint32_t), hipMemcpyHostToDevice, st));
 
     uint64_t attn_keys = 0;  // sum over rows of the keys each row reads
     for (int r = 0; r < n; r++) attn_keys += (uint64_t)rows[r].pos + 1;
@@ -703,7 +730,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
         at.out = b.d_att; at.ldo = m.d_pad;
         HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d, [&] {
-            return mfma_attn ? hs::launch_attend_groups(at, b.d_groups, (int)groups.size(), st)
+            return mfma_attn ? hs::launch_attend_groups(at, b.d_groups, n_groups, st)
                              : hs::launch_attend(at, n, st);
         }));
         HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
@@ -712,8 +739,10 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
     }
     if (n_out == 0) {
-        if (b.profiling) {
+        b.inflight = true;
+        if (b.profiling && b.pending.size() > 8192) {
             HIP_TRY(hipStreamSynchronize(st));
+            b.inflight = false;
             HIP_TRY(b.collect());
         }
         return HS_OK;
@@ -723,7 +752,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     head.w = m.wte; head.m = m.logit_m; head.s = m.host.logit_s; head.n = m.V; head.k = m.d;
     head.n_pad = m.V_pad; head.k_pad = m.d_pad;
     const size_t per_row = out == Out::Weights ? (size_t)m.V : 3;
-    std::vector<uint64_t> host((size_t)n_out * per_row);
+    std::vector<uint64_t> host(out == Out::Weights ? (size_t)n_out * per_row : 0);
     for (int c0 = 0; c0 < n_out; c0 += (int)b.chunk_rows) {
         const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
         if (m.compact) {
@@ -758,11 +787,13 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
                                    hipMemcpyDeviceToHost, st));
     }
     if (out == Out::Intervals)
-        HIP_TRY(hipMemcpyAsync(host.data(), b.d_intervals, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipMemcpyAsync(b.h_intervals, b.d_intervals, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
-    if (b.profiling) HIP_TRY(b.collect());
+    const uint64_t *res = out == Out::Intervals ? b.h_intervals : host.data();
+    // The event times are read back in bulk (hs_batch_profile), not inside every call.
+    if (b.profiling && b.pending.size() > 8192) HIP_TRY(b.collect());
     for (int i = 0; i < n_out; i++)
-        std::memcpy(sink + (size_t)owner[i] * per_row, host.data() + (size_t)i * per_row, per_row * 8);
+        std::memcpy(sink + (size_t)owner[i] * per_row, res + (size_t)i * per_row, per_row * 8);
     return HS_OK;
 }
 
@@ -997,6 +1028,15 @@ extern "C" hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, co
 
 extern "C" hs_status hs_batch_set_profiling(hs_batch *b, int on) {
     if (!b) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL batch");
+    if (on) {
+        // Events for the next few thousand launches, made now rather than inside timed calls.
+        HIP_TRY(hipSetDevice(b->model->dev->ordinal));
+        while (b->event_pool.size() < 8192) {
+            hipEvent_t e;
+            HIP_TRY(hipEventCreate(&e));
+            b->event_pool.push_back(e);
+        }
+    }
     b->profiling = on != 0;
     return HS_OK;
 }
@@ -1004,6 +1044,9 @@ extern "C" hs_status hs_batch_set_profiling(hs_batch *b, int on) {
 extern "C" size_t hs_batch_profile(hs_batch *b, char *labels, uint64_t *ns, uint64_t *launches,
                                    uint64_t *ops, size_t cap, int clear) {
     if (!b) return 0;
+    if (!b->pending.empty()) {  // every pending launch finished: each call synchronizes its stream
+        if (hipStreamSynchronize(b->st) != hipSuccess || b->collect() != hipSuccess) return 0;
+    }
     const size_t n = b->prof.size();
     for (size_t i = 0; i < n && i < cap; i++) {
         if (labels) {

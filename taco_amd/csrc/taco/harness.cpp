@@ -4,8 +4,13 @@
 // crates/taco/src/payload.rs:20-60 (LEB128), crates/taco-coder/src/{encoder,decoder}.rs (the
 // range coder) and crates/taco-format/src/writer.rs:245-288 (the container).
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <cstring>
+#include <functional>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../common.h"
@@ -141,6 +146,75 @@ bool read_varint(const uint8_t *b, size_t len, uint64_t &value, size_t &used) { 
     return false;
 }
 
+// A persistent pool of host threads: run(n, f) calls f(0) .. f(n - 1) on the workers and the
+// calling thread and returns when all are done. Blocks are independent streams, so their range
+// coders run in parallel (the reference codes blocks in parallel too, crates/taco/src/parallel.rs).
+// The pool is never destroyed: its threads wait for work until the process ends.
+class Pool {
+  public:
+    static Pool &get() {
+        static Pool *p = new Pool();
+        return *p;
+    }
+    void run(size_t n, const std::function<void(size_t)> &f) {
+        if (n <= 1 || workers_ == 0) {
+            for (size_t i = 0; i < n; i++) f(i);
+            return;
+        }
+        std::unique_lock<std::mutex> lk(mu_);
+        job_ = &f;
+        n_ = n;
+        next_ = 0;
+        done_ = 0;
+        gen_++;
+        lk.unlock();
+        cv_.notify_all();
+        work();
+        lk.lock();
+        done_cv_.wait(lk, [&] { return done_ == n_; });
+        job_ = nullptr;
+    }
+
+  private:
+    Pool() {
+        const unsigned hw = std::thread::hardware_concurrency();
+        workers_ = std::min<unsigned>(hw > 1 ? hw - 1 : 0, 15);
+        for (unsigned i = 0; i < workers_; i++) std::thread([this] { loop(); }).detach();
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return gen_ != seen; });
+                seen = gen_;
+            }
+            work();
+        }
+    }
+    void work() {
+        for (;;) {
+            const std::function<void(size_t)> *fn;
+            size_t i;
+            {
+                std::lock_guard<std::mutex> lk(mu_);
+                if (!job_ || next_ >= n_) return;
+                fn = job_;
+                i = next_++;
+            }
+            (*fn)(i);
+            std::lock_guard<std::mutex> lk(mu_);
+            if (++done_ == n_) done_cv_.notify_all();
+        }
+    }
+    unsigned workers_ = 0;
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    const std::function<void(size_t)> *job_ = nullptr;
+    size_t n_ = 0, next_ = 0, done_ = 0;
+    uint64_t gen_ = 0;
+};
+
 // A context window of a block (gpu_fold.rs:128-134).
 struct Window {
     size_t block, first, len;
@@ -229,15 +303,29 @@ extern "C" hs_status tc_fold_blocks(hs_batch *batch, uint32_t overlap, const uin
         hs_status s = hs_batch_run_coded(batch, inputs.data(), queries.data(), inputs.size(),
                                          TC_FREQ_BITS, answers.data());
         if (s != HS_OK) return s;
-        // The rows are in window order, so each block's tokens reach its encoder in order.
+        // The rows are in window order: the rows of a block in this wave are one run, so each
+        // block's tokens reach its encoder in order, and the blocks' coders run in parallel.
+        std::vector<std::pair<size_t, size_t>> runs;  // [begin, end) of each block's coded rows
         for (size_t i = 0; i < inputs.size(); i++) {
             if (owner[i] < 0) continue;
-            const hs_interval &a = answers[i];
-            // lanes.rs:121-128: a bad interval or last-symbol flag is a fault of the device
-            if (a.freq == 0 || a.start > TOTAL || a.freq > TOTAL - a.start || a.symbol != queries[i].value)
-                return hs::fail(HS_DEVICE_ERROR, 0, "the coder op gave a bad interval");
-            enc[(size_t)owner[i]].push(a.start, a.freq);
+            if (runs.empty() || (size_t)owner[runs.back().first] != (size_t)owner[i]) runs.push_back({i, i});
+            runs.back().second = i + 1;
         }
+        std::atomic<bool> bad(false);
+        Pool::get().run(runs.size(), [&](size_t r) {
+            BlockEnc &be = enc[(size_t)owner[runs[r].first]];
+            for (size_t i = runs[r].first; i < runs[r].second; i++) {
+                if (owner[i] < 0) continue;
+                const hs_interval &a = answers[i];
+                // lanes.rs:121-128: a bad interval or last-symbol flag is a fault of the device
+                if (a.freq == 0 || a.start > TOTAL || a.freq > TOTAL - a.start || a.symbol != queries[i].value) {
+                    bad = true;
+                    return;
+                }
+                be.push(a.start, a.freq);
+            }
+        });
+        if (bad) return hs::fail(HS_DEVICE_ERROR, 0, "the coder op gave a bad interval");
     }
     for (size_t b = 0; b < count; b++) {
         BlockEnc &e = enc[b];

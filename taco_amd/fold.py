@@ -91,18 +91,20 @@ def container(model_hash: bytes, original: bytes, block_size: int, overlap: int,
             kinds[b] = 1
             parts.append(p)
         offs.append(offs[-1] + (len(p) if kinds[b] == 1 else 0))
-    blob = np.frombuffer(b"".join(parts) or b"\0", np.uint8).copy()
+    blob = np.frombuffer(b"".join(parts) or b"\0", np.uint8)
     offa = np.asarray(offs, np.uint64)
-    mh = np.frombuffer(model_hash, np.uint8).copy()
-    orig = np.frombuffer(original or b"\0", np.uint8).copy()
+    mh = np.frombuffer(model_hash, np.uint8)
+    orig = np.frombuffer(original or b"\0", np.uint8)
+    # 104-byte header, 5 bytes per block, and stored blocks no larger than the original bytes
+    cap = 104 + 5 * count + len(original)
+    out = np.empty(cap, np.uint8)
     n = lib().tc_container_build(_p(mh), _p(orig), len(original), block_size, overlap, _p(kinds),
-                                 _p(blob), _p(offa), None, 0)
+                                 _p(blob), _p(offa), _p(out), cap)
     if n == 0:
         raise ValueError("the container was refused")
-    out = np.zeros(n, np.uint8)
-    lib().tc_container_build(_p(mh), _p(orig), len(original), block_size, overlap, _p(kinds),
-                             _p(blob), _p(offa), _p(out), n)
-    return out.tobytes()
+    if n > cap:
+        raise RuntimeError("the container is larger than its bound")
+    return out[:n].tobytes()
 
 
 def token_bytes(tokens: np.ndarray) -> bytes:

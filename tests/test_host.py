@@ -273,3 +273,40 @@ def test_synthetic_workload_is_pinned():
     assert synth.sha256_tokens(synth.zipf_tokens(16384)) == \
         "dd627cc10d96abd5e4f8649b46f3ac1ef238f0415636c7f33a3d51f15b6cc6ce"
     assert validate(b)[0] == HS_OK
+
+
+SHA_CHECK = r"""
+import ctypes as C, hashlib, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from taco_amd import fold
+L = fold.lib()
+P = lambda a: a.ctypes.data_as(C.c_void_p)
+rng = np.random.default_rng(5)
+bad = 0
+for n in list(range(0, 200)) + [1000, 4095, 4096, 65537, 1 << 20]:
+    orig = rng.integers(0, 256, max(n, 1), dtype=np.uint8)
+    cnt = (n + 1023) // 1024
+    kinds = np.zeros(max(cnt, 1), np.uint8)
+    offa = np.zeros(cnt + 1, np.uint64)
+    out = np.zeros(200 + 5 * cnt + n, np.uint8)
+    L.tc_container_build(P(np.zeros(32, np.uint8)), P(orig), n, 1024, 0, P(kinds), P(orig), P(offa),
+                         P(out), len(out))
+    bad += out[48:80].tobytes() != hashlib.sha256(orig[:n].tobytes()).digest()
+print(bad)
+"""
+
+
+@pytest.mark.parametrize("portable", [False, True])
+def test_sha256_of_the_container_equals_hashlib(portable):
+    """The original-bytes checksum of the container (crates/taco-format/src/header.rs), with the
+    x86 SHA extensions where the CPU has them and with the portable compression."""
+    import subprocess
+    import sys
+    env = dict(os.environ)
+    if portable:
+        env["HS_SHA256_PORTABLE"] = "1"
+    r = subprocess.run([sys.executable, "-c", SHA_CHECK, ROOT], capture_output=True, text=True,
+                       env=env, timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "0"
