@@ -493,10 +493,11 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     b->hist.assign(slots * m.C, 0);
     b->streams.assign(slots, StreamState{});
     b->prev.assign(slots, {});
-    // The LM head runs on chunks of output rows: compact logits (2 B per logit) up to 4 GiB a
-    // chunk, i64 logits up to 1 GiB.
+    // The LM head runs on chunks of output rows: compact logits (2 B per logit) up to 192 MiB a
+    // chunk, so the coder op reads them back from the 256 MB Infinity Cache; i64 logits up to
+    // 1 GiB.
     const size_t per_row = m.compact ? 2ull * m.ld16 : 8ull * m.V_pad;
-    const size_t budget = m.compact ? (4ull << 30) : (1ull << 30);
+    const size_t budget = m.compact ? (192ull << 20) : (1ull << 30);
     b->chunk_rows = std::max<size_t>(hs::GEMM_BM, round_up(std::min<size_t>(b->rows_pad, budget / per_row), hs::GEMM_BM));
     b->chunk_rows = std::min(b->chunk_rows, b->rows_pad);
     const size_t R = b->max_rows, RP = b->rows_pad;

@@ -45,7 +45,7 @@ struct GemmArgs {
 };
 
 
-// Tile sizes of the MFMA GEMM: a rows are padded to GEMM_BM, w rows to GEMM_BN, k to 64.
+// Tile sizes of the MFMA GEMM: a rows are padded to GEMM_BM, w rows to GEMM_BN, k to GEMM_BK.
 constexpr int GEMM_BM = 256, GEMM_BN = 128, GEMM_BK = 64;
 
 // The group size of the XCD-aware tile order: one band of M-tiles per XCD.

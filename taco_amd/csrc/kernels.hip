@@ -1179,27 +1179,37 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     }
     __syncthreads();
 
-    // One pass: 8 consecutive symbols per thread and step (one 16-byte load; the 8 share a
-    // 64-column tile). A group whose tile max is zcut or more below M has only weight-0 symbols.
+    // One pass: 8 consecutive symbols per thread and group (one 16-byte load; the 8 share a
+    // 64-column tile), four groups in flight per step. A group whose tile max is zcut or more
+    // below M has only weight-0 symbols.
     int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0 < zcut)
-    for (int g0 = tid * 8; g0 < V; g0 += 256 * 8) {
-        const int64_t base64 = M - tm[g0 >> 6];
-        if (base64 >= zc) continue;
-        const uint4 raw = *(const uint4 *)(d16 + g0);
-        const uint16_t *dv = (const uint16_t *)&raw;
-        const int base = (int)base64;
+    for (int g0 = tid * 8; g0 < V; g0 += 4 * 256 * 8) {
+        uint4 raw[4];
+        int64_t b64[4];
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int j = g0 + q;
-            const int dd = base + (int)dv[q];
-            if (j < V && dd < zc) {  // then dd <= last: d = dd
-                if (packed) {
-                    atomicAdd(&hist[dd], (uint32_t)j < tok ? 0x10001u : 1u);
-                } else {
-                    atomicAdd(&hist[dd], 1u);
-                    if ((uint32_t)j < tok) atomicAdd(&hist[zc + dd], 1u);
+        for (int u = 0; u < 4; u++) {
+            const int gq = g0 + u * 256 * 8;
+            b64[u] = gq < V ? M - tm[gq >> 6] : (int64_t)zc;
+            if (b64[u] < zc) raw[u] = *(const uint4 *)(d16 + gq);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (b64[u] >= zc) continue;
+            const int gq = g0 + u * 256 * 8, base = (int)b64[u];
+            const uint16_t *dv = (const uint16_t *)&raw[u];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = gq + q;
+                const int dd = base + (int)dv[q];
+                if (j < V && dd < zc) {  // then dd <= last: d = dd
+                    if (packed) {
+                        atomicAdd(&hist[dd], (uint32_t)j < tok ? 0x10001u : 1u);
+                    } else {
+                        atomicAdd(&hist[dd], 1u);
+                        if ((uint32_t)j < tok) atomicAdd(&hist[zc + dd], 1u);
+                    }
+                    if (dd <= a.d0 && j < first) first = j;
                 }
-                if (dd <= a.d0 && j < first) first = j;
             }
         }
     }
