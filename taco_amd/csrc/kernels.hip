@@ -674,7 +674,7 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
 // =============================================================================================
 // Prefill attention on MFMA (head_dim 64). One workgroup = one group of <= 64 rows x one head;
 // wave w owns rows 16w .. 16w + 15. S = Q K^T comes from v_mfma_i32_16x16x64_i8 (exact i32) for
-// a super-block of up to AT_SB key blocks of 64, held in registers: with n_ctx <= 256 keys the
+// a super-block of up to AT_SB key blocks of 64, held in registers: with <= 256 keys the
 // product runs once, else once per pass. Pass 1 takes the row max (from the extreme dots: the
 // score is monotone in the dot), pass 2 turns the dots into table indices min(M - s, last) in
 // place and sums the table entries, pass 3 forms p = floor(e 2^P / S) (a 64-bit reciprocal of S
@@ -721,8 +721,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     // attn_exp into LDS (every score of passes 2 and 3 reads it); the launch gives the dynamic
     // LDS only when the table fits (exp_len <= ATTN_LDS_TABLE).
     const bool lds_table = a.exp_len <= ATTN_LDS_TABLE;
-    if (lds_table)
-        for (int i = tid; i < a.exp_len; i += 256) s_exp[i] = a.exp_table[i];
+    if (lds_table) {  // 16-byte copies when the table is 16-byte aligned (a device allocation)
+        const bool vec = ((uintptr_t)a.exp_table & 15) == 0;
+        const int n4 = vec ? a.exp_len / 4 : 0;
+        for (int i = tid; i < n4; i += 256) ((v4i *)s_exp)[i] = ((const v4i *)a.exp_table)[i];
+        for (int i = 4 * n4 + tid; i < a.exp_len; i += 256) s_exp[i] = a.exp_table[i];
+    }
     const int32_t *etab = lds_table ? (const int32_t *)s_exp : a.exp_table;
     {
         const int r = tid >> 2, c = (tid & 3) * 16;
@@ -749,17 +753,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         return NOCLAMP ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
     };
     v4i S[AT_SB][4];  // the dots (then the table indices) of one super-block
+    // this thread's 16 bytes of key (or value) block kb: key kb * 64 + tid / 4, bytes 16 (tid % 4)
+    auto kv_load = [&](const int8_t *cache, int kb) {
+        const int key = kb * 64 + (tid >> 2), c = (tid & 3) * 16;
+        v4i v = {0, 0, 0, 0};
+        if (key < nk) v = *(const v4i *)(cache + base + (size_t)key * 64 + c);
+        return v;
+    };
     auto qk_super = [&](int sb) {
+        v4i kreg[AT_SB];  // every key block of the super-block in flight at once
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++)
+            if (sb * AT_SB + b < nkb) kreg[b] = kv_load(a.kc, sb * AT_SB + b);
 #pragma unroll
         for (int b = 0; b < AT_SB; b++) {
             const int kb = sb * AT_SB + b;
             if (kb >= nkb) break;
-            {
-                const int key = kb * 64 + (tid >> 2), c = (tid & 3) * 16;
-                v4i v = {0, 0, 0, 0};
-                if (key < nk) v = *(const v4i *)(a.kc + base + (size_t)key * 64 + c);
-                *(v4i *)&sK[(tid >> 2) * AT_ST + c] = v;
-            }
+            *(v4i *)&sK[(tid >> 2) * AT_ST + (tid & 3) * 16] = kreg[b];
             __syncthreads();
 #pragma unroll
             for (int t = 0; t < 4; t++) {
@@ -845,14 +855,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             qk_super(sb);
             to_index(sb);
         }
+        v4i vnext = sb * AT_SB < nkb ? kv_load(a.vc, sb * AT_SB) : v4i{0, 0, 0, 0};
 #pragma unroll
         for (int b = 0; b < AT_SB; b++) {
             const int kb = sb * AT_SB + b;
             if (kb >= nkb) break;
-            {  // V^T of the block into LDS
-                const int kl = tid >> 2, key = kb * 64 + kl, c = (tid & 3) * 16;
-                v4i v = {0, 0, 0, 0};
-                if (key < nk) v = *(const v4i *)(a.vc + base + (size_t)key * 64 + c);
+            {  // V^T of the block into LDS; the next block's values load meanwhile
+                const int kl = tid >> 2, c = (tid & 3) * 16;
+                const v4i v = vnext;
+                if (b + 1 < AT_SB && kb + 1 < nkb) vnext = kv_load(a.vc, kb + 1);
                 const int8_t *bv = (const int8_t *)&v;
 #pragma unroll
                 for (int i = 0; i < 16; i++) sVt[(c + i) * AT_ST + kl] = bv[i];
