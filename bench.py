@@ -1,12 +1,12 @@
 #!/usr/bin/env python3
 """Fold throughput of the HardShell hot path on one MI355X.
 
-Workload (the north-star configuration): a GPT-2-small-shape integer model in .hsm layout
-(12 layers, d_model 768, 12 heads x 64, d_ff 3072, vocab 50,257, n_ctx 1,024) with seeded
-uniform int8 weights, folding a 16,384-token Zipf(1.1) stream as 64 independent 256-token
-windows (blocks of 1,024 bytes of fixed-width 4-byte tokens) batched on one GPU. One step is
-one whole fold: the integer forward pass of all 16,384 rows, the logits -> CDF coder op on the
-GPU, the host range coder, the block payloads and the .taco container.
+Default workload: a GPT-2-small-shape integer model in .hsm layout (12 layers, d_model 768,
+12 heads x 64, d_ff 3072, vocab 50,257, n_ctx 1,024) with seeded uniform int8 weights, folding
+a 16,384-token Zipf(1.1) stream as 64 independent 256-token windows (blocks of 1,024 bytes of
+fixed-width 4-byte tokens) batched on one GPU. One step is one whole fold: the integer forward
+pass of all 16,384 rows, the logits -> CDF coder op on the GPU, the host range coder, the block
+payloads and the .taco container.
 
 Prints one JSON line. `value` is fold tokens per second with the token stream and the model
 already resident (model upload and token staging are outside the timed region; per step the
@@ -15,9 +15,16 @@ MI355X dense int8 MFMA peak, from hipEvents around every launch in the timed ste
 `cpu_baseline` is the oracle's C++ restatement of the reference CPU fast path (AVX2 products,
 prefill chunk 32, one window per thread) timed on a sample of the same windows in the same run;
 its payloads must equal the GPU's.
+
+Other workloads (--workload) measure the other configurations of the path, each with its own
+line: the c_attn GEMM alone (gemm-qkv: M 256 and 16,384, K 768, N 2,304), decode attention over
+HBM-resident caches (attend-decode: 64 streams x 12 heads x 64, contexts 128 / 512 / 1,024),
+the GPT-2-medium fold with the full unfold round trip (fold-gpt2-medium: 256 x 256 tokens) and
+the GPT-2-XL fold (fold-gpt2-xl: 512 x 512 tokens).
 """
 
 import argparse
+import ctypes as C
 import hashlib
 import json
 import os
@@ -32,38 +39,44 @@ sys.path.insert(0, ROOT)
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
 HBM_PEAK_GBS = 8000.0
 
+FOLDS = {  # workload -> (dims name, windows, tokens per window, CPU-baseline windows per thread)
+    "fold-gpt2-small": ("GPT2_SMALL", 64, 256, 2),
+    "fold-gpt2-medium": ("GPT2_MEDIUM", 256, 256, 2),
+    "fold-gpt2-xl": ("GPT2_XL", 512, 512, 1),
+}
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--windows", type=int, default=64)
-    ap.add_argument("--window-tokens", type=int, default=256)
-    ap.add_argument("--cpu-windows", type=int, default=0,
-                    help="windows in the CPU-baseline sample (0: one per thread)")
-    ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="first copy this many MiB device to device (the known-size copy that "
-                         "scales FETCH_SIZE / WRITE_SIZE counters)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}): the fold shards by windows "
-              "with no exchange between GPUs, and this build measures the one-GPU share",
-              file=sys.stderr)
-        sys.exit(2)
+def read_profile(hip, batch):
+    cap = 32
+    labels = C.create_string_buffer(32 * cap)
+    ns = np.zeros(cap, np.uint64)
+    launches = np.zeros(cap, np.uint64)
+    ops = np.zeros(cap, np.uint64)
+    k = hip.lib().hs_batch_profile(batch.h, labels, ns.ctypes.data_as(C.c_void_p),
+                                   launches.ctypes.data_as(C.c_void_p),
+                                   ops.ctypes.data_as(C.c_void_p), cap, 1)
+    prof = {}
+    for i in range(k):
+        name = labels.raw[32 * i:32 * i + 32].split(b"\0")[0].decode()
+        prof[name] = dict(ns=int(ns[i]), launches=int(launches[i]), ops=int(ops[i]))
+    return prof
 
+
+def run_fold(args):
     from taco_amd import fold, hip, synth
-
+    dims_name, W, n, cpu_per_thread = FOLDS[args.workload]
+    if args.windows:
+        W = args.windows
+    if args.window_tokens:
+        n = args.window_tokens
+    dims = getattr(synth, dims_name)
     t0 = time.time()
-    dims = synth.GPT2_SMALL
+    log(f"building the {dims_name} model and {W} x {n} tokens")
     model_bytes = synth.build_model(dims)
-    W, n = args.windows, args.window_tokens
     tokens = synth.zipf_tokens(W * n)
     blocks = [tokens[w * n:(w + 1) * n] for w in range(W)]
     original = fold.token_bytes(tokens)
@@ -74,7 +87,6 @@ def main():
 
     dev = hip.HipDevice.open(0)
     if args.calib_copy_mib:
-        import ctypes as C
         nb = args.calib_copy_mib << 20
         src, dst = C.c_void_p(), C.c_void_p()
         hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(src)))
@@ -111,22 +123,11 @@ def main():
         payloads, cont = step()
     elapsed = time.perf_counter() - ts
     hip._check(hip.lib().hs_batch_set_profiling(batch.h, 0))
-    import ctypes as C
-    cap = 32
-    labels = C.create_string_buffer(32 * cap)
-    ns = np.zeros(cap, np.uint64)
-    launches = np.zeros(cap, np.uint64)
-    ops = np.zeros(cap, np.uint64)
-    k = hip.lib().hs_batch_profile(batch.h, labels, ns.ctypes.data_as(C.c_void_p),
-                                   launches.ctypes.data_as(C.c_void_p),
-                                   ops.ctypes.data_as(C.c_void_p), cap, 1)
-    prof = {}
-    for i in range(k):
-        name = labels.raw[32 * i:32 * i + 32].split(b"\0")[0].decode()
-        prof[name] = dict(ns=int(ns[i]), launches=int(launches[i]), ops=int(ops[i]))
-    gemm_ns = sum(v["ns"] for kk, v in prof.items() if kk.startswith("gemm"))
-    gemm_ops = sum(v["ops"] for kk, v in prof.items() if kk.startswith("gemm"))
-    gemm_launches = sum(v["launches"] for kk, v in prof.items() if kk.startswith("gemm"))
+    prof = read_profile(hip, batch)
+    gemm = [v for kk, v in prof.items() if kk.startswith("gemm")]
+    gemm_ns = sum(v["ns"] for v in gemm)
+    gemm_ops = sum(v["ops"] for v in gemm)
+    gemm_launches = sum(v["launches"] for v in gemm)
     achieved = gemm_ops / gemm_ns / 1e3 if gemm_ns else 0.0  # ops/ns -> TOPS
     tokens_per_step = W * n
     value = tokens_per_step * args.steps / elapsed
@@ -141,12 +142,25 @@ def main():
         log(f"  {kk:12s} {v['ns'] / 1e6 / args.steps:8.3f} ms/step  {v['launches'] // args.steps:5d} "
             f"launches/step" + (f"  {v['ops'] / v['ns'] / 1e3:7.1f} TOPS" if v["ops"] and v["ns"] else ""))
 
+    unfold = None
+    if args.workload == "fold-gpt2-medium" and not args.no_unfold:
+        # the full round trip: every block decoded on the GPU (one row per slot per call)
+        ts = time.perf_counter()
+        back = fold.unfold_blocks(batch, payloads, 0, cap=n)
+        u_s = time.perf_counter() - ts
+        same = all(np.array_equal(back[w], blocks[w]) for w in range(W))
+        log(f"unfold: {W} blocks in {u_s:.3f}s -> {W * n / u_s:.0f} tokens/s; round trip equal: {same}")
+        if not same:
+            log("ROUND TRIP FAILURE: the unfolded tokens differ")
+            sys.exit(1)
+        unfold = {"tokens_per_s": round(W * n / u_s, 1), "seconds": round(u_s, 3),
+                  "round_trip_equal": same}
+
     cpu = None
     if not args.no_cpu:
         from oracle import oracle as O
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        cw = args.cpu_windows or 2 * threads
-        cw = min(cw, W)
+        cw = min(args.cpu_windows or cpu_per_thread * threads, W)
         om = O.Model(model_bytes)
         ts = time.perf_counter()
         cpu_payloads = O.fold_payloads(om, tokens[:cw * n], cw, n, chunk=32, threads=threads)
@@ -159,12 +173,15 @@ def main():
             sys.exit(1)
         cpu = {"value": round(cw * n / cpu_s, 2), "unit": "tokens/s", "cores": threads,
                "kind": "port",
-               "sample": f"the first {cw} of the {W} windows ({cw * n} tokens), two windows per "
-                         f"thread, AVX2 restatement of the reference CPU fast path, chunk 32",
+               "sample": f"the first {cw} of the {W} windows ({cw * n} tokens), {cpu_per_thread} "
+                         f"window(s) per thread, AVX2 restatement of the reference CPU fast path, "
+                         f"chunk 32",
                "payloads_equal_gpu": same}
 
+    label = {"fold-gpt2-small": "GPT-2 124M", "fold-gpt2-medium": "GPT-2 medium 355M",
+             "fold-gpt2-xl": "GPT-2 XL 1.5B"}[args.workload]
     out = {
-        "metric": "fold tokens/sec on 1 MI355X (GPT-2 124M int8, bit-exact); int8 MFMA % of peak",
+        "metric": f"fold tokens/sec on 1 MI355X ({label} int8, bit-exact); int8 MFMA % of peak",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -176,7 +193,8 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": f"gpt2-small-shape fold: {W} windows x {n} Zipf(1.1) tokens",
+        "config": {"workload": f"{dims_name.lower().replace('_', '-')}-shape fold: {W} windows x "
+                               f"{n} Zipf(1.1) tokens",
                    "layers": dims.n_layer, "d_model": dims.d_model, "heads": dims.n_head,
                    "d_ff": dims.d_ff, "vocab": dims.vocab, "n_ctx": dims.n_ctx,
                    "tokens_per_step": tokens_per_step, "container_sha256": cont_sha,
@@ -190,7 +208,186 @@ def main():
         "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / args.steps, 3) for kk, v in prof.items()},
         "cpu_baseline": cpu,
     }
+    if unfold:
+        out["unfold"] = unfold
     print(json.dumps(out), flush=True)
+
+
+def _dev_buf(hip, dev, arr):
+    p = C.c_void_p()
+    hip._check(hip.lib().hs_device_alloc(dev.h, arr.nbytes, C.byref(p)))
+    hip._check(hip.lib().hs_device_upload(dev.h, p, arr.ctypes.data_as(C.c_void_p), arr.nbytes))
+    return p
+
+
+def run_gemm(args):
+    """The c_attn linear alone (i8 x i8 -> i32, bias, per-channel rescale, clamp to +-127):
+    K 768, N 2,304 at M 256 (one decode batch) and M 16,384 (the fold pass)."""
+    from oracle import oracle as O
+    from taco_amd import hip
+    dev = hip.HipDevice.open(0)
+    rng = np.random.default_rng(0xC1)
+    K, N, shift = 768, 2304, 42
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    bias = rng.integers(-(1 << 16), (1 << 16) + 1, N).astype(np.int32)
+    mult = rng.integers(1 << 30, 1 << 31, N).astype(np.int64).astype(np.int32)
+    results = []
+    for M, reps in ((256, 2000), (16384, 50)):
+        a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+        mp, np_, kp = hip.gemm_layout(M, N, K)
+        wp = np.zeros((np_, kp), np.int8)
+        wp[:N, :K] = w
+        ap = np.zeros((mp, kp), np.int8)
+        ap[:M, :K] = a
+        bufs = [_dev_buf(hip, dev, x) for x in (wp, ap, bias, mult)]
+        out = np.zeros((M, N), np.int8)
+        dout = _dev_buf(hip, dev, out)
+        ns = C.c_uint64()
+        hip._check(hip.lib().hs_op_gemm_requant_gpu_ns(dev.h, bufs[0], bufs[1], bufs[2], bufs[3],
+                                                         shift, M, N, K, dout, 10, C.byref(ns)))
+        hip._check(hip.lib().hs_op_gemm_requant_gpu_ns(dev.h, bufs[0], bufs[1], bufs[2], bufs[3],
+                                                         shift, M, N, K, dout, reps, C.byref(ns)))
+        hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                out.nbytes))
+        for p in bufs + [dout]:
+            hip.lib().hs_device_free(dev.h, p)
+        us = ns.value / reps / 1e3
+        ops = 2 * M * N * K
+        rows = min(M, 256)  # the oracle's rows (the first 256)
+        want = O.linear_act_ref(w, a[:rows], bias, mult, shift)
+        same = bool(np.array_equal(out[:rows], want))
+        ts = time.perf_counter()
+        O.matmul_i8(w, a[:rows])
+        cpu_s = time.perf_counter() - ts
+        log(f"gemm M {M}: {us:.2f} us per launch, {ops / us / 1e6:.1f} TOPS, "
+            f"rows 0..{rows - 1} equal to the oracle: {same}; CPU AVX2 product of {rows} rows "
+            f"{cpu_s * 1e3:.2f} ms")
+        if not same:
+            log("PARITY FAILURE")
+            sys.exit(1)
+        results.append(dict(M=M, us=round(us, 3), tops=round(ops / us / 1e6, 2),
+                            cpu_ms_256_rows=round(cpu_s * 1e3, 3), equal_to_oracle=same))
+    big = results[-1]
+    print(json.dumps({
+        "metric": "int8 c_attn GEMM with requantize epilogue on 1 MI355X (K 768, N 2304)",
+        "value": big["tops"], "unit": "TOPS", "n_gpus": 1, "steps": 50, "warmup": 10,
+        "ms_per_step": round(big["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "c_attn GEMM, A [M, 768] x W [2304, 768] i8, bias, rescale shift 42",
+                   "shapes": results},
+        "roofline": {"bound": "mfma", "kernel": "k_gemm<Act>", "achieved": big["tops"],
+                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": round(big["tops"] / INT8_PEAK_TOPS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(2 * 256 * N * K / (results[0]["cpu_ms_256_rows"] * 1e9), 4),
+                         "unit": "TOPS", "cores": 1, "kind": "port",
+                         "sample": "the oracle's AVX2 product of 256 rows (one thread)"},
+    }), flush=True)
+
+
+def run_attend(args):
+    """Decode attention, one query row per stream: 64 streams x 12 heads x 64 over caches of
+    ctx positions, rotating over cache sets that together exceed the 256 MB Infinity Cache."""
+    from oracle import oracle as O
+    from taco_amd import hip
+    dev = hip.HipDevice.open(0)
+    rng = np.random.default_rng(0xC3)
+    B, H, hd = 64, 12, 64
+    table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
+    score_m, score_s, out_m, out_s = 1_400_000_000, 34, 1_300_000_000, 53
+    dtab = _dev_buf(hip, dev, table)
+    rows = []
+    for ctx in (128, 512, 1024):
+        sets = max(3, (768 << 20) // (2 * B * H * ctx * hd))  # >= 768 MB of caches
+        q = rng.integers(-127, 128, (B, H, hd)).astype(np.int8)
+        ctxs = np.full(B, ctx, np.uint32)
+        dq, dctx = _dev_buf(hip, dev, q), _dev_buf(hip, dev, ctxs)
+        caches = []
+        for s in range(sets):
+            kc = rng.integers(-127, 128, (B, H, ctx, hd)).astype(np.int8)
+            vc = rng.integers(-127, 128, (B, H, ctx, hd)).astype(np.int8)
+            caches.append((kc, vc, _dev_buf(hip, dev, kc), _dev_buf(hip, dev, vc)))
+        out = np.zeros((B, H * hd), np.int8)
+        dout = _dev_buf(hip, dev, out)
+        total, reps = 0, 0
+        ns = C.c_uint64()
+        for r in range(2 * sets):  # one launch per set in turn: every launch reads cold caches
+            kc, vc, dk, dv = caches[r % sets]
+            hip._check(hip.lib().hs_op_attend_decode_gpu_ns(
+                dev.h, dq, dk, dv, dctx, B, H, hd, ctx, score_m, score_s, out_m, out_s, dtab,
+                len(table), 30, dout, 1, C.byref(ns)))
+            if r >= sets:  # the first round warms up
+                total += ns.value
+                reps += 1
+        hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                out.nbytes))
+        kc, vc = caches[(2 * sets - 1) % sets][:2]
+        ts = time.perf_counter()
+        want = O.attend_decode_ref(q, kc, vc, ctxs, score_m, score_s, out_m, out_s, table, 30)
+        cpu_s = time.perf_counter() - ts
+        same = bool(np.array_equal(out, want))
+        us = total / reps / 1e3
+        nbytes = 2 * B * H * ctx * hd + 2 * B * H * hd
+        gbs = nbytes / us / 1e3
+        log(f"attend ctx {ctx}: {us:.2f} us per launch over {sets} cache sets, {gbs:.0f} GB/s, "
+            f"equal to the oracle: {same}; oracle {cpu_s * 1e3:.1f} ms")
+        if not same:
+            log("PARITY FAILURE")
+            sys.exit(1)
+        rows.append(dict(ctx=ctx, us=round(us, 3), gbs=round(gbs, 1), bytes=nbytes,
+                         cache_sets=sets, cpu_ms=round(cpu_s * 1e3, 2), equal_to_oracle=same))
+        for _, _, dk, dv in caches:
+            hip.lib().hs_device_free(dev.h, dk)
+            hip.lib().hs_device_free(dev.h, dv)
+        for p in (dq, dctx, dout):
+            hip.lib().hs_device_free(dev.h, p)
+    hip.lib().hs_device_free(dev.h, dtab)
+    big = rows[-1]
+    print(json.dumps({
+        "metric": "integer decode attention over an HBM KV cache on 1 MI355X (64 x 12 x 64)",
+        "value": big["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": rows[-1]["cache_sets"],
+        "warmup": rows[-1]["cache_sets"], "ms_per_step": round(big["us"] / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "decode attention, 64 streams x 12 heads x 64, ctx sweep",
+                   "contexts": rows},
+        "roofline": {"bound": "hbm", "kernel": "k_attend", "achieved": big["gbs"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(big["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": {"value": round(big["bytes"] / (big["cpu_ms"] * 1e6), 3), "unit": "GB/s",
+                         "cores": 1, "kind": "port",
+                         "sample": "the oracle's scalar decode attention of one cache set"},
+    }), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="fold-gpt2-small",
+                    choices=sorted(FOLDS) + ["gemm-qkv", "attend-decode"])
+    ap.add_argument("--windows", type=int, default=0)
+    ap.add_argument("--window-tokens", type=int, default=0)
+    ap.add_argument("--cpu-windows", type=int, default=0,
+                    help="windows in the CPU-baseline sample (0: the workload's default)")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-unfold", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first copy this many MiB device to device (the known-size copy that "
+                         "scales FETCH_SIZE / WRITE_SIZE counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}): the fold shards by windows "
+              "with no exchange between GPUs, and this build measures the one-GPU share",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.workload in FOLDS:
+        run_fold(args)
+    elif args.workload == "gemm-qkv":
+        run_gemm(args)
+    else:
+        run_attend(args)
 
 
 if __name__ == "__main__":

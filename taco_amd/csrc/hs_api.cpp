@@ -1096,9 +1096,13 @@ extern "C" hs_status hs_op_gemm_requant_gpu_ns(hs_device *dev, const int8_t *w, 
     if (m == 0 || n == 0 || k == 0 || k > 65536) return hs::fail(HS_UNSUPPORTED, 0, "bad GEMM shape");
     size_t kp;
     hs_op_gemm_layout(m, n, k, nullptr, nullptr, &kp);
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    std::vector<int32_t> hb(n);  // the bias bound of the fast epilogue, as the forward pass has it
+    HIP_TRY(hipMemcpy(hb.data(), bias, n * sizeof(int32_t), hipMemcpyDeviceToHost));
     hs::GemmArgs g;
     g.a = a; g.w = w; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
     g.bias = bias; g.mult = mult; g.shift = shift; g.out = out; g.ldo = (int)n;
+    g.fast32 = fits_i32(k, hb.data(), n);
     return time_reps(dev, reps, ns, [&] { return hs::launch_gemm(Epi::Act, g, dev->stream); });
 }
 
