@@ -398,6 +398,8 @@ struct hs_batch {
     uint32_t *h_queries = nullptr;
     uint64_t *h_intervals = nullptr;
     bool inflight = false;  // a pass returned with copies or kernels still queued on `st`
+    void *split = nullptr;  // scratch of the split decode attention (grown on demand)
+    size_t split_bytes = 0;
     int8_t *d_a = nullptr, *d_qkv = nullptr, *d_att = nullptr, *d_g = nullptr, *d_af = nullptr;
     int64_t *d_logits = nullptr;
     uint16_t *d_d16 = nullptr;
@@ -429,6 +431,7 @@ struct hs_batch {
         if (st) (void)hipStreamSynchronize(st);
         for (void *p : {(void *)h_rows, (void *)h_groups, (void *)h_src, (void *)h_queries, (void *)h_intervals})
             if (p) (void)hipHostFree(p);
+        if (split) (void)hipFree(split);
         if (st) (void)hipStreamDestroy(st);
     }
     hipError_t event(hipEvent_t &e) {
@@ -706,6 +709,31 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
     };
     const bool kv_fused = m.hd % 16 == 0 && m.d % 16 == 0;
+    // Decode-shaped passes (short runs): attention split over key chunks when the scratch fits
+    // (at most 1 GiB), else the row kernel.
+    bool split_attn = false;
+    hs::SplitPlan split_plan;
+    if (!mfma_attn && hs::attend_split_ok(m.hd)) {
+        int max_keys = 1;
+        for (int r = 0; r < n; r++) max_keys = std::max<int>(max_keys, (int)rows[r].pos + 1);
+        split_plan = hs::attend_split_plan(n, m.H, max_keys);
+        hs::AttnArgs probe;
+        probe.n_head = m.H; probe.hd = m.hd; probe.ctx_cap = m.C;
+        const size_t need = hs::attend_split_bytes(probe, n, split_plan);
+        if (need <= (1ull << 30)) {
+            if (need > b.split_bytes) {
+                if (b.split) {
+                    HIP_TRY(hipStreamSynchronize(st));
+                    HIP_TRY(hipFree(b.split));
+                    b.split = nullptr;
+                    b.split_bytes = 0;
+                }
+                HIP_TRY(hipMalloc(&b.split, need));
+                b.split_bytes = need;
+            }
+            split_attn = true;
+        }
+    }
     for (int l = 0; l < m.L; l++) {
         const DevBlock &blk = m.blocks[l];
         HIP_TRY(ln(blk.ln1, nullptr, n, b.d_a));
@@ -731,8 +759,9 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
         at.out = b.d_att; at.ldo = m.d_pad;
         HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d, [&] {
-            return mfma_attn ? hs::launch_attend_groups(at, b.d_groups, n_groups, st)
-                             : hs::launch_attend(at, n, st);
+            if (mfma_attn) return hs::launch_attend_groups(at, b.d_groups, n_groups, st);
+            if (split_attn) return hs::launch_attend_split(at, n, split_plan, b.split, st);
+            return hs::launch_attend(at, n, st);
         }));
         HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
         HIP_TRY(ln(blk.ln2, nullptr, n, b.d_a));
@@ -1019,7 +1048,19 @@ extern "C" hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, co
     at.n_head = (int)h; at.hd = (int)hd; at.ctx_cap = (int)ctx_cap; at.score_m = score_m;
     at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
     at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
-    HIP_TRY(hs::launch_attend(at, (int)b, stream ? (hipStream_t)stream : dev->stream));
+    hipStream_t st = stream ? (hipStream_t)stream : dev->stream;
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    if (hs::attend_split_ok((int)hd)) {  // split over key chunks, scratch ordered on the stream
+        const hs::SplitPlan plan = hs::attend_split_plan((int)b, (int)h, (int)ctx_cap);
+        void *scratch = nullptr;
+        HIP_TRY(hipMallocAsync(&scratch, hs::attend_split_bytes(at, (int)b, plan), st));
+        const hipError_t e = hs::launch_attend_split(at, (int)b, plan, scratch, st);
+        const hipError_t f = hipFreeAsync(scratch, st);
+        HIP_TRY(e);
+        HIP_TRY(f);
+        return HS_OK;
+    }
+    HIP_TRY(hs::launch_attend(at, (int)b, st));
     return HS_OK;
 }
 
@@ -1122,6 +1163,17 @@ extern "C" hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q,
     at.n_head = (int)h; at.hd = (int)hd; at.ctx_cap = (int)ctx_cap; at.score_m = score_m;
     at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
     at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    if (hs::attend_split_ok((int)hd)) {
+        const hs::SplitPlan plan = hs::attend_split_plan((int)b, (int)h, (int)ctx_cap);
+        void *scratch = nullptr;
+        HIP_TRY(hipMalloc(&scratch, hs::attend_split_bytes(at, (int)b, plan)));
+        const hs_status st = time_reps(dev, reps, ns, [&] {
+            return hs::launch_attend_split(at, (int)b, plan, scratch, dev->stream);
+        });
+        (void)hipFree(scratch);
+        return st;
+    }
     return time_reps(dev, reps, ns, [&] { return hs::launch_attend(at, (int)b, dev->stream); });
 }
 

@@ -100,6 +100,18 @@ struct AttnArgs {
 };
 hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream);
 
+// Decode attention split over key chunks (head_dim 16, 32, 64, 128 or 256): four launches over
+// (row, head, chunk) with exact integer partials in `scratch` (attend_split_bytes bytes, 256-byte
+// aligned). `max_keys` bounds every row's key count.
+struct SplitPlan {
+    int chunks = 1, chunk_keys = 64;
+};
+inline bool attend_split_ok(int hd) { return hd >= 16 && hd <= 256 && (hd & (hd - 1)) == 0; }
+SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys);
+size_t attend_split_bytes(const AttnArgs &a, int n_rows, const SplitPlan &p);
+hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p, void *scratch,
+                               hipStream_t stream);
+
 // Prefill attention on MFMA for head_dim 64: a group is up to 64 consecutive rows of one slot
 // at consecutive positions (rows first .. first + count - 1 at positions pos0 ..).
 struct AttnGroup {

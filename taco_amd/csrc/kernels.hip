@@ -672,6 +672,231 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
 }
 
 // =============================================================================================
+// Decode attention split over key chunks, for few rows over long contexts (the row kernel above
+// has only rows x heads waves). The same integer steps as reference.rs:254-283, over
+// (row, head, chunk) waves in four launches:
+//   1. the dots q . k of the chunk's keys (kept) and the chunk's smallest and largest dot;
+//   2. the row max M (the score is monotone in the dot: the largest score is the score of the
+//      largest or of the smallest dot over all chunks) and the chunk's sum of the table entries
+//      e = table[min(M - s, last)];
+//   3. S = the sum over chunks, p = floor(e 2^P / S) from the kept dots again and the chunk's sum
+//      of p v per channel in i64 (hd / 16 lanes x 16 channels per key, 16-byte loads of V);
+//   4. the sum of the chunk partials and the output rescale.
+// Integer sums are exact in any order, so the result is the reference's.
+// =============================================================================================
+
+// score = clamp(rescale(dot, m, s), +-2^40): |dot| <= hd 2^14 <= 2^22, so |dot m| < 2^53 and one
+// multiply-add and an arithmetic shift are exact (a shift of 63 or more gives 0). With s >= 13
+// the score stays within +-2^40 and the clamp is a no-op.
+__host__ __device__ inline bool attn_noclamp(const AttnArgs &a) { return a.score_s >= 13; }
+
+template <bool NOCLAMP>
+__device__ __forceinline__ int64_t attn_score(const AttnArgs &a, int32_t dot) {
+    const int s_eff = a.score_s < 63 ? a.score_s : 63;
+    const int64_t s_half = s_eff ? (int64_t)1 << (s_eff - 1) : 0;
+    const int64_t r = ((int64_t)dot * a.score_m + s_half) >> s_eff;
+    return NOCLAMP ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
+}
+
+struct SplitScratch {
+    int32_t *dots, *mm;
+    uint64_t *ps;
+    int64_t *part;
+};
+
+__device__ __forceinline__ SplitScratch split_scratch(void *base, int n_rows, int H, int cap, int chunks, int hd) {
+    SplitScratch s;
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    char *p = (char *)base;
+    const size_t rh = (size_t)n_rows * H;
+    s.dots = (int32_t *)p;
+    p += al(rh * cap * 4);
+    s.mm = (int32_t *)p;
+    p += al(rh * chunks * 8);
+    s.ps = (uint64_t *)p;
+    p += al(rh * chunks * 8);
+    s.part = (int64_t *)p;
+    return s;
+}
+
+__device__ __forceinline__ int split_keys(const AttnArgs &a, int r) {
+    int keys = a.keys ? (int)a.keys[r] : a.rows[r].pos + 1;
+    return keys < 1 ? 1 : (keys > a.ctx_cap ? a.ctx_cap : keys);
+}
+
+__device__ __forceinline__ int split_slot(const AttnArgs &a, int r) { return a.rows ? a.rows[r].slot : r; }
+
+// The row maximum of the scores, from every chunk's extreme dots (the score is monotone in the dot).
+template <bool NOCLAMP>
+__device__ __forceinline__ int64_t split_max(const AttnArgs &a, const SplitScratch &S, const SplitPlan &pl,
+                                             int rh, int nch) {
+    int64_t M = INT64_MIN;
+    for (int cc = 0; cc < nch; cc++) {
+        const int32_t mn = S.mm[((size_t)rh * pl.chunks + cc) * 2], mx = S.mm[((size_t)rh * pl.chunks + cc) * 2 + 1];
+        const int64_t s0 = attn_score<NOCLAMP>(a, mn), s1 = attn_score<NOCLAMP>(a, mx);
+        M = s0 > M ? s0 : M;
+        M = s1 > M ? s1 : M;
+    }
+    return M;
+}
+
+__global__ __launch_bounds__(64) void k_split_dots(AttnArgs a, int n_rows, SplitPlan pl, void *scratch) {
+    __shared__ __attribute__((aligned(16))) int s_q[64];  // hd <= 256 bytes
+    const int rh = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const int r = rh / a.n_head, h = rh - r * a.n_head, hd = a.hd;
+    const SplitScratch S = split_scratch(scratch, n_rows, a.n_head, a.ctx_cap, pl.chunks, hd);
+    const int keys = split_keys(a, r), k0 = c * pl.chunk_keys;
+    const int k1 = k0 + pl.chunk_keys < keys ? k0 + pl.chunk_keys : keys;
+    if (lane < hd / 4) s_q[lane] = ((const int *)(a.q + (size_t)r * a.ldq + h * hd))[lane];
+    __syncthreads();
+    const int8_t *K = a.kc + ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * hd;
+    int32_t dmin = INT32_MAX, dmax = INT32_MIN;
+    for (int k = k0 + lane; k < k1; k += 64) {
+        int32_t d = 0;
+        const v4i *k16 = (const v4i *)(K + (size_t)k * hd);
+        for (int t = 0; t < hd / 16; t++) {
+            const v4i kk = k16[t];
+            d = __builtin_amdgcn_sdot4(s_q[4 * t], kk[0], d, false);
+            d = __builtin_amdgcn_sdot4(s_q[4 * t + 1], kk[1], d, false);
+            d = __builtin_amdgcn_sdot4(s_q[4 * t + 2], kk[2], d, false);
+            d = __builtin_amdgcn_sdot4(s_q[4 * t + 3], kk[3], d, false);
+        }
+        S.dots[(size_t)rh * a.ctx_cap + k] = d;
+        dmin = d < dmin ? d : dmin;
+        dmax = d > dmax ? d : dmax;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int32_t u = __shfl_xor(dmin, o, 64), v = __shfl_xor(dmax, o, 64);
+        dmin = u < dmin ? u : dmin;
+        dmax = v > dmax ? v : dmax;
+    }
+    if (lane == 0) {  // an empty chunk keeps (min, max) = (INT32_MAX, INT32_MIN)
+        S.mm[((size_t)rh * pl.chunks + c) * 2] = dmin;
+        S.mm[((size_t)rh * pl.chunks + c) * 2 + 1] = dmax;
+    }
+}
+
+template <bool NOCLAMP>
+__global__ __launch_bounds__(64) void k_split_sum(AttnArgs a, int n_rows, SplitPlan pl, void *scratch) {
+    const int rh = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const int r = rh / a.n_head;
+    const SplitScratch S = split_scratch(scratch, n_rows, a.n_head, a.ctx_cap, pl.chunks, a.hd);
+    const int keys = split_keys(a, r), k0 = c * pl.chunk_keys;
+    const int k1 = k0 + pl.chunk_keys < keys ? k0 + pl.chunk_keys : keys;
+    const int64_t M = split_max<NOCLAMP>(a, S, pl, rh, (keys + pl.chunk_keys - 1) / pl.chunk_keys);
+    const int64_t last = a.exp_len - 1;
+    uint64_t sum = 0;
+    for (int k = k0 + lane; k < k1; k += 64) {
+        const int64_t dd = M - attn_score<NOCLAMP>(a, S.dots[(size_t)rh * a.ctx_cap + k]);
+        sum += (uint64_t)a.exp_table[dd < last ? dd : last];
+    }
+    sum = (uint64_t)wave_sum64((int64_t)sum);
+    if (lane == 0) S.ps[(size_t)rh * pl.chunks + c] = sum;
+}
+
+template <bool NOCLAMP>
+__global__ __launch_bounds__(64) void k_split_pv(AttnArgs a, int n_rows, SplitPlan pl, void *scratch) {
+    extern __shared__ uint32_t s_p[];  // chunk_keys entries
+    const int rh = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const int r = rh / a.n_head, h = rh - r * a.n_head, hd = a.hd;
+    const SplitScratch S = split_scratch(scratch, n_rows, a.n_head, a.ctx_cap, pl.chunks, hd);
+    const int keys = split_keys(a, r), k0 = c * pl.chunk_keys;
+    const int k1 = k0 + pl.chunk_keys < keys ? k0 + pl.chunk_keys : keys;
+    if (k0 >= k1) {  // an empty chunk contributes nothing
+        for (int i = lane; i < hd; i += 64) S.part[((size_t)rh * pl.chunks + c) * hd + i] = 0;
+        return;
+    }
+    const int nch = (keys + pl.chunk_keys - 1) / pl.chunk_keys;
+    const int64_t M = split_max<NOCLAMP>(a, S, pl, rh, nch);
+    uint64_t sum = 0;
+    for (int cc = 0; cc < nch; cc++) sum += S.ps[(size_t)rh * pl.chunks + cc];
+    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+    const int64_t last = a.exp_len - 1;
+    for (int k = k0 + lane; k < k1; k += 64) {
+        const int64_t dd = M - attn_score<NOCLAMP>(a, S.dots[(size_t)rh * a.ctx_cap + k]);
+        const uint64_t num = (uint64_t)a.exp_table[dd < last ? dd : last] << a.softmax_p;
+        uint64_t q = num;
+        if (sum >= 2) {
+            q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
+            if (num - q * sum >= sum) q++;
+        }
+        s_p[k - k0] = (uint32_t)q;  // <= 2^P <= 2^30
+    }
+    __syncthreads();
+    // lane l: channels 16 (l % G) .. +16 of rows k0 + l / G, k0 + l / G + 64 / G, ... (G = hd / 16,
+    // a power of two, so the lanes of one channel group differ exactly in the bits >= G)
+    const int G = hd / 16, R = 64 / G;
+    int64_t acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0;
+    const int8_t *V = a.vc + ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * hd;
+    for (int k = k0 + lane / G; k < k1; k += R) {
+        const int64_t p = s_p[k - k0];
+        const v4i raw = *(const v4i *)(V + (size_t)k * hd + (lane % G) * 16);
+        const int8_t *v = (const int8_t *)&raw;
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] += p * v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        for (int o = G; o < 64; o <<= 1) acc[i] += __shfl_xor(acc[i], o, 64);
+    if (lane < G) {
+        int64_t *dst = S.part + ((size_t)rh * pl.chunks + c) * hd + lane * 16;
+#pragma unroll
+        for (int i = 0; i < 16; i++) dst[i] = acc[i];
+    }
+}
+
+__global__ void k_split_out(AttnArgs a, int n_rows, SplitPlan pl, void *scratch) {
+    const int rh = blockIdx.x, t = threadIdx.x;
+    const int r = rh / a.n_head, h = rh - r * a.n_head, hd = a.hd;
+    if (t >= hd) return;
+    const SplitScratch S = split_scratch(scratch, n_rows, a.n_head, a.ctx_cap, pl.chunks, hd);
+    const int keys = split_keys(a, r), nch = (keys + pl.chunk_keys - 1) / pl.chunk_keys;
+    int64_t o = 0;
+    for (int cc = 0; cc < nch; cc++) o += S.part[((size_t)rh * pl.chunks + cc) * hd + t];
+    a.out[(size_t)r * a.ldo + h * hd + t] = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
+}
+
+SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys) {
+    // about 4096 waves over (row, head, chunk), chunks of a multiple of 64 keys
+    SplitPlan p;
+    const long long rh = (long long)n_rows * n_head;
+    const int blocks64 = (max_keys + 63) / 64;
+    int want = (int)((4096 + rh - 1) / (rh > 0 ? rh : 1));
+    want = want < 1 ? 1 : (want > blocks64 ? blocks64 : want);
+    p.chunk_keys = 64 * ((blocks64 + want - 1) / want);
+    p.chunk_keys = p.chunk_keys > 4096 ? 4096 : p.chunk_keys;  // the p values of a chunk in LDS
+    p.chunks = (max_keys + p.chunk_keys - 1) / p.chunk_keys;
+    return p;
+}
+
+size_t attend_split_bytes(const AttnArgs &a, int n_rows, const SplitPlan &p) {
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    const size_t rh = (size_t)n_rows * a.n_head;
+    return al(rh * a.ctx_cap * 4) + 2 * al(rh * p.chunks * 8) + al(rh * p.chunks * a.hd * 8);
+}
+
+hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p, void *scratch,
+                               hipStream_t stream) {
+    if (n_rows <= 0) return hipSuccess;
+    if (!attend_split_ok(a.hd) || p.chunk_keys % 64 != 0 || p.chunk_keys > 4096) return hipErrorInvalidValue;
+    const dim3 grid(n_rows * a.n_head, p.chunks);
+    const size_t lds = p.chunk_keys * sizeof(uint32_t);
+    hipLaunchKernelGGL(k_split_dots, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
+    if (attn_noclamp(a)) {
+        hipLaunchKernelGGL(k_split_sum<true>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
+        hipLaunchKernelGGL(k_split_pv<true>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);
+    } else {
+        hipLaunchKernelGGL(k_split_sum<false>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
+        hipLaunchKernelGGL(k_split_pv<false>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);
+    }
+    hipLaunchKernelGGL(k_split_out, dim3(n_rows * a.n_head), dim3(a.hd), 0, stream, a, n_rows, p, scratch);
+    return hipGetLastError();
+}
+
+// =============================================================================================
 // Prefill attention on MFMA (head_dim 64). One workgroup = one group of <= 64 rows x one head;
 // wave w owns rows 16w .. 16w + 15. S = Q K^T comes from v_mfma_i32_16x16x64_i8 (exact i32) for
 // a super-block of up to AT_SB key blocks of 64, held in registers: with <= 256 keys the
