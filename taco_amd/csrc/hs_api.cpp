@@ -87,7 +87,19 @@ struct DevLinear {
     int32_t *b = nullptr, *m = nullptr;
     int s = 0, n = 0, k = 0, n_pad = 0, k_pad = 0;
     int fast32 = 0;  // k * 2^14 + max|b| < 2^31: every acc + b fits i32
+    int32_t *wsum = nullptr;  // sum_k w[n][k], for an i16 input as planes (|wsum| <= 2^23)
 };
+
+// The row sums of w [n, k] (i8), exact in i32 (|sum| <= k 2^7 <= 2^23).
+std::vector<int32_t> row_sums(const int8_t *w, size_t n, size_t k, size_t n_pad) {
+    std::vector<int32_t> s(n_pad, 0);
+    for (size_t r = 0; r < n; r++) {
+        int32_t t = 0;
+        for (size_t c = 0; c < k; c++) t += w[r * k + c];
+        s[r] = t;
+    }
+    return s;
+}
 
 // |acc| <= k * 128 * 128 for i8 operands, so acc + b fits i32 when k * 2^14 + max|b| < 2^31.
 int fits_i32(size_t k, const int32_t *b, size_t n) {
@@ -110,6 +122,7 @@ struct DevBlock {
     int32_t score_m = 0, out_m = 0;
     int score_s = 0, out_s = 0;
     int8_t *gelu = nullptr;
+    int16_t *gelu16 = nullptr;  // an i16 table (version 2): c_fc writes planes, mlp_proj reads them
     int gelu_off = 0;
 };
 
@@ -122,6 +135,8 @@ struct hs_model {
     int d = 0, f = 0, V = 0, C = 0, H = 0, hd = 0, L = 0;
     int d_pad = 0, f_pad = 0, V_pad = 0;
     int8_t *wte = nullptr;  // [V_pad, d_pad]: the LM head operand; the embedding reads row tok
+    int32_t *wte_sum = nullptr;  // row sums of wte, for a 16-bit ln_f (version 2)
+    bool wide_ln_f = false, wide_gelu = false;
     int8_t *wpe = nullptr;  // [C, d]
     int32_t *embed_m = nullptr, *logit_m = nullptr, *pos_m = nullptr;
     std::vector<DevBlock> blocks;
@@ -229,8 +244,6 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
     hs::ModelError err{};
     if (!hs::load_host_model(bytes, len, m->host, err)) return hs::fail(HS_MODEL_ERROR, err.kind, err.msg);
     const hs::HostModel &h = m->host;
-    if (h.is_wide())
-        return hs::fail(HS_UNSUPPORTED, 0, "model-file version 2 rules (i16 activations, ln_beta_frac) are not implemented by the gfx950 backend yet");
     if (h.head_dim % 4 != 0 || h.head_dim > 256)
         return hs::fail(HS_UNSUPPORTED, 0, "head_dim must be a multiple of 4 and at most 256");
     HIP_TRY(hipSetDevice(dev->ordinal));
@@ -246,6 +259,11 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
         std::vector<int8_t> w((size_t)m->V_pad * m->d_pad, 0);
         for (int v = 0; v < m->V; v++) std::memcpy(&w[(size_t)v * m->d_pad], h.wte + (size_t)v * m->d, m->d);
         if ((st = mem.upload(m->wte, w.data(), w.size())) != HS_OK) return st;
+    }
+    m->wide_ln_f = h.ln_f_bits == 16;
+    if (m->wide_ln_f) {
+        const std::vector<int32_t> ws = row_sums(h.wte, m->V, m->d, m->V_pad);
+        if ((st = mem.upload(m->wte_sum, ws.data(), ws.size())) != HS_OK) return st;
     }
     if ((st = mem.upload(m->wpe, h.wpe, (size_t)m->C * m->d)) != HS_OK) return st;
     if ((st = mem.upload(m->embed_m, h.embed_m.data(), h.embed_m.size())) != HS_OK) return st;
@@ -263,7 +281,14 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
         if ((st = upload_linear(mem, hb.mlp_proj, b.mlp_proj)) != HS_OK) return st;
         b.score_m = hb.score_m; b.score_s = hb.score_s;
         b.out_m = hb.out_m; b.out_s = hb.out_s;
-        if ((st = mem.upload(b.gelu, hb.gelu8.data(), hb.gelu8.size())) != HS_OK) return st;
+        if (hb.gelu_wide) {
+            m->wide_gelu = true;
+            if ((st = mem.upload(b.gelu16, hb.gelu16.data(), hb.gelu16.size())) != HS_OK) return st;
+            const std::vector<int32_t> ws = row_sums(hb.mlp_proj.w, hb.mlp_proj.rows, hb.mlp_proj.cols, b.mlp_proj.n_pad);
+            if ((st = mem.upload(b.mlp_proj.wsum, ws.data(), ws.size())) != HS_OK) return st;
+        } else if ((st = mem.upload(b.gelu, hb.gelu8.data(), hb.gelu8.size())) != HS_OK) {
+            return st;
+        }
         b.gelu_off = (int)hb.gelu_len / 2;
     }
     if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
@@ -511,10 +536,11 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     if ((s = mem.alloc(b->d_groups, R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_x, R * m.d)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_a, RP * m.d_pad)) != HS_OK) return s;
-    if ((s = mem.alloc(b->d_af, RP * m.d_pad)) != HS_OK) return s;
+    // an i16 activation row is two operand rows (its planes)
+    if ((s = mem.alloc(b->d_af, (m.wide_ln_f ? 2 : 1) * RP * m.d_pad)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_qkv, R * 3 * m.d)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_att, RP * m.d_pad)) != HS_OK) return s;
-    if ((s = mem.alloc(b->d_g, RP * m.f_pad)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_g, (m.wide_gelu ? 2 : 1) * RP * m.f_pad)) != HS_OK) return s;
     if (m.compact) {
         if ((s = mem.alloc(b->d_d16, b->chunk_rows * m.ld16)) != HS_OK) return s;
         if ((s = mem.alloc(b->d_tmax, b->chunk_rows * m.ntiles)) != HS_OK) return s;
@@ -691,20 +717,22 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         return hs::launch_embed(b.d_rows, n, m.wte, m.d_pad, m.wpe, m.embed_m, m.host.embed_s,
                                 m.pos_m, m.host.pos_s, m.d, b.d_x, st);
     }));
-    auto ln = [&](const DevLn &l, const int32_t *src_rows, int rows_n, int8_t *dst) {
+    auto ln = [&](const DevLn &l, const int32_t *src_rows, int rows_n, int8_t *dst, int out_bits = 8) {
         hs::LnArgs a;
+        a.bits = out_bits;
         a.x = b.d_x; a.d = m.d; a.gamma = l.g; a.beta = l.b; a.m = l.m; a.s = l.s;
         a.beta_frac = m.host.ln_beta_frac; a.k = m.host.ln_k; a.j = m.host.ln_j; a.eps = m.host.ln_eps;
         a.out = dst; a.ldo = m.d_pad; a.src = src_rows; a.gm = l.gm;
         return b.launch("layer_norm", 0, [&] { return hs::launch_layernorm(a, rows_n, st); });
     };
     auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int rows_n,
-                    void *o, int ldo, const int8_t *gelu = nullptr, int gelu_off = 0) {
+                    void *o, int ldo, const int8_t *gelu = nullptr, int gelu_off = 0,
+                    const int16_t *gelu16 = nullptr) {
         hs::GemmArgs g;
         g.a = a; g.w = lin.w; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
-        g.fast32 = lin.fast32;
-        g.gelu = gelu; g.gelu_off = gelu_off;
+        g.fast32 = epi == Epi::ResidualWide ? 0 : lin.fast32;
+        g.gelu = gelu; g.gelu16 = gelu16; g.gelu_off = gelu_off; g.wsum = lin.wsum;
         const uint64_t ops = 2ull * (uint64_t)rows_n * (uint64_t)lin.n * (uint64_t)lin.k;
         return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
     };
@@ -765,8 +793,14 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         }));
         HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
         HIP_TRY(ln(blk.ln2, nullptr, n, b.d_a));
-        HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
-        HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
+        if (blk.gelu16) {  // i16 GELU outputs as planes, mlp_proj over 2n operand rows
+            HIP_TRY(gemm("gemm_fc", Epi::GeluWide, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, nullptr, blk.gelu_off,
+                         blk.gelu16));
+            HIP_TRY(gemm("gemm_mlp", Epi::ResidualWide, blk.mlp_proj, b.d_g, 2 * n, b.d_x, m.d));
+        } else {
+            HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
+            HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
+        }
     }
     if (n_out == 0) {
         b.inflight = true;
@@ -777,21 +811,25 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         }
         return HS_OK;
     }
-    HIP_TRY(ln(m.ln_f, b.d_src, n_out, b.d_af));
+    // a 16-bit ln_f (version 2) writes two operand rows (planes) per output row
+    const int pr = m.wide_ln_f ? 2 : 1;
+    HIP_TRY(ln(m.ln_f, b.d_src, n_out, b.d_af, m.wide_ln_f ? 16 : 8));
     DevLinear head;
     head.w = m.wte; head.m = m.logit_m; head.s = m.host.logit_s; head.n = m.V; head.k = m.d;
-    head.n_pad = m.V_pad; head.k_pad = m.d_pad;
+    head.n_pad = m.V_pad; head.k_pad = m.d_pad; head.wsum = m.wte_sum;
     const size_t per_row = out == Out::Weights ? (size_t)m.V : 3;
     std::vector<uint64_t> host(out == Out::Weights ? (size_t)n_out * per_row : 0);
     for (int c0 = 0; c0 < n_out; c0 += (int)b.chunk_rows) {
         const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
         if (m.compact) {
             hs::GemmArgs g;
-            g.a = b.d_af + (size_t)c0 * m.d_pad; g.w = m.wte; g.m = cn; g.n = m.V; g.k_pad = m.d_pad;
+            g.a = b.d_af + (size_t)pr * c0 * m.d_pad; g.w = m.wte; g.m = pr * cn; g.n = m.V; g.k_pad = m.d_pad;
             g.mult = m.logit_m; g.shift = m.host.logit_s; g.out = b.d_d16; g.ldo = m.ld16;
             g.tmax = b.d_tmax; g.tmax_ld = m.ntiles; g.cap16 = (int)m.host.logits_exp.size() - 1;
-            const uint64_t ops = 2ull * (uint64_t)cn * (uint64_t)m.V * (uint64_t)m.d;
-            HIP_TRY(b.launch("gemm_logits", ops, [&] { return hs::launch_gemm(Epi::LogitsCompact, g, st); }));
+            g.wsum = m.wte_sum;
+            const uint64_t ops = 2ull * (uint64_t)pr * cn * (uint64_t)m.V * (uint64_t)m.d;
+            const Epi epi = m.wide_ln_f ? Epi::LogitsCompactWide : Epi::LogitsCompact;
+            HIP_TRY(b.launch("gemm_logits", ops, [&] { return hs::launch_gemm(epi, g, st); }));
             hs::CompactCoderArgs ca;
             ca.d16 = b.d_d16; ca.ld16 = m.ld16; ca.tmax = b.d_tmax; ca.ntiles = m.ntiles; ca.vocab = m.V;
             ca.table = m.logits_exp; ca.table_len = (int)m.host.logits_exp.size(); ca.d0 = m.d0;
@@ -802,7 +840,8 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             ca.weights = out == Out::Weights ? b.d_weights : nullptr;
             HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder_compact(ca, cn, st); }));
         } else {
-            HIP_TRY(gemm("gemm_logits", Epi::Logits, head, b.d_af + (size_t)c0 * m.d_pad, cn, b.d_logits, m.V));
+            HIP_TRY(gemm("gemm_logits", m.wide_ln_f ? Epi::LogitsWide : Epi::Logits, head,
+                         b.d_af + (size_t)pr * c0 * m.d_pad, pr * cn, b.d_logits, m.V));
             hs::CoderArgs ca;
             ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
             ca.table_len = (int)m.host.logits_exp.size();

@@ -14,7 +14,16 @@ struct RowInfo {
     int32_t slot, token, pos, out;
 };
 
-enum class Epi : int { Raw = 0, Act = 1, Residual = 2, Gelu = 3, Logits = 4, LogitsCompact = 5 };
+enum class Epi : int {
+    Raw = 0, Act = 1, Residual = 2, Gelu = 3, Logits = 4, LogitsCompact = 5,
+    // Model-file version 2 (i16 activations, crates/hardshell/src/gpt2/ops.rs:178-206,246-277).
+    // An i16 activation v is stored as two i8 planes in adjacent operand rows: row 2r holds
+    // hi = v >> 8, row 2r + 1 holds lo = (v & 255) - 128, so v = 256 hi + lo + 128.
+    GeluWide = 6,          // c_fc + i16 GELU table (gelu16), out: the two planes of each row
+    ResidualWide = 7,      // m = 2 x rows of planes; x += rescale(256 hi + lo + 128 wsum + b)
+    LogitsWide = 8,        // as Logits over planes (i64 out)
+    LogitsCompactWide = 9  // as LogitsCompact over planes
+};
 
 struct GemmArgs {
     const int8_t *a = nullptr;  // [m_pad, k_pad]
@@ -25,8 +34,10 @@ struct GemmArgs {
     int shift = 0;
     void *out = nullptr;  // Raw: i32; Act/Gelu: i8; Residual: i32 x (read-modify-write); Logits: i64
     int ldo = 0;          // elements per output row
-    const int8_t *gelu = nullptr;  // Gelu table, i8 entries
-    int gelu_off = 0;              // 128 or 32768
+    const int8_t *gelu = nullptr;     // Gelu table, i8 entries
+    const int16_t *gelu16 = nullptr;  // GeluWide table, i16 entries
+    int gelu_off = 0;                 // half the table length (128 or 32768)
+    const int32_t *wsum = nullptr;    // the wide epilogues: sum_k w[n][k] per output column
     // LogitsCompact: out is u16 [m, ldo] = min(tilemax - logit, cap16) and tmax [m, tmax_ld] is
     // the largest logit of each 64-column tile.
     int64_t *tmax = nullptr;
@@ -74,6 +85,8 @@ struct LnArgs {
     int ldo = 0;
     const int32_t *src = nullptr;  // optional: output row i reads x row src[i]
     const int64_t *gm = nullptr;   // gamma[j] * m, exact in i64 (|gamma m| < 2^46)
+    int bits = 8;                  // 16: clamp to +-32767 and write the two i8 planes of each row
+                                   // (hi to out row 2i, lo to row 2i + 1), as the wide GEMMs read
 };
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream);
 

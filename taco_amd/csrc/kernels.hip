@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     // stages are free after the barrier below) and stores them back as 16-byte row pieces, 8-32
     // stores per wave instead of one per element. Needs 16-byte aligned output rows.
     constexpr int ES = EPI == (int)Epi::Residual ? 4 : (EPI == (int)Epi::LogitsCompact ? 2 : 1);
-    constexpr bool STAGEABLE = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu ||
+    constexpr bool STAGEABLE = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide ||
                                EPI == (int)Epi::Residual || EPI == (int)Epi::LogitsCompact;
     if (STAGEABLE && ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0) {
         __syncthreads();  // every wave finished reading the stages
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             bias[j] = (okn[j] && EPI != (int)Epi::LogitsCompact) ? g.bias[n] : 0;
             mult[j] = okn[j] ? g.mult[n] : 0;
         }
-        if (EPI == (int)Epi::Act || EPI == (int)Epi::Gelu) {
+        if (EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide) {
             if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62: table[clamp(r) + off]
 #pragma unroll
                 for (int i = 0; i < 8; i++)
@@ -195,6 +195,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                         for (int e = 0; e < 4; e++) acc[i][j][e] = gemm_lds[acc[i][j][e]];
                 __syncthreads();  // the table reads are done before the regions are written
             }
+            if (EPI == (int)Epi::GeluWide) {  // the i16 table (128 KiB) is read through the caches
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
+                            const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
+                                                     : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
+                            acc[i][j][e] = g.gelu16[y + g.gelu_off];
+                        }
+            }
+            // GeluWide: the hi plane of every row, then the lo plane (this wave's region is
+            // rewritten only after its own reads: LDS operations of a wave stay in order)
+            constexpr int PLANES = EPI == (int)Epi::GeluWide ? 2 : 1;
+#pragma unroll
+            for (int pl = 0; pl < PLANES; pl++) {
 #pragma unroll
             for (int i = 0; i < 8; i++)
 #pragma unroll
@@ -205,6 +223,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                         if (EPI == (int)Epi::Act) {  // ops.rs:123-130
                             const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
                             v = NARROW ? med3_i32((int32_t)r, -127, 127) : (int32_t)clamp64(r, -127, 127);
+                        } else if (EPI == (int)Epi::GeluWide) {
+                            v = pl == 0 ? acc[i][j][e] >> 8 : (acc[i][j][e] & 255) - 128;
                         } else {
                             v = acc[i][j][e];
                         }
@@ -227,7 +247,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                              (((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc) = v;
                     continue;
                 }
-                int8_t *o = (int8_t *)g.out + (size_t)m * g.ldo + n;
+                const size_t orow = EPI == (int)Epi::GeluWide ? 2 * (size_t)m + pl : (size_t)m;
+                int8_t *o = (int8_t *)g.out + orow * g.ldo + n;
                 if (n + 16 <= g.n) {
                     *(v4i *)o = v;
                 } else {
@@ -235,6 +256,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                     for (int t = 0; t < 16; t++)
                         if (n + t < g.n) o[t] = (int8_t)(v[t >> 2] >> (8 * (t & 3)));
                 }
+            }
             }
             return;
         }
@@ -320,6 +342,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             return;
         }
     }
+    if (EPI == (int)Epi::ResidualWide || EPI == (int)Epi::LogitsWide || EPI == (int)Epi::LogitsCompactWide) {
+        // i16 operand rows as planes (ops.rs:178-206,246-277): the lane holds plane rows
+        // 4 (lane / 16) + e of each 16-row tile, so e = 0, 1 are the hi and lo planes of one row
+        // and e = 2, 3 those of the next. dot(w, v) = 256 dot(w, hi) + dot(w, lo) + 128 wsum:
+        // |dot| <= K 2^22 <= 2^38, so dot + b is an i64 and rescale takes the i128 product.
+        const int tile_n0 = n0 + wn * 64;
+        int32_t mlt[4];
+        int64_t add[4];
+        bool okn[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = tile_n0 + j * 16 + (lane & 15);
+            okn[j] = n < g.n;
+            mlt[j] = okn[j] ? g.mult[n] : 0;
+            add[j] = okn[j] ? 128 * (int64_t)g.wsum[n] + (EPI == (int)Epi::ResidualWide ? g.bias[n] : 0) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const int mp = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + 2 * p;  // the hi plane row
+                const int m = mp >> 1;
+                const bool okm = mp < g.m;
+                int64_t l[4], mx = INT64_MIN;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int64_t dot = 256 * (int64_t)acc[i][j][2 * p] + acc[i][j][2 * p + 1] + add[j];
+                    const i128 r = rescale_full(dot, mlt[j], g.shift);
+                    const int n = tile_n0 + j * 16 + (lane & 15);
+                    if (EPI == (int)Epi::ResidualWide) {  // x = clamp(x + r, +-R), as Residual
+                        if (okm && okn[j]) {
+                            int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n;
+                            *x = (int32_t)clamp64((int64_t)*x + clamp128(r, INT32_MIN, INT32_MAX), -RES, RES);
+                        }
+                    } else if (EPI == (int)Epi::LogitsWide) {
+                        if (okm && okn[j]) ((int64_t *)g.out)[(size_t)m * g.ldo + n] = clamp128(r, -SCORE_LIMIT, SCORE_LIMIT);
+                    } else {
+                        l[j] = okn[j] ? clamp128(r, -SCORE_LIMIT, SCORE_LIMIT) : INT64_MIN;
+                        mx = l[j] > mx ? l[j] : mx;
+                    }
+                }
+                if (EPI == (int)Epi::LogitsCompactWide) {
+#pragma unroll
+                    for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes that hold this row
+                        const int64_t u = __shfl_xor(mx, o, 64);
+                        mx = u > mx ? u : mx;
+                    }
+                    if (okm) {
+                        if ((lane & 15) == 0 && tile_n0 < g.n) g.tmax[(size_t)m * g.tmax_ld + tile_n0 / 64] = mx;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            if (!okn[j]) continue;
+                            const int64_t dd = mx - l[j];
+                            ((uint16_t *)g.out)[(size_t)m * g.ldo + tile_n0 + j * 16 + (lane & 15)] =
+                                (uint16_t)(dd < g.cap16 ? dd : g.cap16);
+                        }
+                    }
+                }
+            }
+        }
+        return;
+    }
     if (EPI == (int)Epi::LogitsCompact) {
         // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the largest
         // logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16) per logit.
@@ -370,7 +454,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int n = n0 + wn * 64 + j * 16 + (lane & 15);
         if (n >= g.n) continue;
         int32_t bias = 0, mult = 0;
-        if (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu) bias = g.bias[n];
+        if (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu ||
+            EPI == (int)Epi::GeluWide)
+            bias = g.bias[n];
         if (EPI != (int)Epi::Raw) mult = g.mult[n];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -404,6 +490,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                     const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
                                              : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
                     ((int8_t *)g.out)[o] = g.gelu[y + g.gelu_off];
+                } else if (EPI == (int)Epi::GeluWide) {  // the two planes of the i16 entry
+                    const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
+                                             : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
+                    const int32_t v = g.gelu16[y + g.gelu_off];
+                    ((int8_t *)g.out)[2 * (size_t)m * g.ldo + n] = (int8_t)(v >> 8);
+                    ((int8_t *)g.out)[(2 * (size_t)m + 1) * g.ldo + n] = (int8_t)((v & 255) - 128);
                 } else {  // Logits: ops.rs:229-234
                     ((int64_t *)g.out)[o] = NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
                 }
@@ -448,6 +540,14 @@ hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
         case Epi::Gelu: return launch_gemm_e<3>(g, grid, stream);
         case Epi::Logits: return launch_gemm_e<4>(g, grid, stream);
         case Epi::LogitsCompact: return launch_gemm_e<5>(g, grid, stream);
+        case Epi::GeluWide: return launch_gemm_e<6>(g, grid, stream);
+        case Epi::ResidualWide:
+        case Epi::LogitsWide:
+        case Epi::LogitsCompactWide:
+            if (!g.wsum || (g.m & 1)) return hipErrorInvalidValue;  // rows of plane pairs
+            if (epi == Epi::ResidualWide) return launch_gemm_t<7, false>(g, grid, stream);
+            if (epi == Epi::LogitsWide) return launch_gemm_t<8, false>(g, grid, stream);
+            return launch_gemm_t<9, false>(g, grid, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -480,7 +580,8 @@ hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int 
 // Integer LayerNorm (crates/hardshell/src/layernorm.rs:201-256), one workgroup per row:
 // mean = floor(sum / n); var = floor(sum (x - mean)^2 / n) in u128; inv = 2^K / isqrt(var *
 // 2^2J + eps); y = rescale_wide((x - mean) * inv * gamma, m, s) + beta (or the one-rounding form
-// with beta_frac); out = clamp(y, -127, 127).
+// with beta_frac); out = clamp(y, -127, 127), or clamp(y, -32767, 32767) as two i8 planes for
+// the 16-bit final LayerNorm of a version-2 model (layernorm.rs:197, ops.rs:246-277).
 // =============================================================================================
 
 __device__ __forceinline__ u128 wave_sum128(u128 v) {
@@ -523,13 +624,23 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     cmax = (uint64_t)wave_max64((int64_t)cmax);
     const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
-    int8_t *out = a.out + (size_t)row * a.ldo;
+    const bool wide = a.bits == 16;
+    int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+    // clamp_act_i8, or clamp_act_i16 stored as the planes hi = v >> 8, lo = (v & 255) - 128
+    auto put = [&](int j, int64_t y) {
+        if (!wide) {
+            out[j] = (int8_t)clamp64(y, -127, 127);
+        } else {
+            const int32_t v = (int32_t)clamp64(y, -32767, 32767);
+            out[j] = (int8_t)(v >> 8);
+            out[a.ldo + j] = (int8_t)((v & 255) - 128);
+        }
+    };
     if (small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126) {
         // the rounding shift from the high word of (c inv) (gamma m) alone (shift_round_hi)
         for (int j = lane; j < d; j += 64) {
             const int64_t c = (int64_t)x[j] - mean;
-            const int64_t y = shift_round_hi(c * (int64_t)inv, a.gm[j], (uint32_t)a.s) + a.beta[j];
-            out[j] = (int8_t)clamp64(y, -127, 127);
+            put(j, shift_round_hi(c * (int64_t)inv, a.gm[j], (uint32_t)a.s) + a.beta[j]);
         }
         return;
     }
@@ -544,7 +655,7 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
             const i128 cb = (i128)a.beta[j] << (a.s - a.beta_frac);
             y = shift_round128(p + cb, a.s, 126);
         }
-        out[j] = (int8_t)clamp128(y, -127, 127);
+        put(j, clamp128(y, -32767, 32767));
     }
 }
 

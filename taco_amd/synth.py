@@ -142,6 +142,14 @@ def _rust_round(v: float) -> int:
     return f
 
 
+def gelu_table_wide() -> np.ndarray:
+    # input unit 1/4000, output unit 1/10240 (i16 entries)
+    out = np.empty(65536, np.int16)
+    for i, q in enumerate(range(-32768, 32768)):
+        out[i] = max(-32767, min(32767, _rust_round(gelu(q / 4000.0) * 10240.0)))
+    return out
+
+
 def gelu_table() -> np.ndarray:
     # input unit 1/4000 (GELU input sigma 8000 is 2.0), output unit 1/40
     out = np.empty(65536, np.int8)
@@ -164,13 +172,21 @@ SIGMA_W_SQ = Fraction(255 * 255 - 1, 12)  # uniform [-127, 127]: variance 5418.6
 SIGMA_ACT_SQ = Fraction(1600 * 1600)       # i8 model activations times weights
 
 
-def build_model(dims: Dims, seed: int = 0x7AC0_5EED) -> bytes:
+def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_len: int = 8192) -> bytes:
+    """The synthetic model. wide=True makes a model-file version 2 model: an i16 GELU table
+    (output unit 1/10240), a 16-bit ln_f (target 10240) and ln_beta_frac = 8 (beta in units of
+    2^-8, uniform in [-4096, 4096]); the shifts that read those activations are 8 larger.
+    table_len sets the length of both exponent tables."""
     d, f, V, C, L, H = dims.d_model, dims.d_ff, dims.vocab, dims.n_ctx, dims.n_layer, dims.n_head
     hd = d // H
     s = Stream(seed)
     w = HsmWriter(n_layer=L, n_head=H, d_model=d, d_ff=f, vocab_size=V, n_ctx=C, eot_token=V - 1,
                   ln_k=48, ln_j=8, ln_eps=1 << 43, softmax_p=30)
     w.set_vocabulary(vocabulary(V))
+    frac = 8 if wide else 0
+    if wide:
+        w.ln_f_bits = 16
+        w.ln_beta_frac = frac
 
     def mult(n):
         return _uniform_int(s, n, 1 << 30, 1 << 31, np.int64).astype(np.int32)
@@ -181,24 +197,23 @@ def build_model(dims: Dims, seed: int = 0x7AC0_5EED) -> bytes:
     # gamma uniform in [2^13, 2^15): E[gamma^2] = (a^2 + ab + b^2) / 3
     a_, b_ = 1 << 13, 1 << 15
     gamma_sq = Fraction(a_ * a_ + a_ * b_ + b_ * b_, 3)
-    ln_shift = shift_for(Fraction(2) ** 80 * gamma_sq, 40)
 
-    def layernorm(prefix):
+    def layernorm(prefix, target=40):
         w.add_tensor(prefix + ".g", _uniform_int(s, d, 1 << 13, 1 << 15, np.int16))
-        w.add_tensor(prefix + ".b", _uniform_int(s, d, -16, 17, np.int32))
-        w.add_tensor(prefix + ".rescale", mult(1), ln_shift)
+        w.add_tensor(prefix + ".b", _uniform_int(s, d, -(16 << frac), (16 << frac) + 1, np.int32))
+        w.add_tensor(prefix + ".rescale", mult(1), shift_for(Fraction(2) ** 80 * gamma_sq, target))
 
-    def linear(prefix, rows, cols, target):
+    def linear(prefix, rows, cols, target, in_scale=1):
         w.add_tensor(prefix + ".w", _uniform_i8(s, (rows, cols)))
         w.add_tensor(prefix + ".b", bias(rows))
-        w.add_tensor(prefix + ".rescale", mult(rows), shift_for(SIGMA_ACT_SQ * cols, target))
+        w.add_tensor(prefix + ".rescale", mult(rows), shift_for(SIGMA_ACT_SQ * cols * in_scale ** 2, target))
 
     w.add_tensor("wte", _uniform_i8(s, (V, d)))
     w.add_tensor("wte.rescale_embed", mult(V), shift_for(SIGMA_W_SQ, 1 << 14))
-    w.add_tensor("wte.rescale_logits", mult(V), shift_for(SIGMA_ACT_SQ * d, 768))
+    w.add_tensor("wte.rescale_logits", mult(V), shift_for(SIGMA_ACT_SQ * d * (65536 if wide else 1), 768))
     w.add_tensor("wpe", _uniform_i8(s, (C, d)))
     w.add_tensor("wpe.rescale", mult(C), shift_for(SIGMA_W_SQ, 1 << 14))
-    table = gelu_table()
+    table = gelu_table_wide() if wide else gelu_table()
     for l in range(L):
         p = f"h.{l}"
         layernorm(p + ".ln_1")
@@ -209,9 +224,9 @@ def build_model(dims: Dims, seed: int = 0x7AC0_5EED) -> bytes:
         layernorm(p + ".ln_2")
         linear(p + ".mlp.c_fc", f, d, 8000)
         w.add_tensor(p + ".mlp.gelu", table)
-        linear(p + ".mlp.c_proj", d, f, 1 << 14)
-    layernorm("ln_f")
-    ae, le = exp_tables()
+        linear(p + ".mlp.c_proj", d, f, 1 << 14, 256 if wide else 1)
+    layernorm("ln_f", 10240 if wide else 40)
+    ae, le = exp_tables(table_len)
     w.add_tensor("attn_exp", ae)
     w.add_tensor("logits_exp", le)
     return w.finish()
