@@ -156,6 +156,56 @@ size_t hs_batch_stream_len(const hs_batch *batch, size_t slot);
 size_t hs_batch_room(const hs_batch *batch, size_t slot);
 hs_status hs_batch_truncate(hs_batch *batch, size_t slot, size_t len);
 
+/* ---- The mixed coder op of the logs profile: crates/hardshell-cuda/src/batch/mixed.rs:23-126,
+ * src/mixed.rs:24-233 (ADR 0010 section 3) ---------------------------------------------------
+ * The GPU gives the statistics of each row's GPT-2 weights w; the host mixer gives q; the GPU
+ * codes with the weights of taco_match::Mixer::mix(w, p): w'[i] = max(1, (w[i] m) >> k) for
+ * i != p and w'[p] = max(1, (R q) >> k), R = max(W - w[p], 1), m = 2^16 - q,
+ * k = max(0, bitlen(R) + 16 - 62) (mixed.rs:65-90); without a prediction max(1, w[i]). */
+#define HS_MIX_NONE 0xFFFFFFFFu   /* a mixed table without a prediction */
+#define HS_MIX_PLAIN 0xFFFFFFFEu  /* the table of GPT-2 alone (MixInput::Plain) */
+typedef struct hs_mix_stats {     /* MixStats (mixed.rs:36-49) */
+    uint64_t total;               /* W = sum(w) (below 2^64: weights <= 2^40, vocab <= 2^20) */
+    uint64_t predicted;           /* w[p] */
+    uint32_t top;                 /* the token of the largest weight, the lowest id on a tie,
+                                     0 if every weight is 0; the agreement bit is top == p */
+    uint32_t pad;
+} hs_mix_stats;
+/* The host step (the mixer of FnMut(usize, MixStats) -> u32): called once for each input with a
+ * prediction, in input order, with `input` its index; returns q in 1..=65535. */
+typedef uint32_t (*hs_mixer_fn)(void *user, size_t input, const hs_mix_stats *stats);
+/* CudaBatch::run_coded_mixed (batch/mixed.rs:48-93): as hs_batch_run_coded, with the table of
+ * input i named by tables[i]: HS_MIX_PLAIN, HS_MIX_NONE or a predicted token (< vocab). A q
+ * outside 1..=65535 or a predicted token out of range is HS_UNSUPPORTED. After an error no
+ * position changed, but the mixer can have been called. */
+hs_status hs_batch_run_coded_mixed(hs_batch *batch, const hs_input *inputs,
+                                   const hs_query *queries, const uint32_t *tables, size_t n,
+                                   uint32_t freq_bits, hs_mixer_fn mixer, void *user,
+                                   hs_interval *out);
+/* CudaBatch::run_coded_dual (batch/mixed.rs:95-126): for each input the interval of tokens[i]
+ * in the table of GPT-2 alone (plain[i]) and in the mixed table with the prediction
+ * predictions[i] (HS_MIX_NONE: none) (mixed[i]), from one forward pass. */
+hs_status hs_batch_run_coded_dual(hs_batch *batch, const hs_input *inputs, const uint32_t *tokens,
+                                  const uint32_t *predictions, size_t n, uint32_t freq_bits,
+                                  hs_mixer_fn mixer, void *user, hs_interval *plain,
+                                  hs_interval *mixed);
+/* mixed_intervals_of_weights (mixed.rs:160-233), for tests: the op on given weights [rows,
+ * vocab] (host; each row's sum below 2^64), predictions[r] a token or HS_MIX_NONE; `stats`
+ * (may be NULL) receives each row's statistics. */
+hs_status hs_op_mixed_coder(hs_device *dev, const uint64_t *weights, size_t rows, size_t vocab,
+                            const hs_query *queries, const uint32_t *predictions,
+                            uint32_t freq_bits, hs_mixer_fn mixer, void *user,
+                            hs_mix_stats *stats, hs_interval *out);
+/* The same op on given i64 logits and a logits table, as hs_op_coder (the compact form of the LM
+ * head for tables of at most 16,384 entries, else i64 logits), for tests: tables[r] is
+ * HS_MIX_PLAIN, HS_MIX_NONE or a predicted token (the mix_stats_* and coder_mixed_* kernels of
+ * crates/hardshell-cuda/kernels/hardshell.cu:1682-1814 on their logits and d16 sources). */
+hs_status hs_op_mixed_coder_logits(hs_device *dev, const int64_t *logits, size_t rows,
+                                   size_t vocab, const uint64_t *table, size_t len,
+                                   const hs_query *queries, const uint32_t *tables,
+                                   uint32_t freq_bits, hs_mixer_fn mixer, void *user,
+                                   hs_mix_stats *stats, hs_interval *out);
+
 /* ---- Op-level entry points (crates/hardshell-cuda/src/ops.rs:142-335) --------------------- */
 /* out[i * n + r] = w[r] . a[i] for w [n, k] and a [m, k] i8 (host pointers), exact i32; the same
  * values as hardshell::kernels::matvec_i8 (ops.rs:142-161 matmul_i8). */

@@ -2001,3 +2001,75 @@ extern "C" void or_attend_decode_ref(const int8_t *q, const int8_t *kc, const in
                 out[s * h * hd + hh * hd + c] = clamp_act_i8(rescale(acc[c], out_m, out_s));
         }
 }
+
+// ============================================================================================
+// The mixed coder op of the logs profile: the weights of taco_match::Mixer::mix for a given
+// probability q of the predicted token (crates/taco-match/src/mixer.rs:256-292, apply :491-516),
+// the statistics of its pass 1 and the host record of rule 5
+// (crates/hardshell-cuda/src/mixed.rs:36-90).
+// ============================================================================================
+
+// Pass 1 of Mixer::mix (mixer.rs:278-288): total = sum w (u128), w[p] (0 if p >= n), top = the
+// first index of the largest weight, 0 when every weight is 0. out: total low, total high, w[p],
+// top.
+extern "C" void or_mix_stats(const uint64_t *w, size_t n, uint32_t p, uint64_t *out) {
+    u128 total = 0;
+    size_t top = 0;
+    uint64_t top_w = 0;
+    for (size_t i = 0; i < n; i++) {
+        total += w[i];
+        if (w[i] > top_w) {
+            top = i;
+            top_w = w[i];
+        }
+    }
+    out[0] = (uint64_t)total;
+    out[1] = (uint64_t)(total >> 64);
+    out[2] = p < n ? w[p] : 0;
+    out[3] = top;
+}
+
+// mix_record (mixed.rs:65-90): R = max(W - w[p], 1), m = 2^16 - q, k = max(0, bitlen(R) + 16 -
+// 62), w'[p] = max(1, (R q) >> k). Returns 1 for q outside 1..=65535, 2 for w[p] > W, 3 for a
+// w'[p] of 2^64 or more.
+extern "C" int or_mix_record(uint64_t total_lo, uint64_t total_hi, uint64_t wp, uint32_t q,
+                             uint32_t *k_out, uint32_t *m_out, uint64_t *wpm_out) {
+    if (q == 0 || q >= (1u << 16)) return 1;
+    const u128 total = ((u128)total_hi << 64) | total_lo;
+    if ((u128)wp > total) return 2;
+    u128 r = total - wp;
+    if (r < 1) r = 1;
+    unsigned bits = 0;
+    for (u128 t = r; t; t >>= 1) bits++;
+    const unsigned k = bits + 16 > 62 ? bits + 16 - 62 : 0;
+    const u128 v = (r * (u128)q) >> k;
+    if (v >> 64) return 3;
+    *k_out = k;
+    *m_out = (1u << 16) - q;
+    *wpm_out = v > 1 ? (uint64_t)v : 1;
+    return 0;
+}
+
+// Mixer::mix's weights for the probability q (mixer.rs:256-292 with apply :491-516): without a
+// prediction (p = UINT32_MAX) every weight becomes max(1, w); else w'[i] = max(1, (w[i] m) >> k)
+// and w'[p] = max(1, (R q) >> k) with R, m, k of or_mix_record. Returns or_mix_record's codes,
+// 4 for p >= n.
+extern "C" int or_mix_apply(uint64_t *w, size_t n, uint32_t p, uint32_t q) {
+    if (p == UINT32_MAX) {
+        for (size_t i = 0; i < n; i++) w[i] = w[i] > 1 ? w[i] : 1;
+        return 0;
+    }
+    if (p >= n) return 4;
+    uint64_t st[4];
+    or_mix_stats(w, n, p, st);
+    uint32_t k = 0, m = 0;
+    uint64_t wpm = 0;
+    const int e = or_mix_record(st[0], st[1], st[2], q, &k, &m, &wpm);
+    if (e) return e;
+    for (size_t i = 0; i < n; i++) {
+        const u128 v = ((u128)w[i] * m) >> k;
+        w[i] = v > 1 ? (uint64_t)v : 1;  // below 2^62 for i != p (w[i] <= R)
+    }
+    w[p] = wpm;
+    return 0;
+}

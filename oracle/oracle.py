@@ -71,6 +71,9 @@ def lib():
         L.or_attend_decode_ref.argtypes = [P, P, P, P, C.c_size_t, C.c_size_t, C.c_size_t,
                                             C.c_size_t, C.c_int32, C.c_uint8, C.c_int32, C.c_uint8,
                                             P, C.c_size_t, C.c_uint8, P]
+        L.or_mix_stats.argtypes = [P, C.c_size_t, C.c_uint32, P]
+        L.or_mix_record.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, P, P, P]
+        L.or_mix_apply.argtypes = [P, C.c_size_t, C.c_uint32, C.c_uint32]
         _lib = L
     return _lib
 
@@ -175,6 +178,49 @@ def freq_from_weights(w, bits):
     if lib().or_freq_from_weights(ptr(w), len(w), bits, ptr(out)) != 0:
         raise ValueError("from_weights refused")
     return out
+
+
+def logits_to_weights(logits, table):
+    """weights_of (crates/hardshell/src/logits.rs:62-72): table[min(max - l, len - 1)]."""
+    l = np.ascontiguousarray(logits, dtype=np.int64)
+    t = np.ascontiguousarray(table, dtype=np.uint64)
+    w = np.zeros(len(l), np.uint64)
+    if lib().or_logits_to_weights(ptr(l), len(l), ptr(t), len(t), ptr(w)) != 0:
+        raise ValueError("weights refused")
+    return w
+
+
+MIX_NONE = 0xFFFFFFFF
+MIX_PLAIN = 0xFFFFFFFE
+
+
+def mix_stats(w, p):
+    """Pass 1 of taco_match::Mixer::mix: (sum of w, w[p] or 0, the first index of the largest
+    weight or 0)."""
+    w = np.ascontiguousarray(w, dtype=np.uint64)
+    out = np.zeros(4, np.uint64)
+    lib().or_mix_stats(ptr(w), len(w), p, ptr(out))
+    return int(out[0]) | (int(out[1]) << 64), int(out[2]), int(out[3])
+
+
+def mix_record(total, wp, q):
+    """(k, m, w'[p]) of rule 5; ValueError for a q outside 1..=65535 or w[p] > total."""
+    k, m, wpm = C.c_uint32(), C.c_uint32(), C.c_uint64()
+    e = lib().or_mix_record(total & ((1 << 64) - 1), total >> 64, wp, q, C.byref(k), C.byref(m),
+                            C.byref(wpm))
+    if e:
+        raise ValueError(f"mix record refused ({e})")
+    return k.value, m.value, wpm.value
+
+
+def mix_apply(w, p, q):
+    """The weights of Mixer::mix(w, p) with the mixer's probability q of p (p = MIX_NONE: no
+    prediction)."""
+    w = np.array(w, dtype=np.uint64)
+    e = lib().or_mix_apply(ptr(w), len(w), p, q)
+    if e:
+        raise ValueError(f"mix refused ({e})")
+    return w
 
 
 def freq_interval(w, bits, symbol):

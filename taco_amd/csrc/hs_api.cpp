@@ -12,6 +12,7 @@
 #include <new>
 #include <string>
 #include <unordered_map>
+#include <functional>
 #include <vector>
 
 #include "common.h"
@@ -38,6 +39,12 @@ hs_status hip_fail(const char *call, hipError_t e) {
     do {                                                 \
         hipError_t e_ = (call);                          \
         if (e_ != hipSuccess) return hip_fail(#call, e_); \
+    } while (0)
+
+#define HS_TRY(call)                       \
+    do {                                   \
+        const hs_status s_ = (call);       \
+        if (s_ != HS_OK) return s_;        \
     } while (0)
 
 // Device allocations owned by a handle; freed in reverse order.
@@ -422,6 +429,9 @@ struct hs_batch {
     int32_t *h_src = nullptr;
     uint32_t *h_queries = nullptr;
     uint64_t *h_intervals = nullptr;
+    // the mixed coder op: records, statistics and the plain intervals of a dual call
+    hs::MixRec *h_mix = nullptr, *d_mix = nullptr;
+    uint64_t *h_stats = nullptr, *d_stats = nullptr, *h_intervals2 = nullptr, *d_intervals2 = nullptr;
     bool inflight = false;  // a pass returned with copies or kernels still queued on `st`
     void *split = nullptr;  // scratch of the split decode attention (grown on demand)
     size_t split_bytes = 0;
@@ -454,7 +464,8 @@ struct hs_batch {
         }
         for (auto e : event_pool) (void)hipEventDestroy(e);
         if (st) (void)hipStreamSynchronize(st);
-        for (void *p : {(void *)h_rows, (void *)h_groups, (void *)h_src, (void *)h_queries, (void *)h_intervals})
+        for (void *p : {(void *)h_rows, (void *)h_groups, (void *)h_src, (void *)h_queries, (void *)h_intervals,
+                        (void *)h_mix, (void *)h_stats, (void *)h_intervals2})
             if (p) (void)hipHostFree(p);
         if (split) (void)hipFree(split);
         if (st) (void)hipStreamDestroy(st);
@@ -549,6 +560,9 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     }
     if ((s = mem.alloc(b->d_queries, 2 * R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_intervals, 3 * R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_intervals2, 3 * R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_stats, 3 * R)) != HS_OK) return s;
+    if ((s = mem.alloc(b->d_mix, R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_weights, b->chunk_rows * m.V)) != HS_OK) return s;
     const size_t cache = slots * (size_t)m.C * m.d;
     b->kc.resize(m.L);
@@ -562,6 +576,9 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     HIP_TRY(hipHostMalloc((void **)&b->h_src, R * sizeof(int32_t), hipHostMallocDefault));
     HIP_TRY(hipHostMalloc((void **)&b->h_queries, 2 * R * sizeof(uint32_t), hipHostMallocDefault));
     HIP_TRY(hipHostMalloc((void **)&b->h_intervals, 3 * R * sizeof(uint64_t), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_intervals2, 3 * R * sizeof(uint64_t), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_stats, 3 * R * sizeof(uint64_t), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void **)&b->h_mix, R * sizeof(hs::MixRec), hipHostMallocDefault));
     HIP_TRY(hipStreamCreate(&b->st));
     *out = b.release();
     return HS_OK;
@@ -665,9 +682,60 @@ void commit(hs_batch &b, Plan &p) {
 
 enum class Out { Weights, Intervals };
 
+// The tables of a mixed call (batch/mixed.rs:23-33): the table word of each input
+// (HS_MIX_PLAIN, HS_MIX_NONE or the predicted token), the host mixer, and for a dual call the
+// intervals of GPT-2 alone.
+struct Mixing {
+    const uint32_t *tables = nullptr;
+    hs_mixer_fn fn = nullptr;
+    void *user = nullptr;
+    uint64_t *plain_sink = nullptr;
+};
+
+// mix_record (crates/hardshell-cuda/src/mixed.rs:65-90): R = max(W - w[p], 1), m = 2^16 - q,
+// k = max(0, bitlen(R) + 16 - 62), w'[p] = max(1, (R q) >> k) (below 2^62).
+hs_status mix_record(const hs_mix_stats &st, uint32_t p, uint32_t q, hs::MixRec &r) {
+    if (q == 0 || q >= (1u << 16)) return hs::fail(HS_UNSUPPORTED, 0, "the mixer probability q must be in 1..=65535");
+    if (st.predicted > st.total) return hs::fail(HS_UNSUPPORTED, 0, "the weight of the prediction is above the sum");
+    const uint64_t R = std::max<uint64_t>(st.total - st.predicted, 1);
+    const uint32_t bits = 64 - (uint32_t)__builtin_clzll(R);
+    const uint32_t k = bits + 16 > 62 ? bits + 16 - 62 : 0;
+    const unsigned __int128 v = ((unsigned __int128)R * q) >> k;
+    r = hs::MixRec{p, k, (1u << 16) - q, 0, v > 1 ? (uint64_t)v : 1, 0};
+    return HS_OK;
+}
+
 // One forward pass over `rows`, then the LM head and the coder op for the rows with an input.
+// The mixed coder op of one LM-head chunk (batch/mixed.rs:128-188): the statistics kernel
+// (launch(0)) on records that carry p only, a read back, the host mixer for each output row in
+// input order and the records of rule 5, then the coder of GPT-2 alone for a dual call
+// (launch(1)) and the mixed coder (launch(2)).
+template <typename L>
+hs_status mix_chunk(hs_batch &b, const Mixing &mx, const std::vector<int64_t> &owner, int c0, int cn, L launch) {
+    hipStream_t st = b.st;
+    for (int r = 0; r < cn; r++) b.h_mix[c0 + r] = hs::MixRec{mx.tables[owner[c0 + r]], 0, 0, 0, 0, 0};
+    HIP_TRY(hipMemcpyAsync(b.d_mix + c0, b.h_mix + c0, cn * sizeof(hs::MixRec), hipMemcpyHostToDevice, st));
+    HIP_TRY(launch(0));
+    HIP_TRY(hipMemcpyAsync(b.h_stats + 3 * (size_t)c0, b.d_stats + 3 * (size_t)c0, 24 * (size_t)cn,
+                           hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    for (int r = 0; r < cn; r++) {
+        const uint32_t t = mx.tables[owner[c0 + r]];
+        if (t == HS_MIX_PLAIN || t == HS_MIX_NONE) continue;  // the record stays {t}
+        const uint64_t *w = b.h_stats + 3 * (size_t)(c0 + r);
+        const hs_mix_stats stats{w[0], w[1], (uint32_t)w[2], 0};
+        const uint32_t q = mx.fn(mx.user, (size_t)owner[c0 + r], &stats);
+        const hs_status s = mix_record(stats, t, q, b.h_mix[c0 + r]);
+        if (s != HS_OK) return s;
+    }
+    HIP_TRY(hipMemcpyAsync(b.d_mix + c0, b.h_mix + c0, cn * sizeof(hs::MixRec), hipMemcpyHostToDevice, st));
+    if (mx.plain_sink) HIP_TRY(launch(1));
+    HIP_TRY(launch(2));
+    return HS_OK;
+}
+
 hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const uint32_t *queries,
-                   uint32_t bits, uint64_t *sink) {
+                   uint32_t bits, uint64_t *sink, const Mixing *mx = nullptr) {
     const hs_model &m = *b.model;
     hipStream_t st = b.st;
     const int n = (int)rows.size();
@@ -725,10 +793,14 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         a.out = dst; a.ldo = m.d_pad; a.src = src_rows; a.gm = l.gm;
         return b.launch("layer_norm", 0, [&] { return hs::launch_layernorm(a, rows_n, st); });
     };
+    // The LM head: the rows of a chunk (at most a few MB of A) stay in every XCD's L2 while
+    // each XCD streams its own slice of wte once (all M-tiles in one group, N outermost).
+    auto head_group = [](int rows) { return (rows + hs::GEMM_BM - 1) / hs::GEMM_BM; };
     auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int rows_n,
                     void *o, int ldo, const int8_t *gelu = nullptr, int gelu_off = 0,
-                    const int16_t *gelu16 = nullptr) {
+                    const int16_t *gelu16 = nullptr, int group = 0) {
         hs::GemmArgs g;
+        g.group = group;
         g.a = a; g.w = lin.w; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
         g.fast32 = epi == Epi::ResidualWide ? 0 : lin.fast32;
@@ -827,6 +899,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             g.mult = m.logit_m; g.shift = m.host.logit_s; g.out = b.d_d16; g.ldo = m.ld16;
             g.tmax = b.d_tmax; g.tmax_ld = m.ntiles; g.cap16 = (int)m.host.logits_exp.size() - 1;
             g.wsum = m.wte_sum;
+            g.group = head_group(g.m);
             const uint64_t ops = 2ull * (uint64_t)pr * cn * (uint64_t)m.V * (uint64_t)m.d;
             const Epi epi = m.wide_ln_f ? Epi::LogitsCompactWide : Epi::LogitsCompact;
             HIP_TRY(b.launch("gemm_logits", ops, [&] { return hs::launch_gemm(epi, g, st); }));
@@ -838,10 +911,25 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             ca.bits = (int)bits;
             ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
             ca.weights = out == Out::Weights ? b.d_weights : nullptr;
-            HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder_compact(ca, cn, st); }));
+            if (mx) {
+                ca.mix = b.d_mix + c0;
+                ca.stats = b.d_stats + 3 * (size_t)c0;
+                HS_TRY(mix_chunk(b, *mx, owner, c0, cn, [&](int what) -> hipError_t {
+                    if (what == 0) return b.launch("mix_stats", 0, [&] { return hs::launch_mix_stats_compact(ca, cn, st); });
+                    if (what == 1) {
+                        hs::CompactCoderArgs cp = ca;
+                        cp.intervals = b.d_intervals2 + 3 * (size_t)c0;
+                        return b.launch("coder", 0, [&] { return hs::launch_coder_compact(cp, cn, st); });
+                    }
+                    return b.launch("coder_mixed", 0, [&] { return hs::launch_coder_compact_mixed(ca, cn, st); });
+                }));
+            } else {
+                HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder_compact(ca, cn, st); }));
+            }
         } else {
             HIP_TRY(gemm("gemm_logits", m.wide_ln_f ? Epi::LogitsWide : Epi::Logits, head,
-                         b.d_af + (size_t)pr * c0 * m.d_pad, pr * cn, b.d_logits, m.V));
+                         b.d_af + (size_t)pr * c0 * m.d_pad, pr * cn, b.d_logits, m.V, nullptr, 0,
+                         nullptr, head_group(pr * cn)));
             hs::CoderArgs ca;
             ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
             ca.table_len = (int)m.host.logits_exp.size();
@@ -849,7 +937,21 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             ca.bits = (int)bits;
             ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
             ca.weights = out == Out::Weights ? b.d_weights : nullptr;
-            HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder(ca, cn, st); }));
+            if (mx) {
+                ca.mix = b.d_mix + c0;
+                ca.stats = b.d_stats + 3 * (size_t)c0;
+                HS_TRY(mix_chunk(b, *mx, owner, c0, cn, [&](int what) -> hipError_t {
+                    if (what == 0) return b.launch("mix_stats", 0, [&] { return hs::launch_mix_stats(ca, cn, st); });
+                    if (what == 1) {
+                        hs::CoderArgs cp = ca;
+                        cp.intervals = b.d_intervals2 + 3 * (size_t)c0;
+                        return b.launch("coder", 0, [&] { return hs::launch_coder(cp, cn, st); });
+                    }
+                    return b.launch("coder_mixed", 0, [&] { return hs::launch_coder_mixed(ca, cn, st); });
+                }));
+            } else {
+                HIP_TRY(b.launch("coder", 0, [&] { return hs::launch_coder(ca, cn, st); }));
+            }
         }
         if (out == Out::Weights)
             HIP_TRY(hipMemcpyAsync(host.data() + (size_t)c0 * m.V, b.d_weights, (size_t)cn * m.V * 8,
@@ -857,12 +959,17 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     }
     if (out == Out::Intervals)
         HIP_TRY(hipMemcpyAsync(b.h_intervals, b.d_intervals, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
+    if (mx && mx->plain_sink)
+        HIP_TRY(hipMemcpyAsync(b.h_intervals2, b.d_intervals2, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
     const uint64_t *res = out == Out::Intervals ? b.h_intervals : host.data();
     // The event times are read back in bulk (hs_batch_profile), not inside every call.
     if (b.profiling && b.pending.size() > 8192) HIP_TRY(b.collect());
     for (int i = 0; i < n_out; i++)
         std::memcpy(sink + (size_t)owner[i] * per_row, res + (size_t)i * per_row, per_row * 8);
+    if (mx && mx->plain_sink)
+        for (int i = 0; i < n_out; i++)
+            std::memcpy(mx->plain_sink + (size_t)owner[i] * 3, b.h_intervals2 + (size_t)i * 3, 24);
     return HS_OK;
 }
 
@@ -882,11 +989,11 @@ hs_status check_inputs(const hs_batch *b, const hs_input *in, size_t n) {
 }
 
 hs_status run(hs_batch *b, const hs_input *in, size_t n, Out out, const uint32_t *queries,
-              uint32_t bits, uint64_t *sink) {
+              uint32_t bits, uint64_t *sink, const Mixing *mx = nullptr) {
     HIP_TRY(hipSetDevice(b->model->dev->ordinal));
     Plan plan = make_plan(*b, in, n);
     for (auto &pass : plan.passes) {
-        hs_status s = run_pass(*b, pass, out, queries, bits, sink);
+        hs_status s = run_pass(*b, pass, out, queries, bits, sink, mx);
         if (s != HS_OK) return s;  // no position changes after an error
     }
     commit(*b, plan);
@@ -903,17 +1010,15 @@ extern "C" hs_status hs_batch_run_weights(hs_batch *b, const hs_input *in, size_
     return run(b, in, n, Out::Weights, nullptr, 0, out);
 }
 
-extern "C" hs_status hs_batch_run_coded(hs_batch *b, const hs_input *in, const hs_query *queries,
-                                        size_t n, uint32_t freq_bits, hs_interval *out) {
-    hs::clear_error();
-    hs_status s = check_inputs(b, in, n);
-    if (s != HS_OK) return s;
-    if (n && (!queries || !out)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
-    const uint32_t V = b->model->host.vocab;
-    // coder_words (batch.rs:647-666)
+namespace {
+
+// coder_words (batch.rs:647-666): the query words, each checked against the vocabulary and
+// the total 2^freq_bits.
+hs_status coder_words(const hs_query *queries, size_t n, uint32_t V, uint32_t freq_bits,
+                      std::vector<uint32_t> &words) {
     if (freq_bits == 0 || freq_bits > 32 || (uint64_t)V > (1ull << freq_bits))
         return hs::fail(HS_UNSUPPORTED, 0, "freq_bits must be in 1..=32 and 2^freq_bits >= vocab");
-    std::vector<uint32_t> words(2 * n);
+    words.resize(2 * n);
     for (size_t i = 0; i < n; i++) {
         const bool ok = (queries[i].kind == 0 && queries[i].value < V) ||
                         (queries[i].kind == 1 && (uint64_t)queries[i].value < (1ull << freq_bits));
@@ -921,7 +1026,71 @@ extern "C" hs_status hs_batch_run_coded(hs_batch *b, const hs_input *in, const h
         words[2 * i] = queries[i].kind;
         words[2 * i + 1] = queries[i].value;
     }
+    return HS_OK;
+}
+
+// table_words / prediction_words (mixed.rs:120-158): a predicted token must be in the vocabulary.
+hs_status check_tables(const uint32_t *tables, size_t n, uint32_t V, bool allow_plain) {
+    for (size_t i = 0; i < n; i++) {
+        const uint32_t t = tables[i];
+        if (t == HS_MIX_NONE || (allow_plain && t == HS_MIX_PLAIN) || t < V) continue;
+        return hs::fail(HS_UNSUPPORTED, 0, "a predicted token is out of range");
+    }
+    return HS_OK;
+}
+
+bool needs_mixer(const uint32_t *tables, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (tables[i] != HS_MIX_NONE && tables[i] != HS_MIX_PLAIN) return true;
+    return false;
+}
+
+}  // namespace
+
+extern "C" hs_status hs_batch_run_coded(hs_batch *b, const hs_input *in, const hs_query *queries,
+                                        size_t n, uint32_t freq_bits, hs_interval *out) {
+    hs::clear_error();
+    hs_status s = check_inputs(b, in, n);
+    if (s != HS_OK) return s;
+    if (n && (!queries || !out)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    std::vector<uint32_t> words;
+    HS_TRY(coder_words(queries, n, b->model->host.vocab, freq_bits, words));
     return run(b, in, n, Out::Intervals, words.data(), freq_bits, (uint64_t *)out);
+}
+
+extern "C" hs_status hs_batch_run_coded_mixed(hs_batch *b, const hs_input *in, const hs_query *queries,
+                                              const uint32_t *tables, size_t n, uint32_t freq_bits,
+                                              hs_mixer_fn mixer, void *user, hs_interval *out) {
+    hs::clear_error();
+    HS_TRY(check_inputs(b, in, n));
+    if (n && (!queries || !tables || !out)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    const uint32_t V = b->model->host.vocab;
+    std::vector<uint32_t> words;
+    HS_TRY(coder_words(queries, n, V, freq_bits, words));
+    HS_TRY(check_tables(tables, n, V, true));
+    if (!mixer && needs_mixer(tables, n)) return hs::fail(HS_INVALID_ARGUMENT, 0, "mixer is NULL");
+    Mixing mx;
+    mx.tables = tables; mx.fn = mixer; mx.user = user;
+    return run(b, in, n, Out::Intervals, words.data(), freq_bits, (uint64_t *)out, &mx);
+}
+
+extern "C" hs_status hs_batch_run_coded_dual(hs_batch *b, const hs_input *in, const uint32_t *tokens,
+                                             const uint32_t *predictions, size_t n, uint32_t freq_bits,
+                                             hs_mixer_fn mixer, void *user, hs_interval *plain,
+                                             hs_interval *mixed) {
+    hs::clear_error();
+    HS_TRY(check_inputs(b, in, n));
+    if (n && (!tokens || !predictions || !plain || !mixed)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    const uint32_t V = b->model->host.vocab;
+    std::vector<hs_query> queries(n);
+    for (size_t i = 0; i < n; i++) queries[i] = hs_query{0, tokens[i]};
+    std::vector<uint32_t> words;
+    HS_TRY(coder_words(queries.data(), n, V, freq_bits, words));
+    HS_TRY(check_tables(predictions, n, V, false));
+    if (!mixer && needs_mixer(predictions, n)) return hs::fail(HS_INVALID_ARGUMENT, 0, "mixer is NULL");
+    Mixing mx;
+    mx.tables = predictions; mx.fn = mixer; mx.user = user; mx.plain_sink = (uint64_t *)plain;
+    return run(b, in, n, Out::Intervals, words.data(), freq_bits, (uint64_t *)mixed, &mx);
 }
 
 extern "C" hs_status hs_batch_step(hs_batch *b, const hs_input *in, size_t n) {
@@ -1260,14 +1429,72 @@ extern "C" hs_status hs_device_copy(hs_device *dev, void *dst, const void *src, 
     return HS_OK;
 }
 
-extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t rows, size_t vocab,
-                                 const uint64_t *table, size_t len, const hs_query *queries,
-                                 uint32_t freq_bits, hs_interval *out) {
+// mixed_intervals_of_weights (crates/hardshell-cuda/src/mixed.rs:160-233): the statistics
+// kernel and the mixed coder kernel on given weights, with the host mixer between them.
+extern "C" hs_status hs_op_mixed_coder(hs_device *dev, const uint64_t *weights, size_t rows, size_t vocab,
+                                       const hs_query *queries, const uint32_t *predictions,
+                                       uint32_t freq_bits, hs_mixer_fn mixer, void *user,
+                                       hs_mix_stats *stats, hs_interval *out) {
     hs::clear_error();
+    if (!dev || (rows && (!weights || !queries || !predictions || !out)))
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (rows == 0) return HS_OK;
+    if (vocab == 0 || vocab > (1u << 30)) return hs::fail(HS_UNSUPPORTED, 0, "the vocabulary is too large");
+    std::vector<uint32_t> q;
+    HS_TRY(coder_words(queries, rows, (uint32_t)vocab, freq_bits, q));
+    HS_TRY(check_tables(predictions, rows, (uint32_t)vocab, false));
+    if (!mixer && needs_mixer(predictions, rows)) return hs::fail(HS_INVALID_ARGUMENT, 0, "mixer is NULL");
+    for (size_t r = 0; r < rows; r++) {  // each row's sum below 2^64
+        uint64_t sum = 0;
+        for (size_t j = 0; j < vocab; j++)
+            if (__builtin_add_overflow(sum, weights[r * vocab + j], &sum))
+                return hs::fail(HS_UNSUPPORTED, 0, "a weight sum is 2^64 or more");
+    }
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    DevMem mem;
+    uint64_t *dw, *dst, *di;
+    uint32_t *dq;
+    hs::MixRec *dm;
+    std::vector<hs::MixRec> rec(rows);
+    for (size_t r = 0; r < rows; r++) rec[r] = hs::MixRec{predictions[r], 0, 0, 0, 0, 0};
+    HS_TRY(mem.upload(dw, weights, rows * vocab));
+    HS_TRY(mem.upload(dq, q.data(), q.size()));
+    HS_TRY(mem.upload(dm, rec.data(), rows));
+    HS_TRY(mem.alloc(dst, 3 * rows));
+    HS_TRY(mem.alloc(di, 3 * rows));
+    hs::CoderArgs ca;
+    ca.wsrc = dw; ca.vocab = (int)vocab; ca.queries = dq; ca.bits = (int)freq_bits; ca.intervals = di;
+    ca.mix = dm; ca.stats = dst;
+    HIP_TRY(hs::launch_mix_stats(ca, (int)rows, dev->stream));
+    std::vector<uint64_t> sv(3 * rows);
+    HIP_TRY(hipMemcpyAsync(sv.data(), dst, 24 * rows, hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    for (size_t r = 0; r < rows; r++) {
+        const hs_mix_stats st{sv[3 * r], sv[3 * r + 1], (uint32_t)sv[3 * r + 2], 0};
+        if (stats) stats[r] = st;
+        if (predictions[r] == HS_MIX_NONE) continue;
+        HS_TRY(mix_record(st, predictions[r], mixer(user, r, &st), rec[r]));
+    }
+    HIP_TRY(hipMemcpyAsync(dm, rec.data(), rows * sizeof(hs::MixRec), hipMemcpyHostToDevice, dev->stream));
+    HIP_TRY(hs::launch_coder_mixed(ca, (int)rows, dev->stream));
+    HIP_TRY(hipMemcpyAsync(out, di, 24 * rows, hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
+}
+
+namespace {
+
+// The coder op on given i64 logits (the compact form when the table has at most
+// CODER_MAX_TABLE entries, else the i64 kernel): plain, or with `predictions` the mixer
+// statistics, the host mixer and the mixed coder (the three weight sources of
+// crates/hardshell-cuda/kernels/hardshell.cu:1682-1814).
+hs_status coder_on_logits(hs_device *dev, const int64_t *logits, size_t rows, size_t vocab,
+                          const uint64_t *table, size_t len, const hs_query *queries, uint32_t freq_bits,
+                          const uint32_t *predictions, hs_mixer_fn mixer, void *user,
+                          hs_mix_stats *stats, hs_interval *out) {
     if (!dev || !logits || !table || !queries || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
     if (rows == 0) return HS_OK;
-    if (vocab == 0 || vocab > (1u << 20) || len == 0 || freq_bits == 0 || freq_bits > 32 ||
-        (uint64_t)vocab > (1ull << freq_bits))
+    if (vocab == 0 || vocab > (1u << 20) || len == 0)
         return hs::fail(HS_UNSUPPORTED, 0, "vocab in 1..=2^20, len >= 1, freq_bits in 1..=32 with 2^freq_bits >= vocab");
     // The table rule of the model loader's logits table (crates/hardshell/src/logits.rs:38-49):
     // non-increasing, first entry >= 1, entries <= 2^40.
@@ -1275,22 +1502,31 @@ extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t r
         return hs::fail(HS_UNSUPPORTED, 0, "the table must start in 1..=2^40");
     for (size_t i = 1; i < len; i++)
         if (table[i] > table[i - 1]) return hs::fail(HS_UNSUPPORTED, 0, "the table must be non-increasing");
-    std::vector<uint32_t> q(2 * rows);
-    for (size_t r = 0; r < rows; r++) {
-        const bool ok = (queries[r].kind == 0 && queries[r].value < vocab) ||
-                        (queries[r].kind == 1 && (uint64_t)queries[r].value < (1ull << freq_bits));
-        if (!ok) return hs::fail(HS_UNSUPPORTED, 0, "a coder token or target is out of range");
-        q[2 * r] = queries[r].kind;
-        q[2 * r + 1] = queries[r].value;
+    std::vector<uint32_t> q;
+    HS_TRY(coder_words(queries, rows, (uint32_t)vocab, freq_bits, q));
+    if (predictions) {
+        HS_TRY(check_tables(predictions, rows, (uint32_t)vocab, true));
+        if (!mixer && needs_mixer(predictions, rows)) return hs::fail(HS_INVALID_ARGUMENT, 0, "mixer is NULL");
     }
     HIP_TRY(hipSetDevice(dev->ordinal));
     DevMem mem;
-    uint64_t *dt, *di;
+    uint64_t *dt, *di, *dst = nullptr;
     uint32_t *dq;
-    hs_status s;
-    if ((s = mem.upload(dt, table, len)) != HS_OK) return s;
-    if ((s = mem.upload(dq, q.data(), q.size())) != HS_OK) return s;
-    if ((s = mem.alloc(di, 3 * rows)) != HS_OK) return s;
+    hs::MixRec *dm = nullptr;
+    std::vector<hs::MixRec> rec(predictions ? rows : 0);
+    for (size_t r = 0; r < rec.size(); r++) rec[r] = hs::MixRec{predictions[r], 0, 0, 0, 0, 0};
+    HS_TRY(mem.upload(dt, table, len));
+    HS_TRY(mem.upload(dq, q.data(), q.size()));
+    HS_TRY(mem.alloc(di, 3 * rows));
+    if (predictions) {
+        HS_TRY(mem.upload(dm, rec.data(), rows));
+        HS_TRY(mem.alloc(dst, 3 * rows));
+    }
+    hipStream_t st = dev->stream;
+    // launch(0): statistics, launch(1): the mixed coder, launch(2): the plain coder
+    std::function<hipError_t(int)> launch;
+    hs::CompactCoderArgs cca;
+    hs::CoderArgs ca;
     if (len <= (size_t)hs::CODER_MAX_TABLE) {
         // the compact form the LM head writes: the max of each 64-column tile and
         // min(tilemax - l, len - 1) as u16
@@ -1307,27 +1543,69 @@ extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t r
             }
         uint16_t *d16;
         int64_t *dtm;
-        if ((s = mem.upload(d16, dd.data(), dd.size())) != HS_OK) return s;
-        if ((s = mem.upload(dtm, tm.data(), tm.size())) != HS_OK) return s;
+        HS_TRY(mem.upload(d16, dd.data(), dd.size()));
+        HS_TRY(mem.upload(dtm, tm.data(), tm.size()));
         int d0 = 0;
         while ((size_t)d0 + 1 < len && table[d0 + 1] == table[0]) d0++;
         int zcut = (int)len;
         while (zcut > 1 && table[zcut - 1] == 0) zcut--;
-        hs::CompactCoderArgs ca;
-        ca.d16 = d16; ca.ld16 = (int)ld16; ca.tmax = dtm; ca.ntiles = (int)nt; ca.vocab = (int)vocab;
-        ca.table = dt; ca.table_len = (int)len; ca.d0 = d0; ca.zcut = zcut; ca.queries = dq;
-        ca.bits = (int)freq_bits;
-        ca.intervals = di;
-        HIP_TRY(hs::launch_coder_compact(ca, (int)rows, dev->stream));
+        cca.d16 = d16; cca.ld16 = (int)ld16; cca.tmax = dtm; cca.ntiles = (int)nt; cca.vocab = (int)vocab;
+        cca.table = dt; cca.table_len = (int)len; cca.d0 = d0; cca.zcut = zcut; cca.queries = dq;
+        cca.bits = (int)freq_bits; cca.intervals = di; cca.mix = dm; cca.stats = dst;
+        launch = [&](int what) {
+            if (what == 0) return hs::launch_mix_stats_compact(cca, (int)rows, st);
+            if (what == 1) return hs::launch_coder_compact_mixed(cca, (int)rows, st);
+            return hs::launch_coder_compact(cca, (int)rows, st);
+        };
     } else {
         int64_t *dl;
-        if ((s = mem.upload(dl, logits, rows * vocab)) != HS_OK) return s;
-        hs::CoderArgs ca;
+        HS_TRY(mem.upload(dl, logits, rows * vocab));
         ca.logits = dl; ca.ld = (int)vocab; ca.vocab = (int)vocab; ca.table = dt; ca.table_len = (int)len;
-        ca.queries = dq; ca.bits = (int)freq_bits; ca.intervals = di;
-        HIP_TRY(hs::launch_coder(ca, (int)rows, dev->stream));
+        ca.queries = dq; ca.bits = (int)freq_bits; ca.intervals = di; ca.mix = dm; ca.stats = dst;
+        launch = [&](int what) {
+            if (what == 0) return hs::launch_mix_stats(ca, (int)rows, st);
+            if (what == 1) return hs::launch_coder_mixed(ca, (int)rows, st);
+            return hs::launch_coder(ca, (int)rows, st);
+        };
     }
-    HIP_TRY(hipMemcpyAsync(out, di, rows * 24, hipMemcpyDeviceToHost, dev->stream));
-    HIP_TRY(hipStreamSynchronize(dev->stream));
+    if (predictions) {
+        HIP_TRY(launch(0));
+        std::vector<uint64_t> sv(3 * rows);
+        HIP_TRY(hipMemcpyAsync(sv.data(), dst, 24 * rows, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+        for (size_t r = 0; r < rows; r++) {
+            const hs_mix_stats s{sv[3 * r], sv[3 * r + 1], (uint32_t)sv[3 * r + 2], 0};
+            if (stats) stats[r] = s;
+            if (predictions[r] == HS_MIX_NONE || predictions[r] == HS_MIX_PLAIN) continue;
+            HS_TRY(mix_record(s, predictions[r], mixer(user, r, &s), rec[r]));
+        }
+        HIP_TRY(hipMemcpyAsync(dm, rec.data(), rows * sizeof(hs::MixRec), hipMemcpyHostToDevice, st));
+        HIP_TRY(launch(1));
+    } else {
+        HIP_TRY(launch(2));
+    }
+    HIP_TRY(hipMemcpyAsync(out, di, rows * 24, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
     return HS_OK;
+}
+
+}  // namespace
+
+extern "C" hs_status hs_op_coder(hs_device *dev, const int64_t *logits, size_t rows, size_t vocab,
+                                 const uint64_t *table, size_t len, const hs_query *queries,
+                                 uint32_t freq_bits, hs_interval *out) {
+    hs::clear_error();
+    return coder_on_logits(dev, logits, rows, vocab, table, len, queries, freq_bits, nullptr, nullptr,
+                           nullptr, nullptr, out);
+}
+
+extern "C" hs_status hs_op_mixed_coder_logits(hs_device *dev, const int64_t *logits, size_t rows,
+                                              size_t vocab, const uint64_t *table, size_t len,
+                                              const hs_query *queries, const uint32_t *tables,
+                                              uint32_t freq_bits, hs_mixer_fn mixer, void *user,
+                                              hs_mix_stats *stats, hs_interval *out) {
+    hs::clear_error();
+    if (rows && !tables) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    return coder_on_logits(dev, logits, rows, vocab, table, len, queries, freq_bits, tables, mixer, user,
+                           stats, out);
 }

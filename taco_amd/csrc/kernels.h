@@ -133,8 +133,19 @@ struct AttnGroup {
 hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups,
                                 hipStream_t stream);
 
+// The mix record of a row for the mixed coder op of the logs profile (8 u32 words, the layout of
+// crates/hardshell-cuda/src/mixed.rs:54-90): the predicted token p (MIX_NONE: no prediction,
+// weights max(1, w); MIX_PLAIN: the weights of GPT-2 alone), k and m of rule 5 (w'[i] = max(1,
+// (w[i] m) >> k) for i != p) and w'[p].
+constexpr uint32_t MIX_NONE = 0xFFFFFFFFu, MIX_PLAIN = 0xFFFFFFFEu;
+struct MixRec {
+    uint32_t p, k, m, pad0;
+    uint64_t wp, pad1;
+};
+
 struct CoderArgs {
     const int64_t *logits = nullptr;  // [rows, ld]
+    const uint64_t *wsrc = nullptr;   // instead of logits + table: the weights [rows, vocab]
     int ld = 0;
     int vocab = 0;
     const uint64_t *table = nullptr;  // logits_exp
@@ -143,8 +154,14 @@ struct CoderArgs {
     int bits = 32;
     uint64_t *intervals = nullptr;  // [rows][3]
     uint64_t *weights = nullptr;    // optional [rows, vocab]: the weights themselves
+    const MixRec *mix = nullptr;    // launch_mix_stats: p of each row; launch_coder_mixed: records
+    uint64_t *stats = nullptr;      // launch_mix_stats: [rows][3] = sum w, w[p], top
 };
 hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream);
+// The statistics of pass 1 of taco_match::Mixer::mix (crates/taco-match/src/mixer.rs:278-288)
+// of each row's GPT-2 weights, and the coder op on the mixed weights of each row's record.
+hipError_t launch_mix_stats(const CoderArgs &a, int n_rows, hipStream_t stream);
+hipError_t launch_coder_mixed(const CoderArgs &a, int n_rows, hipStream_t stream);
 
 // The coder op over compact logits (the LogitsCompact GEMM epilogue): d16 [rows, ld16] u16 and
 // tmax [rows, ntiles] i64, with a non-increasing table of table_len <= CODER_MAX_TABLE entries.
@@ -163,7 +180,11 @@ struct CompactCoderArgs {
     int bits = 32;
     uint64_t *intervals = nullptr;
     uint64_t *weights = nullptr;
+    const MixRec *mix = nullptr;  // as CoderArgs
+    uint64_t *stats = nullptr;
 };
 hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream);
+hipError_t launch_mix_stats_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream);
+hipError_t launch_coder_compact_mixed(const CompactCoderArgs &a, int n_rows, hipStream_t stream);
 
 }  // namespace hs

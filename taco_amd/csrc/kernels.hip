@@ -1285,6 +1285,36 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
 // =============================================================================================
 
 
+// The weight of symbol j of a row: the table entry of its logit (SRC 0) or given weights
+// (SRC 1); MODE 2 maps it by the row's mix record (mixer.rs:491-516): max(1, w) without a
+// prediction, w'[p] for the prediction, max(1, (w m) >> k) for the others (an exact u128
+// product: given weights may reach 2^64 - 1).
+template <int SRC, int MODE>
+struct RowWeights {
+    const int64_t *l;
+    const uint64_t *w;
+    const uint64_t *table;
+    int64_t M;
+    int last;
+    MixRec rec;
+    __device__ __forceinline__ uint64_t base(int j) const {
+        if (SRC == 1) return w[j];
+        const int64_t dd = M - l[j];
+        return table[dd < last ? dd : last];
+    }
+    __device__ __forceinline__ uint64_t at(int j) const {
+        const uint64_t v = base(j);
+        if (MODE != 2 || rec.p == MIX_PLAIN) return v;
+        if (rec.p == MIX_NONE) return v > 1 ? v : 1;
+        if ((uint32_t)j == rec.p) return rec.wp;
+        const u128 x = ((u128)v * rec.m) >> rec.k;
+        return x > 1 ? (uint64_t)x : 1;
+    }
+};
+
+// MODE 0: the coder op; 1: the mixer statistics (sum w, w[p], top) of each row; 2: the coder op
+// on the mixed weights of each row's record.
+template <int SRC, int MODE>
 __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
     __shared__ int64_t s_i64[256];
     __shared__ uint64_t s_u64[256];
@@ -1295,27 +1325,32 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
     const int V = a.vocab;
     const int chunk = (V + 255) / 256;
     const int j0 = tid * chunk, j1 = min(V, j0 + chunk);
-    const int64_t *l = a.logits + (size_t)row * a.ld;
-    const int last = a.table_len - 1;
+    RowWeights<SRC, MODE> rw;
+    rw.l = SRC == 0 ? a.logits + (size_t)row * a.ld : nullptr;
+    rw.w = SRC == 1 ? a.wsrc + (size_t)row * V : nullptr;
+    rw.table = a.table;
+    rw.last = a.table_len - 1;
+    rw.M = 0;
+    if (MODE != 0) rw.rec = a.mix[row];
 
-    // pass 1: the largest logit
-    int64_t mx = INT64_MIN;
-    for (int j = j0; j < j1; j++) mx = l[j] > mx ? l[j] : mx;
-    s_i64[tid] = mx;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) s_i64[tid] = s_i64[tid + o] > s_i64[tid] ? s_i64[tid + o] : s_i64[tid];
+    if (SRC == 0) {  // pass 1: the largest logit
+        int64_t mx = INT64_MIN;
+        for (int j = j0; j < j1; j++) mx = rw.l[j] > mx ? rw.l[j] : mx;
+        s_i64[tid] = mx;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) s_i64[tid] = s_i64[tid + o] > s_i64[tid] ? s_i64[tid + o] : s_i64[tid];
+            __syncthreads();
+        }
+        rw.M = s_i64[0];
         __syncthreads();
     }
-    const int64_t M = s_i64[0];
-    __syncthreads();
     // pass 2: W = sum w and the largest weight (the lowest id on a tie)
     uint64_t W = 0, best = 0;
     uint32_t bidx = 0xFFFFFFFFu;
     for (int j = j0; j < j1; j++) {
-        const int64_t dd = M - l[j];
-        const uint64_t w = a.table[dd < last ? dd : last];
-        if (a.weights) a.weights[(size_t)row * V + j] = w;
+        const uint64_t w = MODE == 1 ? rw.base(j) : rw.at(j);
+        if (MODE == 0 && a.weights) a.weights[(size_t)row * V + j] = w;
         W += w;
         if (bidx == 0xFFFFFFFFu || w > best) {
             best = w;
@@ -1340,6 +1375,16 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
         }
         __syncthreads();
     }
+    if (MODE == 1) {  // mixer.rs:278-288: top is token 0 when every weight is 0
+        if (tid == 0) {
+            const uint32_t p = rw.rec.p;
+            uint64_t *st = a.stats + 3 * (size_t)row;
+            st[0] = s_u64[0];
+            st[1] = p < (uint32_t)V ? rw.base((int)p) : 0;
+            st[2] = s_u64[0] == 0 ? 0 : s_idx[0];
+        }
+        return;
+    }
     if (tid == 0) {
         uint64_t Wt = s_u64[0];
         uint32_t largest = s_idx[0];
@@ -1363,8 +1408,7 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
     // pass 3: the sum of f over the chunk, and over the symbols below the encode token
     uint64_t F = 0, Fbelow = 0, ftok = 0;
     for (int j = j0; j < j1; j++) {
-        const int64_t dd = M - l[j];
-        const uint64_t w = all_zero ? 1 : a.table[dd < last ? dd : last];
+        const uint64_t w = all_zero ? 1 : rw.at(j);
         const uint64_t f = 1 + quotient(w, spare, Wt, frac);
         F += f;
         if (kind == 0 && (uint32_t)j < value) Fbelow += f;
@@ -1406,8 +1450,7 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
     int cand = -1;
     uint64_t cstart = 0, cfreq = 0;
     for (int j = j0; j < j1; j++) {
-        const int64_t dd = M - l[j];
-        const uint64_t w = all_zero ? 1 : a.table[dd < last ? dd : last];
+        const uint64_t w = all_zero ? 1 : rw.at(j);
         const uint64_t f = 1 + quotient(w, spare, Wt, frac);
         const uint64_t start = run + ((uint32_t)j > largest ? rem : 0);
         run += f;
@@ -1433,10 +1476,25 @@ __global__ __launch_bounds__(256) void k_coder(CoderArgs a) {
     }
 }
 
-hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream) {
+template <int MODE>
+static hipError_t launch_coder_mode(const CoderArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_coder, dim3(n_rows), dim3(256), 0, stream, a);
+    if (MODE != 0 && !a.mix) return hipErrorInvalidValue;
+    if (a.wsrc)
+        hipLaunchKernelGGL((k_coder<1, MODE>), dim3(n_rows), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((k_coder<0, MODE>), dim3(n_rows), dim3(256), 0, stream, a);
     return hipGetLastError();
+}
+
+hipError_t launch_coder(const CoderArgs &a, int n_rows, hipStream_t stream) {
+    return launch_coder_mode<0>(a, n_rows, stream);
+}
+hipError_t launch_mix_stats(const CoderArgs &a, int n_rows, hipStream_t stream) {
+    return a.stats ? launch_coder_mode<1>(a, n_rows, stream) : hipErrorInvalidValue;
+}
+hipError_t launch_coder_mixed(const CoderArgs &a, int n_rows, hipStream_t stream) {
+    return launch_coder_mode<2>(a, n_rows, stream);
 }
 
 
@@ -1499,6 +1557,9 @@ __device__ __forceinline__ uint64_t block_sum64w(uint64_t v, uint64_t *s4, int t
 // bins with a nonzero weight); with V < 2^16 the count and the count below the Encode token
 // share one u32 (low and high half), else they are two arrays. Symbols with d >= zcut have
 // weight 0, f = 1 and no share of the spare, and need no count.
+// STATS: the mixer statistics of the row (sum w, w[p] for the record's p, the top token = the
+// largest) instead of the coder interval.
+template <bool STATS>
 __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     extern __shared__ uint32_t hist[];
     __shared__ int64_t s_i[256];
@@ -1512,13 +1573,13 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     const int64_t *tm = a.tmax + (size_t)row * a.ntiles;
     const uint32_t kind = a.queries ? a.queries[2 * row] : 0;
     const uint32_t value = a.queries ? a.queries[2 * row + 1] : 0;
-    const uint32_t tok = kind == 0 ? value : 0;  // Encode token (0: no symbol below)
+    const uint32_t tok = kind == 0 && !STATS ? value : 0;  // Encode token (0: no symbol below)
 
     int64_t mx = INT64_MIN;
     for (int t = tid; t < a.ntiles; t += 256) mx = tm[t] > mx ? tm[t] : mx;
     const int64_t M = block_max64w(mx, s_i, tid);
     for (int d = tid; d < (packed ? zc : 2 * zc); d += 256) hist[d] = 0;
-    if (a.weights) {  // the weights themselves (run_weights)
+    if (!STATS && a.weights) {  // the weights themselves (run_weights)
         for (int j = tid; j < V; j += 256) {
             const int64_t dd = M - tm[j >> 6] + d16[j];
             a.weights[(size_t)row * V + j] = a.table[dd < last ? dd : last];
@@ -1569,6 +1630,21 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
         W += (uint64_t)c * a.table[d];
     }
     W = block_sum64w(W, s_u, tid);
+    if (STATS) {  // mixer.rs:278-288 (W >= table[0] >= 1, so top is the largest)
+        if (tid == 0) {
+            const uint32_t p = a.mix[row].p;
+            uint64_t wp = 0;
+            if (p < (uint32_t)V) {
+                const int64_t dp = M - tm[p >> 6] + d16[p];
+                wp = a.table[dp < last ? dp : last];
+            }
+            uint64_t *st = a.stats + 3 * (size_t)row;
+            st[0] = W;
+            st[1] = wp;
+            st[2] = (uint64_t)largest;
+        }
+        return;
+    }
     const uint64_t total = (uint64_t)1 << a.bits, spare = total - (uint64_t)V;
     if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0;
     __syncthreads();
@@ -1660,18 +1736,270 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     }
 }
 
-hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
+// The mixed coder op over compact logits: k_coder_compact with the weights of each row's mix
+// record (mixer.rs:256-292, 491-516). The histogram leaves out the predicted token p; the
+// weight of bin d is g(d) = max(1, (table[d] m) >> k) (max(1, table[d]) without a prediction,
+// table[d] for a plain row), non-increasing in d, and every symbol with d >= zcut (table 0)
+// weighs g_rest = 1 (0 for a plain row), counted as V - (p) - the binned symbols. Then
+//   W' = sum_d cnt[d] g(d) + n_rest g_rest + w'[p],
+//   sum_{j<tok} f = tok + sum_d cnt_lo[d] q(g(d)) + rest_lo q(g_rest) + [p < tok] q(w'[p]).
+// The largest weight of the others is g of their smallest bin; the first symbol other than p
+// whose weight reaches it (d <= dthr) comes from a pass that skips tiles by their max, and
+// competes with w'[p] (the lower id on a tie).
+__global__ __launch_bounds__(256) void k_coder_compact_mixed(CompactCoderArgs a) {
+    extern __shared__ uint32_t hist[];
+    __shared__ int64_t s_i[256];
+    __shared__ uint64_t s_u[256];
+    __shared__ uint64_t s_frac;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int V = a.vocab, len = a.table_len, last = len - 1;
+    const int zc = a.zcut;
+    const bool packed = V < 65536;
+    const uint16_t *d16 = a.d16 + (size_t)row * a.ld16;
+    const int64_t *tm = a.tmax + (size_t)row * a.ntiles;
+    const uint32_t kind = a.queries ? a.queries[2 * row] : 0;
+    const uint32_t value = a.queries ? a.queries[2 * row + 1] : 0;
+    const uint32_t tok = kind == 0 ? value : 0;
+    const MixRec rec = a.mix[row];
+    const bool plain = rec.p == MIX_PLAIN, none = rec.p == MIX_NONE, has_p = !plain && !none;
+    const uint32_t p = has_p ? rec.p : 0xFFFFFFFFu;  // the host checked p < V
+    const uint32_t mk = rec.k;
+    const uint64_t mm = rec.m, wpm = rec.wp;
+    auto g = [&](int d) -> uint64_t {  // table[d] <= 2^40 and m <= 2^16: the product fits u64
+        const uint64_t w = a.table[d];
+        if (plain) return w;
+        if (none) return w > 1 ? w : 1;
+        const uint64_t v = mk < 64 ? (w * mm) >> mk : 0;
+        return v > 1 ? v : 1;
+    };
+    const uint64_t g_rest = plain ? 0 : 1;
+
+    int64_t mx = INT64_MIN;
+    for (int t = tid; t < a.ntiles; t += 256) mx = tm[t] > mx ? tm[t] : mx;
+    const int64_t M = block_max64w(mx, s_i, tid);
+    for (int d = tid; d < (packed ? zc : 2 * zc); d += 256) hist[d] = 0;
+    __syncthreads();
+    int64_t first = INT64_MAX;  // plain rows: the first symbol with weight table[0]
+    for (int g0 = tid * 8; g0 < V; g0 += 4 * 256 * 8) {
+        uint4 raw[4];
+        int64_t b64[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int gq = g0 + u * 256 * 8;
+            b64[u] = gq < V ? M - tm[gq >> 6] : (int64_t)zc;
+            if (b64[u] < zc) raw[u] = *(const uint4 *)(d16 + gq);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (b64[u] >= zc) continue;
+            const int gq = g0 + u * 256 * 8, base = (int)b64[u];
+            const uint16_t *dv = (const uint16_t *)&raw[u];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = gq + q;
+                const int dd = base + (int)dv[q];
+                if (j < V && dd < zc && (uint32_t)j != p) {
+                    if (packed) {
+                        atomicAdd(&hist[dd], (uint32_t)j < tok ? 0x10001u : 1u);
+                    } else {
+                        atomicAdd(&hist[dd], 1u);
+                        if ((uint32_t)j < tok) atomicAdd(&hist[zc + dd], 1u);
+                    }
+                    if (dd <= a.d0 && j < first) first = j;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // the binned sums, the smallest bin in use
+    uint64_t W = 0, n_in = 0, n_lo = 0;
+    int64_t dmin = INT64_MAX;
+    for (int d = tid; d < zc; d += 256) {
+        const uint32_t h = hist[d];
+        const uint32_t c = packed ? (h & 0xffffu) : h, clo = packed ? (h >> 16) : hist[zc + d];
+        W += (uint64_t)c * g(d);
+        n_in += c;
+        n_lo += clo;
+        if (c && d < dmin) dmin = d;
+    }
+    W = block_sum64w(W, s_u, tid);
+    n_in = block_sum64w(n_in, s_u, tid);
+    n_lo = block_sum64w(n_lo, s_u, tid);
+    dmin = -block_max64w(-dmin, s_i, tid);
+    const uint64_t n_rest = (uint64_t)V - (has_p ? 1 : 0) - n_in;
+    const uint64_t rest_lo = (uint64_t)tok - (has_p && p < tok ? 1 : 0) - n_lo;
+    W += n_rest * g_rest + (has_p ? wpm : 0);
+    const uint64_t total = (uint64_t)1 << a.bits, spare = total - (uint64_t)V;
+    if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0;
+    __syncthreads();
+    const uint64_t frac = s_frac;
+
+    // the largest weight (mixer weights are >= 1, so W' >= V and plain rows have W >= table[0])
+    int64_t largest;
+    if (plain) {
+        largest = -block_max64w(-first, s_i, tid);
+    } else {
+        // gmax: the largest weight among the symbols other than p; dthr: the largest d with g(d)
+        // >= gmax (a prefix, g is non-increasing); INT64_MAX when every index reaches it
+        const uint64_t gmax = dmin != INT64_MAX ? g((int)dmin) : (n_rest ? g_rest : 0);
+        int64_t dthr = -1;
+        for (int d = tid; d < len; d += 256)
+            if (g(d) >= gmax && d > dthr) dthr = d;
+        dthr = block_max64w(dthr, s_i, tid);
+        if (dthr == last) dthr = INT64_MAX;
+        int64_t fo = INT64_MAX;  // the first symbol other than p with d <= dthr
+        if (gmax) {
+            for (int g0 = tid * 8; g0 < V; g0 += 256 * 8) {
+                const int64_t base = M - tm[g0 >> 6];
+                if (base > dthr) continue;  // every symbol of the tile has d >= base
+                const uint4 raw = *(const uint4 *)(d16 + g0);
+                const uint16_t *dv = (const uint16_t *)&raw;
+                bool hit = false;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int j = g0 + q;
+                    const int64_t dd = base + dv[q];
+                    if (!hit && j < V && (uint32_t)j != p && (dd < last ? dd : last) <= dthr) {
+                        fo = j;
+                        hit = true;
+                    }
+                }
+                if (hit) break;  // this thread's later symbols are larger
+            }
+        }
+        fo = -block_max64w(-fo, s_i, tid);
+        if (!has_p) largest = fo;
+        else if (fo == INT64_MAX || wpm > gmax) largest = (int64_t)p;
+        else if (wpm == gmax) largest = (int64_t)p < fo ? (int64_t)p : fo;
+        else largest = fo;
+    }
+
+    uint64_t S = 0, Slo = 0;
+    for (int d = tid; d < zc; d += 256) {
+        const uint32_t h = hist[d];
+        const uint32_t c = packed ? (h & 0xffffu) : h, clo = packed ? (h >> 16) : hist[zc + d];
+        if (!c) continue;
+        const uint64_t q = quotient(g(d), spare, W, frac);
+        S += (uint64_t)c * q;
+        Slo += (uint64_t)clo * q;
+    }
+    S = block_sum64w(S, s_u, tid);
+    Slo = block_sum64w(Slo, s_u + 8, tid);
+    const uint64_t q_rest = g_rest ? quotient(g_rest, spare, W, frac) : 0;
+    S += n_rest * q_rest;
+    Slo += rest_lo * q_rest;
+    if (has_p) {
+        const uint64_t qp = quotient(wpm, spare, W, frac);
+        S += qp;
+        if (p < tok) Slo += qp;
+    }
+    const uint64_t rem = total - ((uint64_t)V + S);
+    uint64_t *out = a.intervals ? a.intervals + 3 * (size_t)row : nullptr;
+    if (!out) return;
+    auto weight = [&](int j, int64_t base_j, uint16_t dj) -> uint64_t {
+        if ((uint32_t)j == p) return wpm;
+        const int64_t dd = base_j + dj;
+        return g((int)(dd < last ? dd : last));
+    };
+    if (kind == 0) {
+        if (tid == 0) {
+            const uint64_t f = 1 + quotient(weight((int)tok, M - tm[tok >> 6], d16[tok]), spare, W, frac);
+            out[0] = tok;
+            out[1] = (uint64_t)tok + Slo + ((int64_t)tok > largest ? rem : 0);
+            out[2] = f + ((int64_t)tok == largest ? rem : 0);
+        }
+        return;
+    }
+    // Decode: the largest i with start_i <= target, in symbol order, 2048 symbols per step.
+    const uint64_t target = value;
+    uint64_t run = 0;
+    int64_t cand = -1;
+    uint64_t cstart = 0, cfreq = 0;
+    for (int b = 0; b < V; b += 2048) {
+        uint64_t f[8];
+        uint64_t local = 0;
+        const int j0 = b + tid * 8;
+        if (j0 < V) {
+            const uint4 raw = *(const uint4 *)(d16 + j0);
+            const uint16_t *dv = (const uint16_t *)&raw;
+            const int64_t base = M - tm[j0 >> 6];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = j0 + q;
+                f[q] = 0;
+                if (j < V) {
+                    f[q] = 1 + quotient(weight(j, base, dv[q]), spare, W, frac) + (j == largest ? rem : 0);
+                    local += f[q];
+                }
+            }
+        }
+        s_u[tid] = local;
+        __syncthreads();
+        if (tid == 0) {  // exclusive scan of the 256 partial sums, in order
+            uint64_t acc = run;
+            for (int t = 0; t < 256; t++) {
+                const uint64_t v = s_u[t];
+                s_u[t] = acc;
+                acc += v;
+            }
+            s_i[0] = (int64_t)acc;
+        }
+        __syncthreads();
+        uint64_t start = s_u[tid];
+        const uint64_t next_run = (uint64_t)s_i[0];
+        __syncthreads();
+        if (j0 < V) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = j0 + q;
+                if (j >= V) break;
+                if (start <= target) {
+                    cand = j;
+                    cstart = start;
+                    cfreq = f[q];
+                }
+                start += f[q];
+            }
+        }
+        run = next_run;
+    }
+    const int64_t best = block_max64(cand, s_i, tid);
+    if (cand >= 0 && cand == best) {
+        out[0] = (uint64_t)cand;
+        out[1] = cstart;
+        out[2] = cfreq;
+    }
+}
+
+template <typename K>
+static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows, size_t *allowed,
+                                 hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
     const size_t lds = (a.vocab < 65536 ? 1 : 2) * sizeof(uint32_t) * (size_t)a.zcut;
-    static size_t allowed = 0;  // raise the dynamic LDS limit once per size
-    if (lds > allowed) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_coder_compact,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (lds > *allowed) {  // raise the dynamic LDS limit once per size
+        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        allowed = lds;
+        *allowed = lds;
     }
-    hipLaunchKernelGGL(k_coder_compact, dim3(n_rows), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL(kernel, dim3(n_rows), dim3(256), lds, stream, a);
     return hipGetLastError();
+}
+
+hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
+    static size_t allowed = 0;
+    return launch_compact(k_coder_compact<false>, a, n_rows, &allowed, stream);
+}
+
+hipError_t launch_mix_stats_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
+    static size_t allowed = 0;
+    if (!a.mix || !a.stats) return hipErrorInvalidValue;
+    return launch_compact(k_coder_compact<true>, a, n_rows, &allowed, stream);
+}
+
+hipError_t launch_coder_compact_mixed(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
+    static size_t allowed = 0;
+    if (!a.mix) return hipErrorInvalidValue;
+    return launch_compact(k_coder_compact_mixed, a, n_rows, &allowed, stream);
 }
 
 }  // namespace hs

@@ -70,6 +70,30 @@ class _Input(C.Structure):
     _fields_ = [("slot", C.c_uint32), ("token", C.c_uint32)]
 
 
+# The mixed coder op of the logs profile (crates/hardshell-cuda/src/mixed.rs).
+HS_MIX_NONE = 0xFFFFFFFF   # a mixed table without a prediction
+HS_MIX_PLAIN = 0xFFFFFFFE  # the table of GPT-2 alone
+
+
+class MixStats(C.Structure):
+    """MixStats (mixed.rs:36-49): total = sum w, predicted = w[p], top = the largest."""
+    _fields_ = [("total", C.c_uint64), ("predicted", C.c_uint64), ("top", C.c_uint32),
+                ("pad", C.c_uint32)]
+
+
+MIXER_FN = C.CFUNCTYPE(C.c_uint32, C.c_void_p, C.c_size_t, C.POINTER(MixStats))
+
+
+def _mixer(fn):
+    """A C callback over fn(input, stats) -> q; an exception gives q = 0 (refused)."""
+    def call(_user, i, st):
+        try:
+            return int(fn(int(i), st.contents))
+        except Exception:  # noqa: BLE001 - the library reports the bad q
+            return 0
+    return MIXER_FN(call)
+
+
 class _Query(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("value", C.c_uint32)]
 
@@ -150,6 +174,10 @@ def lib() -> C.CDLL:
         L.hs_batch_model.argtypes = [P]
         L.hs_model_validate.argtypes = [P, S, P]
         L.hs_op_coder.argtypes = [P, P, S, S, P, S, P, U32, P]
+        L.hs_batch_run_coded_mixed.argtypes = [P, P, P, P, S, U32, MIXER_FN, P, P]
+        L.hs_batch_run_coded_dual.argtypes = [P, P, P, P, S, U32, MIXER_FN, P, P, P]
+        L.hs_op_mixed_coder.argtypes = [P, P, S, S, P, P, U32, MIXER_FN, P, P, P]
+        L.hs_op_mixed_coder_logits.argtypes = [P, P, S, S, P, S, P, P, U32, MIXER_FN, P, P, P]
         _lib = L
     return _lib
 
@@ -312,6 +340,31 @@ class HipBatch:
         raw = self.run_coded_raw(inputs, queries, freq_bits)
         return [CoderInterval(int(s), int(st), int(f), int(s) + 1 == self.vocab) for s, st, f in raw]
 
+    def run_coded_mixed(self, inputs, queries, tables, freq_bits, mixer) -> np.ndarray:
+        """CudaBatch::run_coded_mixed: tables[i] is HS_MIX_PLAIN, HS_MIX_NONE or the predicted
+        token; mixer(i, stats) -> q. The intervals as an [n, 3] u64 array."""
+        a = _inputs(inputs)
+        q = np.ascontiguousarray(np.asarray(queries, dtype=np.uint32).reshape(-1, 2))
+        t = np.ascontiguousarray(np.asarray(tables, dtype=np.uint32))
+        out = np.zeros((len(a), 3), np.uint64)
+        cb = _mixer(mixer)
+        _check(lib().hs_batch_run_coded_mixed(self.h, _ptr(a), _ptr(q), _ptr(t), len(a), freq_bits,
+                                              cb, None, _ptr(out)))
+        return out
+
+    def run_coded_dual(self, inputs, tokens, predictions, freq_bits, mixer):
+        """CudaBatch::run_coded_dual: (plain, mixed) intervals as two [n, 3] u64 arrays;
+        predictions[i] is a token or HS_MIX_NONE."""
+        a = _inputs(inputs)
+        tk = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+        pr = np.ascontiguousarray(np.asarray(predictions, dtype=np.uint32))
+        plain = np.zeros((len(a), 3), np.uint64)
+        mixed = np.zeros((len(a), 3), np.uint64)
+        cb = _mixer(mixer)
+        _check(lib().hs_batch_run_coded_dual(self.h, _ptr(a), _ptr(tk), _ptr(pr), len(a), freq_bits,
+                                             cb, None, _ptr(plain), _ptr(mixed)))
+        return plain, mixed
+
     def step(self, inputs):
         a = _inputs(inputs)
         _check(lib().hs_batch_step(self.h, _ptr(a), len(a)))
@@ -391,6 +444,42 @@ def gemm_layout(m: int, n: int, k: int) -> Tuple[int, int, int]:
     a, b, c = C.c_size_t(), C.c_size_t(), C.c_size_t()
     lib().hs_op_gemm_layout(m, n, k, C.byref(a), C.byref(b), C.byref(c))
     return a.value, b.value, c.value
+
+
+def mixed_intervals_of_weights(dev: HipDevice, weights: np.ndarray, queries, predictions,
+                               freq_bits: int, mixer):
+    """mixed_intervals_of_weights (mixed.rs:160-233): the statistics [rows, 3] (total,
+    predicted, top) and the intervals [rows, 3] of the mixed tables of given weights."""
+    w = np.ascontiguousarray(weights, dtype=np.uint64)
+    rows, vocab = w.shape
+    q = np.ascontiguousarray(np.asarray(queries, dtype=np.uint32).reshape(-1, 2))
+    pr = np.ascontiguousarray(np.asarray(predictions, dtype=np.uint32))
+    stats = (MixStats * rows)()
+    out = np.zeros((rows, 3), np.uint64)
+    cb = _mixer(mixer)
+    _check(lib().hs_op_mixed_coder(dev.h, _ptr(w), rows, vocab, _ptr(q), _ptr(pr), freq_bits, cb,
+                                   None, C.cast(stats, C.c_void_p), _ptr(out)))
+    st = np.array([[s.total, s.predicted, s.top] for s in stats], dtype=np.uint64).reshape(rows, 3)
+    return st, out
+
+
+def mixed_coder_logits(dev: HipDevice, logits: np.ndarray, table: np.ndarray, queries, tables,
+                       freq_bits: int, mixer):
+    """The mixed coder op on given i64 logits [rows, vocab] and a logits table (the compact
+    form for tables of at most 16,384 entries): statistics [rows, 3] and intervals [rows, 3]."""
+    logits = np.ascontiguousarray(logits, dtype=np.int64)
+    table = np.ascontiguousarray(table, dtype=np.uint64)
+    rows, vocab = logits.shape
+    q = np.ascontiguousarray(np.asarray(queries, dtype=np.uint32).reshape(-1, 2))
+    t = np.ascontiguousarray(np.asarray(tables, dtype=np.uint32))
+    stats = (MixStats * rows)()
+    out = np.zeros((rows, 3), np.uint64)
+    cb = _mixer(mixer)
+    _check(lib().hs_op_mixed_coder_logits(dev.h, _ptr(logits), rows, vocab, _ptr(table), len(table),
+                                          _ptr(q), _ptr(t), freq_bits, cb, None,
+                                          C.cast(stats, C.c_void_p), _ptr(out)))
+    st = np.array([[s.total, s.predicted, s.top] for s in stats], dtype=np.uint64).reshape(rows, 3)
+    return st, out
 
 
 def coder(dev: HipDevice, logits: np.ndarray, table: np.ndarray, queries, freq_bits: int = 32
