@@ -1034,6 +1034,282 @@ bool read_varint(const uint8_t *b, size_t len, uint64_t &value, size_t &used) {
 
 }  // namespace
 
+// ============================================================================================
+// 8b. The logs profile: the match model and the mixer of one block, mixer rule version 1
+//     (crates/taco-match/src/{logistic,matcher,mixer,skip}.rs; crates/taco/src/mix.rs).
+// ============================================================================================
+
+namespace {
+
+// logistic.rs:25-75: squash over x in -4095..=4095 (units of 1/256 nat) from E[j] = 2^62
+// exp(-j/256) by a rounded recurrence, and stretch(p) = the smallest x with squash(x) >= p.
+struct Logistic {
+    static constexpr int XM = 4095;
+    std::vector<uint16_t> sq;
+    std::vector<int16_t> st;
+    Logistic() {
+        const u128 C = (u128)4593706758521714574ull;
+        std::vector<u128> e(XM + 1);
+        e[0] = (u128)1 << 62;
+        for (int j = 0; j < XM; j++) e[j + 1] = (e[j] * C + ((u128)1 << 61)) >> 62;
+        sq.assign(2 * XM + 1, 0);
+        auto clampp = [](int64_t v) { return (uint16_t)(v < 1 ? 1 : (v > 65535 ? 65535 : v)); };
+        for (int x = 0; x <= XM; x++) {
+            const u128 d = ((u128)1 << 62) + e[x];
+            const int64_t v = (int64_t)((((u128)1 << 78) + d / 2) / d);
+            sq[XM + x] = clampp(v);
+            sq[XM - x] = clampp(65536 - v);
+        }
+        st.assign(1 << 16, 0);
+        size_t x = 0;
+        for (uint32_t q = 0; q < (1u << 16); q++) {
+            while (x < sq.size() && sq[x] < q) x++;
+            st[q] = (int16_t)((int)std::min<size_t>(x, 2 * XM) - XM);
+        }
+    }
+    uint32_t squash(int64_t x) const { return sq[(size_t)(std::min<int64_t>(std::max<int64_t>(x, -XM), XM) + XM)]; }
+    int32_t stretch(uint32_t q) const { return st[std::min<uint32_t>(q, 65535)]; }
+};
+
+const Logistic &logistic() {
+    static const Logistic t;
+    return t;
+}
+
+// skip.rs:44-62: a 22-bit hit probability moving to y 2^22 by floor(2 d / (2n + 3)).
+struct Adaptive {
+    uint32_t hit = 1u << 21;
+    uint16_t count = 0;
+    void update(bool y, uint16_t limit) {
+        const uint32_t n = count, h = hit, den = 2 * n + 3;
+        hit = y ? h + (((1u << 22) - h) * 2) / den : h - (h * 2) / den;
+        count = (uint16_t)std::min<uint32_t>(n + 1, limit);
+    }
+};
+
+// mixer.rs:470-480: L - 1 below 16, then one bucket per octave, at most 20.
+int mix_bucket(uint32_t len) {
+    if (len < 16) return (int)len - 1;
+    const int bits = 32 - __builtin_clz(len);
+    return std::min(15 + bits - 5, 20);
+}
+
+// The mixer of rule version 1 (mixer.rs:49-86 constants, :399-470 update and probability).
+struct MixerV1 {
+    static constexpr int SETS = 42;
+    Adaptive buckets[21];
+    int32_t w[SETS][3];
+    uint32_t updates[SETS];
+    bool pending = false;
+    uint32_t p_token = 0, p_q = 0;
+    int p_bucket = 0, p_set = 0;
+    int32_t p_xs[3] = {0, 0, 0};
+    MixerV1() {
+        for (int c = 0; c < SETS; c++) {
+            w[c][0] = 1 << 16;
+            w[c][1] = 1 << 16;
+            w[c][2] = 0;
+            updates[c] = 0;
+        }
+    }
+    static int64_t rate(uint32_t n) {  // max(16, floor(160 * 64 / (n + 64)))
+        const uint32_t r = 160u * 64u / (n + 64u);
+        return (int64_t)std::max<uint32_t>(r, 16);
+    }
+    // rules 2 to 5 and the pending state (mixer.rs:302-315, :452-467)
+    uint32_t mix_stats(u128 total, uint64_t wp, bool agree, uint32_t token, uint32_t len) {
+        const Logistic &t = logistic();
+        uint64_t pg = total ? (uint64_t)(((u128)wp << 16) / total) : 1;
+        pg = std::min<uint64_t>(std::max<uint64_t>(pg, 1), 65535);
+        const int b = mix_bucket(len);
+        const int32_t xs[3] = {t.stretch((uint32_t)pg), t.stretch(buckets[b].hit >> 6), 256};
+        const int set = 2 * b + (agree ? 1 : 0);
+        int64_t dot = 0;
+        for (int i = 0; i < 3; i++) dot += (int64_t)w[set][i] * xs[i];
+        int64_t x = (dot + (1 << 15)) >> 16;
+        x = std::min<int64_t>(std::max<int64_t>(x, -4095), 4095);
+        const uint32_t q = t.squash(x);
+        pending = true;
+        p_token = token;
+        p_q = q;
+        p_bucket = b;
+        p_set = set;
+        for (int i = 0; i < 3; i++) p_xs[i] = xs[i];
+        return q;
+    }
+    void clear() { pending = false; }
+    // rule 7 (mixer.rs:399-432)
+    void update(uint32_t actual) {
+        if (!pending) return;
+        pending = false;
+        const bool y = actual == p_token;
+        const int64_t err = (y ? 65536 : 0) - (int64_t)p_q;
+        const uint32_t n = updates[p_set];
+        const int64_t lr = rate(n);
+        updates[p_set] = std::min<uint32_t>(n + 1, 1u << 20);
+        for (int i = 0; i < 3; i++) {
+            const int64_t d = ((int64_t)p_xs[i] * err * lr + (1 << 19)) >> 20;
+            const int64_t v = std::min<int64_t>(std::max<int64_t>((int64_t)w[p_set][i] + d, -(1 << 22)), 1 << 22);
+            w[p_set][i] = (int32_t)v;
+        }
+        buckets[p_bucket].update(y, 255);
+    }
+};
+
+// The match model of rule version 1 (matcher.rs:40-90 constants, :318-415 rules).
+struct MatchV1 {
+    static constexpr int ORDERS = 6, HASH_BITS = 20, VERIFY = 64;
+    static constexpr uint32_t MAX_LEN = 65535;
+    static constexpr int order_of[ORDERS] = {32, 16, 8, 4, 2, 1};
+    std::vector<uint32_t> tables, hist;
+    size_t ptr = 0;
+    uint32_t len = 0;
+    MatchV1() : tables((size_t)ORDERS << HASH_BITS, 0) {}
+    bool predict(uint32_t &token, uint32_t &length) const {
+        if (len == 0 || ptr >= hist.size()) return false;
+        token = hist[ptr];
+        length = len;
+        return true;
+    }
+    void observe(uint32_t t) {
+        if (len > 0) {
+            if (ptr < hist.size() && hist[ptr] == t) {
+                ptr++;
+                len = std::min(len + 1, MAX_LEN);
+            } else {
+                len = 0;
+            }
+        }
+        hist.push_back(t);
+        const size_t i = hist.size();
+        // the slot of each order at position i (rule 1)
+        int64_t slots[ORDERS];
+        for (int o = 0; o < ORDERS; o++) slots[o] = -1;
+        uint64_t acc = 0, bk = 1;
+        int next = ORDERS;
+        for (size_t k = 1; k <= (size_t)order_of[0] && k <= i; k++) {
+            acc += ((uint64_t)hist[i - k] + 1) * bk;
+            bk *= 0x9E3779B97F4A7C15ull;
+            while (next > 0 && (size_t)order_of[next - 1] == k) {
+                const uint64_t x = (acc ^ (acc >> 32)) * 0xD6E8FEB86659FD93ull;
+                slots[next - 1] = (int64_t)(x >> (64 - HASH_BITS));
+                next--;
+            }
+        }
+        // rule 3.3: the longest verified match, longest order first
+        if (len < (uint32_t)order_of[0]) {
+            for (int o = 0; o < ORDERS; o++) {
+                if ((uint32_t)order_of[o] <= len) break;
+                if (slots[o] < 0) continue;
+                const uint32_t e = tables[((size_t)o << HASH_BITS) + (size_t)slots[o]];
+                if (e == 0) continue;
+                const size_t c = e - 1;
+                const size_t limit = std::min<size_t>(VERIFY, c);
+                uint32_t v = 0;
+                while (v < limit && hist[c - v - 1] == hist[i - v - 1]) v++;
+                if (v >= (uint32_t)order_of[o]) {
+                    ptr = c;
+                    len = v;
+                    break;
+                }
+            }
+        }
+        for (int o = 0; o < ORDERS; o++)
+            if (slots[o] >= 0) tables[((size_t)o << HASH_BITS) + (size_t)slots[o]] = (uint32_t)(i + 1);
+    }
+};
+
+// Rule 6 of Mixer::mix (mixer.rs:491-516) for the statistics total and w[p] = w_p and the
+// probability q: w'[i] = max(1, (w[i] m) >> k), then w'[p] = max(1, (R q) >> k).
+int mix_apply_q(uint64_t *w, size_t n, uint32_t p, u128 total, uint32_t q) {
+    if (p >= n) return 4;
+    if (q == 0 || q >= (1u << 16)) return 1;
+    const uint64_t wp = w[p];
+    if ((u128)wp > total) return 2;
+    u128 r = total - wp;
+    if (r < 1) r = 1;
+    unsigned bits = 0;
+    for (u128 t = r; t; t >>= 1) bits++;
+    const unsigned k = bits + 16 > 62 ? bits + 16 - 62 : 0;
+    const u128 vp = (r * (u128)q) >> k;
+    if (vp >> 64) return 3;
+    const uint32_t m = (1u << 16) - q;
+    for (size_t i = 0; i < n; i++) {
+        const u128 v = ((u128)w[i] * m) >> k;
+        w[i] = v > 1 ? (uint64_t)v : 1;  // below 2^62 for i != p (w[i] <= R)
+    }
+    w[p] = vp > 1 ? (uint64_t)vp : 1;
+    return 0;
+}
+
+// Pass 1 of Mixer::mix (mixer.rs:278-288): the u128 sum, w[p] and the first index of the
+// largest weight (0 when every weight is 0).
+void mix_pass1(const uint64_t *w, size_t n, uint32_t p, u128 &total, uint64_t &wp, size_t &top) {
+    total = 0;
+    top = 0;
+    uint64_t top_w = 0;
+    for (size_t i = 0; i < n; i++) {
+        total += w[i];
+        if (w[i] > top_w) {
+            top = i;
+            top_w = w[i];
+        }
+    }
+    wp = p < n ? w[p] : 0;
+}
+
+}  // namespace
+
+// The match model and the mixer of one block (crates/taco/src/mix.rs:30-111).
+struct or_mix_state {
+    MatchV1 model;
+    MixerV1 mixer;
+};
+
+extern "C" or_mix_state *or_mix_state_new() { return new or_mix_state(); }
+extern "C" void or_mix_state_free(or_mix_state *s) { delete s; }
+// MatchModel::predict: 1 and (token, length), or 0 without a prediction.
+extern "C" int or_mix_state_predict(const or_mix_state *s, uint32_t *token, uint32_t *length) {
+    return s->model.predict(*token, *length) ? 1 : 0;
+}
+// MixState::mix_stats (mix.rs:90-100): q from the statistics of the GPT-2 weights, 0 without a
+// prediction (the pending state is cleared then).
+extern "C" uint32_t or_mix_state_mix_stats(or_mix_state *s, uint64_t total, uint64_t predicted,
+                                           uint32_t top) {
+    uint32_t tok, len;
+    s->mixer.clear();
+    if (!s->model.predict(tok, len)) return 0;
+    return s->mixer.mix_stats(total, predicted, tok == top, tok, len);
+}
+// Mixer::mix (mixer.rs:256-292): the weights in place, with the model's prediction.
+extern "C" int or_mix_state_mix(or_mix_state *s, uint64_t *w, size_t n) {
+    uint32_t tok, len;
+    s->mixer.clear();
+    if (!s->model.predict(tok, len)) {
+        for (size_t i = 0; i < n; i++) w[i] = w[i] > 1 ? w[i] : 1;
+        return 0;
+    }
+    if (tok >= n) return -1;
+    u128 total;
+    uint64_t wp;
+    size_t top;
+    mix_pass1(w, n, tok, total, wp, top);
+    const uint32_t q = s->mixer.mix_stats(total, wp, top == tok, tok, len);
+    return mix_apply_q(w, n, tok, total, q);
+}
+// MixState::observe (mix.rs:71-74): Mixer::update, then MatchModel::observe.
+extern "C" void or_mix_state_observe(or_mix_state *s, uint32_t token) {
+    s->mixer.update(token);
+    s->model.observe(token);
+}
+// The synthetic-log vectors of crates/taco-match/tests/golden.rs:20-44 with custom match
+// parameters are not needed: rule version 1 fixes them.
+extern "C" void or_logistic_tables(uint16_t *squash, int16_t *stretch) {
+    const Logistic &t = logistic();
+    std::memcpy(squash, t.sq.data(), t.sq.size() * 2);
+    std::memcpy(stretch, t.st.data(), t.st.size() * 2);
+}
+
 extern "C" size_t or_encode_block(const or_model *m, uint32_t overlap, const uint32_t *tokens,
                                   size_t n, size_t stop, uint8_t *out, size_t cap) {
     const size_t prefix = varint_len(n);
@@ -1081,6 +1357,67 @@ extern "C" long or_decode_block(const or_model *m, uint32_t overlap, const uint8
         interval_of(st, 32, sym, start, freq);
         if (!d.decode_interval(start, freq, 32)) return -1;
         tokens[i] = (uint32_t)sym;
+        if (i + 1 < count && s.step((uint32_t)sym) != 0) return -1;
+    }
+    return (long)count;
+}
+
+// A mixed block (codec.rs:19-22, 354-370): the calls of a coded block, with the weights of the
+// match model and the mixer between the session and the table, and MixState::observe after
+// each token.
+extern "C" size_t or_encode_mixed_block(const or_model *m, uint32_t overlap, const uint32_t *tokens,
+                                        size_t n, uint8_t *out, size_t cap) {
+    or_session s(m, overlap);
+    or_mix_state ms;
+    Encoder e;
+    std::vector<uint32_t> st;
+    std::vector<uint64_t> w(m->vocab);
+    if (n > 0) {
+        if (s.step(m->eot) != 0) return (size_t)-1;
+        for (size_t i = 0; i < n; i++) {
+            if (tokens[i] >= m->vocab) return (size_t)-1;
+            std::copy(s.weights.begin(), s.weights.end(), w.begin());
+            if (or_mix_state_mix(&ms, w.data(), w.size()) != 0) return (size_t)-1;
+            from_weights(w.data(), m->vocab, 32, st);
+            uint64_t start, freq;
+            interval_of(st, 32, tokens[i], start, freq);
+            e.encode_parts(start, freq, start + freq == ((uint64_t)1 << 32), 32);
+            or_mix_state_observe(&ms, tokens[i]);
+            if (i + 1 < n && s.step(tokens[i]) != 0) return (size_t)-1;
+        }
+    }
+    std::vector<uint8_t> payload;
+    write_varint(n, payload);
+    std::vector<uint8_t> coded = e.finish();
+    payload.insert(payload.end(), coded.begin(), coded.end());
+    if (payload.size() <= cap) std::memcpy(out, payload.data(), payload.size());
+    return payload.size();
+}
+
+extern "C" long or_decode_mixed_block(const or_model *m, uint32_t overlap, const uint8_t *payload,
+                                      size_t len, uint32_t *tokens, size_t cap) {
+    uint64_t count;
+    size_t used;
+    if (!read_varint(payload, len, count, used) || count == 0 || count > cap) return -1;
+    or_decoder d;
+    d.in.assign(payload + used, payload + len);
+    for (int i = 0; i < 8; i++) d.code = (d.code << 8) | d.next();
+    or_session s(m, overlap);
+    or_mix_state ms;
+    if (s.step(m->eot) != 0) return -1;
+    std::vector<uint32_t> st;
+    std::vector<uint64_t> w(m->vocab);
+    for (uint64_t i = 0; i < count; i++) {
+        std::copy(s.weights.begin(), s.weights.end(), w.begin());
+        if (or_mix_state_mix(&ms, w.data(), w.size()) != 0) return -1;
+        from_weights(w.data(), m->vocab, 32, st);
+        const uint64_t t = d.target(32);
+        const size_t sym = find_symbol(st, t);
+        uint64_t start, freq;
+        interval_of(st, 32, sym, start, freq);
+        if (!d.decode_interval(start, freq, 32)) return -1;
+        tokens[i] = (uint32_t)sym;
+        or_mix_state_observe(&ms, (uint32_t)sym);
         if (i + 1 < count && s.step((uint32_t)sym) != 0) return -1;
     }
     return (long)count;
@@ -2013,19 +2350,13 @@ extern "C" void or_attend_decode_ref(const int8_t *q, const int8_t *kc, const in
 // first index of the largest weight, 0 when every weight is 0. out: total low, total high, w[p],
 // top.
 extern "C" void or_mix_stats(const uint64_t *w, size_t n, uint32_t p, uint64_t *out) {
-    u128 total = 0;
-    size_t top = 0;
-    uint64_t top_w = 0;
-    for (size_t i = 0; i < n; i++) {
-        total += w[i];
-        if (w[i] > top_w) {
-            top = i;
-            top_w = w[i];
-        }
-    }
+    u128 total;
+    uint64_t wp;
+    size_t top;
+    mix_pass1(w, n, p, total, wp, top);
     out[0] = (uint64_t)total;
     out[1] = (uint64_t)(total >> 64);
-    out[2] = p < n ? w[p] : 0;
+    out[2] = wp;
     out[3] = top;
 }
 
@@ -2051,25 +2382,17 @@ extern "C" int or_mix_record(uint64_t total_lo, uint64_t total_hi, uint64_t wp, 
 }
 
 // Mixer::mix's weights for the probability q (mixer.rs:256-292 with apply :491-516): without a
-// prediction (p = UINT32_MAX) every weight becomes max(1, w); else w'[i] = max(1, (w[i] m) >> k)
-// and w'[p] = max(1, (R q) >> k) with R, m, k of or_mix_record. Returns or_mix_record's codes,
-// 4 for p >= n.
+// prediction (p = UINT32_MAX) every weight becomes max(1, w); else rule 6 with the statistics of
+// w. Returns or_mix_record's codes, 4 for p >= n.
 extern "C" int or_mix_apply(uint64_t *w, size_t n, uint32_t p, uint32_t q) {
     if (p == UINT32_MAX) {
         for (size_t i = 0; i < n; i++) w[i] = w[i] > 1 ? w[i] : 1;
         return 0;
     }
     if (p >= n) return 4;
-    uint64_t st[4];
-    or_mix_stats(w, n, p, st);
-    uint32_t k = 0, m = 0;
-    uint64_t wpm = 0;
-    const int e = or_mix_record(st[0], st[1], st[2], q, &k, &m, &wpm);
-    if (e) return e;
-    for (size_t i = 0; i < n; i++) {
-        const u128 v = ((u128)w[i] * m) >> k;
-        w[i] = v > 1 ? (uint64_t)v : 1;  // below 2^62 for i != p (w[i] <= R)
-    }
-    w[p] = wpm;
-    return 0;
+    u128 total;
+    uint64_t wp;
+    size_t top;
+    mix_pass1(w, n, p, total, wp, top);
+    return mix_apply_q(w, n, p, total, q);
 }

@@ -72,6 +72,18 @@ def lib():
                                             C.c_size_t, C.c_int32, C.c_uint8, C.c_int32, C.c_uint8,
                                             P, C.c_size_t, C.c_uint8, P]
         L.or_mix_stats.argtypes = [P, C.c_size_t, C.c_uint32, P]
+        L.or_mix_state_new.restype = P
+        L.or_mix_state_free.argtypes = [P]
+        L.or_mix_state_predict.argtypes = [P, P, P]
+        L.or_mix_state_mix_stats.restype = C.c_uint32
+        L.or_mix_state_mix_stats.argtypes = [P, C.c_uint64, C.c_uint64, C.c_uint32]
+        L.or_mix_state_mix.argtypes = [P, P, C.c_size_t]
+        L.or_mix_state_observe.argtypes = [P, C.c_uint32]
+        L.or_logistic_tables.argtypes = [P, P]
+        L.or_encode_mixed_block.restype = C.c_size_t
+        L.or_encode_mixed_block.argtypes = [P, C.c_uint32, P, C.c_size_t, P, C.c_size_t]
+        L.or_decode_mixed_block.restype = C.c_long
+        L.or_decode_mixed_block.argtypes = [P, C.c_uint32, P, C.c_size_t, P, C.c_size_t]
         L.or_mix_record.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, P, P, P]
         L.or_mix_apply.argtypes = [P, C.c_size_t, C.c_uint32, C.c_uint32]
         _lib = L
@@ -221,6 +233,63 @@ def mix_apply(w, p, q):
     if e:
         raise ValueError(f"mix refused ({e})")
     return w
+
+
+class MixState:
+    """The match model and the mixer of one block, mixer rule version 1 (crates/taco/src/mix.rs)."""
+
+    def __init__(self):
+        self.h = lib().or_mix_state_new()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_mix_state_free(self.h)
+            self.h = None
+
+    def predict(self):
+        """(token, length) of the match model, or None."""
+        t, n = C.c_uint32(), C.c_uint32()
+        return (t.value, n.value) if lib().or_mix_state_predict(self.h, C.byref(t), C.byref(n)) else None
+
+    def mix_stats(self, total, predicted, top):
+        """q for the model's prediction from the statistics of the GPT-2 weights (0: none)."""
+        return lib().or_mix_state_mix_stats(self.h, total, predicted, top)
+
+    def mix(self, w):
+        """Mixer::mix of the weights with the model's prediction."""
+        w = np.array(w, dtype=np.uint64)
+        if lib().or_mix_state_mix(self.h, ptr(w), len(w)) != 0:
+            raise ValueError("mix refused")
+        return w
+
+    def observe(self, token):
+        lib().or_mix_state_observe(self.h, token)
+
+
+def logistic_tables():
+    sq = np.zeros(8191, np.uint16)
+    st = np.zeros(65536, np.int16)
+    lib().or_logistic_tables(ptr(sq), ptr(st))
+    return sq, st
+
+
+def encode_mixed_block(model, tokens, overlap=0):
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    cap = 16 + 8 * len(t)
+    out = np.zeros(cap, np.uint8)
+    n = lib().or_encode_mixed_block(model.h, overlap, ptr(t), len(t), ptr(out), cap)
+    if n == (1 << 64) - 1:
+        raise ValueError("encode failed")
+    return out[:n].tobytes()
+
+
+def decode_mixed_block(model, payload, overlap=0, cap=1 << 20):
+    p = np.frombuffer(payload, np.uint8).copy()
+    out = np.zeros(cap, np.uint32)
+    n = lib().or_decode_mixed_block(model.h, overlap, ptr(p), len(p), ptr(out), cap)
+    if n < 0:
+        raise ValueError("decode failed")
+    return out[:n].copy()
 
 
 def freq_interval(w, bits, symbol):

@@ -306,3 +306,105 @@ def test_mixed_op_on_logits_equals_the_cpu_table(dev, vocab, kind):
         total, wp, top = O.mix_stats(w, p)
         assert tuple(int(x) for x in stats[i]) == (total, wp, top), i
         assert tuple(int(x) for x in got[i]) == want_interval(w, p, qs[i], 32, queries[i]), i
+
+
+def _leb(n):
+    head = bytearray()
+    while True:
+        lo = n & 0x7F
+        n >>= 7
+        head.append(lo | (0x80 if n else 0))
+        if not n:
+            return bytes(head)
+
+
+@pytest.mark.parametrize("name", ["predicted_logs_k0", "predicted_logs_default_k", "all_kinds_logs"])
+def test_conformance_mixed_blocks_through_the_gpu(dev, name):
+    """The mixed blocks (kind 3) of the conformance/v2 logs containers, decoded on the GPU with
+    the mixed coder op (Decode queries, one row per block per call, as gpu_unfold.rs with
+    MIXED-INTEGRATION.md section 5; the host mixer is the oracle's match model and mixer of
+    crates/taco/src/mix.rs), restore their bytes; fold's dual op on the decoded tokens (all
+    rows of a block in one call, section 4) re-encodes the same payloads, and its plain
+    intervals are the coded block's."""
+    import os
+    from taco_amd import hip
+    from tests.conftest import GOLDEN
+    from tests.test_oracle import read_container, vocab_of
+    hsm = open(os.path.join(GOLDEN, "tiny.hsm"), "rb").read()
+    om, hm = O.Model(hsm), hip.HipModel.load(dev, hsm)
+    vocab = vocab_of(hsm)
+    data = open(os.path.join(GOLDEN, name + ".taco"), "rb").read()
+    original = open(os.path.join(GOLDEN, name + ".in"), "rb").read()
+    c = read_container(data)
+    blocks = [(i, p) for i, (k, p) in enumerate(c["blocks"]) if k == 3]
+    assert blocks
+    n_b = len(blocks)
+    b = hip.HipBatch(hm, n_b, 64)
+    b.set_overlap(c["overlap"])
+    decs, counts, toks, states = [], [], [], []
+    for _, payload in blocks:
+        n, used, shift = 0, 0, 0
+        while True:
+            byte = payload[used]
+            n |= (byte & 0x7F) << shift
+            used += 1
+            shift += 7
+            if byte < 0x80:
+                break
+        decs.append(O.Decoder(payload[used:]))
+        counts.append(n)
+        toks.append([])
+        states.append(O.MixState())
+    nxt = [om.eot] * n_b
+    while any(len(toks[s]) < counts[s] for s in range(n_b)):
+        live = [s for s in range(n_b) if len(toks[s]) < counts[s]]
+        preds = [states[s].predict() for s in live]
+        tables = [p[0] if p else hip.HS_MIX_NONE for p in preds]
+
+        def mixer(i, st):  # the host step of unfold: mix_stats only (the token is not known)
+            return states[live[i]].mix_stats(int(st.total), int(st.predicted), int(st.top))
+
+        got = b.run_coded_mixed([(s, nxt[s]) for s in live], [(1, decs[s].target(32)) for s in live],
+                                tables, 32, mixer)
+        for s, (sym, start, freq) in zip(live, got):
+            decs[s].decode_interval(int(start), int(freq), 32)
+            states[s].observe(int(sym))
+            toks[s].append(int(sym))
+            nxt[s] = int(sym)
+    for s, (i, payload) in enumerate(blocks):
+        piece = original[i * c["block_size"]:(i + 1) * c["block_size"]]
+        assert b"".join(vocab[t] for t in toks[s]) == piece, s
+    # fold: every row of every block in one dual call; the match model runs ahead (it depends
+    # only on the tokens), the mixer steps in input order inside the host step
+    b2 = hip.HipBatch(hm, n_b, 512)
+    b2.set_overlap(c["overlap"])
+    inputs, tokens, predictions, owner = [], [], [], []
+    for s in range(n_b):
+        ahead = O.MixState()
+        for j, t in enumerate(toks[s]):
+            p = ahead.predict()
+            inputs.append((s, om.eot if j == 0 else toks[s][j - 1]))
+            tokens.append(t)
+            predictions.append(p[0] if p else hip.HS_MIX_NONE)
+            owner.append((s, j))
+            ahead.observe(t)
+    mixers = [O.MixState() for _ in range(n_b)]
+    done = [0] * n_b  # tokens each block's mixer has observed
+
+    def dual_mixer(i, st):
+        s, j = owner[i]
+        while done[s] < j:  # rows without a prediction had no call: observe them now
+            mixers[s].observe(toks[s][done[s]])
+            done[s] += 1
+        q = mixers[s].mix_stats(int(st.total), int(st.predicted), int(st.top))
+        mixers[s].observe(toks[s][j])
+        done[s] = j + 1
+        return q
+
+    plain, mixed = b2.run_coded_dual(inputs, tokens, predictions, 32, dual_mixer)
+    for s, (i, payload) in enumerate(blocks):
+        rows = [r for r, (ss, _) in enumerate(owner) if ss == s]
+        ops = [[0, int(mixed[r][1]), int(mixed[r][2]), 32] for r in rows]
+        assert _leb(len(rows)) + O.encode_script(ops) == payload, s
+        ops = [[0, int(plain[r][1]), int(plain[r][2]), 32] for r in rows]
+        assert _leb(len(rows)) + O.encode_script(ops) == O.encode_block(om, toks[s], overlap=c["overlap"])

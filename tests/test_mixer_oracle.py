@@ -90,3 +90,113 @@ def test_mixed_table_interval():
     mw = O.mix_apply(w, 3, 49152)  # q = 3/4
     start, freq = O.freq_interval(mw, 20, 3)
     assert abs(freq / (1 << 20) - 0.75) < 1e-4
+
+
+# ---------------------------------------------------------------------------------------------
+# The match model and the mixer of the logs profile, mixer rule version 1: the golden vectors of
+# crates/taco-match (logistic tables, the synthetic log of tests/golden.rs) and the mixed blocks
+# of the conformance/v2 containers.
+
+import hashlib
+import os
+
+from tests.conftest import GOLDEN
+from tests.test_oracle import read_container, vocab_of
+
+M64 = (1 << 64) - 1
+
+
+class SplitMix64:
+    """crates/taco-match/tests/common/mod.rs:7-22."""
+
+    def __init__(self, s):
+        self.s = s & M64
+
+    def next_u64(self):
+        self.s = (self.s + 0x9E3779B97F4A7C15) & M64
+        z = self.s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+        return z ^ (z >> 31)
+
+    def below(self, n):
+        return self.next_u64() % n
+
+
+def synthetic_log(seed, count, vocab=1000, newline=198):
+    """tests/common/mod.rs:28-50: 8 templates with variable fields."""
+    rng = SplitMix64(seed)
+    templates = []
+    for _ in range(8):
+        n = 5 + rng.below(20)
+        templates.append([rng.below(vocab) for _ in range(n)])
+    out = []
+    while len(out) < count:
+        for tok in templates[rng.below(8)]:
+            out.append(tok)
+            if rng.below(4) == 0:
+                for _ in range(1 + rng.below(3)):
+                    out.append(rng.below(vocab))
+        out.append(newline)
+    return out[:count]
+
+
+def test_logistic_tables_match_the_golden_hashes():
+    # crates/taco-match/src/logistic.rs:147-156
+    sq, st = O.logistic_tables()
+    assert hashlib.sha256(sq.astype("<u2").tobytes()).hexdigest() == \
+        "345a564594a6032f8b2f13850e4b38ce420a8c50c4953f2cffd244e9d29781bc"
+    assert hashlib.sha256(st.astype("<i2").tobytes()).hexdigest() == \
+        "c1ed057a2aed7ea9f38e6cce27eaee39ccee69719aba90c0bb39ba5d02aad142"
+    assert sq[4095] == 32768 and sq[0] == 1 and sq[-1] == 65535
+
+
+def test_match_model_and_mixer_golden_vectors():
+    # crates/taco-match/tests/golden.rs:20-50: 4,000 tokens of the synthetic log, the weights of
+    # tests/common/mod.rs:52-59, then predict / mix / update / observe at each position.
+    seed = 20_261_018
+    tokens = synthetic_log(seed, 4000)
+    rng = SplitMix64(seed ^ 0xA5A5)
+    st = O.MixState()
+    hp, hw = hashlib.sha256(), hashlib.sha256()
+    for t in tokens:
+        p = st.predict()
+        w = np.zeros(1000, np.uint64)
+        for i in range(1000):
+            v = rng.next_u64()
+            w[i] = v >> (20 + rng.below(44))
+        if rng.below(2) == 0:
+            w[t] = 1 << 40
+        out = st.mix(w)
+        st.observe(t)
+        tok, ln = p if p else (0xFFFFFFFF, 0)
+        hp.update(tok.to_bytes(4, "little") + ln.to_bytes(4, "little"))
+        hw.update(out.astype("<u8").tobytes())
+    assert hp.hexdigest() == "a7ccc360407bc350f5444defc5dcb8b173ec6e7ee8c17b02998d70c20c73b23d"
+    assert hw.hexdigest() == "31d87e9efc45a331b7019e4c8f6058cea247637a5a29a3b0016981407821d614"
+
+
+MIXED_CONTAINERS = ["predicted_logs_k0", "predicted_logs_default_k", "all_kinds_logs"]
+
+
+@pytest.mark.parametrize("name", MIXED_CONTAINERS)
+def test_conformance_mixed_blocks_decode_and_reencode(name):
+    # conformance/v2/vectors.tsv:14-15,19: the mixed blocks (kind 3) restore their bytes and
+    # re-encode to the same payloads.
+    hsm = open(os.path.join(GOLDEN, "tiny.hsm"), "rb").read()
+    m = O.Model(hsm)
+    vocab = vocab_of(hsm)
+    data = open(os.path.join(GOLDEN, name + ".taco"), "rb").read()
+    original = open(os.path.join(GOLDEN, name + ".in"), "rb").read()
+    c = read_container(data)
+    assert c["checksum"] == hashlib.sha256(original).digest()
+    mixed = 0
+    for i, (kind, payload) in enumerate(c["blocks"]):
+        if kind != 3:
+            continue
+        piece = original[i * c["block_size"]:(i + 1) * c["block_size"]]
+        toks = O.decode_mixed_block(m, payload, overlap=c["overlap"])
+        assert b"".join(vocab[t] for t in toks) == piece
+        assert O.encode_mixed_block(m, toks, overlap=c["overlap"]) == payload
+        mixed += 1
+    assert mixed >= 1
