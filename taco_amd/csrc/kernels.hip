@@ -87,15 +87,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int K = g.k_pad, nk = K / GEMM_BK;
 
     // This wave loads fragments GEMM_LOADS * wave .. +GEMM_LOADS of each stage (0..15: A row
-    // blocks, 16..23: W row blocks); lane l reads row l % 16 of the block at k 16 (l / 16).
+    // blocks, 16..23: W row blocks of 16 rows x 64 bytes). Each lane quad reads one row's 64
+    // contiguous bytes (lane l: row l / 4, 16-byte chunk (l % 4) ^ sw(row)), so a load touches
+    // 16 lines, one per quad. The fragment lands in LDS in lane order, so chunk c of row r sits
+    // at 16-byte slot 4 r + (c ^ sw(r)); sw(r) = (r / 4) % 4 makes the MFMA operand reads (lane
+    // l: row l % 16, chunk l / 16) of any 16 consecutive lanes hit 16 distinct bank groups.
     const int8_t *src[GEMM_LOADS];
 #pragma unroll
     for (int i = 0; i < GEMM_LOADS; i++) {
         const int f = wave * GEMM_LOADS + i;
-        const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + (lane & 15);
-        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) +
-                 (lane >> 4) * 16;
+        const int r = lane >> 2, c = (lane & 3) ^ ((r >> 2) & 3);
+        const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + r;
+        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) + c * 16;
     }
+    const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ (((lane & 15) >> 2) & 3));
     auto issue = [&](int kt, int stage) {
         int8_t *base = gemm_lds + stage * (GEMM_FRAGS * 1024) + wave * GEMM_LOADS * 1024;
 #pragma unroll
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         // stages still in flight.
         asm volatile("s_barrier" ::: "memory");
         if (kt + GEMM_STAGES - 1 < nk) issue(kt + GEMM_STAGES - 1, (kt + GEMM_STAGES - 1) % GEMM_STAGES);
-        const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (GEMM_FRAGS * 1024) + lane * 16;
+        const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (GEMM_FRAGS * 1024) + rd_slot * 16;
         v4i af[8], bf[4];
 #pragma unroll
         for (int i = 0; i < 8; i++) af[i] = *(const v4i *)(st + (wm * 8 + i) * 1024);
