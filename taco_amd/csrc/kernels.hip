@@ -90,17 +90,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     // blocks, 16..23: W row blocks of 16 rows x 64 bytes). Each lane quad reads one row's 64
     // contiguous bytes (lane l: row l / 4, 16-byte chunk (l % 4) ^ sw(row)), so a load touches
     // 16 lines, one per quad. The fragment lands in LDS in lane order, so chunk c of row r sits
-    // at 16-byte slot 4 r + (c ^ sw(r)); sw(r) = (r / 4) % 4 makes the MFMA operand reads (lane
-    // l: row l % 16, chunk l / 16) of any 16 consecutive lanes hit 16 distinct bank groups.
+    // at 16-byte slot 4 r + (c ^ sw(r)); sw(r) = ((r >> 1) ^ (r >> 3)) % 4 makes the MFMA operand
+    // reads (lane l: row l % 16, chunk l / 16) of any 8 (and any 16) consecutive lanes hit
+    // distinct 16-byte bank groups.
+    auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
     const int8_t *src[GEMM_LOADS];
 #pragma unroll
     for (int i = 0; i < GEMM_LOADS; i++) {
         const int f = wave * GEMM_LOADS + i;
-        const int r = lane >> 2, c = (lane & 3) ^ ((r >> 2) & 3);
+        const int r = lane >> 2, c = (lane & 3) ^ sw(r);
         const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + r;
         src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) + c * 16;
     }
-    const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ (((lane & 15) >> 2) & 3));
+    const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ sw(lane & 15));
     auto issue = [&](int kt, int stage) {
         int8_t *base = gemm_lds + stage * (GEMM_FRAGS * 1024) + wave * GEMM_LOADS * 1024;
 #pragma unroll
@@ -664,9 +666,105 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     }
 }
 
+// One wave per row, the row in registers as NG groups of 4 consecutive columns per lane
+// (d % 4 == 0, d <= 256 NG): 16-byte loads of x and beta, 32-byte loads of gamma m, one 4-byte
+// store per 4 outputs. One pass gives sum x, sum x^2 (u64 squares, |x| <= 2^30, with a carry
+// word), min and max; then sum (x - mean)^2 = sum x^2 - 2 mean sum x + d mean^2 (the same
+// integer) and max|x - mean| = max(max - mean, mean - min).
+template <int NG>
+__global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;
+    const int d = a.d;
+    const int32_t *x = a.x + (size_t)(a.src ? a.src[row] : row) * d;
+    v4i xv[NG];
+    int64_t sum = 0;
+    uint64_t lo = 0, hi = 0;
+    int32_t mx = INT32_MIN, mn = INT32_MAX;
+#pragma unroll
+    for (int t = 0; t < NG; t++) {
+        const int j = 4 * (lane + 64 * t);
+        xv[t] = j < d ? *(const v4i *)(x + j) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int t = 0; t < NG; t++) {
+        const int j = 4 * (lane + 64 * t);
+        if (j >= d) continue;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int32_t v = xv[t][e];
+            sum += v;
+            const uint32_t u = (uint32_t)(v < 0 ? -v : v);
+            const uint64_t p = (uint64_t)u * u;
+            lo += p;
+            hi += lo < p;
+            mx = v > mx ? v : mx;
+            mn = v < mn ? v : mn;
+        }
+    }
+    sum = wave_sum64(sum);
+    const u128 Q = wave_sum128(((u128)hi << 64) | lo);
+    mx = (int32_t)wave_max64(mx);
+    mn = (int32_t)-wave_max64(-(int64_t)mn);
+    const int64_t mean = floor_div64(sum, d);
+    const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
+    const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
+    const int64_t c1 = (int64_t)mx - mean, c2 = mean - (int64_t)mn;
+    const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
+    const bool small = (u128)cmax * inv < ((u128)1 << 63);
+    const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
+    const bool wide = a.bits == 16;
+    int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+#pragma unroll
+    for (int t = 0; t < NG; t++) {
+        const int j = 4 * (lane + 64 * t);
+        if (j >= d) continue;
+        const v4i bv = *(const v4i *)(a.beta + j);
+        const int64_t *gp = a.gm + j;
+        uint32_t packed = 0, packed_lo = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int64_t c = (int64_t)xv[t][e] - mean;
+            int64_t y;
+            if (fast) {  // the rounding shift from the high word of (c inv) (gamma m)
+                y = shift_round_hi(c * (int64_t)inv, gp[e], (uint32_t)a.s) + bv[e];
+            } else {
+                const i128 cinv = small ? (i128)(c * (int64_t)inv) : (i128)c * (i128)(u128)inv;
+                const i128 p = cinv * (i128)gp[e];
+                i128 yy;
+                if (a.beta_frac == 0) {
+                    yy = shift_round128(p, a.s, 126) + (i128)bv[e];
+                } else {
+                    const i128 cb = (i128)bv[e] << (a.s - a.beta_frac);
+                    yy = shift_round128(p + cb, a.s, 126);
+                }
+                y = clamp128(yy, -32767, 32767);
+            }
+            if (!wide) {
+                packed |= (uint32_t)(uint8_t)(int8_t)clamp64(y, -127, 127) << (8 * e);
+            } else {
+                const int32_t v = (int32_t)clamp64(y, -32767, 32767);
+                packed |= (uint32_t)(uint8_t)(v >> 8) << (8 * e);
+                packed_lo |= (uint32_t)(uint8_t)((v & 255) - 128) << (8 * e);
+            }
+        }
+        *(uint32_t *)(out + j) = packed;
+        if (wide) *(uint32_t *)(out + a.ldo + j) = packed_lo;
+    }
+}
+
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_layernorm, dim3((n_rows + 3) / 4), dim3(256), 0, stream, a, n_rows);
+    const dim3 grid((n_rows + 3) / 4);
+    // the vector forms need 4-aligned rows: d and ldo multiples of 4
+    if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 1024) {
+        hipLaunchKernelGGL(k_layernorm_rows<4>, grid, dim3(256), 0, stream, a, n_rows);
+    } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
+        hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
+    } else {
+        hipLaunchKernelGGL(k_layernorm, dim3((n_rows + 3) / 4), dim3(256), 0, stream, a, n_rows);
+    }
     return hipGetLastError();
 }
 
