@@ -1199,6 +1199,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         if (key < nk) v = *(const v4i *)(cache + base + (size_t)key * 64 + c);
         return v;
     };
+    // this thread's 4 keys x 4 channels of value block kb (one word per key): keys kb * 64 +
+    // 4 (tid / 16) .. +4, channels 4 (tid % 16) .. +4
+    auto vt_load = [&](int kb) {
+        const int k0 = kb * 64 + 4 * (tid >> 4), c = 4 * (tid & 15);
+        v4i v = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (k0 + i < nk) v[i] = *(const int32_t *)(a.vc + base + (size_t)(k0 + i) * 64 + c);
+        return v;
+    };
     auto qk_super = [&](int sb) {
         v4i kreg[AT_SB];  // every key block of the super-block in flight at once
 #pragma unroll
@@ -1249,8 +1259,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int64_t a0 = score(dmax[e]), a1 = score(dmin[e]);
         mx[e] = a0 > a1 ? a0 : a1;  // rows past the group's count: unused
     }
-    // the dots of super-block sb -> table indices min(M - s, last), -1 for a masked key
-    auto to_index = [&](int sb) {
+    // the dots of super-block sb -> the table entries e = attn_exp[min(M - s, last)] (>= 0), 0 for
+    // a masked key (it adds nothing to S and gets p = 0)
+    auto to_weight = [&](int sb) {
 #pragma unroll
         for (int b = 0; b < AT_SB; b++)
 #pragma unroll
@@ -1259,7 +1270,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int64_t dd = mx[e] - score(S[b][t][e]);
-                    S[b][t][e] = (key <= posr[e] && key < nk) ? (int32_t)(dd < last ? dd : last) : -1;
+                    S[b][t][e] = (key <= posr[e] && key < nk) ? etab[dd < last ? dd : last] : 0;
                 }
             }
     };
@@ -1267,14 +1278,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     int64_t sum[4] = {0, 0, 0, 0};
     for (int sb = 0; sb < nsb; sb++) {
         if (nsb > 1) qk_super(sb);
-        to_index(sb);
+        to_weight(sb);
 #pragma unroll
         for (int b = 0; b < AT_SB; b++)
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (S[b][t][e] >= 0) sum[e] += etab[S[b][t][e]];
+                for (int e = 0; e < 4; e++) sum[e] += (uint32_t)S[b][t][e];
     }
     uint64_t frac[4];
 #pragma unroll
@@ -1292,37 +1302,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     for (int sb = 0; sb < nsb; sb++) {
         if (nsb > 1) {
             qk_super(sb);
-            to_index(sb);
+            to_weight(sb);
         }
-        v4i vnext = sb * AT_SB < nkb ? kv_load(a.vc, sb * AT_SB) : v4i{0, 0, 0, 0};
+        v4i vnext = sb * AT_SB < nkb ? vt_load(sb * AT_SB) : v4i{0, 0, 0, 0};
 #pragma unroll
         for (int b = 0; b < AT_SB; b++) {
             const int kb = sb * AT_SB + b;
             if (kb >= nkb) break;
-            {  // V^T of the block into LDS; the next block's values load meanwhile
-                const int kl = tid >> 2, c = (tid & 3) * 16;
+            {  // V^T of the block into LDS (4 x 4 byte transposes); the next block loads meanwhile
                 const v4i v = vnext;
-                if (b + 1 < AT_SB && kb + 1 < nkb) vnext = kv_load(a.vc, kb + 1);
-                const int8_t *bv = (const int8_t *)&v;
+                if (b + 1 < AT_SB && kb + 1 < nkb) vnext = vt_load(kb + 1);
+                uint32_t tw[4];
+                byte_transpose((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], tw);
+                const int kg = tid >> 4, cg = tid & 15;  // keys 4 kg .. +4, channels 4 cg .. +4
 #pragma unroll
-                for (int i = 0; i < 16; i++) sVt[(c + i) * AT_ST + kl] = bv[i];
+                for (int j = 0; j < 4; j++) *(uint32_t *)&sVt[(4 * cg + j) * AT_ST + 4 * kg] = tw[j];
             }
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int32_t idx = S[b][t][e];
-                    uint32_t p = 0;
-                    if (idx >= 0) {
-                        const uint64_t num = (uint64_t)etab[idx] << a.softmax_p;
-                        const uint64_t Sv = (uint64_t)sum[e];
-                        uint64_t q = num;
-                        if (Sv >= 2) {
-                            q = __umul64hi(num, frac[e]);  // q <= floor(num / S) <= q + 1
-                            if (num - q * Sv >= Sv) q++;
-                        }
-                        p = (uint32_t)q;  // <= 2^P <= 2^30
+                    const uint64_t num = (uint64_t)(uint32_t)S[b][t][e] << a.softmax_p;
+                    const uint64_t Sv = (uint64_t)sum[e];
+                    uint64_t q = num;
+                    if (Sv >= 2) {
+                        q = __umul64hi(num, frac[e]);  // q <= floor(num / S) <= q + 1
+                        if (num - q * Sv >= Sv) q++;
                     }
+                    const uint32_t p = (uint32_t)q;  // <= 2^P <= 2^30
                     sP[row[e] * AT_PP + t * 16 + (lane & 15)] = (p + 0x80808080u) ^ 0x80808080u;
                 }
             __syncthreads();
