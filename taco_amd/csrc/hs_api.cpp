@@ -162,7 +162,7 @@ namespace {
 hs_status upload_linear(DevMem &mem, const hs::HostLinear &l, DevLinear &o) {
     o.n = (int)l.rows;
     o.k = (int)l.cols;
-    o.n_pad = (int)round_up(l.rows, hs::GEMM_BN);
+    o.n_pad = (int)round_up(l.rows, hs::GEMM_NPAD);
     o.k_pad = (int)round_up(l.cols, hs::GEMM_BK);
     std::vector<int8_t> w((size_t)o.n_pad * o.k_pad, 0);
     for (uint32_t r = 0; r < l.rows; r++) std::memcpy(&w[(size_t)r * o.k_pad], l.w + (size_t)r * l.cols, l.cols);
@@ -259,7 +259,7 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
     m->H = (int)h.n_head; m->hd = (int)h.head_dim; m->L = (int)h.n_layer;
     m->d_pad = (int)round_up(h.d_model, hs::GEMM_BK);
     m->f_pad = (int)round_up(h.d_ff, hs::GEMM_BK);
-    m->V_pad = (int)round_up(h.vocab, hs::GEMM_BN);
+    m->V_pad = (int)round_up(h.vocab, hs::GEMM_NPAD);
     DevMem &mem = m->mem;
     hs_status st;
     {
@@ -1167,7 +1167,7 @@ extern "C" hs_status hs_batch_truncate(hs_batch *b, size_t slot, size_t len) {
 
 extern "C" void hs_op_gemm_layout(size_t m, size_t n, size_t k, size_t *m_pad, size_t *n_pad, size_t *k_pad) {
     if (m_pad) *m_pad = round_up(std::max<size_t>(m, 1), hs::GEMM_BM);
-    if (n_pad) *n_pad = round_up(std::max<size_t>(n, 1), hs::GEMM_BN);
+    if (n_pad) *n_pad = round_up(std::max<size_t>(n, 1), hs::GEMM_NPAD);
     if (k_pad) *k_pad = round_up(std::max<size_t>(k, 1), hs::GEMM_BK);
 }
 

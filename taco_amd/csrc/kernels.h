@@ -56,8 +56,9 @@ struct GemmArgs {
 };
 
 
-// Tile sizes of the MFMA GEMM: a rows are padded to GEMM_BM, w rows to GEMM_BN, k to GEMM_BK.
-constexpr int GEMM_BM = 256, GEMM_BN = 128, GEMM_BK = 64;
+// Tile sizes of the MFMA GEMM (256 x 128 or 256 x 256 by N): a rows are padded to GEMM_BM, w rows
+// to GEMM_NPAD, k to GEMM_BK.
+constexpr int GEMM_BM = 256, GEMM_BK = 64, GEMM_NPAD = 256;
 
 // The group size of the XCD-aware tile order: one band of M-tiles per XCD.
 inline int gemm_group(int m) {

@@ -49,9 +49,7 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 // =============================================================================================
 
 constexpr int GEMM_STAGES = 3;
-constexpr int GEMM_FRAGS = GEMM_BM / 16 + GEMM_BN / 16;  // 24 fragments of 1 KiB per stage
-constexpr int GEMM_LOADS = GEMM_FRAGS / 4;                // per wave and stage
-static_assert(GEMM_BM == 256 && GEMM_BN == 128 && GEMM_BK == 64, "tile shape of k_gemm");
+static_assert(GEMM_BM == 256 && GEMM_BK == 64 && GEMM_NPAD % 256 == 0, "tile shape of k_gemm");
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -63,18 +61,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // NARROW: g.fast32 holds and the shift is at least 32, so every rescaled value fits i32.
-template <int EPI, bool NARROW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
-    extern __shared__ __attribute__((aligned(1024))) int8_t gemm_lds[];  // [stages][24][1024]
+// BN = 128 (4 waves, 2 x 2) or 256 (8 waves, 2 x 4); every wave computes 128 x 64.
+template <int EPI, bool NARROW, int BN>
+__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
+    constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16, LOADS = FRAGS / WAVES;
+    static_assert(FRAGS % WAVES == 0, "whole fragments per wave");
+    extern __shared__ __attribute__((aligned(1024))) int8_t gemm_lds[];  // [stages][FRAGS][1024]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / (WAVES / 2), wn = wave % (WAVES / 2);
     // XCD-aware tile order: workgroup L runs on XCD L % 8, and XCD x takes the x-th contiguous
     // chunk of a grouped order (groups of `group` M-tiles, N outermost inside a group), so an
     // A row-tile stays in one XCD's L2 while the W tiles stream past it.
     int mt, nt;
     {
-        const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + GEMM_BN - 1) / GEMM_BN;
+        const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + BN - 1) / BN;
         const int T = gm * gn, L = blockIdx.x, x = L & 7, k = L >> 3;
         const int q = T >> 3, r = T & 7;
         const int p = x * q + (x < r ? x : r) + k;
@@ -83,30 +84,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         nt = in / gs;
         mt = grp * G + in % gs;
     }
-    const int m0 = mt * GEMM_BM, n0 = nt * GEMM_BN;
+    const int m0 = mt * GEMM_BM, n0 = nt * BN;
     const int K = g.k_pad, nk = K / GEMM_BK;
 
-    // This wave loads fragments GEMM_LOADS * wave .. +GEMM_LOADS of each stage (0..15: A row
-    // blocks, 16..23: W row blocks of 16 rows x 64 bytes). Each lane quad reads one row's 64
+    // This wave loads fragments LOADS * wave .. +LOADS of each stage (0..15: A row blocks, then
+    // the W row blocks, of 16 rows x 64 bytes). Each lane quad reads one row's 64
     // contiguous bytes (lane l: row l / 4, 16-byte chunk (l % 4) ^ sw(row)), so a load touches
     // 16 lines, one per quad. The fragment lands in LDS in lane order, so chunk c of row r sits
     // at 16-byte slot 4 r + (c ^ sw(r)); sw(r) = ((r >> 1) ^ (r >> 3)) % 4 makes the MFMA operand
     // reads (lane l: row l % 16, chunk l / 16) of any 8 (and any 16) consecutive lanes hit
     // distinct 16-byte bank groups.
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
-    const int8_t *src[GEMM_LOADS];
+    const int8_t *src[LOADS];
 #pragma unroll
-    for (int i = 0; i < GEMM_LOADS; i++) {
-        const int f = wave * GEMM_LOADS + i;
+    for (int i = 0; i < LOADS; i++) {
+        const int f = wave * LOADS + i;
         const int r = lane >> 2, c = (lane & 3) ^ sw(r);
         const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + r;
         src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) + c * 16;
     }
     const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ sw(lane & 15));
     auto issue = [&](int kt, int stage) {
-        int8_t *base = gemm_lds + stage * (GEMM_FRAGS * 1024) + wave * GEMM_LOADS * 1024;
+        int8_t *base = gemm_lds + stage * (FRAGS * 1024) + wave * LOADS * 1024;
 #pragma unroll
-        for (int i = 0; i < GEMM_LOADS; i++)
+        for (int i = 0; i < LOADS; i++)
             __builtin_amdgcn_global_load_lds((const void *)(src[i] + kt * GEMM_BK),
                                              (lds_void *)(base + i * 1024), 16, 0, 0);
     };
@@ -122,17 +123,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         if (s < nk) issue(s, s);
     for (int kt = 0; kt < nk; kt++) {
         // this wave's loads of stage kt have landed once at most (stages issued after it)
-        // x GEMM_LOADS loads are outstanding
+        // x LOADS loads are outstanding
         const int after = nk - 1 - kt < GEMM_STAGES - 2 ? nk - 1 - kt : GEMM_STAGES - 2;
-        if (after >= 2) wait_vmcnt<2 * GEMM_LOADS>();
-        else if (after == 1) wait_vmcnt<GEMM_LOADS>();
+        if (after >= 2) wait_vmcnt<2 * LOADS>();
+        else if (after == 1) wait_vmcnt<LOADS>();
         else wait_vmcnt<0>();
         // Every wave's loads of stage kt landed; every wave finished reading stage kt - 1. A bare
         // s_barrier (a compiler memory barrier, no fence): a fence would also wait for the
         // stages still in flight.
         asm volatile("s_barrier" ::: "memory");
         if (kt + GEMM_STAGES - 1 < nk) issue(kt + GEMM_STAGES - 1, (kt + GEMM_STAGES - 1) % GEMM_STAGES);
-        const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (GEMM_FRAGS * 1024) + rd_slot * 16;
+        const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (FRAGS * 1024) + rd_slot * 16;
         v4i af[8], bf[4];
 #pragma unroll
         for (int i = 0; i < 8; i++) af[i] = *(const v4i *)(st + (wm * 8 + i) * 1024);
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                                EPI == (int)Epi::Residual || EPI == (int)Epi::LogitsCompact;
     if (STAGEABLE && ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0) {
         __syncthreads();  // every wave finished reading the stages
-        int8_t *wr = gemm_lds + wave * 18432;  // this wave's region (4 x 18 KiB = the stages)
+        int8_t *wr = gemm_lds + wave * 18432;  // this wave's region (18 KiB)
         const int rw = m0 + wm * 128, cw = n0 + wn * 64;  // the wave's sub-tile origin
         const int g4 = (lane >> 4) * 4, c16 = lane & 15;
         int32_t bias[4], mult[4];
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                                            g.gelu_off;
                         }
                 const int T = 2 * g.gelu_off;  // 256 or 65,536 entries, copied into LDS
-                for (int c = threadIdx.x; c < T / 16; c += 256)
+                for (int c = threadIdx.x; c < T / 16; c += 2 * BN)
                     *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
                 __syncthreads();
 #pragma unroll
@@ -511,50 +512,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
 }
 
-template <int EPI, bool NARROW>
-static hipError_t launch_gemm_t(const GemmArgs &g, dim3 grid, hipStream_t stream) {
-    constexpr size_t lds = (size_t)GEMM_STAGES * GEMM_FRAGS * 1024;
+template <int EPI, bool NARROW, int BN>
+static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
+    constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16;
+    // the stages, and the per-wave epilogue regions of 18 KiB
+    constexpr size_t stages = (size_t)GEMM_STAGES * FRAGS * 1024, regions = (size_t)WAVES * 18432;
+    constexpr size_t lds = stages > regions ? stages : regions;
     static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
     if (!ready) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         ready = true;
     }
-    hipLaunchKernelGGL((k_gemm<EPI, NARROW>), grid, dim3(256), lds, stream, g);
+    const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN>), dim3(gm * gn), dim3(2 * BN), lds, stream, g);
     return hipGetLastError();
 }
 
+// 256 x 128 tiles (two workgroups per CU, so one's epilogue overlaps the other's main loop),
+// except for the i8 GELU epilogue of a wide product: each workgroup copies the 64 KiB table
+// into LDS, and 256 x 256 tiles halve those copies (measured: c_fc 5% faster; the other wide
+// products are slower with one workgroup per CU).
+template <int EPI, bool NARROW>
+static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
+    if (EPI == (int)Epi::Gelu && g.n > 1024) return launch_gemm_t<EPI, NARROW, 256>(g, stream);
+    return launch_gemm_t<EPI, NARROW, 128>(g, stream);
+}
+
 template <int EPI>
-static hipError_t launch_gemm_e(const GemmArgs &g, dim3 grid, hipStream_t stream) {
+static hipError_t launch_gemm_e(const GemmArgs &g, hipStream_t stream) {
     const bool fast = EPI == (int)Epi::Logits || EPI == (int)Epi::LogitsCompact || g.fast32;
-    if (fast && g.shift >= 32) return launch_gemm_t<EPI, true>(g, grid, stream);
-    return launch_gemm_t<EPI, false>(g, grid, stream);
+    if (fast && g.shift >= 32) return launch_gemm_w<EPI, true>(g, stream);
+    return launch_gemm_w<EPI, false>(g, stream);
 }
 
 hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
     GemmArgs g = ga;
     if (g.m <= 0 || g.n <= 0) return hipSuccess;
     if (g.k_pad % GEMM_BK != 0) return hipErrorInvalidValue;
-    const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + GEMM_BN - 1) / GEMM_BN;
+    const int gm = (g.m + GEMM_BM - 1) / GEMM_BM;
     if (g.group == 0) g.group = gemm_group(g.m);
     if (g.group < 1 || g.group > gm) return hipErrorInvalidValue;
-    const dim3 grid(gm * gn);
     switch (epi) {
-        case Epi::Raw: return launch_gemm_t<0, false>(g, grid, stream);
-        case Epi::Act: return launch_gemm_e<1>(g, grid, stream);
-        case Epi::Residual: return launch_gemm_e<2>(g, grid, stream);
-        case Epi::Gelu: return launch_gemm_e<3>(g, grid, stream);
-        case Epi::Logits: return launch_gemm_e<4>(g, grid, stream);
-        case Epi::LogitsCompact: return launch_gemm_e<5>(g, grid, stream);
-        case Epi::GeluWide: return launch_gemm_e<6>(g, grid, stream);
+        case Epi::Raw: return launch_gemm_w<0, false>(g, stream);
+        case Epi::Act: return launch_gemm_e<1>(g, stream);
+        case Epi::Residual: return launch_gemm_e<2>(g, stream);
+        case Epi::Gelu: return launch_gemm_e<3>(g, stream);
+        case Epi::Logits: return launch_gemm_e<4>(g, stream);
+        case Epi::LogitsCompact: return launch_gemm_e<5>(g, stream);
+        case Epi::GeluWide: return launch_gemm_e<6>(g, stream);
         case Epi::ResidualWide:
         case Epi::LogitsWide:
         case Epi::LogitsCompactWide:
             if (!g.wsum || (g.m & 1)) return hipErrorInvalidValue;  // rows of plane pairs
-            if (epi == Epi::ResidualWide) return launch_gemm_t<7, false>(g, grid, stream);
-            if (epi == Epi::LogitsWide) return launch_gemm_t<8, false>(g, grid, stream);
-            return launch_gemm_t<9, false>(g, grid, stream);
+            if (epi == Epi::ResidualWide) return launch_gemm_w<7, false>(g, stream);
+            if (epi == Epi::LogitsWide) return launch_gemm_w<8, false>(g, stream);
+            return launch_gemm_w<9, false>(g, stream);
     }
     return hipErrorInvalidValue;
 }
