@@ -118,32 +118,53 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-#pragma unroll
-    for (int s = 0; s < GEMM_STAGES - 1; s++)
-        if (s < nk) issue(s, s);
-    for (int kt = 0; kt < nk; kt++) {
-        // this wave's loads of stage kt have landed once at most (stages issued after it)
-        // x LOADS loads are outstanding
-        const int after = nk - 1 - kt < GEMM_STAGES - 2 ? nk - 1 - kt : GEMM_STAGES - 2;
-        if (after >= 2) wait_vmcnt<2 * LOADS>();
-        else if (after == 1) wait_vmcnt<LOADS>();
-        else wait_vmcnt<0>();
-        // Every wave's loads of stage kt landed; every wave finished reading stage kt - 1. A bare
-        // s_barrier (a compiler memory barrier, no fence): a fence would also wait for the
-        // stages still in flight.
-        asm volatile("s_barrier" ::: "memory");
-        if (kt + GEMM_STAGES - 1 < nk) issue(kt + GEMM_STAGES - 1, (kt + GEMM_STAGES - 1) % GEMM_STAGES);
+    // The operand fragments of k-step kt + 1 are read from LDS while the MFMAs of k-step kt
+    // run on registers read the step before. Of the three stages one is being read and two
+    // are in flight.
+    auto read_frags = [&](int kt, v4i *af, v4i *bf) {
         const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (FRAGS * 1024) + rd_slot * 16;
-        v4i af[8], bf[4];
 #pragma unroll
         for (int i = 0; i < 8; i++) af[i] = *(const v4i *)(st + (wm * 8 + i) * 1024);
 #pragma unroll
         for (int j = 0; j < 4; j++) bf[j] = *(const v4i *)(st + (GEMM_BM / 16 + wn * 4 + j) * 1024);
+    };
+#pragma unroll
+    for (int s = 0; s < GEMM_STAGES; s++)
+        if (s < nk) issue(s, s);
+    // stage 0 landed (the later stages' loads may be outstanding); a bare s_barrier (a compiler
+    // memory barrier, no fence: a fence would also wait for the stages in flight)
+    if (nk >= 3) wait_vmcnt<2 * LOADS>();
+    else if (nk == 2) wait_vmcnt<LOADS>();
+    else wait_vmcnt<0>();
+    asm volatile("s_barrier" ::: "memory");
+    v4i af[8], bf[4];
+    read_frags(0, af, bf);
+    for (int kt = 0; kt < nk; kt++) {
+        v4i an[8], bn[4];
+        const bool more = kt + 1 < nk;
+        if (more) {
+            // stage kt + 1 landed (stage kt + 2's loads may be outstanding); this wave's reads of
+            // stage kt % 3 (issued the step before) completed, so after the barrier no wave
+            // reads it and it takes k-step kt + 3
+            if (kt + 2 < nk) wait_vmcnt<LOADS>();
+            else wait_vmcnt<0>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (kt + GEMM_STAGES < nk) issue(kt + GEMM_STAGES, kt % GEMM_STAGES);
+        }
+        // unconditional (the last step re-reads its own stage), so the reads share the MFMAs'
+        // basic block and no wait for them lands before the MFMAs; the empty asm keeps the
+        // compiler from sinking them into the next step (where they would wait at its barrier)
+        read_frags(more ? kt + 1 : kt, an, bn);
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int i = 0; i < 8; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; i++) af[i] = an[i];
+#pragma unroll
+        for (int j = 0; j < 4; j++) bf[j] = bn[j];
     }
 
     // Epilogue: lane holds C[4 * (lane / 16) + e][lane % 16] of each 16 x 16 tile.
