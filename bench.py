@@ -50,6 +50,60 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def traffic_summary(fetch_csv, write_csv, calib_mib, tokens_sha, command):
+    """HBM bytes per dispatch of each kernel from two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch). Each counter is scaled by what it reads for the calibration
+    copy of calib_mib MiB (the largest __amd_rocclr_copyBuffer dispatch of the run)."""
+    import csv
+    import collections
+
+    def load(path):
+        per = collections.defaultdict(float)
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"].split("(")[0].replace("void ", "").strip()
+            per[(name, r["Dispatch_Id"])] += float(r["Counter_Value"])
+        return per
+
+    fetch, write = load(fetch_csv), load(write_csv)
+    copy_kib = calib_mib * 1024.0
+    f_copy = max(v for (k, _), v in fetch.items() if "copyBuffer" in k)
+    w_copy = max(v for (k, _), v in write.items() if "copyBuffer" in k)
+    f_scale, w_scale = copy_kib / f_copy, copy_kib / w_copy
+    agg = collections.defaultdict(lambda: [0, 0.0, 0.0])
+    for (k, d), v in fetch.items():
+        if "rocclr" in k:
+            continue
+        agg[k][0] += 1
+        agg[k][1] += v * f_scale * 1024
+    for (k, d), v in write.items():
+        if "rocclr" in k:
+            continue
+        agg[k][2] += v * w_scale * 1024
+    return {"tokens_sha256": tokens_sha, "command": command, "calibration_mib": calib_mib,
+            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+            "kernels": {k: {"dispatches": n, "fetch_bytes": round(fb / n), "write_bytes": round(wb / n)}
+                        for k, (n, fb, wb) in sorted(agg.items())}}
+
+
+def committed_traffic(workload, tokens_sha):
+    """The GEMM HBM bytes per launch of the committed traffic summary of this workload (the same
+    token stream), or None."""
+    path = os.path.join(HERE, "profiles", workload.replace("-", "_") + "_traffic.json")
+    if not os.path.exists(path):
+        return None
+    t = json.load(open(path))
+    if t.get("tokens_sha256") != tokens_sha:
+        return None
+    g = [v for k, v in t["kernels"].items() if "k_gemm" in k]
+    n = sum(v["dispatches"] for v in g)
+    if n == 0:
+        return None
+    return round(sum((v["fetch_bytes"] + v["write_bytes"]) * v["dispatches"] for v in g) / n)
+
+
 def read_profile(hip, batch):
     cap = 32
     labels = C.create_string_buffer(32 * cap)
@@ -202,7 +256,10 @@ def run_fold(args):
         "roofline": {"bound": "mfma", "kernel": "k_gemm (all int8 GEMMs of the pass)",
                      "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": None, "launches": gemm_launches,
+                     "traffic": committed_traffic(args.workload, synth.sha256_tokens(tokens)),
+                     "traffic_unit": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated; "
+                                     "profiles/" + args.workload.replace("-", "_") + "_traffic.json)",
+                     "launches": gemm_launches,
                      "ops_per_launch": gemm_ops // max(1, gemm_launches),
                      "avg_launch_us": round(gemm_ns / max(1, gemm_launches) / 1e3, 2)},
         "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / args.steps, 3) for kk, v in prof.items()},
@@ -359,7 +416,21 @@ def run_attend(args):
     }), flush=True)
 
 
+def main_traffic(argv):
+    """python bench.py --traffic-summary FETCH.csv WRITE.csv CALIB_MIB WORKLOAD: the summary of
+    two rocprofv3 counter runs of `bench.py --workload WORKLOAD --calib-copy-mib CALIB_MIB`."""
+    from taco_amd import synth
+    fetch_csv, write_csv, calib, workload = argv
+    dims_name, W, n, _ = FOLDS[workload]
+    tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
+    cmd = (f"rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -- python3 bench.py "
+           f"--workload {workload} --steps 1 --warmup 0 --no-cpu --calib-copy-mib {calib}")
+    print(json.dumps(traffic_summary(fetch_csv, write_csv, int(calib), tokens_sha, cmd), indent=1))
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--traffic-summary":
+        return main_traffic(sys.argv[2:])
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
