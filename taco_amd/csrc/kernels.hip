@@ -62,10 +62,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // NARROW: g.fast32 holds and the shift is at least 32, so every rescaled value fits i32.
 // BN = 128 (4 waves, 2 x 2) or 256 (8 waves, 2 x 4); every wave computes 128 x 64.
-template <int EPI, bool NARROW, int BN>
+// VEC: the output rows are 16-byte aligned (checked by the launcher); the four-columns epilogues
+// then stage and store 16-byte pieces, else they store each output on its own.
+template <int EPI, bool NARROW, int BN, bool VEC>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
     constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16, LOADS = FRAGS / WAVES;
     static_assert(FRAGS % WAVES == 0, "whole fragments per wave");
+    // The i16-plane epilogues pair rows 2r and 2r + 1 in one lane and keep the W-as-columns
+    // layout; every other epilogue takes four consecutive columns of a row per lane.
+    constexpr bool SWAP = EPI != (int)Epi::ResidualWide && EPI != (int)Epi::LogitsWide &&
+                          EPI != (int)Epi::LogitsCompactWide;
     extern __shared__ __attribute__((aligned(1024))) int8_t gemm_lds[];  // [stages][FRAGS][1024]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -160,14 +166,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         for (int i = 0; i < 8; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
+                                 : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 8; i++) af[i] = an[i];
 #pragma unroll
         for (int j = 0; j < 4; j++) bf[j] = bn[j];
     }
 
-    // Epilogue: lane holds C[4 * (lane / 16) + e][lane % 16] of each 16 x 16 tile.
+    // Epilogue. Lane layout of each 16 x 16 tile (i, j) of the wave: with SWAP (the W fragment is
+    // the MFMA's first operand) the lane holds C[16 i + lane % 16][16 j + 4 (lane / 16) + e], four
+    // consecutive columns of one row; otherwise C[16 i + 4 (lane / 16) + e][16 j + lane % 16].
     // rescale(a + bias, mult, shift) (int.rs:63-67). With the host's bound |a + bias| < 2^31
     // (fast32; the logits have no bias and |a| <= 2^30), |(a + bias) mult| < 2^62: one i64
     // multiply-add and an arithmetic shift are exact, and a shift of 63 or more gives 0 as
@@ -179,91 +188,269 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         if (NARROW || fast) return ((int64_t)(a + bias) * mult + half) >> s_eff;
         return rescale_small((int64_t)a + bias, mult, g.shift);
     };
-    // Staged epilogue: each wave writes its 128 x 64 results into its own LDS region (the
-    // stages are free after the barrier below) and stores them back as 16-byte row pieces, 8-32
-    // stores per wave instead of one per element. Needs 16-byte aligned output rows.
-    constexpr int ES = EPI == (int)Epi::Residual ? 4 : (EPI == (int)Epi::LogitsCompact ? 2 : 1);
-    constexpr bool STAGEABLE = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide ||
-                               EPI == (int)Epi::Residual || EPI == (int)Epi::LogitsCompact;
-    if (STAGEABLE && ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0) {
-        __syncthreads();  // every wave finished reading the stages
-        int8_t *wr = gemm_lds + wave * 18432;  // this wave's region (18 KiB)
-        const int rw = m0 + wm * 128, cw = n0 + wn * 64;  // the wave's sub-tile origin
-        const int g4 = (lane >> 4) * 4, c16 = lane & 15;
-        int32_t bias[4], mult[4];
-        bool okn[4];
+    const int rw = m0 + wm * 128, cw = n0 + wn * 64;  // the wave's sub-tile origin
+    if (SWAP) {
+        const int rl = lane & 15, cg = lane >> 4;
+        constexpr bool HAS_BIAS = EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu ||
+                                  EPI == (int)Epi::GeluWide;
+        constexpr bool vec = VEC;
+        // The rescale parameters of column group j of the lane (columns cw + 16 j + 4 cg + e).
+        auto params = [&](int j, int32_t *bj, int32_t *mj) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = cw + j * 16 + c16;
-            okn[j] = n < g.n;
-            bias[j] = (okn[j] && EPI != (int)Epi::LogitsCompact) ? g.bias[n] : 0;
-            mult[j] = okn[j] ? g.mult[n] : 0;
+            for (int e = 0; e < 4; e++) {
+                const int n = cw + 16 * j + 4 * cg + e;
+                const bool ok = n < g.n;
+                bj[e] = (HAS_BIAS && ok) ? g.bias[n] : 0;
+                mj[e] = (EPI != (int)Epi::Raw && ok) ? g.mult[n] : 0;
+            }
+        };
+        // Act, Gelu, GeluWide, Residual: the op's rule in place, one column group at a time.
+        if (EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide || EPI == (int)Epi::Residual) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                int32_t bj[4], mj[4];
+                params(j, bj, mj);
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int64_t r = rq(acc[i][j][e], bj[e], mj[e]);
+                        int32_t v;
+                        if (EPI == (int)Epi::Act) {  // ops.rs:123-130
+                            v = NARROW ? med3_i32((int32_t)r, -127, 127) : (int32_t)clamp64(r, -127, 127);
+                        } else if (EPI == (int)Epi::Residual) {
+                            v = NARROW ? (int32_t)r : (int32_t)clamp64(r, INT32_MIN, INT32_MAX);
+                        } else {  // ops.rs:146-154, gelu.rs:58-62: table[clamp(r) + off]
+                            v = (NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
+                                        : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1)) +
+                                g.gelu_off;
+                            if (EPI == (int)Epi::GeluWide) v = g.gelu16[v];  // the i16 table through the caches
+                        }
+                        acc[i][j][e] = v;
+                    }
+                asm volatile("" ::: "memory");  // the next group's parameter loads stay below
+            }
         }
-        if (EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide) {
-            if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62: table[clamp(r) + off]
+        if (EPI == (int)Epi::Residual) {  // ops.rs:131-145
+            // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R.
+            if (!vec) {
 #pragma unroll
                 for (int i = 0; i < 8; i++)
 #pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int m = rw + 16 * i + rl, n4 = cw + 16 * j + 4 * cg;
+                        if (m >= g.m) continue;
+                        int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n4;
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (n4 + e < g.n) x[e] = (int32_t)clamp64((int64_t)x[e] + acc[i][j][e], -RES, RES);
+                    }
+                return;
+            }
+            // Staged in two halves of 64 rows through this wave's region (64 rows x 272 B): the
+            // lane's four outputs of a row are one 16-byte LDS write; the read-modify-write of x
+            // then covers 256 contiguous bytes of 4 rows per instruction, all 16 loads of a half
+            // in flight together.
+            __syncthreads();  // every wave finished reading the stages
+            int8_t *wr = gemm_lds + wave * 18432;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ii++)
+#pragma unroll
                     for (int j = 0; j < 4; j++)
+                        *(v4i *)(wr + (16 * ii + rl) * 272 + (16 * j + 4 * cg) * 4) = acc[4 * h + ii][j];
+                v4i xv[16], rv[16];
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int rl2 = q * 4 + (lane >> 4), cl = (lane & 15) * 4;
+                    const int m = rw + 64 * h + rl2, n = cw + cl;
+                    rv[q] = *(const v4i *)(wr + rl2 * 272 + cl * 4);
+                    xv[q] = (m < g.m && n + 4 <= g.n) ? *(const v4i *)((const int32_t *)g.out + (size_t)m * g.ldo + n)
+                                                       : v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int rl2 = q * 4 + (lane >> 4), cl = (lane & 15) * 4;
+                    const int m = rw + 64 * h + rl2, n = cw + cl;
+                    if (m >= g.m) continue;
+                    int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n;
+                    if (n + 4 <= g.n) {
+                        v4i o;
+#pragma unroll
+                        for (int t = 0; t < 4; t++) o[t] = (int32_t)clamp64((int64_t)xv[q][t] + rv[q][t], -RES, RES);
+                        *(v4i *)x = o;
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 4; t++)
+                            if (n + t < g.n) x[t] = (int32_t)clamp64((int64_t)x[t] + rv[q][t], -RES, RES);
+                    }
+                }
+            }
+            return;
+        }
+        if (EPI == (int)Epi::Raw || EPI == (int)Epi::Logits) {  // i32 products; ops.rs:229-234 (i64)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                int32_t bj[4], mj[4];
+                params(j, bj, mj);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int m = rw + 16 * i + rl, n4 = cw + 16 * j + 4 * cg;
+                    if (m >= g.m || n4 >= g.n) continue;
+                    if (EPI == (int)Epi::Raw) {
+                        int32_t *o = (int32_t *)g.out + (size_t)m * g.ldo + n4;
+                        if (vec && n4 + 4 <= g.n) *(v4i *)o = acc[i][j];
+                        else
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                if (n4 + e < g.n) o[e] = acc[i][j][e];
+                    } else {
+                        int64_t *o = (int64_t *)g.out + (size_t)m * g.ldo + n4;
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
-                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
-                            acc[i][j][e] = (NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
-                                                   : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1)) +
-                                           g.gelu_off;
+                            const int64_t r = rq(acc[i][j][e], 0, mj[e]);
+                            if (n4 + e < g.n) o[e] = NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
                         }
-                const int T = 2 * g.gelu_off;  // 256 or 65,536 entries, copied into LDS
-                for (int c = threadIdx.x; c < T / 16; c += 2 * BN)
-                    *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
-                __syncthreads();
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) acc[i][j][e] = gemm_lds[acc[i][j][e]];
-                __syncthreads();  // the table reads are done before the regions are written
+                    }
+                }
             }
-            if (EPI == (int)Epi::GeluWide) {  // the i16 table (128 KiB) is read through the caches
+            return;
+        }
+        if (EPI == (int)Epi::LogitsCompact) {
+            // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the
+            // largest logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16)
+            // per logit; the table index min(max - l, len - 1) follows exactly from them, because
+            // max - l = (max - tilemax) + (tilemax - l) and cap16 >= len - 1. Each row's 64
+            // columns are 16 in each of the 4 lanes lane % 16 + 16 c.
+            int32_t mult[4][4];
 #pragma unroll
-                for (int i = 0; i < 8; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
-                            const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
-                                                     : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
-                            acc[i][j][e] = g.gelu16[y + g.gelu_off];
-                        }
+            for (int j = 0; j < 4; j++) {
+                int32_t bj[4];
+                params(j, bj, mult[j]);
             }
-            // GeluWide: the hi plane of every row, then the lo plane (this wave's region is
-            // rewritten only after its own reads: LDS operations of a wave stay in order)
-            constexpr int PLANES = EPI == (int)Epi::GeluWide ? 2 : 1;
+            int8_t *wr = gemm_lds + wave * 18432;  // this wave's staging region: 128 rows x 144 B
+            if (vec) __syncthreads();              // every wave finished reading the stages
 #pragma unroll
-            for (int pl = 0; pl < PLANES; pl++) {
-#pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < 8; i++) {
+                int64_t l[4][4], mx = INT64_MIN;
 #pragma unroll
                 for (int j = 0; j < 4; j++)
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        int32_t v;
-                        if (EPI == (int)Epi::Act) {  // ops.rs:123-130
-                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
-                            v = NARROW ? med3_i32((int32_t)r, -127, 127) : (int32_t)clamp64(r, -127, 127);
-                        } else if (EPI == (int)Epi::GeluWide) {
-                            v = pl == 0 ? acc[i][j][e] >> 8 : (acc[i][j][e] & 255) - 128;
-                        } else {
-                            v = acc[i][j][e];
-                        }
-                        wr[(i * 16 + g4 + e) * 80 + j * 16 + c16] = (int8_t)v;
+                        const int64_t r = rq(acc[i][j][e], 0, mult[j][e]);
+                        const bool ok = cw + 16 * j + 4 * cg + e < g.n;
+                        l[j][e] = ok ? (NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : INT64_MIN;
+                        mx = l[j][e] > mx ? l[j][e] : mx;
                     }
 #pragma unroll
+                for (int o = 16; o < 64; o <<= 1) {
+                    const int64_t u = __shfl_xor(mx, o, 64);
+                    mx = u > mx ? u : mx;
+                }
+                const int m = rw + 16 * i + rl;
+                if (m < g.m && cg == 0 && cw < g.n) g.tmax[(size_t)m * g.tmax_ld + cw / 64] = mx;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t w2[2];
+#pragma unroll
+                    for (int p = 0; p < 2; p++) {
+                        const int64_t d0 = mx - l[j][2 * p], d1 = mx - l[j][2 * p + 1];
+                        const uint32_t u0 = (uint32_t)(d0 < g.cap16 ? d0 : g.cap16);
+                        const uint32_t u1 = (uint32_t)(d1 < g.cap16 ? d1 : g.cap16);
+                        w2[p] = (u0 & 0xFFFF) | (u1 << 16);
+                    }
+                    if (vec) {
+                        *(uint2 *)(wr + (16 * i + rl) * 144 + (16 * j + 4 * cg) * 2) = make_uint2(w2[0], w2[1]);
+                    } else if (m < g.m) {
+                        uint16_t *o = (uint16_t *)g.out + (size_t)m * g.ldo + cw + 16 * j + 4 * cg;
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (cw + 16 * j + 4 * cg + e < g.n) o[e] = (uint16_t)(w2[e >> 1] >> (16 * (e & 1)));
+                    }
+                }
+            }
+            if (!vec) return;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int rl2 = q * 8 + (lane >> 3), cl = (lane & 7) * 8;
+                const v4i v = *(const v4i *)(wr + rl2 * 144 + cl * 2);
+                const int m = rw + rl2, n = cw + cl;
+                if (m >= g.m) continue;
+                uint16_t *o = (uint16_t *)g.out + (size_t)m * g.ldo + n;
+                if (n + 8 <= g.n) {
+                    *(v4i *)o = v;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; t++)
+                        if (n + t < g.n) o[t] = (uint16_t)((uint32_t)v[t >> 1] >> (16 * (t & 1)));
+                }
+            }
+            return;
+        }
+        // Act, Gelu, GeluWide: i8 outputs (GeluWide: the two planes of each i16 output), staged
+        // per wave in LDS (128 rows x 80 B) and stored as 16-byte row pieces. Gelu copies its
+        // table (256 or 65,536 entries) into LDS first; the staging regions follow it.
+        int toff = 0;
+        if (vec) {
+            __syncthreads();  // every wave finished reading the stages
+            if (EPI == (int)Epi::Gelu) {
+                const int T = 2 * g.gelu_off;
+                for (int c = threadIdx.x; c < T / 16; c += 2 * BN)
+                    *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
+                __syncthreads();
+                toff = (T + 1023) & ~1023;
+            }
+        }
+        int8_t *wr = gemm_lds + toff + wave * 10240;
+        // GeluWide: the hi plane of every row, then the lo plane (this wave's region is rewritten
+        // only after its own reads: LDS operations of a wave stay in order)
+        constexpr int PLANES = EPI == (int)Epi::GeluWide ? 2 : 1;
+#pragma unroll
+        for (int pl = 0; pl < PLANES; pl++) {
+            auto byte_of = [&](int32_t v) -> uint32_t {
+                if (EPI == (int)Epi::GeluWide) return (uint32_t)(pl == 0 ? v >> 8 : (v & 255) - 128) & 255;
+                return (uint32_t)v & 255;
+            };
+            if (!vec) {  // unaligned output rows: one byte store per output
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int m = rw + 16 * i + rl, n = cw + 16 * j + 4 * cg + e;
+                            if (m >= g.m || n >= g.n) continue;
+                            const int32_t a = EPI == (int)Epi::Gelu ? (int32_t)g.gelu[acc[i][j][e]] : acc[i][j][e];
+                            const int8_t v = (int8_t)byte_of(a);
+                            if (EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
+                                const RowInfo ri = g.kv_rows[m];
+                                const int part = n >= 2 * g.kv_d, c = n - (part + 1) * g.kv_d;
+                                const int hh = c / g.kv_hd, cc = c - hh * g.kv_hd;
+                                (part ? g.vc : g.kc)[(((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc] = v;
+                                continue;
+                            }
+                            const size_t orow = EPI == (int)Epi::GeluWide ? 2 * (size_t)m + pl : (size_t)m;
+                            ((int8_t *)g.out)[orow * g.ldo + n] = v;
+                        }
+                continue;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t b[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)gemm_lds[acc[i][j][e]] : byte_of(acc[i][j][e]);
+                    *(uint32_t *)(wr + (16 * i + rl) * 80 + 16 * j + 4 * cg) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+                    if (EPI == (int)Epi::Gelu && j == 3) asm volatile("" ::: "memory");  // 16 lookups in flight at most
+                }
+#pragma unroll
             for (int q = 0; q < 8; q++) {
-                const int rl = q * 16 + (lane >> 2), cl = (lane & 3) * 16;
-                const v4i v = *(const v4i *)(wr + rl * 80 + cl);
-                const int m = rw + rl, n = cw + cl;
+                const int rl2 = q * 16 + (lane >> 2), cl = (lane & 3) * 16;
+                const v4i v = *(const v4i *)(wr + rl2 * 80 + cl);
+                const int m = rw + rl2, n = cw + cl;
                 if (m >= g.m) continue;
                 if (EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
                     // K or V of the row straight into the cache (kv_d, kv_hd multiples of 16);
@@ -286,91 +473,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                         if (n + t < g.n) o[t] = (int8_t)(v[t >> 2] >> (8 * (t & 3)));
                 }
             }
-            }
-            return;
         }
-        if (EPI == (int)Epi::Residual) {  // ops.rs:131-145, in two halves of 64 rows
-            // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-#pragma unroll
-                for (int i = 4 * h; i < 4 * h + 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int64_t r = rq(acc[i][j][e], bias[j], mult[j]);
-                            *(int32_t *)(wr + ((i - 4 * h) * 16 + g4 + e) * 272 + (j * 16 + c16) * 4) =
-                                NARROW ? (int32_t)r : (int32_t)clamp64(r, INT32_MIN, INT32_MAX);
-                        }
-#pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const int rl = q * 4 + (lane >> 4), cl = (lane & 15) * 4;
-                    const v4i v = *(const v4i *)(wr + rl * 272 + cl * 4);
-                    const int m = rw + 64 * h + rl, n = cw + cl;
-                    if (m >= g.m) continue;
-                    int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n;
-                    if (n + 4 <= g.n) {
-                        v4i xv = *(const v4i *)x;
-#pragma unroll
-                        for (int t = 0; t < 4; t++) xv[t] = (int32_t)clamp64((int64_t)xv[t] + v[t], -RES, RES);
-                        *(v4i *)x = xv;
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < 4; t++)
-                            if (n + t < g.n) x[t] = (int32_t)clamp64((int64_t)x[t] + v[t], -RES, RES);
-                    }
-                }
-            }
-            return;
-        }
-        if (EPI == (int)Epi::LogitsCompact) {
-            // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the
-            // largest logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16)
-            // per logit; the table index min(max - l, len - 1) follows exactly from them.
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    int64_t l[4], mx = INT64_MIN;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int64_t r = rq(acc[i][j][e], 0, mult[j]);
-                        l[j] = okn[j] ? (NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : INT64_MIN;
-                        mx = l[j] > mx ? l[j] : mx;
-                    }
-#pragma unroll
-                    for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes that hold this row
-                        const int64_t u = __shfl_xor(mx, o, 64);
-                        mx = u > mx ? u : mx;
-                    }
-                    const int rl = i * 16 + g4 + e, m = rw + rl;
-                    if (m < g.m && c16 == 0 && cw < g.n) g.tmax[(size_t)m * g.tmax_ld + cw / 64] = mx;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int64_t dd = mx - l[j];
-                        *(uint16_t *)(wr + rl * 144 + (j * 16 + c16) * 2) = (uint16_t)(dd < g.cap16 ? dd : g.cap16);
-                    }
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                const int rl = q * 8 + (lane >> 3), cl = (lane & 7) * 8;
-                const v4i v = *(const v4i *)(wr + rl * 144 + cl * 2);
-                const int m = rw + rl, n = cw + cl;
-                if (m >= g.m) continue;
-                uint16_t *o = (uint16_t *)g.out + (size_t)m * g.ldo + n;
-                if (n + 8 <= g.n) {
-                    *(v4i *)o = v;
-                } else {
-#pragma unroll
-                    for (int t = 0; t < 8; t++)
-                        if (n + t < g.n) o[t] = (uint16_t)((uint32_t)v[t >> 1] >> (16 * (t & 1)));
-                }
-            }
-            return;
-        }
+        return;
     }
+    // The wide epilogues (no SWAP)
     if (EPI == (int)Epi::ResidualWide || EPI == (int)Epi::LogitsWide || EPI == (int)Epi::LogitsCompactWide) {
         // i16 operand rows as planes (ops.rs:178-206,246-277): the lane holds plane rows
         // 4 (lane / 16) + e of each 16-row tile, so e = 0, 1 are the hi and lo planes of one row
@@ -433,132 +539,56 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         return;
     }
-    if (EPI == (int)Epi::LogitsCompact) {
-        // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the largest
-        // logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16) per logit.
-        // The table index min(max - l, len - 1) is recovered exactly from them, because
-        // max - l = (max - tilemax) + (tilemax - l) and cap16 >= len - 1.
-        const int tile_n0 = n0 + wn * 64;
-        int32_t mlt[4];
-        bool okn[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = tile_n0 + j * 16 + (lane & 15);
-            okn[j] = n < g.n;
-            mlt[j] = okn[j] ? g.mult[n] : 0;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + e;
-                int64_t l[4], mx = INT64_MIN;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int64_t r = rq(acc[i][j][e], 0, mlt[j]);
-                    l[j] = okn[j] ? (NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : INT64_MIN;
-                    mx = l[j] > mx ? l[j] : mx;
-                }
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes that hold this row
-                    const int64_t u = __shfl_xor(mx, o, 64);
-                    mx = u > mx ? u : mx;
-                }
-                if (m < g.m) {
-                    if ((lane & 15) == 0 && tile_n0 < g.n) g.tmax[(size_t)m * g.tmax_ld + tile_n0 / 64] = mx;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        if (!okn[j]) continue;
-                        const int64_t dd = mx - l[j];
-                        ((uint16_t *)g.out)[(size_t)m * g.ldo + tile_n0 + j * 16 + (lane & 15)] =
-                            (uint16_t)(dd < g.cap16 ? dd : g.cap16);
-                    }
-                }
-            }
-        }
-        return;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-        if (n >= g.n) continue;
-        int32_t bias = 0, mult = 0;
-        if (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu ||
-            EPI == (int)Epi::GeluWide)
-            bias = g.bias[n];
-        if (EPI != (int)Epi::Raw) mult = g.mult[n];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm * 128 + i * 16 + (lane >> 4) * 4 + e;
-                if (m >= g.m) continue;
-                const int32_t a = acc[i][j][e];
-                const size_t o = (size_t)m * g.ldo + n;
-                if (EPI == (int)Epi::Raw) {
-                    ((int32_t *)g.out)[o] = a;
-                    continue;
-                }
-                const int64_t r = rq(a, bias, mult);
-                if (EPI == (int)Epi::Act) {  // ops.rs:123-130
-                    const int8_t v = (int8_t)(NARROW ? med3_i32((int32_t)r, -127, 127) : clamp64(r, -127, 127));
-                    if (g.kv_rows && n >= g.kv_d) {
-                        const RowInfo ri = g.kv_rows[m];
-                        const int part = n >= 2 * g.kv_d, c = n - (part + 1) * g.kv_d;
-                        const int hh = c / g.kv_hd, cc = c - hh * g.kv_hd;
-                        (part ? g.vc : g.kc)[(((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc] = v;
-                    } else {
-                        ((int8_t *)g.out)[o] = v;
-                    }
-                } else if (EPI == (int)Epi::Residual) {  // ops.rs:131-145
-                    // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R
-                    int32_t *x = (int32_t *)g.out + o;
-                    const int64_t rs = NARROW ? (int64_t)(int32_t)r : clamp64(r, INT32_MIN, INT32_MAX);
-                    *x = (int32_t)clamp64((int64_t)*x + rs, -RES, RES);
-                } else if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62
-                    const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
-                                             : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
-                    ((int8_t *)g.out)[o] = g.gelu[y + g.gelu_off];
-                } else if (EPI == (int)Epi::GeluWide) {  // the two planes of the i16 entry
-                    const int32_t y = NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
-                                             : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1);
-                    const int32_t v = g.gelu16[y + g.gelu_off];
-                    ((int8_t *)g.out)[2 * (size_t)m * g.ldo + n] = (int8_t)(v >> 8);
-                    ((int8_t *)g.out)[(2 * (size_t)m + 1) * g.ldo + n] = (int8_t)((v & 255) - 128);
-                } else {  // Logits: ops.rs:229-234
-                    ((int64_t *)g.out)[o] = NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
-                }
-            }
-        }
-    }
 }
 
-template <int EPI, bool NARROW, int BN>
+template <int EPI, bool NARROW, int BN, bool VEC>
 static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
     constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16;
-    // the stages, and the per-wave epilogue regions of 18 KiB
-    constexpr size_t stages = (size_t)GEMM_STAGES * FRAGS * 1024, regions = (size_t)WAVES * 18432;
-    constexpr size_t lds = stages > regions ? stages : regions;
+    // the stages, and the epilogue's LDS: per-wave staging regions (18 KiB for the u16 logits
+    // and the i16-plane epilogues, 10 KiB for i8 outputs), after the GELU table for Gelu
+    constexpr size_t stages = (size_t)GEMM_STAGES * FRAGS * 1024;
+    constexpr bool I8OUT = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
+    constexpr size_t regions = (size_t)WAVES * (I8OUT ? 10240 : 18432);
+    constexpr size_t lds_max = (EPI == (int)Epi::Gelu ? 65536 : 0) + (stages > regions ? stages : regions);
     static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
     if (!ready) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
         if (e != hipSuccess) return e;
         ready = true;
     }
+    size_t lds = stages > regions ? stages : regions;
+    if (EPI == (int)Epi::Gelu && VEC) {
+        const size_t t = ((size_t)2 * g.gelu_off + 1023) & ~(size_t)1023;
+        lds = stages > t + regions ? stages : t + regions;
+    }
     const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN>), dim3(gm * gn), dim3(2 * BN), lds, stream, g);
+    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC>), dim3(gm * gn), dim3(2 * BN), lds, stream, g);
     return hipGetLastError();
 }
 
 // 256 x 128 tiles (two workgroups per CU, so one's epilogue overlaps the other's main loop),
 // except for the i8 GELU epilogue of a wide product: each workgroup copies the 64 KiB table
 // into LDS, and 256 x 256 tiles halve those copies (measured: c_fc 5% faster; the other wide
-// products are slower with one workgroup per CU).
+// products are slower with one workgroup per CU). Outputs whose rows are not 16-byte aligned
+// take the per-output store path.
 template <int EPI, bool NARROW>
 static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
-    if (EPI == (int)Epi::Gelu && g.n > 1024) return launch_gemm_t<EPI, NARROW, 256>(g, stream);
-    return launch_gemm_t<EPI, NARROW, 128>(g, stream);
+    constexpr bool WIDE = EPI == (int)Epi::ResidualWide || EPI == (int)Epi::LogitsWide ||
+                          EPI == (int)Epi::LogitsCompactWide;
+    if constexpr (WIDE) {
+        return launch_gemm_t<EPI, NARROW, 128, true>(g, stream);
+    } else {
+        constexpr size_t ES = EPI == (int)Epi::Residual || EPI == (int)Epi::Raw ? 4
+                              : EPI == (int)Epi::LogitsCompact ? 2
+                              : EPI == (int)Epi::Logits ? 8 : 1;
+        const bool vec = ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0;
+        if (!vec) return launch_gemm_t<EPI, NARROW, 128, false>(g, stream);
+        if constexpr (EPI == (int)Epi::Gelu) {
+            if (g.n > 1024) return launch_gemm_t<EPI, NARROW, 256, true>(g, stream);
+        }
+        return launch_gemm_t<EPI, NARROW, 128, true>(g, stream);
+    }
 }
 
 template <int EPI>
