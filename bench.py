@@ -11,7 +11,9 @@ payloads and the .taco container.
 Prints one JSON line. `value` is fold tokens per second with the token stream and the model
 already resident (model upload and token staging are outside the timed region; per step the
 host sends 8 B and receives 24 B per token). `roofline` is the int8 GEMM kernels against the
-MI355X dense int8 MFMA peak, from hipEvents around every launch in the timed steps.
+MI355X dense int8 MFMA peak, from hipEvents around every launch on the batch stream in as many
+profiled steps, run right after the timed ones (events around every launch leave the GPU idle
+about 10 us between kernels, so the timed steps run without them).
 `cpu_baseline` is the oracle's C++ restatement of the reference CPU fast path (AVX2 products,
 prefill chunk 32, one window per thread) timed on a sample of the same windows in the same run;
 its payloads must equal the GPU's.
@@ -169,15 +171,27 @@ def run_fold(args):
         ts = time.time()
         payloads, cont = step()
         log(f"warmup {i}: {time.time() - ts:.3f}s, container {len(cont)} B")
-    hip._check(hip.lib().hs_batch_set_profiling(batch.h, 1))
-    hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
+    # The timed steps run without per-launch events (an event pair around every launch costs
+    # about 10 us of idle GPU between kernels); the per-op times and the roofline come from the
+    # same number of profiled steps right after them.
     phase.update(fold=0.0, container=0.0)
     ts = time.perf_counter()
     for i in range(args.steps):
         payloads, cont = step()
     elapsed = time.perf_counter() - ts
+    timed_phase = dict(phase)
+    psteps = max(1, args.steps)
+    hip._check(hip.lib().hs_batch_set_profiling(batch.h, 1))
+    hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
+    tp = time.perf_counter()
+    for i in range(psteps):
+        ppay, pcont = step()
+    profiled_s = time.perf_counter() - tp
     hip._check(hip.lib().hs_batch_set_profiling(batch.h, 0))
     prof = read_profile(hip, batch)
+    if pcont != cont:
+        log("PARITY FAILURE: the profiled steps gave another container")
+        sys.exit(1)
     gemm = [v for kk, v in prof.items() if kk.startswith("gemm")]
     gemm_ns = sum(v["ns"] for v in gemm)
     gemm_ops = sum(v["ops"] for v in gemm)
@@ -189,11 +203,12 @@ def run_fold(args):
     coded = sum(1 for p in payloads if p is not None and len(p) < block_size)
     log(f"timed: {args.steps} steps in {elapsed:.3f}s -> {value:.0f} tokens/s; container "
         f"{len(cont)} B sha256 {cont_sha[:16]}, {coded}/{W} blocks coded")
-    gpu_ms = sum(v["ns"] for v in prof.values()) / 1e6 / args.steps
-    log(f"  per step: fold call {1e3 * phase['fold'] / args.steps:.3f} ms (kernels {gpu_ms:.3f} ms), "
-        f"container {1e3 * phase['container'] / args.steps:.3f} ms")
+    gpu_ms = sum(v["ns"] for v in prof.values()) / 1e6 / psteps
+    log(f"  per step: fold call {1e3 * timed_phase['fold'] / args.steps:.3f} ms, container "
+        f"{1e3 * timed_phase['container'] / args.steps:.3f} ms; profiled steps "
+        f"{1e3 * profiled_s / psteps:.3f} ms (kernels {gpu_ms:.3f} ms)")
     for kk, v in sorted(prof.items(), key=lambda x: -x[1]["ns"]):
-        log(f"  {kk:12s} {v['ns'] / 1e6 / args.steps:8.3f} ms/step  {v['launches'] // args.steps:5d} "
+        log(f"  {kk:12s} {v['ns'] / 1e6 / psteps:8.3f} ms/step  {v['launches'] // psteps:5d} "
             f"launches/step" + (f"  {v['ops'] / v['ns'] / 1e3:7.1f} TOPS" if v["ops"] and v["ns"] else ""))
 
     unfold = None
@@ -262,7 +277,9 @@ def run_fold(args):
                      "launches": gemm_launches,
                      "ops_per_launch": gemm_ops // max(1, gemm_launches),
                      "avg_launch_us": round(gemm_ns / max(1, gemm_launches) / 1e3, 2)},
-        "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / args.steps, 3) for kk, v in prof.items()},
+        "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / psteps, 3) for kk, v in prof.items()},
+        "profiled_steps": {"steps": psteps, "ms_per_step": round(1e3 * profiled_s / psteps, 3),
+                           "kernel_ms_per_step": round(gpu_ms, 3)},
         "cpu_baseline": cpu,
     }
     if unfold:
