@@ -3,7 +3,9 @@
 // avoid generic 128-bit division, which the GPU compiler expands into a bit-serial loop.
 #pragma once
 
+#include <cmath>
 #include <cstdint>
+#include <cstring>
 
 #if defined(__HIPCC__)
 #include <hip/hip_runtime.h>
@@ -168,6 +170,25 @@ HS_HD int64_t shift_round_hi(int64_t t, int64_t g, uint32_t s) {
     if (s == 64) return hi + (int64_t)((uint64_t)p >> 63);
     const uint32_t u = s - 64;
     return (hi + ((int64_t)1 << (u - 1))) >> u;
+}
+
+// floor((c inv gamma m + 2^(s - 1)) / 2^s) (the LayerNorm element rule, layernorm.rs:66-108,
+// s <= 126) in double precision, with kr = ldexp((double)inv * m, -s) of the row:
+// v = fma(c kr, gamma, 1/2). The roundings (inv to double, inv m, c kr, the fma) keep
+// |v - (z + 1/2)| <= 4 2^-53 (|z| + 1) < 2^-20 for |v| <= 2^30 (z the exact quotient), so
+// floor(v) is floor(z + 1/2) when v lies at least 2^-20 from an integer. Adding 1.5 2^52 rounds
+// v to the nearest integer r (exact for |v| <= 2^30; r is the low word of the sum's encoding) and
+// dl = v - r is exact, so floor(v) = r - [dl < 0]. Returns false (f unset) when the distance test
+// fails: the caller then takes the integer rule. |f| <= 2^30.
+HS_HD bool ln_elem_f64(int32_t c, double kr, double gamma, int32_t *f) {
+    const double v = fma((double)c * kr, gamma, 0.5);
+    const double t = v + 6755399441055744.0;
+    const double dl = v - (t - 6755399441055744.0);
+    if (!(fabs(v) <= 1073741824.0 && fabs(dl) >= 0x1p-20)) return false;
+    uint64_t bits;
+    memcpy(&bits, &t, sizeof bits);
+    *f = (int32_t)(uint32_t)bits - (dl < 0.0 ? 1 : 0);
+    return true;
 }
 
 // The LayerNorm scale of a row (layernorm.rs:188-256): inv = floor(2^k / isqrt(var 2^(2j) + eps))

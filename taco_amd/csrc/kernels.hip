@@ -781,18 +781,32 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
     const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
     const bool wide = a.bits == 16;
     int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+    // Each element first takes the double-precision form of the rule (ln_elem_f64), which gives
+    // the exact integer or declines; a declined element takes the integer rule below.
+    const bool fpath = a.beta_frac == 0 && a.s <= 126;
+    const double kr = ldexp((double)inv * (double)a.m, -a.s);
+    const int32_t mean32 = (int32_t)mean;  // |x|, |mean| < 2^30, so x - mean fits i32
 #pragma unroll
     for (int t = 0; t < NG; t++) {
         const int j = 4 * (lane + 64 * t);
         if (j >= d) continue;
         const v4i bv = *(const v4i *)(a.beta + j);
         const int64_t *gp = a.gm + j;
+        const uint2 graw = *(const uint2 *)(a.gamma + j);  // four i16 gammas (j % 4 == 0)
         uint32_t packed = 0, packed_lo = 0;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int64_t c = (int64_t)xv[t][e] - mean;
-            int64_t y;
-            if (fast) {  // the rounding shift from the high word of (c inv) (gamma m)
+            int64_t y = 0;
+            bool done = false;
+            if (fpath) {
+                const int32_t ge = (int32_t)(int16_t)((e < 2 ? graw.x : graw.y) >> (16 * (e & 1)));
+                int32_t f = 0;
+                done = ln_elem_f64(xv[t][e] - mean32, kr, (double)ge, &f);
+                y = (int64_t)f + bv[e];
+            }
+            if (done) {
+            } else if (fast) {  // the rounding shift from the high word of (c inv) (gamma m)
                 y = shift_round_hi(c * (int64_t)inv, gp[e], (uint32_t)a.s) + bv[e];
             } else {
                 const i128 cinv = small ? (i128)(c * (int64_t)inv) : (i128)c * (i128)(u128)inv;
@@ -819,12 +833,151 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
     }
 }
 
+// Four rows per wave, 16 lanes per row (d % 4 == 0, d <= 64 NG <= 1024): the per-row work (the
+// lane reductions, mean, ln_inv) runs for four rows in one instruction stream, over 4 butterfly
+// steps of 16 lanes. Lane q of a row holds columns 4 (q + 16 t) .. +4 for t < NG. beta and gamma
+// (the same columns for every row) are copied into LDS once per workgroup while x loads.
+template <int NG>
+__global__ __launch_bounds__(256) void k_layernorm_rows4(LnArgs a, int n_rows) {
+    __shared__ __attribute__((aligned(16))) int32_t s_beta[64 * NG];
+    __shared__ __attribute__((aligned(16))) double s_gamma[64 * NG];
+    const int lane = threadIdx.x & 63, q = lane & 15;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool live = row < n_rows;
+    const int d = a.d;
+    const int32_t *x = a.x + (size_t)(live ? (a.src ? a.src[row] : row) : 0) * d;
+    v4i xv[NG];
+#pragma unroll
+    for (int t = 0; t < NG; t++) {
+        const int j = 4 * (q + 16 * t);
+        xv[t] = (live && j < d) ? *(const v4i *)(x + j) : v4i{0, 0, 0, 0};
+    }
+    for (int c = threadIdx.x; c < d; c += 256) {  // gamma as doubles (exact)
+        s_beta[c] = a.beta[c];
+        s_gamma[c] = (double)a.gamma[c];
+    }
+    int64_t sum = 0;
+    uint64_t lo = 0, hi = 0;
+    int32_t mx = INT32_MIN, mn = INT32_MAX;
+#pragma unroll
+    for (int t = 0; t < NG; t++) {
+        const int j = 4 * (q + 16 * t);
+        if (j >= d) continue;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int32_t v = xv[t][e];
+            sum += v;
+            const uint32_t u = (uint32_t)(v < 0 ? -v : v);
+            const uint64_t p = (uint64_t)u * u;
+            lo += p;
+            hi += lo < p;
+            mx = v > mx ? v : mx;
+            mn = v < mn ? v : mn;
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes of this row
+        sum += __shfl_xor(sum, o, 64);
+        const uint64_t lo2 = __shfl_xor(lo, o, 64), hi2 = __shfl_xor(hi, o, 64);
+        lo += lo2;
+        hi += hi2 + (lo < lo2);
+        const int32_t mx2 = __shfl_xor(mx, o, 64), mn2 = __shfl_xor(mn, o, 64);
+        mx = mx2 > mx ? mx2 : mx;
+        mn = mn2 < mn ? mn2 : mn;
+    }
+    __syncthreads();  // beta and gamma are in LDS
+    if (!live) return;
+    const u128 Q = ((u128)hi << 64) | lo;
+    const int64_t mean = floor_div64(sum, d);
+    const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
+    const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
+    const int64_t c1 = (int64_t)mx - mean, c2 = mean - (int64_t)mn;
+    const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
+    const bool small = (u128)cmax * inv < ((u128)1 << 63);
+    const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
+    const bool wide = a.bits == 16;
+    int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+    // Each element first takes the double-precision form of the rule (ln_elem_f64), which gives
+    // the exact integer or declines. Every group is stored from it; the groups with a declined
+    // element are then recomputed by the integer rule and stored again (the same lane rewrites
+    // its own bytes, in order).
+    const bool fpath = a.beta_frac == 0 && a.s <= 126;
+    const double kr = ldexp((double)inv * (double)a.m, -a.s);
+    const int32_t lim = wide ? 32767 : 127;
+    const int32_t mean32 = (int32_t)mean;  // |x|, |mean| < 2^30, so x - mean fits i32
+    auto put = [&](int j, const int32_t *y) {
+        uint32_t packed = 0, packed_lo = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (!wide) {
+                packed |= (uint32_t)(uint8_t)(int8_t)y[e] << (8 * e);
+            } else {
+                packed |= (uint32_t)(uint8_t)(y[e] >> 8) << (8 * e);
+                packed_lo |= (uint32_t)(uint8_t)((y[e] & 255) - 128) << (8 * e);
+            }
+        }
+        *(uint32_t *)(out + j) = packed;
+        if (wide) *(uint32_t *)(out + a.ldo + j) = packed_lo;
+    };
+    uint32_t redo = fpath ? 0u : ~0u;  // bit t: group t takes the integer rule
+    if (fpath) {
+#pragma unroll
+        for (int t = 0; t < NG; t++) {
+            const int j = 4 * (q + 16 * t);
+            if (j >= d) continue;
+            int32_t y[4];
+            bool all = true;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int32_t f = 0;
+                all &= ln_elem_f64(xv[t][e] - mean32, kr, s_gamma[j + e], &f);
+                // a saturated f + beta lies beyond the clamp exactly when the sum does
+                y[e] = med3_i32(__builtin_elementwise_add_sat(f, s_beta[j + e]), -lim, lim);
+            }
+            put(j, y);
+            redo |= all ? 0u : 1u << t;
+        }
+    }
+    if (redo == 0) return;
+#pragma unroll
+    for (int t = 0; t < NG; t++) {
+        const int j = 4 * (q + 16 * t);
+        if (j >= d || !((redo >> t) & 1)) continue;
+        const int64_t *gp = a.gm + j;
+        const int32_t *bp = a.beta + j;
+        int32_t y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int64_t c = (int64_t)xv[t][e] - mean;
+            int64_t yy64;
+            if (fast) {  // the rounding shift from the high word of (c inv) (gamma m)
+                yy64 = shift_round_hi(c * (int64_t)inv, gp[e], (uint32_t)a.s) + bp[e];
+            } else {
+                const i128 cinv = small ? (i128)(c * (int64_t)inv) : (i128)c * (i128)(u128)inv;
+                const i128 p = cinv * (i128)gp[e];
+                i128 yy;
+                if (a.beta_frac == 0) {
+                    yy = shift_round128(p, a.s, 126) + (i128)bp[e];
+                } else {
+                    const i128 cb = (i128)bp[e] << (a.s - a.beta_frac);
+                    yy = shift_round128(p + cb, a.s, 126);
+                }
+                yy64 = clamp128(yy, -32767, 32767);
+            }
+            y[e] = (int32_t)clamp64(yy64, -lim, lim);
+        }
+        put(j, y);
+    }
+}
+
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
     const dim3 grid((n_rows + 3) / 4);
     // the vector forms need 4-aligned rows: d and ldo multiples of 4
-    if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 1024) {
-        hipLaunchKernelGGL(k_layernorm_rows<4>, grid, dim3(256), 0, stream, a, n_rows);
+    if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 768) {
+        hipLaunchKernelGGL(k_layernorm_rows4<12>, dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
+    } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 1024) {
+        hipLaunchKernelGGL(k_layernorm_rows4<16>, dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
         hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
     } else {

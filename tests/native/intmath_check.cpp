@@ -155,6 +155,48 @@ int main(int argc, char **argv) {
         CHECK(hs::ln_inv(sq, nn, k, j, eps) == want, "ln_inv");
         count++;
     }
+    // ln_elem_f64 against floor((c inv gamma m + 2^(s-1)) / 2^s) in i128 (|product| < 2^126):
+    // every value it returns is exact; it may only decline.
+    auto exact_ln = [](int32_t c, uint64_t inv, int32_t g, int32_t m, uint32_t s) -> i128 {
+        const i128 p = (i128)c * (i128)inv * (i128)g * (i128)m;
+        return s == 0 ? p : (p + ((i128)1 << (s - 1))) >> s;
+    };
+    long declined = 0, taken = 0;
+    auto check_ln = [&](int32_t c, uint64_t inv, int32_t g, int32_t m, uint32_t s) -> bool {
+        const double kr = std::ldexp((double)inv * (double)m, -(int)s);
+        int32_t f = 0;
+        if (!hs::ln_elem_f64(c, kr, (double)g, &f)) {
+            declined++;
+            return true;
+        }
+        taken++;
+        return (i128)f == exact_ln(c, inv, g, m, s);
+    };
+    for (long i = 0; i < n; i++) {
+        // the fold's range: |c| < 2^31, inv < 2^64, |gamma| < 2^15, m < 2^31, |product| < 2^126
+        const int32_t c = (int32_t)(next() >> (33 + next() % 31)) * ((next() & 1) ? -1 : 1);
+        const int32_t g = (int32_t)(next() % 65535) - 32767;
+        const int32_t m = (int32_t)(next() >> (33 + next() % 31));
+        uint64_t inv = rnd_bits();
+        const int lc = 64 - hs::clz64((uint64_t)(c < 0 ? -(int64_t)c : c)), lg = 16, lm = 64 - hs::clz64((uint64_t)m);
+        const int room = 125 - lc - lg - lm;
+        if (room < 64) inv = room <= 0 ? 0 : inv & ((1ull << room) - 1);
+        const uint32_t s = (uint32_t)(next() % 127);
+        CHECK(check_ln(c, inv, g, m, s), "ln_elem_f64 c %d inv %llu g %d m %d s %u", c, (unsigned long long)inv, g, m, s);
+        count++;
+    }
+    // adversarial: quotients exactly on and just beside a half (p = k 2^s + 2^(s-1) + delta)
+    for (uint32_t s = 1; s <= 63; s++)
+        for (long k = -70; k <= 70; k += 7)
+            for (int delta = -3; delta <= 3; delta++) {
+                const i128 p = (i128)k * ((i128)1 << s) + ((i128)1 << (s - 1)) + delta;
+                if (p <= 0 || p >= ((i128)1 << 64)) continue;
+                CHECK(check_ln(1, (uint64_t)p, 1, 1, s), "ln_elem_f64 half s %u k %ld d %d", s, k, delta);
+                CHECK(check_ln(-1, (uint64_t)p, 1, 1, s), "ln_elem_f64 -half s %u k %ld d %d", s, k, delta);
+                CHECK(check_ln(1, (uint64_t)p, -1, 1, s), "ln_elem_f64 -g half s %u k %ld d %d", s, k, delta);
+                count += 3;
+            }
+    CHECK(taken > n / 2, "ln_elem_f64 declined too often (%ld of %ld)", declined, declined + taken);
     std::printf("ok %ld\n", count);
     return 0;
 }
