@@ -299,7 +299,8 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
         b.gelu_off = (int)hb.gelu_len / 2;
     }
     if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
-    if ((st = mem.upload(m->attn_exp, h.attn_exp.data(), h.attn_exp.size())) != HS_OK) return st;
+    // padded to a multiple of 256 entries: the prefill attention loads it in 1 KiB chunks
+    if ((st = mem.upload(m->attn_exp, h.attn_exp.data(), h.attn_exp.size(), (h.attn_exp.size() + 255) / 256 * 256)) != HS_OK) return st;
     if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size())) != HS_OK) return st;
     m->compact = h.logits_exp.size() <= (size_t)hs::CODER_MAX_TABLE;
     while ((size_t)m->d0 + 1 < h.logits_exp.size() && h.logits_exp[m->d0 + 1] == h.logits_exp[0]) m->d0++;
@@ -765,11 +766,12 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     HIP_TRY(hipMemcpyAsync(b.d_rows, info, n * sizeof(RowInfo), hipMemcpyHostToDevice, st));
     // Attention groups (runs of one slot at consecutive positions, at most 64 rows each) for
     // the MFMA prefill kernel; decode-shaped passes (short runs) use the row kernel.
-    int n_groups = 0;
+    int n_groups = 0, group_keys = 1;  // the largest key count of a group
     for (int r = 0; r < n;) {
         int c = 1;
         while (r + c < n && c < 64 && rows[r + c].slot == rows[r].slot && rows[r + c].pos == rows[r].pos + (uint32_t)c) c++;
         b.h_groups[n_groups++] = hs::AttnGroup{r, c, (int32_t)rows[r].slot, (int32_t)rows[r].pos};
+        group_keys = std::max<int>(group_keys, std::min<int>((int)rows[r].pos + c, (int)m.C));
         r += c;
     }
     const bool mfma_attn = m.hd == 64 && n >= 16 * n_groups;
@@ -859,7 +861,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
         at.out = b.d_att; at.ldo = m.d_pad;
         HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d, [&] {
-            if (mfma_attn) return hs::launch_attend_groups(at, b.d_groups, n_groups, st);
+            if (mfma_attn) return hs::launch_attend_groups(at, b.d_groups, n_groups, group_keys, st);
             if (split_attn) return hs::launch_attend_split(at, n, split_plan, b.split, st);
             return hs::launch_attend(at, n, st);
         }));

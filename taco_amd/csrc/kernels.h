@@ -131,7 +131,11 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
 struct AttnGroup {
     int32_t first, count, slot, pos0;
 };
-hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups,
+// max_keys bounds every group's key count (pos0 + count, at most ctx_cap); at most 256 keys take a
+// kernel without the recompute path of longer contexts, which reads exp_table in whole 1 KiB
+// chunks: the table must be readable (device memory) up to a multiple of 256 entries.
+// out + row ldo + head 64 must be 4-byte aligned.
+hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups, int max_keys,
                                 hipStream_t stream);
 
 // The mix record of a row for the mixed coder op of the logs profile (8 u32 words, the layout of

@@ -1330,20 +1330,22 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
 
 // =============================================================================================
 // Prefill attention on MFMA (head_dim 64). One workgroup = one group of <= 64 rows x one head;
-// wave w owns rows 16w .. 16w + 15. S = Q K^T comes from v_mfma_i32_16x16x64_i8 (exact i32) for
-// a super-block of up to AT_SB key blocks of 64, held in registers: with <= 256 keys the
-// product runs once, else once per pass. Pass 1 takes the row max (from the extreme dots: the
-// score is monotone in the dot), pass 2 turns the dots into table indices min(M - s, last) in
-// place and sums the table entries, pass 3 forms p = floor(e 2^P / S) (a 64-bit reciprocal of S
-// and one correction) and sum_j p_j v_j. The PV product splits p into four balanced signed
-// base-256 digits (crates/hardshell/src/gpt2/attention.rs:36-46): for p < 2^31 the bytes of
-// (p + 0x80808080) ^ 0x80808080 are those digits, so one word per score goes to LDS and a 4 x 4
-// byte transpose (8 v_perm_b32) gives the four digit-plane MFMA operands. Each plane is an exact
-// i8 product: |sum_j d_j v_j| <= 2^16 * 128 * 127 < 2^31.
+// wave w owns rows 16w .. 16w + 15, lane l the row 16w + l % 16. QK^T comes from
+// v_mfma_i32_16x16x64_i8 with K as the first operand (exact i32), for a super-block of up to
+// AT_SB key blocks of 64 held in registers: lane l holds the dots of its row with the keys
+// 16t + 4(l / 16) + e (t, e < 4) of each block. With <= 256 keys the product runs once, else
+// once per pass. Pass 1 takes the row max (from the extreme dots: the score is monotone in the
+// dot), pass 2 turns the dots into the table entries attn_exp[min(M - s, last)] in place and
+// sums them, pass 3 forms p = floor(e 2^P / S) and sum_j p_j v_j. The PV product splits p into
+// four balanced signed base-256 digits (crates/hardshell/src/gpt2/attention.rs:36-46): for
+// p < 2^31 the bytes of (p + 0x80808080) ^ 0x80808080 are those digits. Each plane is an exact
+// i8 product (|sum_j d_j v_j| <= 2^16 128 127 < 2^31) with V^T first: the key order inside a
+// block is permuted (key 16t + 4g + e at byte 16g + 4t + e) so that the digits a lane needs as
+// the second operand are the ones it already holds (4 x 4 byte transposes, no LDS round trip),
+// and V^T enters LDS in the same order.
 // =============================================================================================
 
 constexpr int AT_ST = 80;               // LDS row stride in bytes (64 + 16)
-constexpr int AT_PP = 68;               // words per row of the packed-digit tile (64 + 4)
 constexpr int AT_SB = 4;                // key blocks of 64 held in registers
 constexpr int ATTN_LDS_TABLE = 16384;   // attn_exp entries kept in LDS (64 KiB)
 
@@ -1361,46 +1363,65 @@ __device__ __forceinline__ void byte_transpose(uint32_t w0, uint32_t w1, uint32_
 }
 
 // NOCLAMP: score_s >= 13, so |dot m| < 2^53 keeps every score within +-2^40 (the clamp is a no-op).
-template <bool NOCLAMP>
+// LDS_TABLE: attn_exp (<= ATTN_LDS_TABLE entries) is read from a copy in LDS.
+// MULTI: some group has more than AT_SB 64 keys (Q K^T is recomputed per pass); without it the
+// kernel holds one super-block and has no recompute path.
+template <bool NOCLAMP, bool LDS_TABLE, bool MULTI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_mfma(AttnArgs a, const AttnGroup *groups) {
     __shared__ __attribute__((aligned(16))) int8_t sQ[64 * AT_ST];
-    __shared__ __attribute__((aligned(16))) int8_t sK[64 * AT_ST];
-    __shared__ __attribute__((aligned(16))) int8_t sVt[64 * AT_ST];
-    __shared__ __attribute__((aligned(16))) uint32_t sP[64 * AT_PP];
-    extern __shared__ __attribute__((aligned(16))) int32_t s_exp[];  // attn_exp when it fits
+    // the K rows of a super-block (AT_SB x 64 keys), later the V^T of its blocks (64 channels each)
+    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * AT_ST];
+    // without MULTI: the V rows of the (single) super-block, as loaded
+    __shared__ __attribute__((aligned(1024))) int8_t sV[MULTI ? 16 : AT_SB * 64 * 64];
+    extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];  // attn_exp when LDS_TABLE
     const AttnGroup G = groups[blockIdx.x];
     const int h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ql = lane & 15, qg = lane >> 4;
     int nk = G.pos0 + G.count;  // keys 0 .. nk - 1, never past the cache
     nk = nk > a.ctx_cap ? a.ctx_cap : nk;
     const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
     const int last = a.exp_len - 1;
-    // attn_exp into LDS (every score of passes 2 and 3 reads it); the launch gives the dynamic
-    // LDS only when the table fits (exp_len <= ATTN_LDS_TABLE).
-    const bool lds_table = a.exp_len <= ATTN_LDS_TABLE;
-    if (lds_table) {  // 16-byte copies when the table is 16-byte aligned (a device allocation)
+    // Dense LDS rows of 64 bytes with 16-byte chunk c of row r at slot 4 r + (c ^ sw(r % 16)), so
+    // the fragment reads of 16 consecutive rows hit distinct bank groups.
+    auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
+    if (!MULTI) {
+        // every K and V row of the group's blocks, and the table, straight into LDS before any
+        // other work (global_load_lds: lane l's 16 bytes land at the wave's base + 16 l). Rows
+        // past the cache read its last row (their keys are masked).
+        const int r = 16 * w + (lane >> 2), c = (lane & 3) ^ sw(r & 15);
+        const int nkb0 = (nk + 63) / 64;
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++) {
+            if (b >= nkb0) break;
+            int key = b * 64 + r;
+            key = key < a.ctx_cap ? key : a.ctx_cap - 1;
+            const size_t off = base + (size_t)key * 64 + 16 * c;
+            __builtin_amdgcn_global_load_lds((const void *)(a.kc + off), (lds_void *)(sKV + (b * 64 + 16 * w) * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(a.vc + off), (lds_void *)(sV + (b * 64 + 16 * w) * 64), 16, 0, 0);
+        }
+        if (LDS_TABLE)  // whole 1 KiB chunks (the table is readable to a multiple of 256 entries)
+            for (int ch = w; ch < (a.exp_len + 255) / 256; ch += 4)
+                __builtin_amdgcn_global_load_lds((const void *)(a.exp_table + ch * 256 + 4 * lane),
+                                                 (lds_void *)(s_exp + ch * 256), 16, 0, 0);
+    } else if (LDS_TABLE) {  // 16-byte copies when the table is 16-byte aligned (a device allocation)
         const bool vec = ((uintptr_t)a.exp_table & 15) == 0;
         const int n4 = vec ? a.exp_len / 4 : 0;
         for (int i = tid; i < n4; i += 256) ((v4i *)s_exp)[i] = ((const v4i *)a.exp_table)[i];
         for (int i = 4 * n4 + tid; i < a.exp_len; i += 256) s_exp[i] = a.exp_table[i];
     }
-    const int32_t *etab = lds_table ? (const int32_t *)s_exp : a.exp_table;
+    const int32_t *etab = LDS_TABLE ? (const int32_t *)s_exp : a.exp_table;
     {
         const int r = tid >> 2, c = (tid & 3) * 16;
         v4i v = {0, 0, 0, 0};
         if (r < G.count) v = *(const v4i *)(a.q + (size_t)(G.first + r) * a.ldq + h * 64 + c);
         *(v4i *)&sQ[r * AT_ST + c] = v;
     }
+    if (!MULTI) wait_vmcnt<0>();  // this wave's direct loads landed (the barrier shows them to all)
     __syncthreads();
-    const v4i qf = *(const v4i *)&sQ[(16 * w + (lane & 15)) * AT_ST + (lane >> 4) * 16];
-    // this lane's rows (e = 0..3) and their positions
-    int row[4], posr[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        row[e] = 16 * w + 4 * (lane >> 4) + e;
-        posr[e] = G.pos0 + row[e];
-    }
-    const int nkb = (nk + 63) / 64, nsb = (nkb + AT_SB - 1) / AT_SB;
+    const v4i qf = *(const v4i *)&sQ[(16 * w + ql) * AT_ST + qg * 16];
+    const int myrow = 16 * w + ql, mypos = G.pos0 + myrow;  // this lane's row and its position
+    const int nkb = (nk + 63) / 64, nsb = MULTI ? (nkb + AT_SB - 1) / AT_SB : 1;
     // score = clamp(rescale(dot, m, s), +-2^40): |dot| <= hd 2^14 <= 2^22, so |dot m| < 2^53 and
     // one multiply-add and an arithmetic shift are exact (a shift of 63 or more gives 0).
     const int s_eff = a.score_s < 63 ? a.score_s : 63;
@@ -1409,12 +1430,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int64_t r = ((int64_t)dot * a.score_m + s_half) >> s_eff;
         return NOCLAMP ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT);
     };
-    v4i S[AT_SB][4];  // the dots (then the table indices) of one super-block
-    // this thread's 16 bytes of key (or value) block kb: key kb * 64 + tid / 4, bytes 16 (tid % 4)
-    auto kv_load = [&](const int8_t *cache, int kb) {
+    auto key_of = [&](int sb, int b, int t, int e) { return (sb * AT_SB + b) * 64 + 16 * t + 4 * qg + e; };
+    v4i S[AT_SB][4];  // S[b][t][e]: the dot (then the table entry) of the row with key_of(sb, b, t, e)
+    // this thread's 16 bytes of key block kb: key kb * 64 + tid / 4, bytes 16 (tid % 4)
+    auto k_load = [&](int kb) {
         const int key = kb * 64 + (tid >> 2), c = (tid & 3) * 16;
         v4i v = {0, 0, 0, 0};
-        if (key < nk) v = *(const v4i *)(cache + base + (size_t)key * 64 + c);
+        if (key < nk) v = *(const v4i *)(a.kc + base + (size_t)key * 64 + c);
         return v;
     };
     // this thread's 4 keys x 4 channels of value block kb (one word per key): keys kb * 64 +
@@ -1428,180 +1450,259 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         return v;
     };
     auto qk_super = [&](int sb) {
+        const int nb = nkb - sb * AT_SB < AT_SB ? nkb - sb * AT_SB : AT_SB;
+        if (!MULTI) {  // the K rows are in LDS (dense, swizzled)
+#pragma unroll
+            for (int b = 0; b < AT_SB; b++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    if (b < nb) {
+                        const int r = t * 16 + ql;
+                        const v4i kf = *(const v4i *)&sKV[(4 * (b * 64 + r) + (qg ^ sw(r & 15))) * 16];
+                        S[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    } else {
+                        S[b][t] = v4i{0, 0, 0, 0};
+                    }
+                }
+            __syncthreads();  // the K rows are read: sKV may take V^T
+            return;
+        }
         v4i kreg[AT_SB];  // every key block of the super-block in flight at once
 #pragma unroll
         for (int b = 0; b < AT_SB; b++)
-            if (sb * AT_SB + b < nkb) kreg[b] = kv_load(a.kc, sb * AT_SB + b);
+            if (b < nb) kreg[b] = k_load(sb * AT_SB + b);
 #pragma unroll
-        for (int b = 0; b < AT_SB; b++) {
-            const int kb = sb * AT_SB + b;
-            if (kb >= nkb) break;
-            *(v4i *)&sK[(tid >> 2) * AT_ST + (tid & 3) * 16] = kreg[b];
-            __syncthreads();
+        for (int b = 0; b < AT_SB; b++)
+            if (b < nb) *(v4i *)&sKV[(b * 64 + (tid >> 2)) * AT_ST + (tid & 3) * 16] = kreg[b];
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++)
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                const v4i kf = *(const v4i *)&sK[(t * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
-                S[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qf, kf, v4i{0, 0, 0, 0}, 0, 0, 0);
+                if (b < nb) {
+                    const v4i kf = *(const v4i *)&sKV[(b * 64 + t * 16 + ql) * AT_ST + qg * 16];
+                    S[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf, v4i{0, 0, 0, 0}, 0, 0, 0);
+                } else {
+                    S[b][t] = v4i{0, 0, 0, 0};
+                }
             }
-            __syncthreads();
-        }
+        __syncthreads();  // the K rows are read: sKV may take the next super-block or V^T
     };
 
     // pass 1: the row max, from the largest and the smallest dot
-    int32_t dmax[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
-    int32_t dmin[4] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX};
+    int32_t dmax = INT32_MIN, dmin = INT32_MAX;
     for (int sb = 0; sb < nsb; sb++) {
         qk_super(sb);
 #pragma unroll
         for (int b = 0; b < AT_SB; b++)
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int key = (sb * AT_SB + b) * 64 + t * 16 + (lane & 15);
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (key <= posr[e] && key < nk) {
-                        dmax[e] = S[b][t][e] > dmax[e] ? S[b][t][e] : dmax[e];
-                        dmin[e] = S[b][t][e] < dmin[e] ? S[b][t][e] : dmin[e];
-                    }
-            }
-    }
-    int64_t mx[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const int32_t u = __shfl_xor(dmax[e], o, 64), v = __shfl_xor(dmin[e], o, 64);
-            dmax[e] = u > dmax[e] ? u : dmax[e];
-            dmin[e] = v < dmin[e] ? v : dmin[e];
-        }
-        const int64_t a0 = score(dmax[e]), a1 = score(dmin[e]);
-        mx[e] = a0 > a1 ? a0 : a1;  // rows past the group's count: unused
-    }
-    // the dots of super-block sb -> the table entries e = attn_exp[min(M - s, last)] (>= 0), 0 for
-    // a masked key (it adds nothing to S and gets p = 0)
-    auto to_weight = [&](int sb) {
-#pragma unroll
-        for (int b = 0; b < AT_SB; b++)
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int key = (sb * AT_SB + b) * 64 + t * 16 + (lane & 15);
+            for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int64_t dd = mx[e] - score(S[b][t][e]);
-                    S[b][t][e] = (key <= posr[e] && key < nk) ? etab[dd < last ? dd : last] : 0;
+                    const int key = key_of(sb, b, t, e);
+                    const bool ok = key <= mypos && key < nk;
+                    const int32_t hiv = ok ? S[b][t][e] : INT32_MIN, lov = ok ? S[b][t][e] : INT32_MAX;
+                    dmax = hiv > dmax ? hiv : dmax;
+                    dmin = lov < dmin ? lov : dmin;
                 }
-            }
+    }
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {  // the 4 lanes of this row
+        const int32_t u = __shfl_xor(dmax, o, 64), v = __shfl_xor(dmin, o, 64);
+        dmax = u > dmax ? u : dmax;
+        dmin = v < dmin ? v : dmin;
+    }
+    const int64_t mx = score(dmax) > score(dmin) ? score(dmax) : score(dmin);
+    // the dots of super-block sb -> the table entries attn_exp[min(M - s, last)] (>= 0), 0 for a
+    // masked key (it adds nothing to S and gets p = 0). Every index is in range and every lookup
+    // is issued (the empty asm keeps each one out of a per-key branch), all before the masking.
+    auto to_weight = [&](int sb) {
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++) {  // one block of 64 keys (16 lookups) at a time
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int64_t dd = mx - score(S[b][t][e]);
+                    S[b][t][e] = dd < 0 ? 0 : (dd < last ? (int)dd : last);
+                }
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    S[b][t][e] = etab[S[b][t][e]];
+                }
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int key = key_of(sb, b, t, e);
+                    S[b][t][e] = (key <= mypos && key < nk) ? S[b][t][e] : 0;
+                }
+        }
     };
     // pass 2: the sum of the table entries
-    int64_t sum[4] = {0, 0, 0, 0};
+    uint64_t sum = 0;
     for (int sb = 0; sb < nsb; sb++) {
-        if (nsb > 1) qk_super(sb);
+        if (MULTI && nsb > 1) qk_super(sb);
         to_weight(sb);
 #pragma unroll
         for (int b = 0; b < AT_SB; b++)
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) sum[e] += (uint32_t)S[b][t][e];
+                for (int e = 0; e < 4; e++) sum += (uint32_t)S[b][t][e];
     }
-    uint64_t frac[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) sum[e] += __shfl_xor(sum[e], o, 64);
-        frac[e] = sum[e] >= 2 ? div_2p64((uint64_t)sum[e]) : 0;  // S = 1 divides exactly
-    }
+    for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    // p = floor(e 2^P / S) (e <= S, P <= 30): v = e R with R = 2^P / S in double takes two
+    // roundings, |v - e 2^P / S| <= 2^-52 2^30; when v lies at least 2^-21 from an integer its
+    // floor is p (1.5 2^52 added rounds v to the nearest integer, the low word of the sum), and
+    // e = 0 gives v = 0 = p. Otherwise the 64-bit reciprocal floor(2^64 / S) and one correction
+    // (S = 1 divides exactly).
+    const double R = ldexp(1.0 / (double)sum, a.softmax_p);
+    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+    auto p_exact = [&](uint32_t ev) -> uint32_t {
+        const uint64_t num = (uint64_t)ev << a.softmax_p;
+        uint64_t q = num;
+        if (sum >= 2) {
+            q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
+            if (num - q * sum >= sum) q++;
+        }
+        return (uint32_t)q;
+    };
     // pass 3: p, its packed digits, and the digit-plane PV products
-    v4i acc[4][4];  // [digit plane][channel tile]
+    v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[k][c] = v4i{0, 0, 0, 0};
     for (int sb = 0; sb < nsb; sb++) {
-        if (nsb > 1) {
+        if (MULTI && nsb > 1) {
             qk_super(sb);
             to_weight(sb);
         }
-        v4i vnext = sb * AT_SB < nkb ? vt_load(sb * AT_SB) : v4i{0, 0, 0, 0};
+        const int nb = nkb - sb * AT_SB < AT_SB ? nkb - sb * AT_SB : AT_SB;
+        {  // V^T of the super-block's blocks into sKV, keys in the operand order
+            v4i vreg[AT_SB];
+            const int kg = tid >> 4, cg = tid & 15;  // keys 4 kg .. +4, channels 4 cg .. +4
+#pragma unroll
+            for (int b = 0; b < AT_SB; b++) {
+                if (b >= nb) continue;
+                if (MULTI) {
+                    vreg[b] = vt_load(sb * AT_SB + b);
+                } else {  // from the dense V rows (a key past nk has p = 0)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int kk = 4 * kg + i;
+                        vreg[b][i] = *(const int32_t *)&sV[(4 * (b * 64 + kk) + ((cg >> 2) ^ sw(kk & 15))) * 16 + 4 * (cg & 3)];
+                    }
+                }
+            }
+            const int pos0 = 16 * (kg & 3) + 4 * (kg >> 2);
+#pragma unroll
+            for (int b = 0; b < AT_SB; b++) {
+                if (b >= nb) continue;
+                uint32_t tw[4];
+                byte_transpose((uint32_t)vreg[b][0], (uint32_t)vreg[b][1], (uint32_t)vreg[b][2], (uint32_t)vreg[b][3], tw);
+#pragma unroll
+                for (int j = 0; j < 4; j++) *(uint32_t *)&sKV[(b * 64 + 4 * cg + j) * AT_ST + pos0] = tw[j];
+            }
+        }
+        __syncthreads();
 #pragma unroll
         for (int b = 0; b < AT_SB; b++) {
-            const int kb = sb * AT_SB + b;
-            if (kb >= nkb) break;
-            {  // V^T of the block into LDS (4 x 4 byte transposes); the next block loads meanwhile
-                const v4i v = vnext;
-                if (b + 1 < AT_SB && kb + 1 < nkb) vnext = vt_load(kb + 1);
-                uint32_t tw[4];
-                byte_transpose((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3], tw);
-                const int kg = tid >> 4, cg = tid & 15;  // keys 4 kg .. +4, channels 4 cg .. +4
-#pragma unroll
-                for (int j = 0; j < 4; j++) *(uint32_t *)&sVt[(4 * cg + j) * AT_ST + 4 * kg] = tw[j];
-            }
+            if (b >= nb) break;
+            uint32_t dg[4][4];
+            bool fast_all = true;
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const uint64_t num = (uint64_t)(uint32_t)S[b][t][e] << a.softmax_p;
-                    const uint64_t Sv = (uint64_t)sum[e];
-                    uint64_t q = num;
-                    if (Sv >= 2) {
-                        q = __umul64hi(num, frac[e]);  // q <= floor(num / S) <= q + 1
-                        if (num - q * Sv >= Sv) q++;
-                    }
-                    const uint32_t p = (uint32_t)q;  // <= 2^P <= 2^30
-                    sP[row[e] * AT_PP + t * 16 + (lane & 15)] = (p + 0x80808080u) ^ 0x80808080u;
+                    const uint32_t ev = (uint32_t)S[b][t][e];
+                    const double v = (double)ev * R;
+                    const double tt = v + 6755399441055744.0;
+                    const double dl = v - (tt - 6755399441055744.0);
+                    fast_all &= ev == 0 || fabs(dl) >= 0x1p-21;  // e = 0 (a masked key) gives p = 0
+                    uint64_t bits;
+                    __builtin_memcpy(&bits, &tt, sizeof bits);
+                    dg[t][e] = (uint32_t)bits - (dl < 0.0 ? 1u : 0u);
                 }
-            __syncthreads();
-            v4i af[4];
-            {
-                const uint32_t *pr = &sP[(16 * w + (lane & 15)) * AT_PP + (lane >> 4) * 16];
+            if (!fast_all) {
 #pragma unroll
-                for (int gq = 0; gq < 4; gq++) {
-                    const v4i wv = *(const v4i *)(pr + 4 * gq);
-                    uint32_t pl[4];
-                    byte_transpose((uint32_t)wv[0], (uint32_t)wv[1], (uint32_t)wv[2], (uint32_t)wv[3], pl);
+                for (int t = 0; t < 4; t++)
 #pragma unroll
-                    for (int k = 0; k < 4; k++) af[k][gq] = (int32_t)pl[k];
-                }
+                    for (int e = 0; e < 4; e++) dg[t][e] = p_exact((uint32_t)S[b][t][e]);
             }
+            v4i pf[4];  // [digit plane]: word t holds the digits of keys 16 t + 4 (l / 16) + e
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const v4i bf = *(const v4i *)&sVt[(c * 16 + (lane & 15)) * AT_ST + (lane >> 4) * 16];
+            for (int t = 0; t < 4; t++) {
+                uint32_t o[4];
+                byte_transpose((dg[t][0] + 0x80808080u) ^ 0x80808080u, (dg[t][1] + 0x80808080u) ^ 0x80808080u,
+                               (dg[t][2] + 0x80808080u) ^ 0x80808080u, (dg[t][3] + 0x80808080u) ^ 0x80808080u, o);
+#pragma unroll
+                for (int k = 0; k < 4; k++) pf[k][t] = (int32_t)o[k];
+            }
+            v4i vf[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) vf[c] = *(const v4i *)&sKV[(b * 64 + 16 * c + ql) * AT_ST + 16 * qg];
+#pragma unroll
+            for (int c = 0; c < 4; c++)
 #pragma unroll
                 for (int k = 0; k < 4; k++)
-                    acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[k], bf, acc[k][c], 0, 0, 0);
+                    acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[c], pf[k], acc[k][c], 0, 0, 0);
+        }
+        __syncthreads();  // V^T is read: sKV may take the next super-block
+    }
+    if (myrow < G.count) {
+        int8_t *o = a.out + (size_t)(G.first + myrow) * a.ldo + h * 64;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int64_t v = (int64_t)acc[0][c][e] + ((int64_t)acc[1][c][e] << 8) +
+                                  ((int64_t)acc[2][c][e] << 16) + ((int64_t)acc[3][c][e] << 24);
+                packed |= (uint32_t)(uint8_t)(int8_t)clamp128(rescale_full(v, a.out_m, a.out_s), -127, 127) << (8 * e);
             }
-            __syncthreads();
+            *(uint32_t *)(o + 16 * c + 4 * qg) = packed;
         }
     }
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (row[e] >= G.count) continue;
-            const int64_t o = (int64_t)acc[0][c][e] + ((int64_t)acc[1][c][e] << 8) +
-                              ((int64_t)acc[2][c][e] << 16) + ((int64_t)acc[3][c][e] << 24);
-            a.out[(size_t)(G.first + row[e]) * a.ldo + h * 64 + c * 16 + (lane & 15)] =
-                (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
-        }
 }
 
-hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups,
-                                hipStream_t stream) {
-    if (n_groups <= 0) return hipSuccess;
-    const size_t lds = a.exp_len <= ATTN_LDS_TABLE ? sizeof(int32_t) * (size_t)a.exp_len : 0;
-    static size_t allowed[2] = {0, 0};  // the dynamic LDS limit, raised once per variant
-    const bool noclamp = a.score_s >= 13;
-    if (lds > allowed[noclamp]) {
-        hipError_t e = hipFuncSetAttribute(noclamp ? (const void *)k_attend_mfma<true> : (const void *)k_attend_mfma<false>,
+template <bool NOCLAMP, bool LDS_TABLE, bool MULTI>
+static hipError_t launch_attend_groups_t(const AttnArgs &a, const AttnGroup *groups, int n_groups,
+                                         hipStream_t stream) {
+    // without MULTI the table lands in whole 1 KiB chunks
+    const size_t lds = LDS_TABLE ? (MULTI ? sizeof(int32_t) * (size_t)a.exp_len : ((size_t)a.exp_len + 255) / 256 * 1024) : 0;
+    static size_t allowed = 0;  // the dynamic LDS limit, raised once per variant
+    if (lds > allowed) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        allowed[noclamp] = lds;
+        allowed = lds;
     }
-    if (noclamp)
-        hipLaunchKernelGGL(k_attend_mfma<true>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
-    else
-        hipLaunchKernelGGL(k_attend_mfma<false>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+    hipLaunchKernelGGL((k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>), dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
     return hipGetLastError();
+}
+
+template <bool NOCLAMP, bool LDS_TABLE>
+static hipError_t launch_attend_groups_m(const AttnArgs &a, const AttnGroup *groups, int n_groups, int max_keys,
+                                         hipStream_t stream) {
+    if (max_keys <= AT_SB * 64) return launch_attend_groups_t<NOCLAMP, LDS_TABLE, false>(a, groups, n_groups, stream);
+    return launch_attend_groups_t<NOCLAMP, LDS_TABLE, true>(a, groups, n_groups, stream);
+}
+
+hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int n_groups, int max_keys,
+                                hipStream_t stream) {
+    if (n_groups <= 0) return hipSuccess;
+    // the output of a row is four 4-byte stores per head
+    if (a.hd != 64 || a.ldo % 4 != 0 || ((uintptr_t)a.out & 3) != 0 || max_keys < 1) return hipErrorInvalidValue;
+    const bool noclamp = a.score_s >= 13, lds_table = a.exp_len <= ATTN_LDS_TABLE;
+    if (noclamp && lds_table) return launch_attend_groups_m<true, true>(a, groups, n_groups, max_keys, stream);
+    if (noclamp) return launch_attend_groups_m<true, false>(a, groups, n_groups, max_keys, stream);
+    if (lds_table) return launch_attend_groups_m<false, true>(a, groups, n_groups, max_keys, stream);
+    return launch_attend_groups_m<false, false>(a, groups, n_groups, max_keys, stream);
 }
 
 // =============================================================================================
