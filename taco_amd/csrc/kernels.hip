@@ -60,7 +60,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// NARROW: g.fast32 holds and the shift is at least 32, so every rescaled value fits i32.
+// NARROW: g.fast32 holds and the shift is at least 31, so every rescaled value fits i32: with
+// |a + bias| <= 2^31 - 1 and -2^31 <= mult < 2^31, |(a + bias) mult| <= (2^31 - 1) 2^31, so
+// ((a + bias) mult + 2^30) >> 31 lies in [-2^31 + 1, 2^31 - 1] (larger shifts shrink it).
 // BN = 128 (4 waves, 2 x 2) or 256 (8 waves, 2 x 4); every wave computes 128 x 64.
 // VEC: the output rows are 16-byte aligned (checked by the launcher); the four-columns epilogues
 // then stage and store 16-byte pieces, else they store each output on its own.
@@ -594,7 +596,7 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
 template <int EPI>
 static hipError_t launch_gemm_e(const GemmArgs &g, hipStream_t stream) {
     const bool fast = EPI == (int)Epi::Logits || EPI == (int)Epi::LogitsCompact || g.fast32;
-    if (fast && g.shift >= 32) return launch_gemm_w<EPI, true>(g, stream);
+    if (fast && g.shift >= 31) return launch_gemm_w<EPI, true>(g, stream);
     return launch_gemm_w<EPI, false>(g, stream);
 }
 

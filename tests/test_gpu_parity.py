@@ -66,7 +66,7 @@ def test_gemm_requant_c1_shape(dev):
     w = r.integers(-127, 128, (2304, 768)).astype(np.int8)
     bias = r.integers(-(1 << 16), 1 << 16, 2304).astype(np.int32)
     mult = r.integers(1 << 30, 1 << 31, 2304).astype(np.int64).astype(np.int32)
-    for shift in (42, 0, 1, 62, 63, 64, 95, 96):
+    for shift in (42, 0, 1, 30, 31, 32, 62, 63, 64, 95, 96):
         got = hip.gemm_requant_i8(dev, w, a, bias, mult, shift)
         want = O.linear_act_ref(w, a, bias, mult, shift)
         assert np.array_equal(got, want), shift
@@ -75,6 +75,24 @@ def test_gemm_requant_c1_shape(dev):
     mult2[:4] = [-(1 << 31), (1 << 31) - 1, 0, -1]
     got = hip.gemm_requant_i8(dev, w, a, bias, mult2, 40)
     assert np.array_equal(got, O.linear_act_ref(w, a, bias, mult2, 40))
+
+
+def test_gemm_requant_at_the_narrow_bound(dev):
+    # The epilogue keeps rescaled values in i32 when the host shows |acc + bias| < 2^31 and the
+    # shift is at least 31: operands at that bound (|acc| = 768 2^14, |bias| = 2^31 - 1 - 768 2^14)
+    # with the extreme multipliers, at shifts 30 .. 33, against the exact rule.
+    from taco_amd import hip
+    k = 768
+    a = np.zeros((4, k), np.int8)
+    a[0], a[1], a[2], a[3] = 127, -128, 1, -1
+    w = np.zeros((256, k), np.int8)
+    w[0::4], w[1::4], w[2::4], w[3::4] = 127, -128, -127, 0
+    big = (1 << 31) - 1 - k * (1 << 14)
+    bias = np.resize(np.array([big, -big, big, -big, 0], np.int64), 256).astype(np.int32)
+    mult = np.resize(np.array([-(1 << 31), (1 << 31) - 1, 1 << 30, -1, 12345], np.int64), 256).astype(np.int32)
+    for shift in (30, 31, 32, 33):
+        got = hip.gemm_requant_i8(dev, w, a, bias, mult, shift)
+        assert np.array_equal(got, O.linear_act_ref(w, a, bias, mult, shift)), shift
 
 
 def test_golden_output_hash_on_gpu(golden):
