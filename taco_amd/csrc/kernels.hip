@@ -2006,6 +2006,24 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     const uint32_t value = a.queries ? a.queries[2 * row + 1] : 0;
     const uint32_t tok = kind == 0 && !STATS ? value : 0;  // Encode token (0: no symbol below)
 
+    // The symbol pass reads 8 consecutive symbols per thread and group (one 16-byte load of d16;
+    // the 8 share a 64-column tile), four groups per step, and the tile maxes of those groups:
+    // d16 rows are padded to whole tiles, so every load is in range. The loads of a step are
+    // issued one step ahead (the first before the row max), so none waits on another.
+    constexpr int STEP = 4 * 256 * 8;
+    uint4 raw[4];
+    int64_t tmv[4];
+    auto fetch = [&](int g0) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int gq = g0 + u * 256 * 8;
+            if (gq < V) {
+                raw[u] = *(const uint4 *)(d16 + gq);
+                tmv[u] = tm[gq >> 6];
+            }
+        }
+    };
+    fetch(tid * 8);
     int64_t mx = INT64_MIN;
     for (int t = tid; t < a.ntiles; t += 256) mx = tm[t] > mx ? tm[t] : mx;
     const int64_t M = block_max64w(mx, s_i, tid);
@@ -2018,24 +2036,36 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     }
     __syncthreads();
 
-    // One pass: 8 consecutive symbols per thread and group (one 16-byte load; the 8 share a
-    // 64-column tile), four groups in flight per step. A group whose tile max is zcut or more
-    // below M has only weight-0 symbols.
+    // A group whose tile max is zcut or more below M has only weight-0 symbols.
     int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0 < zcut)
-    for (int g0 = tid * 8; g0 < V; g0 += 4 * 256 * 8) {
-        uint4 raw[4];
+    for (int g0 = tid * 8; g0 < V; g0 += STEP) {
+        uint4 cur[4];
         int64_t b64[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int gq = g0 + u * 256 * 8;
-            b64[u] = gq < V ? M - tm[gq >> 6] : (int64_t)zc;
-            if (b64[u] < zc) raw[u] = *(const uint4 *)(d16 + gq);
+            cur[u] = raw[u];
+            b64[u] = gq < V ? M - tmv[u] : (int64_t)zc;
         }
+        if (g0 + STEP < V) fetch(g0 + STEP);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             if (b64[u] >= zc) continue;
             const int gq = g0 + u * 256 * 8, base = (int)b64[u];
-            const uint16_t *dv = (const uint16_t *)&raw[u];
+            const uint16_t *dv = (const uint16_t *)&cur[u];
+            // per group: all 8 symbols below the Encode token, none, or some; a symbol reaches
+            // the top weight only if the tile's base is at most d0 (d16 >= 0)
+            const bool whole = gq + 8 <= V, all_lo = gq + 8 <= (int)tok, none_lo = gq >= (int)tok;
+            const bool top = base <= a.d0;
+            if (packed && whole && (all_lo || none_lo) && !top) {
+                const uint32_t inc = all_lo ? 0x10001u : 1u;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int dd = base + (int)dv[q];
+                    if (dd < zc) atomicAdd(&hist[dd], inc);  // then dd <= last: d = dd
+                }
+                continue;
+            }
 #pragma unroll
             for (int q = 0; q < 8; q++) {
                 const int j = gq + q;
@@ -2080,12 +2110,28 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0;
     __syncthreads();
     const uint64_t frac = s_frac;
+    // q(d) = floor(table[d] spare / W) < 2^32: v = table[d] R with R = spare / W in double takes
+    // three roundings (W to double, the quotient, the product), |v - q| < 2^32 4 2^-53 = 2^-19;
+    // when v lies at least 2^-18 from an integer, floor(v) is q (1.5 2^52 added rounds v to the
+    // nearest integer, the low word of the sum), else the exact quotient.
+    const double Rq = (double)spare / (double)W;
     uint64_t S = 0, Slo = 0;
     for (int d = tid; d < zc; d += 256) {
         const uint32_t h = hist[d];
         const uint32_t c = packed ? (h & 0xffffu) : h, clo = packed ? (h >> 16) : hist[zc + d];
         if (!c) continue;
-        const uint64_t q = quotient(a.table[d], spare, W, frac);
+        const uint64_t td = a.table[d];
+        const double v = (double)td * Rq;
+        const double t = v + 6755399441055744.0;
+        const double dl = v - (t - 6755399441055744.0);
+        uint64_t q;
+        if (fabs(dl) >= 0x1p-18) {
+            uint64_t bits;
+            __builtin_memcpy(&bits, &t, sizeof bits);
+            q = (uint64_t)(uint32_t)bits - (dl < 0.0 ? 1 : 0);
+        } else {
+            q = quotient(td, spare, W, frac);
+        }
         S += (uint64_t)c * q;
         Slo += (uint64_t)clo * q;
     }
