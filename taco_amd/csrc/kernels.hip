@@ -1672,6 +1672,268 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
 }
 
+// =============================================================================================
+// Prefill attention, the common case: head_dim 64, at most 4 key blocks of 64 per group, attn_exp
+// in LDS, score shift 22 .. 63 and P <= 30. The algorithm and the layouts are k_attend_mfma's;
+// the per-score work is smaller:
+//  - |dot| <= 64 2^14 and |m| <= 2^31, so |score| <= 2^29 + 1 for s >= 22: the distance M - s is
+//    an i32 and its clamp to [0, last] one med3;
+//  - blocks past the group's keys are skipped, and the causal mask is applied only to the
+//    blocks that some row of the wave does not fully see (a wave-uniform test per block);
+//  - p = floor(e 2^P / S) + 0x80808080 (the packed-digit offset) comes from w = e R + 0x80808080
+//    in double precision: R = 2^P / S and the fused multiply-add take one rounding each, so
+//    |w - (t + 0x80808080)| < 2^-21 for t = e 2^P / S <= 2^30; when w lies at least 2^-20 from
+//    an integer its truncation is exact. e = 0 gives w = 0x80808080 exactly (p = 0). Otherwise
+//    the block takes the 64-bit reciprocal with one correction;
+//  - the output rescale floor(v m 2^-s + 1/2), clamped to +-127, is one fused multiply-add in
+//    double precision: v = sum of the four digit-plane products is an exact double (|v| <= 2^30
+//    128 < 2^38 and every partial sum stays below 2^41), so y = v m 2^-s + 1/2 carries one
+//    rounding (relative 2^-53); when |y| >= 256 the clamp decides, when y lies at least 2^-30
+//    from an integer floor(y) is exact, else the element takes the i128 rule.
+//  - the Q fragment is read straight from global memory (each lane's 16 bytes of its row).
+// =============================================================================================
+// v_med3_i32(x, 0, hi) for a wave-uniform hi (the compiler forms med3 only for constant bounds)
+__device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
+    int32_t r;
+    asm("v_med3_i32 %0, %1, 0, %2" : "=v"(r) : "v"(x), "s"(hi));
+    return r;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
+    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * AT_ST];  // K rows, then V^T
+    __shared__ __attribute__((aligned(1024))) int8_t sV[AT_SB * 64 * 64];      // V rows, as loaded
+    extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];          // attn_exp
+    const AttnGroup G = groups[blockIdx.x];
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ql = lane & 15, qg = lane >> 4;
+    const int nk = G.pos0 + G.count < a.ctx_cap ? G.pos0 + G.count : a.ctx_cap;
+    const int nkb = (nk + 63) / 64;  // 1 .. AT_SB (checked by the launcher)
+    const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
+    const int last = a.exp_len - 1;
+    auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
+    {
+        // the K and V rows of the group's blocks and the table, straight into LDS (dense rows,
+        // 16-byte chunk c of row r at slot 4 r + (c ^ sw(r % 16))); rows past the cache read
+        // its last row (their keys are masked)
+        const int r = 16 * w + (lane >> 2), c = (lane & 3) ^ sw(r & 15);
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++) {
+            if (b >= nkb) break;
+            int key = b * 64 + r;
+            key = key < a.ctx_cap ? key : a.ctx_cap - 1;
+            const size_t off = base + (size_t)key * 64 + 16 * c;
+            __builtin_amdgcn_global_load_lds((const void *)(a.kc + off), (lds_void *)(sKV + (b * 64 + 16 * w) * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(a.vc + off), (lds_void *)(sV + (b * 64 + 16 * w) * 64), 16, 0, 0);
+        }
+        for (int ch = w; ch < (a.exp_len + 255) / 256; ch += 4)  // whole 1 KiB chunks
+            __builtin_amdgcn_global_load_lds((const void *)(a.exp_table + ch * 256 + 4 * lane),
+                                             (lds_void *)(s_exp + ch * 256), 16, 0, 0);
+    }
+    const int myrow = 16 * w + ql, mypos = G.pos0 + myrow;  // this lane's row and its position
+    v4i qf = {0, 0, 0, 0};
+    if (myrow < G.count) qf = *(const v4i *)(a.q + (size_t)(G.first + myrow) * a.ldq + h * 64 + 16 * qg);
+    wait_vmcnt<0>();  // this wave's direct loads landed (the barrier shows them to all)
+    __syncthreads();
+    // S[b][t][e]: the dot (then the table entry) of this lane's row with key 64 b + 16 t + 4 qg + e
+    v4i S[AT_SB][4];
+#pragma unroll
+    for (int b = 0; b < AT_SB; b++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (b < nkb) {
+                const int r = t * 16 + ql;
+                const v4i kf = *(const v4i *)&sKV[(4 * (b * 64 + r) + (qg ^ sw(r & 15))) * 16];
+                S[b][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf, v4i{0, 0, 0, 0}, 0, 0, 0);
+            } else {
+                S[b][t] = v4i{0, 0, 0, 0};
+            }
+        }
+    // key 64 b + 16 t + 4 qg + e is visible to this lane's row iff 16 t + e <= lim - 64 b - 4 qg;
+    // block b is visible to every row of the wave iff 64 b + 63 <= wlim (uniform)
+    const int lim = mypos < nk - 1 ? mypos : nk - 1;
+    const int wlim = G.pos0 + 16 * w < nk - 1 ? G.pos0 + 16 * w : nk - 1;
+    // pass 1: the row max, from the largest and the smallest visible dot
+    int32_t dmax = INT32_MIN, dmin = INT32_MAX;
+#pragma unroll
+    for (int b = 0; b < AT_SB; b++) {
+        if (b >= nkb) break;
+        if (64 * b + 63 <= wlim) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    dmax = S[b][t][e] > dmax ? S[b][t][e] : dmax;
+                    dmin = S[b][t][e] < dmin ? S[b][t][e] : dmin;
+                }
+        } else {
+            const int L = lim - 64 * b - 4 * qg;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const bool ok = 16 * t + e <= L;
+                    const int32_t hiv = ok ? S[b][t][e] : INT32_MIN, lov = ok ? S[b][t][e] : INT32_MAX;
+                    dmax = hiv > dmax ? hiv : dmax;
+                    dmin = lov < dmin ? lov : dmin;
+                }
+        }
+    }
+    __syncthreads();  // the K rows are read: sKV may take V^T
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {  // the 4 lanes of this row
+        const int32_t u = __shfl_xor(dmax, o, 64), v = __shfl_xor(dmin, o, 64);
+        dmax = u > dmax ? u : dmax;
+        dmin = v < dmin ? v : dmin;
+    }
+    // score = (dot m + 2^(s-1)) >> s (exact in i64: |dot m| <= 2^51), an i32 for s >= 22
+    const int s_eff = a.score_s < 63 ? a.score_s : 63;
+    const int64_t s_half = (int64_t)1 << (s_eff - 1);
+    auto score = [&](int32_t dot) -> int32_t { return (int32_t)(((int64_t)dot * a.score_m + s_half) >> s_eff); };
+    const int32_t mx = score(dmax) > score(dmin) ? score(dmax) : score(dmin);
+    // pass 2: the table entries attn_exp[min(M - s, last)] (0 for a masked key) and their sum
+    uint64_t sum = 0;
+#pragma unroll
+    for (int b = 0; b < AT_SB; b++) {
+        if (b >= nkb) break;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) S[b][t][e] = clamp0_uniform(mx - score(S[b][t][e]), last);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) S[b][t][e] = s_exp[S[b][t][e]];
+        if (64 * b + 63 > wlim) {
+            const int L = lim - 64 * b - 4 * qg;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) S[b][t][e] = 16 * t + e <= L ? S[b][t][e] : 0;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++)  // entries are < 2^31: a pair sums in u32
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) sum += (uint32_t)S[b][t][e] + (uint32_t)S[b][t][e + 1];
+    }
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    const double R = ldexp(1.0 / (double)sum, a.softmax_p);
+    {  // V^T of the blocks into sKV, keys in the operand order (key 16 t + 4 g + e at byte 16 g + 4 t + e)
+        v4i vreg[AT_SB];
+        const int kg = tid >> 4, cg = tid & 15;  // keys 4 kg .. +4, channels 4 cg .. +4
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++) {
+            if (b >= nkb) break;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = 4 * kg + i;
+                vreg[b][i] = *(const int32_t *)&sV[(4 * (b * 64 + kk) + ((cg >> 2) ^ sw(kk & 15))) * 16 + 4 * (cg & 3)];
+            }
+        }
+        const int pos0 = 16 * (kg & 3) + 4 * (kg >> 2);
+#pragma unroll
+        for (int b = 0; b < AT_SB; b++) {
+            if (b >= nkb) break;
+            uint32_t tw[4];
+            byte_transpose((uint32_t)vreg[b][0], (uint32_t)vreg[b][1], (uint32_t)vreg[b][2], (uint32_t)vreg[b][3], tw);
+#pragma unroll
+            for (int j = 0; j < 4; j++) *(uint32_t *)&sKV[(b * 64 + 4 * cg + j) * AT_ST + pos0] = tw[j];
+        }
+    }
+    __syncthreads();
+    // pass 3: p + 0x80808080 (the packed digits), and the digit-plane PV products
+    v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[k][c] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < AT_SB; b++) {
+        if (b >= nkb) break;
+        uint32_t dg[4][4];
+        bool fast_all = true;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t ev = (uint32_t)S[b][t][e];
+                const double wv = fma((double)ev, R, 2155905152.0);
+                const double f = __builtin_amdgcn_fract(wv);
+                fast_all &= ev == 0 || fabs(f - 0.5) <= 0.5 - 0x1p-20;
+                dg[t][e] = (uint32_t)wv;
+            }
+        if (!fast_all) {
+            const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint64_t num = (uint64_t)(uint32_t)S[b][t][e] << a.softmax_p;
+                    uint64_t q = num;
+                    if (sum >= 2) {
+                        q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
+                        if (num - q * sum >= sum) q++;
+                    }
+                    dg[t][e] = (uint32_t)q + 0x80808080u;
+                }
+        }
+        v4i pf[4];  // [digit plane]: word t holds the digits of keys 16 t + 4 (l / 16) + e
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            uint32_t o[4];
+            byte_transpose(dg[t][0], dg[t][1], dg[t][2], dg[t][3], o);
+#pragma unroll
+            for (int k = 0; k < 4; k++) pf[k][t] = (int32_t)(o[k] ^ 0x80808080u);
+        }
+        v4i vf[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) vf[c] = *(const v4i *)&sKV[(b * 64 + 16 * c + ql) * AT_ST + 16 * qg];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[c], pf[k], acc[k][c], 0, 0, 0);
+    }
+    if (myrow < G.count) {
+        // rescale: s = 0 keeps v m, a shift above 95 gives 0
+        const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
+        uint32_t packed[4];
+        bool ok = true;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            packed[c] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const double v = (((double)acc[3][c][e] * 16777216.0 + (double)acc[2][c][e] * 65536.0) +
+                                  (double)acc[1][c][e] * 256.0) + (double)acc[0][c][e];
+                const double y = fma(v, mo, 0.5);
+                const double f = __builtin_amdgcn_fract(y);
+                ok &= fabs(y) >= 256.0 || fabs(f - 0.5) <= 0.5 - 0x1p-30;
+                const int32_t r = (int32_t)fmin(fmax(y - f, -127.0), 127.0);
+                packed[c] |= (uint32_t)(uint8_t)(int8_t)r << (8 * e);
+            }
+        }
+        if (!ok) {  // some element lies too close to a rounding boundary: the i128 rule for all
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                packed[c] = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int64_t vi = (int64_t)acc[0][c][e] + ((int64_t)acc[1][c][e] << 8) +
+                                       ((int64_t)acc[2][c][e] << 16) + ((int64_t)acc[3][c][e] << 24);
+                    const int32_t r = (int32_t)clamp128(rescale_full(vi, a.out_m, a.out_s), -127, 127);
+                    packed[c] |= (uint32_t)(uint8_t)(int8_t)r << (8 * e);
+                }
+            }
+        }
+        int8_t *o = a.out + (size_t)(G.first + myrow) * a.ldo + h * 64;
+#pragma unroll
+        for (int c = 0; c < 4; c++) *(uint32_t *)(o + 16 * c + 4 * qg) = packed[c];
+    }
+}
+
 template <bool NOCLAMP, bool LDS_TABLE, bool MULTI>
 static hipError_t launch_attend_groups_t(const AttnArgs &a, const AttnGroup *groups, int n_groups,
                                          hipStream_t stream) {
@@ -1701,6 +1963,17 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
     // the output of a row is four 4-byte stores per head
     if (a.hd != 64 || a.ldo % 4 != 0 || ((uintptr_t)a.out & 3) != 0 || max_keys < 1) return hipErrorInvalidValue;
     const bool noclamp = a.score_s >= 13, lds_table = a.exp_len <= ATTN_LDS_TABLE;
+    if (lds_table && max_keys <= AT_SB * 64 && a.score_s >= 22 && a.softmax_p <= 30 && a.out_s >= 0) {
+        const size_t lds = ((size_t)a.exp_len + 255) / 256 * 1024;  // whole 1 KiB chunks
+        static size_t allowed = 0;  // the dynamic LDS limit, raised once
+        if (lds > allowed) {
+            hipError_t e = hipFuncSetAttribute((const void *)k_attend_short, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            allowed = lds;
+        }
+        hipLaunchKernelGGL(k_attend_short, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+        return hipGetLastError();
+    }
     if (noclamp && lds_table) return launch_attend_groups_m<true, true>(a, groups, n_groups, max_keys, stream);
     if (noclamp) return launch_attend_groups_m<true, false>(a, groups, n_groups, max_keys, stream);
     if (lds_table) return launch_attend_groups_m<false, true>(a, groups, n_groups, max_keys, stream);

@@ -172,11 +172,13 @@ SIGMA_W_SQ = Fraction(255 * 255 - 1, 12)  # uniform [-127, 127]: variance 5418.6
 SIGMA_ACT_SQ = Fraction(1600 * 1600)       # i8 model activations times weights
 
 
-def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_len: int = 8192) -> bytes:
+def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_len: int = 8192,
+                score_target: int = 768) -> bytes:
     """The synthetic model. wide=True makes a model-file version 2 model: an i16 GELU table
     (output unit 1/10240), a 16-bit ln_f (target 10240) and ln_beta_frac = 8 (beta in units of
     2^-8, uniform in [-4096, 4096]); the shifts that read those activations are 8 larger.
-    table_len sets the length of both exponent tables."""
+    table_len sets the length of both exponent tables; score_target the typical attention score
+    (larger targets give smaller score shifts)."""
     d, f, V, C, L, H = dims.d_model, dims.d_ff, dims.vocab, dims.n_ctx, dims.n_layer, dims.n_head
     hd = d // H
     s = Stream(seed)
@@ -218,7 +220,7 @@ def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_l
         p = f"h.{l}"
         layernorm(p + ".ln_1")
         linear(p + ".attn.c_attn", 3 * d, d, 40)
-        w.add_tensor(p + ".attn.score.rescale", mult(1), shift_for(SIGMA_ACT_SQ * hd, 768))
+        w.add_tensor(p + ".attn.score.rescale", mult(1), shift_for(SIGMA_ACT_SQ * hd, score_target))
         w.add_tensor(p + ".attn.out.rescale", mult(1), shift_for(Fraction(2) ** 60 * 1600, 40))
         linear(p + ".attn.c_proj", d, d, 1 << 14)
         layernorm(p + ".ln_2")

@@ -401,6 +401,26 @@ def test_head_dim_64_prefill_equals_the_reference(dev, overlap):
         assert got[i] == O.encode_block(om, blk, overlap=overlap), i
 
 
+@pytest.mark.parametrize("score_target,shift", [(768, 34), (1 << 22, 22), (1 << 23, 21)])
+def test_head_dim_64_prefill_score_shifts(dev, score_target, shift):
+    """The two prefill attention kernels for head_dim 64 and at most 256 keys: score shifts of 22
+    or more (every score and distance an i32) take the short kernel, smaller ones the general
+    kernel. Ragged groups (windows of 1 to 300 tokens, n_ctx 256)."""
+    from taco_amd import fold, hip, synth
+    from tests.test_oracle import read_hsm
+    b = synth.build_model(synth.Dims(2, 4, 256, 512, 1000, 256), seed=0x5C0E, score_target=score_target)
+    _, ts = read_hsm(b)
+    assert ts["h.0.attn.score.rescale"][1] == shift
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    lens = [1, 40, 64, 100, 256, 300]
+    blocks = [np.array(splitmix_tokens(90 + i, n, 999), np.uint32) for i, n in enumerate(lens)]
+    batch = hip.HipBatch(hm, 4, 512)
+    got = fold.fold_blocks(batch, blocks, 0)
+    for i, blk in enumerate(blocks):
+        print(f"score shift {shift}: block {i} ({len(blk)} tokens)", flush=True)
+        assert got[i] == O.encode_block(om, blk, overlap=0), i
+
+
 @pytest.mark.parametrize("overlap", [0, 100])
 def test_head_dim_64_long_contexts_equal_the_reference(dev, overlap):
     """More than 256 keys per row (the MFMA prefill kernel recomputes Q K^T per pass for
