@@ -1906,8 +1906,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             packed[c] = 0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const double v = (((double)acc[3][c][e] * 16777216.0 + (double)acc[2][c][e] * 65536.0) +
-                                  (double)acc[1][c][e] * 256.0) + (double)acc[0][c][e];
+                // |acc| <= 256 2^7 2^7 = 2^22 per plane, so each pair of planes sums in i32
+                const int32_t hi = (int32_t)((uint32_t)acc[3][c][e] << 8) + acc[2][c][e];
+                const int32_t lo = (int32_t)((uint32_t)acc[1][c][e] << 8) + acc[0][c][e];
+                const double v = fma((double)hi, 65536.0, (double)lo);
                 const double y = fma(v, mo, 0.5);
                 const double f = __builtin_amdgcn_fract(y);
                 ok &= fabs(y) >= 256.0 || fabs(f - 0.5) <= 0.5 - 0x1p-30;
