@@ -52,6 +52,8 @@ constexpr int GEMM_STAGES = 3;
 static_assert(GEMM_BM == 256 && GEMM_BK == 64 && GEMM_NPAD % 256 == 0, "tile shape of k_gemm");
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 // s_waitcnt vmcnt(N) with the other counters left at their maximum (gfx9 encoding).
 template <int N>
@@ -1700,8 +1702,8 @@ __device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
-    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * AT_ST];  // K rows, then V^T
-    __shared__ __attribute__((aligned(1024))) int8_t sV[AT_SB * 64 * 64];      // V rows, as loaded
+    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * 64];  // K rows, as loaded
+    __shared__ __attribute__((aligned(1024))) int8_t sV[AT_SB * 64 * 64];   // V rows, as loaded
     extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];          // attn_exp
     const AttnGroup G = groups[blockIdx.x];
     const int h = blockIdx.y;
@@ -1780,7 +1782,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 }
         }
     }
-    __syncthreads();  // the K rows are read: sKV may take V^T
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) {  // the 4 lanes of this row
         const int32_t u = __shfl_xor(dmax, o, 64), v = __shfl_xor(dmin, o, 64);
@@ -1820,29 +1821,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
-    {  // V^T of the blocks into sKV, keys in the operand order (key 16 t + 4 g + e at byte 16 g + 4 t + e)
-        v4i vreg[AT_SB];
-        const int kg = tid >> 4, cg = tid & 15;  // keys 4 kg .. +4, channels 4 cg .. +4
-#pragma unroll
-        for (int b = 0; b < AT_SB; b++) {
-            if (b >= nkb) break;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int kk = 4 * kg + i;
-                vreg[b][i] = *(const int32_t *)&sV[(4 * (b * 64 + kk) + ((cg >> 2) ^ sw(kk & 15))) * 16 + 4 * (cg & 3)];
-            }
-        }
-        const int pos0 = 16 * (kg & 3) + 4 * (kg >> 2);
-#pragma unroll
-        for (int b = 0; b < AT_SB; b++) {
-            if (b >= nkb) break;
-            uint32_t tw[4];
-            byte_transpose((uint32_t)vreg[b][0], (uint32_t)vreg[b][1], (uint32_t)vreg[b][2], (uint32_t)vreg[b][3], tw);
-#pragma unroll
-            for (int j = 0; j < 4; j++) *(uint32_t *)&sKV[(b * 64 + 4 * cg + j) * AT_ST + pos0] = tw[j];
-        }
-    }
-    __syncthreads();
+    // The V^T operand comes straight from the V rows: ds_read_b64_tr_b8 gives lane 8 h + j of each
+    // 16-lane group byte j of the 8-byte pieces that lanes h, h + 2, .., h + 14 address. Lane i of
+    // group qg addresses key 16 t + 4 qg + e (t = 2 r + i / 8, e = (i / 2) % 4 for read r) at
+    // channels 16 c + 8 (i % 2) .. +8, so lane l receives channel 16 c + l % 16 of the keys of
+    // operand bytes 8 r .. 8 r + 7 (byte 4 t + e holds key 16 t + 4 qg + e, as in the digits).
+    const int tr_k = ql >> 1, tr_h = ql & 1;
+    const int tr_key0 = 16 * (tr_k >> 2) + 4 * qg + (tr_k & 3);  // read 0; read 1 is 32 keys on
+    auto vt_frag = [&](int b, int c) -> v4i {
+        const int8_t *p0 = sV + (4 * (b * 64 + tr_key0) + (c ^ sw(tr_key0 & 15))) * 16 + 8 * tr_h;
+        const v2i r0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)p0);
+        const v2i r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(p0 + 32 * 64));
+        return v4i{r0[0], r0[1], r1[0], r1[1]};
+    };
     // pass 3: p + 0x80808080 (the packed digits), and the digit-plane PV products
     v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
 #pragma unroll
@@ -1889,7 +1880,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
         v4i vf[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) vf[c] = *(const v4i *)&sKV[(b * 64 + 16 * c + ql) * AT_ST + 16 * qg];
+        for (int c = 0; c < 4; c++) vf[c] = vt_frag(b, c);
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
