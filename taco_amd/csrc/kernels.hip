@@ -1701,10 +1701,10 @@ __device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
     return r;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
-    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * 64];  // K rows, as loaded
-    __shared__ __attribute__((aligned(1024))) int8_t sV[AT_SB * 64 * 64];   // V rows, as loaded
-    extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];          // attn_exp
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
+    // the K rows, then the V rows (as loaded): 48 KiB of LDS with the table, three workgroups a CU
+    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * 64];
+    extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];  // attn_exp
     const AttnGroup G = groups[blockIdx.x];
     const int h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1715,10 +1715,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
     const int last = a.exp_len - 1;
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
-    {
-        // the K and V rows of the group's blocks and the table, straight into LDS (dense rows,
-        // 16-byte chunk c of row r at slot 4 r + (c ^ sw(r % 16))); rows past the cache read
-        // its last row (their keys are masked)
+    // the K (then V) rows of the group's blocks straight into LDS (dense rows, 16-byte chunk c of
+    // row r at slot 4 r + (c ^ sw(r % 16))); rows past the cache read its last row (their keys
+    // are masked)
+    auto rows_to_lds = [&](const int8_t *cache) {
         const int r = 16 * w + (lane >> 2), c = (lane & 3) ^ sw(r & 15);
 #pragma unroll
         for (int b = 0; b < AT_SB; b++) {
@@ -1726,9 +1726,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             int key = b * 64 + r;
             key = key < a.ctx_cap ? key : a.ctx_cap - 1;
             const size_t off = base + (size_t)key * 64 + 16 * c;
-            __builtin_amdgcn_global_load_lds((const void *)(a.kc + off), (lds_void *)(sKV + (b * 64 + 16 * w) * 64), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void *)(a.vc + off), (lds_void *)(sV + (b * 64 + 16 * w) * 64), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(cache + off), (lds_void *)(sKV + (b * 64 + 16 * w) * 64), 16, 0, 0);
         }
+    };
+    {
+        rows_to_lds(a.kc);
         for (int ch = w; ch < (a.exp_len + 255) / 256; ch += 4)  // whole 1 KiB chunks
             __builtin_amdgcn_global_load_lds((const void *)(a.exp_table + ch * 256 + 4 * lane),
                                              (lds_void *)(s_exp + ch * 256), 16, 0, 0);
@@ -1752,6 +1754,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                 S[b][t] = v4i{0, 0, 0, 0};
             }
         }
+    __syncthreads();  // every K row is read: the V rows load in their place during passes 1 and 2
+    rows_to_lds(a.vc);
     // key 64 b + 16 t + 4 qg + e is visible to this lane's row iff 16 t + e <= lim - 64 b - 4 qg;
     // block b is visible to every row of the wave iff 64 b + 63 <= wlim (uniform)
     const int lim = mypos < nk - 1 ? mypos : nk - 1;
@@ -1829,11 +1833,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int tr_k = ql >> 1, tr_h = ql & 1;
     const int tr_key0 = 16 * (tr_k >> 2) + 4 * qg + (tr_k & 3);  // read 0; read 1 is 32 keys on
     auto vt_frag = [&](int b, int c) -> v4i {
-        const int8_t *p0 = sV + (4 * (b * 64 + tr_key0) + (c ^ sw(tr_key0 & 15))) * 16 + 8 * tr_h;
+        const int8_t *p0 = sKV + (4 * (b * 64 + tr_key0) + (c ^ sw(tr_key0 & 15))) * 16 + 8 * tr_h;
         const v2i r0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)p0);
         const v2i r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(p0 + 32 * 64));
         return v4i{r0[0], r0[1], r1[0], r1[1]};
     };
+    wait_vmcnt<0>();  // this wave's V rows landed (the barrier shows them to all)
+    __syncthreads();
     // pass 3: p + 0x80808080 (the packed digits), and the digit-plane PV products
     v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
 #pragma unroll
