@@ -121,6 +121,7 @@ struct DevLn {
     int32_t *b = nullptr;
     int32_t m = 0;
     int s = 0;
+    bool beta_small = false;  // every |b[j]| <= 256
 };
 
 struct DevBlock {
@@ -182,6 +183,8 @@ hs_status upload_ln(DevMem &mem, const hs::HostLayerNorm &l, DevLn &o) {
     if (st == HS_OK) st = mem.upload(o.b, l.b.data(), l.b.size());
     o.m = l.m;
     o.s = l.s;
+    o.beta_small = true;
+    for (int32_t v : l.b) o.beta_small = o.beta_small && v >= -256 && v <= 256;
     return st;
 }
 
@@ -792,7 +795,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         a.bits = out_bits;
         a.x = b.d_x; a.d = m.d; a.gamma = l.g; a.beta = l.b; a.m = l.m; a.s = l.s;
         a.beta_frac = m.host.ln_beta_frac; a.k = m.host.ln_k; a.j = m.host.ln_j; a.eps = m.host.ln_eps;
-        a.out = dst; a.ldo = m.d_pad; a.src = src_rows; a.gm = l.gm;
+        a.out = dst; a.ldo = m.d_pad; a.src = src_rows; a.gm = l.gm; a.beta_small = l.beta_small;
         return b.launch("layer_norm", 0, [&] { return hs::launch_layernorm(a, rows_n, st); });
     };
     // The LM head: the rows of a chunk (at most a few MB of A) stay in every XCD's L2 while

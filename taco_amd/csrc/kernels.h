@@ -88,6 +88,7 @@ struct LnArgs {
     const int64_t *gm = nullptr;   // gamma[j] * m, exact in i64 (|gamma m| < 2^46)
     int bits = 8;                  // 16: clamp to +-32767 and write the two i8 planes of each row
                                    // (hi to out row 2i, lo to row 2i + 1), as the wide GEMMs read
+    int beta_small = 0;            // every |beta[j]| <= 256 (allows the single-precision rule)
 };
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream);
 
