@@ -172,6 +172,24 @@ HS_HD int64_t shift_round_hi(int64_t t, int64_t g, uint32_t s) {
     return (hi + ((int64_t)1 << (u - 1))) >> u;
 }
 
+// The LayerNorm element rule in single precision for 8-bit outputs with |beta| <= 256:
+// clamp(floor(X + 1/2) + beta, +-127) for X = c inv m gamma 2^-s, from y = c k + b with
+// k = float(inv m 2^-s) gamma (two roundings) and b = 1/2 + beta (exact), one fused
+// multiply-add. |y - (X + b)| <= 3.0001 2^-24 |X| + 2^-24 |y|. y is clamped to +-200.25: inside,
+// |X| < 458 and the error is below 1575 2^-24 < 2^-13, so floor(y) is exact when y lies at
+// least 2^-13 from an integer; outside, y has the sign and size of X + b, the output clamp
+// decides, and +-200.25 lie 1/4 from an integer. |k| <= 2^110 keeps y finite or an infinity of
+// the sign of c k (never NaN). Returns false (declines) near an integer; *out is then unused.
+HS_HD bool ln_elem_f32(int32_t c, float k, float b, int32_t *out) {
+    const float y = fmaf((float)c, k, b);
+    const float yc = fminf(fmaxf(y, -200.25f), 200.25f);
+    const float fl = floorf(yc);
+    const float f = yc - fl;
+    const int32_t r = (int32_t)fl;
+    *out = r < -127 ? -127 : (r > 127 ? 127 : r);
+    return fabsf(f - 0.5f) <= 0.5f - 0x1p-13f;
+}
+
 // floor((c inv gamma m + 2^(s - 1)) / 2^s) (the LayerNorm element rule, layernorm.rs:66-108,
 // s <= 126) in double precision, with kr = ldexp((double)inv * m, -s) of the row:
 // v = fma(c kr, gamma, 1/2). The roundings (inv to double, inv m, c kr, the fma) keep

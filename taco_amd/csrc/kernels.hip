@@ -843,14 +843,9 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
 // (the same columns for every row) are copied into LDS once per workgroup while x loads.
 // The input is the residual stream (|x| <= RES = 2^30 - 1): every square is below 2^60, so the
 // four of a group sum in i64 without a carry.
-// F32 (8-bit outputs, beta_frac 0, |beta| <= 256): each element takes the rule in single
-// precision, y = c K + (1/2 + beta) with K = float(inv m 2^-s) gamma and one fused multiply-add
-// (|K| <= 2^110, so y is finite or an infinity of the sign of c K, never NaN). With X =
-// c inv m gamma 2^-s exactly, |y - (X + 1/2 + beta)| <= 3.0001 2^-24 |X| + 2^-24 |y|. y is first
-// clamped to +-200.25: inside, |X| < 458 and the error is below 1575 2^-24 < 2^-13, so floor(y) is
-// exact when y lies at least 2^-13 from an integer; outside, y has the sign and size of X + beta
-// and the output clamp (+-127) decides, and +-200.25 lie 1/4 from an integer. Declined groups
-// take the integer rule, as in the double-precision form.
+// F32 (8-bit outputs, beta_frac 0, |beta| <= 256): each element takes the single-precision rule
+// (ln_elem_f32, with beta folded into the addend); declined groups take the integer rule, as in
+// the double-precision form.
 template <int NG, bool F32>
 __global__ __launch_bounds__(256) void k_layernorm_rows4(LnArgs a, int n_rows) {
     __shared__ __attribute__((aligned(16))) int32_t s_beta[64 * NG];
@@ -952,11 +947,7 @@ __global__ __launch_bounds__(256) void k_layernorm_rows4(LnArgs a, int n_rows) {
             bool all = true;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float yv = fmaf((float)(xv[t][e] - mean32), krf * s_gammaf[j + e], s_betaf[j + e]);
-                const float yc = __builtin_amdgcn_fmed3f(yv, -200.25f, 200.25f);
-                const float f = __builtin_amdgcn_fractf(yc);
-                all &= fabsf(f - 0.5f) <= 0.5f - 0x1p-13f;
-                y[e] = med3_i32((int32_t)(yc - f), -127, 127);
+                all &= ln_elem_f32(xv[t][e] - mean32, krf * s_gammaf[j + e], s_betaf[j + e], &y[e]);
             }
             put(j, y);
             redo |= all ? 0u : 1u << t;

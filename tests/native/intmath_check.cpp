@@ -197,6 +197,49 @@ int main(int argc, char **argv) {
                 count += 3;
             }
     CHECK(taken > n / 2, "ln_elem_f64 declined too often (%ld of %ld)", declined, declined + taken);
+    // ln_elem_f32 against clamp(floor((c inv gamma m + 2^(s-1)) / 2^s) + beta, +-127) in i128 for
+    // |beta| <= 256, with k and b formed as the kernel forms them: every value it returns is exact.
+    long declined32 = 0, taken32 = 0;
+    auto check_ln32 = [&](int32_t c, uint64_t inv, int32_t g, int32_t m, uint32_t s, int32_t beta) -> bool {
+        const float krf = (float)std::ldexp((double)inv * (double)m, -(int)s);
+        int32_t y = 0;
+        if (!hs::ln_elem_f32(c, krf * (float)g, 0.5f + (float)beta, &y)) {
+            declined32++;
+            return true;
+        }
+        taken32++;
+        i128 want = exact_ln(c, inv, g, m, s) + beta;
+        want = want < -127 ? -127 : (want > 127 ? 127 : want);
+        return (i128)y == want;
+    };
+    for (long i = 0; i < n; i++) {
+        const int32_t c = (int32_t)(next() >> (33 + next() % 31)) * ((next() & 1) ? -1 : 1);
+        const int32_t g = (int32_t)(next() % 65535) - 32767;
+        const int32_t m = (int32_t)(next() >> (33 + next() % 31)) * ((next() & 1) ? -1 : 1);
+        uint64_t inv = rnd_bits();
+        const int lc = 64 - hs::clz64((uint64_t)(c < 0 ? -(int64_t)c : c)), lg = 16;
+        const int lm = 64 - hs::clz64((uint64_t)(m < 0 ? -(int64_t)m : m));
+        const int room = 125 - lc - lg - lm;
+        if (room < 64) inv = room <= 0 ? 0 : inv & ((1ull << room) - 1);
+        const uint32_t s = (uint32_t)(next() % 127);
+        const int32_t beta = (int32_t)(next() % 513) - 256;
+        CHECK(check_ln32(c, inv, g, m, s, beta), "ln_elem_f32 c %d inv %llu g %d m %d s %u beta %d", c,
+              (unsigned long long)inv, g, m, s, beta);
+        count++;
+    }
+    // outputs near the clamp and quotients on and beside a half
+    for (uint32_t s = 1; s <= 63; s++)
+        for (long k = -400; k <= 400; k += 13)
+            for (int delta = -3; delta <= 3; delta++) {
+                const i128 p = (i128)k * ((i128)1 << s) + ((i128)1 << (s - 1)) + delta;
+                if (p <= 0 || p >= ((i128)1 << 64)) continue;
+                for (int32_t beta : {-256, -130, -1, 0, 1, 127, 256}) {
+                    CHECK(check_ln32(1, (uint64_t)p, 1, 1, s, beta), "ln_elem_f32 half s %u k %ld d %d b %d", s, k, delta, beta);
+                    CHECK(check_ln32(-1, (uint64_t)p, 1, 1, s, beta), "ln_elem_f32 -half s %u k %ld d %d b %d", s, k, delta, beta);
+                    count += 2;
+                }
+            }
+    CHECK(taken32 > n / 2, "ln_elem_f32 declined too often (%ld of %ld)", declined32, declined32 + taken32);
     std::printf("ok %ld\n", count);
     return 0;
 }
