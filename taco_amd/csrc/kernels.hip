@@ -1707,7 +1707,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // =============================================================================================
-// Prefill attention, the common case: head_dim 64, at most 4 key blocks of 64 per group, attn_exp
+// Prefill attention, the common case: head_dim 64, at most 8 key blocks of 64 per group, attn_exp
 // in LDS, score shift 22 .. 63 and P <= 30. The algorithm and the layouts are k_attend_mfma's;
 // the per-score work is smaller:
 //  - |dot| <= 64 2^14 and |m| <= 2^31, so |score| <= 2^29 + 1 for s >= 22: the distance M - s is
@@ -1721,7 +1721,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 //    the block takes the 64-bit reciprocal with one correction;
 //  - the output rescale floor(v m 2^-s + 1/2), clamped to +-127, is one fused multiply-add in
 //    double precision: v = sum of the four digit-plane products is an exact double (|v| <= 2^30
-//    128 < 2^38 and every partial sum stays below 2^41), so y = v m 2^-s + 1/2 carries one
+//    128 < 2^38 and every partial sum stays below 2^47), so y = v m 2^-s + 1/2 carries one
 //    rounding (relative 2^-53); when |y| >= 256 the clamp decides, when y lies at least 2^-30
 //    from an integer floor(y) is exact, else the element takes the i128 rule.
 //  - the Q fragment is read straight from global memory (each lane's 16 bytes of its row).
@@ -1733,9 +1733,11 @@ __device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
     return r;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
-    // the K rows, then the V rows (as loaded): 48 KiB of LDS with the table, three workgroups a CU
-    __shared__ __attribute__((aligned(1024))) int8_t sKV[AT_SB * 64 * 64];
+// NB: key blocks of 64 (4: three workgroups per CU with a 32 KiB table; 8: two).
+template <int NB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3 : 2))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
+    // the K rows, then the V rows (as loaded)
+    __shared__ __attribute__((aligned(1024))) int8_t sKV[NB * 64 * 64];
     extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];  // attn_exp
     const AttnGroup G = groups[blockIdx.x];
     const int h = blockIdx.y;
@@ -1743,7 +1745,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 15, qg = lane >> 4;
     const int nk = G.pos0 + G.count < a.ctx_cap ? G.pos0 + G.count : a.ctx_cap;
-    const int nkb = (nk + 63) / 64;  // 1 .. AT_SB (checked by the launcher)
+    const int nkb = (nk + 63) / 64;  // 1 .. NB (checked by the launcher)
     const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
     const int last = a.exp_len - 1;
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
@@ -1753,7 +1755,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     auto rows_to_lds = [&](const int8_t *cache) {
         const int r = 16 * w + (lane >> 2), c = (lane & 3) ^ sw(r & 15);
 #pragma unroll
-        for (int b = 0; b < AT_SB; b++) {
+        for (int b = 0; b < NB; b++) {
             if (b >= nkb) break;
             int key = b * 64 + r;
             key = key < a.ctx_cap ? key : a.ctx_cap - 1;
@@ -1773,9 +1775,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     wait_vmcnt<0>();  // this wave's direct loads landed (the barrier shows them to all)
     __syncthreads();
     // S[b][t][e]: the dot (then the table entry) of this lane's row with key 64 b + 16 t + 4 qg + e
-    v4i S[AT_SB][4];
+    v4i S[NB][4];
 #pragma unroll
-    for (int b = 0; b < AT_SB; b++)
+    for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             if (b < nkb) {
@@ -1795,7 +1797,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     // pass 1: the row max, from the largest and the smallest visible dot
     int32_t dmax = INT32_MIN, dmin = INT32_MAX;
 #pragma unroll
-    for (int b = 0; b < AT_SB; b++) {
+    for (int b = 0; b < NB; b++) {
         if (b >= nkb) break;
         if (64 * b + 63 <= wlim) {
 #pragma unroll
@@ -1832,7 +1834,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
     // pass 2: the table entries attn_exp[min(M - s, last)] (0 for a masked key) and their sum
     uint64_t sum = 0;
 #pragma unroll
-    for (int b = 0; b < AT_SB; b++) {
+    for (int b = 0; b < NB; b++) {
         if (b >= nkb) break;
 #pragma unroll
         for (int t = 0; t < 4; t++)
@@ -1879,7 +1881,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[k][c] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int b = 0; b < AT_SB; b++) {
+    for (int b = 0; b < NB; b++) {
         if (b >= nkb) break;
         uint32_t dg[4][4];
         bool fast_all = true;
@@ -1935,10 +1937,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
             packed[c] = 0;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                // |acc| <= 256 2^7 2^7 = 2^22 per plane, so each pair of planes sums in i32
-                const int32_t hi = (int32_t)((uint32_t)acc[3][c][e] << 8) + acc[2][c][e];
-                const int32_t lo = (int32_t)((uint32_t)acc[1][c][e] << 8) + acc[0][c][e];
-                const double v = fma((double)hi, 65536.0, (double)lo);
+                double v;
+                if (NB <= 4) {  // |acc| <= 256 2^7 2^7 = 2^22 per plane: each pair of planes sums in i32
+                    const int32_t hi = (int32_t)((uint32_t)acc[3][c][e] << 8) + acc[2][c][e];
+                    const int32_t lo = (int32_t)((uint32_t)acc[1][c][e] << 8) + acc[0][c][e];
+                    v = fma((double)hi, 65536.0, (double)lo);
+                } else {  // |acc| <= 2^23: the planes in double precision (every partial sum exact)
+                    v = (((double)acc[3][c][e] * 16777216.0 + (double)acc[2][c][e] * 65536.0) +
+                         (double)acc[1][c][e] * 256.0) + (double)acc[0][c][e];
+                }
                 const double y = fma(v, mo, 0.5);
                 const double f = __builtin_amdgcn_fract(y);
                 ok &= fabs(y) >= 256.0 || fabs(f - 0.5) <= 0.5 - 0x1p-30;
@@ -1994,15 +2001,18 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
     // the output of a row is four 4-byte stores per head
     if (a.hd != 64 || a.ldo % 4 != 0 || ((uintptr_t)a.out & 3) != 0 || max_keys < 1) return hipErrorInvalidValue;
     const bool noclamp = a.score_s >= 13, lds_table = a.exp_len <= ATTN_LDS_TABLE;
-    if (lds_table && max_keys <= AT_SB * 64 && a.score_s >= 22 && a.softmax_p <= 30 && a.out_s >= 0) {
+    if (lds_table && max_keys <= 8 * 64 && a.score_s >= 22 && a.softmax_p <= 30 && a.out_s >= 0) {
         const size_t lds = ((size_t)a.exp_len + 255) / 256 * 1024;  // whole 1 KiB chunks
-        static size_t allowed = 0;  // the dynamic LDS limit, raised once
-        if (lds > allowed) {
-            hipError_t e = hipFuncSetAttribute((const void *)k_attend_short, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const bool four = max_keys <= 4 * 64;
+        const void *fn = four ? (const void *)k_attend_short<4> : (const void *)k_attend_short<8>;
+        static size_t allowed[2] = {0, 0};  // the dynamic LDS limit, raised once per form
+        if (lds > allowed[four]) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
-            allowed = lds;
+            allowed[four] = lds;
         }
-        hipLaunchKernelGGL(k_attend_short, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+        if (four) hipLaunchKernelGGL(k_attend_short<4>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+        else hipLaunchKernelGGL(k_attend_short<8>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
         return hipGetLastError();
     }
     if (noclamp && lds_table) return launch_attend_groups_m<true, true>(a, groups, n_groups, max_keys, stream);
