@@ -421,6 +421,23 @@ def test_head_dim_64_prefill_score_shifts(dev, score_target, shift):
         assert got[i] == O.encode_block(om, blk, overlap=0), i
 
 
+@pytest.mark.parametrize("score_target", [768, 1 << 23])
+def test_head_dim_64_prefill_up_to_512_keys(dev, score_target):
+    """Groups of 257 to 512 keys: the 8-block form of the short prefill kernel (score shift 34)
+    and the general kernel with its per-super-block recompute (score shift 21); n_ctx 512, a
+    513-token window restarts."""
+    from taco_amd import fold, hip, synth
+    b = synth.build_model(synth.Dims(2, 4, 256, 512, 1000, 512), seed=0x5C0F, score_target=score_target)
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    lens = [257, 300, 420, 512, 513]
+    blocks = [np.array(splitmix_tokens(110 + i, n, 999), np.uint32) for i, n in enumerate(lens)]
+    batch = hip.HipBatch(hm, 5, 4096)
+    got = fold.fold_blocks(batch, blocks, 0)
+    for i, blk in enumerate(blocks):
+        print(f"score target {score_target}: block {i} ({len(blk)} tokens)", flush=True)
+        assert got[i] == O.encode_block(om, blk, overlap=0), i
+
+
 @pytest.mark.parametrize("overlap", [0, 100])
 def test_head_dim_64_long_contexts_equal_the_reference(dev, overlap):
     """More than 256 keys per row (the MFMA prefill kernel recomputes Q K^T per pass for
