@@ -872,7 +872,8 @@ __global__ __launch_bounds__(256) void k_layernorm_rows4(LnArgs a, int n_rows) {
             s_gamma[c] = (double)a.gamma[c];
         }
     }
-    // squares: eight to an i64 partial (each < 2^60), the partials into a 128-bit lo/hi with carries
+    // squares: the four of a group to an i64 partial (each < 2^60), the partials into a 128-bit
+    // lo/hi with carries
     int64_t sum = 0;
     uint64_t lo = 0, hi = 0;
     int32_t mx = INT32_MIN, mn = INT32_MAX;
