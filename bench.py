@@ -15,8 +15,9 @@ MI355X dense int8 MFMA peak, from hipEvents around every launch on the batch str
 profiled steps, run right after the timed ones (events around every launch leave the GPU idle
 about 10 us between kernels, so the timed steps run without them).
 `cpu_baseline` is the oracle's C++ restatement of the reference CPU fast path (AVX2 products,
-prefill chunk 32, one window per thread) timed on a sample of the same windows in the same run;
-its payloads must equal the GPU's.
+prefill chunk 32, one window per thread) timed on a sample of the same windows in the same run,
+on up to 16 host threads and (`one_thread`) on one thread over the first window; its payloads
+must equal the GPU's.
 
 Other workloads (--workload) measure the other configurations of the path, each with its own
 line: the c_attn GEMM alone (gemm-qkv: M 256 and 16,384, K 768, N 2,304), decode attention over
@@ -240,12 +241,23 @@ def run_fold(args):
         if not same:
             log("PARITY FAILURE: the CPU and GPU payloads differ")
             sys.exit(1)
+        # the same restatement on one thread, over the first window
+        ts = time.perf_counter()
+        one = O.fold_payloads(om, tokens[:n], 1, n, chunk=32, threads=1)
+        one_s = time.perf_counter() - ts
+        same1 = one[0] == payloads[0]
+        log(f"cpu baseline, one thread: 1 window x {n} tokens in {one_s:.2f}s; payload equal to the GPU's: {same1}")
+        if not same1:
+            log("PARITY FAILURE: the one-thread CPU payload differs")
+            sys.exit(1)
         cpu = {"value": round(cw * n / cpu_s, 2), "unit": "tokens/s", "cores": threads,
                "kind": "port",
                "sample": f"the first {cw} of the {W} windows ({cw * n} tokens), {cpu_per_thread} "
                          f"window(s) per thread, AVX2 restatement of the reference CPU fast path, "
                          f"chunk 32",
-               "payloads_equal_gpu": same}
+               "payloads_equal_gpu": same,
+               "one_thread": {"value": round(n / one_s, 2), "unit": "tokens/s", "cores": 1,
+                              "sample": f"the first window ({n} tokens)", "payload_equal_gpu": same1}}
 
     label = {"fold-gpt2-small": "GPT-2 124M", "fold-gpt2-medium": "GPT-2 medium 355M",
              "fold-gpt2-xl": "GPT-2 XL 1.5B"}[args.workload]
