@@ -1,6 +1,9 @@
-// gfx950 (CDNA4, MI355X) kernels of the HardShell forward pass. Integer only; every result is
-// the exact value of the reference CPU rule it cites (crates/hardshell/src/...). No atomics: all
-// reductions are fixed-order wave/LDS trees, so results do not depend on scheduling.
+// gfx950 (CDNA4, MI355X) kernels of the HardShell forward pass. Every result is the exact integer
+// value of the reference CPU rule it cites (crates/hardshell/src/...); where a kernel takes a
+// floating-point shortcut, it proves or checks exactness and otherwise takes the integer rule.
+// Reductions are fixed-order wave/LDS trees, and the only atomics are the coder op's integer
+// histogram counts in LDS, whose sums do not depend on order: results do not depend on
+// scheduling.
 #include <hip/hip_runtime.h>
 
 #include "intmath.h"
