@@ -436,7 +436,7 @@ def run_attend(args):
         "data": "synthetic",
         "config": {"workload": "decode attention, 64 streams x 12 heads x 64, ctx sweep",
                    "contexts": rows},
-        "roofline": {"bound": "hbm", "kernel": "k_split_dots + k_split_sum + k_split_pv + k_split_out", "achieved": big["gbs"],
+        "roofline": {"bound": "hbm", "kernel": "k_attend_decode64", "achieved": big["gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(big["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": {"value": round(big["bytes"] / (big["cpu_ms"] * 1e6), 3), "unit": "GB/s",

@@ -115,11 +115,13 @@ struct AttnArgs {
 };
 hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream);
 
-// Decode attention split over key chunks (head_dim 16, 32, 64, 128 or 256): four launches over
-// (row, head, chunk) with exact integer partials in `scratch` (attend_split_bytes bytes, 256-byte
-// aligned). `max_keys` bounds every row's key count.
+// Decode attention (head_dim 16, 32, 64, 128 or 256). head_dim 64 with at most 1,024 keys: one
+// launch, a workgroup per (row, head), `scratch` unused. Otherwise split over key chunks: four
+// launches over (row, head, chunk) with exact integer partials in `scratch` (attend_split_bytes
+// bytes, 256-byte aligned). The plan's `max_keys` bounds every row's key count.
 struct SplitPlan {
     int chunks = 1, chunk_keys = 64;
+    int max_keys = 0;  // the bound on every row's key count the plan was made for
 };
 inline bool attend_split_ok(int hd) { return hd >= 16 && hd <= 256 && (hd & (hd - 1)) == 0; }
 SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys);

@@ -1212,30 +1212,47 @@ __device__ __forceinline__ int64_t split_max(const AttnArgs &a, const SplitScrat
     return M;
 }
 
+// HD = the head dimension (16 .. 256, a power of two). A lane takes J keys per round and issues
+// the loads of all J (HD bytes each) before the first dot, so a wave keeps up to 1 KB per lane
+// of K in flight instead of one key's.
+template <int HD>
 __global__ __launch_bounds__(64) void k_split_dots(AttnArgs a, int n_rows, SplitPlan pl, void *scratch) {
+    constexpr int NT = HD / 16, J = NT >= 16 ? 1 : (16 / NT > 4 ? 4 : 16 / NT);
     __shared__ __attribute__((aligned(16))) int s_q[64];  // hd <= 256 bytes
     const int rh = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
-    const int r = rh / a.n_head, h = rh - r * a.n_head, hd = a.hd;
-    const SplitScratch S = split_scratch(scratch, n_rows, a.n_head, a.ctx_cap, pl.chunks, hd);
+    const int r = rh / a.n_head, h = rh - r * a.n_head;
+    const SplitScratch S = split_scratch(scratch, n_rows, a.n_head, a.ctx_cap, pl.chunks, HD);
     const int keys = split_keys(a, r), k0 = c * pl.chunk_keys;
     const int k1 = k0 + pl.chunk_keys < keys ? k0 + pl.chunk_keys : keys;
-    if (lane < hd / 4) s_q[lane] = ((const int *)(a.q + (size_t)r * a.ldq + h * hd))[lane];
+    if (lane < HD / 4) s_q[lane] = ((const int *)(a.q + (size_t)r * a.ldq + h * HD))[lane];
     __syncthreads();
-    const int8_t *K = a.kc + ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * hd;
+    const int8_t *K = a.kc + ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * HD;
     int32_t dmin = INT32_MAX, dmax = INT32_MIN;
-    for (int k = k0 + lane; k < k1; k += 64) {
-        int32_t d = 0;
-        const v4i *k16 = (const v4i *)(K + (size_t)k * hd);
-        for (int t = 0; t < hd / 16; t++) {
-            const v4i kk = k16[t];
-            d = __builtin_amdgcn_sdot4(s_q[4 * t], kk[0], d, false);
-            d = __builtin_amdgcn_sdot4(s_q[4 * t + 1], kk[1], d, false);
-            d = __builtin_amdgcn_sdot4(s_q[4 * t + 2], kk[2], d, false);
-            d = __builtin_amdgcn_sdot4(s_q[4 * t + 3], kk[3], d, false);
+    for (int kb = k0 + lane; kb < k1; kb += J * 64) {
+        v4i kk[J][NT];
+#pragma unroll
+        for (int j = 0; j < J; j++) {  // a key past the chunk reloads the lane's first key
+            const int k = kb + 64 * j;
+            const v4i *k16 = (const v4i *)(K + (size_t)(k < k1 ? k : kb) * HD);
+#pragma unroll
+            for (int t = 0; t < NT; t++) kk[j][t] = k16[t];
         }
-        S.dots[(size_t)rh * a.ctx_cap + k] = d;
-        dmin = d < dmin ? d : dmin;
-        dmax = d > dmax ? d : dmax;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int k = kb + 64 * j;
+            if (k >= k1) break;
+            int32_t d = 0;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                d = __builtin_amdgcn_sdot4(s_q[4 * t], kk[j][t][0], d, false);
+                d = __builtin_amdgcn_sdot4(s_q[4 * t + 1], kk[j][t][1], d, false);
+                d = __builtin_amdgcn_sdot4(s_q[4 * t + 2], kk[j][t][2], d, false);
+                d = __builtin_amdgcn_sdot4(s_q[4 * t + 3], kk[j][t][3], d, false);
+            }
+            S.dots[(size_t)rh * a.ctx_cap + k] = d;
+            dmin = d < dmin ? d : dmin;
+            dmax = d > dmax ? d : dmax;
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -1331,6 +1348,154 @@ __global__ void k_split_out(AttnArgs a, int n_rows, SplitPlan pl, void *scratch)
     a.out[(size_t)r * a.ldo + h * hd + t] = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
 }
 
+// Decode attention for head_dim 64 and at most 1,024 keys in one launch: one workgroup (4 waves)
+// per (row, head). The row's K rows go to registers (thread t: keys t + 256 j) and its V rows to
+// LDS (global_load_lds) in one round of loads; the dots, the row max, the table sum, the weights
+// p and the sums p v then come from registers and LDS with the rules of the split kernels above.
+// Dynamic LDS: kmax64 = 64 ceil(kmax / 64) V rows of 64 bytes, then kmax64 weights.
+template <bool NOCLAMP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_decode64(AttnArgs a,
+                                                                                                  int kmax) {
+    extern __shared__ __attribute__((aligned(16))) int8_t s_dyn[];
+    __shared__ __attribute__((aligned(16))) int s_q[16];
+    __shared__ int32_t s_mm[2][4];
+    __shared__ uint64_t s_sum[4];
+    __shared__ int64_t s_acc[4][64];
+    const int rh = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r = rh / a.n_head, h = rh - r * a.n_head;
+    const int kmax64 = (kmax + 63) & ~63;
+    int keys = split_keys(a, r);
+    keys = keys < kmax ? keys : kmax;  // the launch's bound holds every row's count
+    int8_t *sV = s_dyn;
+    uint32_t *s_p = (uint32_t *)(s_dyn + (size_t)kmax64 * 64);
+    const size_t base = ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * 64;
+    if (tid < 16) s_q[tid] = ((const int *)(a.q + (size_t)r * a.ldq + h * 64))[tid];
+    // K: four keys per thread (a key past the row reloads the row's last key)
+    v4i kk[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int k = tid + 256 * j;
+        const v4i *k16 = (const v4i *)(a.kc + base + (size_t)(k < keys ? k : keys - 1) * 64);
+#pragma unroll
+        for (int t = 0; t < 4; t++) kk[j][t] = k16[t];
+    }
+    // V: per round of 64 keys, wave w loads keys 16 w .. 16 w + 15 (lane l: key + l / 4, bytes
+    // 16 (l % 4)); its 1 KiB lands contiguously, so sV is [key][64]
+    for (int k0 = 0; k0 < keys; k0 += 64) {
+        int key = k0 + 16 * w + (lane >> 2);
+        key = key < keys ? key : keys - 1;
+        __builtin_amdgcn_global_load_lds((const void *)(a.vc + base + (size_t)key * 64 + 16 * (lane & 3)),
+                                         (lds_void *)(sV + (size_t)(k0 + 16 * w) * 64), 16, 0, 0);
+    }
+    wait_vmcnt<0>();  // this wave's loads landed (the barrier shows the LDS ones to all)
+    __syncthreads();
+    int32_t d[4];
+    int32_t dmin = INT32_MAX, dmax = INT32_MIN;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int32_t x = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            x = __builtin_amdgcn_sdot4(s_q[4 * t], kk[j][t][0], x, false);
+            x = __builtin_amdgcn_sdot4(s_q[4 * t + 1], kk[j][t][1], x, false);
+            x = __builtin_amdgcn_sdot4(s_q[4 * t + 2], kk[j][t][2], x, false);
+            x = __builtin_amdgcn_sdot4(s_q[4 * t + 3], kk[j][t][3], x, false);
+        }
+        d[j] = x;
+        if (tid + 256 * j < keys) {
+            dmin = x < dmin ? x : dmin;
+            dmax = x > dmax ? x : dmax;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int32_t u = __shfl_xor(dmin, o, 64), v = __shfl_xor(dmax, o, 64);
+        dmin = u < dmin ? u : dmin;
+        dmax = v > dmax ? v : dmax;
+    }
+    if (lane == 0) {
+        s_mm[0][w] = dmin;
+        s_mm[1][w] = dmax;
+    }
+    __syncthreads();
+    // the row max of the scores: the score is monotone in the dot, so it is the score of the
+    // smallest or of the largest dot
+    int64_t M = INT64_MIN;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int32_t mn = s_mm[0][i], mx = s_mm[1][i];
+        if (mn > mx) continue;  // a wave with no key
+        const int64_t s0 = attn_score<NOCLAMP>(a, mn), s1 = attn_score<NOCLAMP>(a, mx);
+        M = s0 > M ? s0 : M;
+        M = s1 > M ? s1 : M;
+    }
+    const int64_t last = a.exp_len - 1;
+    uint32_t e[4];
+    uint64_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        e[j] = 0;
+        if (tid + 256 * j < keys) {
+            const int64_t dd = M - attn_score<NOCLAMP>(a, d[j]);
+            e[j] = (uint32_t)a.exp_table[dd < last ? dd : last];
+            sum += e[j];
+        }
+    }
+    sum = (uint64_t)wave_sum64((int64_t)sum);
+    if (lane == 0) s_sum[w] = sum;
+    __syncthreads();
+    sum = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int k = tid + 256 * j;
+        if (k < keys) {
+            const uint64_t num = (uint64_t)e[j] << a.softmax_p;
+            uint64_t q = num;
+            if (sum >= 2) {
+                q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
+                if (num - q * sum >= sum) q++;
+            }
+            s_p[k] = (uint32_t)q;  // <= 2^P <= 2^30
+        }
+    }
+    __syncthreads();
+    // sum p v: thread t takes channels 16 (t % 4) .. +16 of keys t / 4 + 64 i. p = 2^16 ph + pl
+    // with pl, ph < 2^16 and |v| <= 128: at most 16 keys per thread keep the i32 sums of both
+    // halves below 2^27, exact (24-bit multiplies)
+    const int g = tid & 3;
+    int32_t lo[16], hi[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) lo[i] = hi[i] = 0;
+    for (int k = tid >> 2; k < keys; k += 64) {
+        const uint32_t p = s_p[k];
+        const int32_t pl = (int32_t)(p & 0xffffu), ph = (int32_t)(p >> 16);
+        const v4i raw = *(const v4i *)(sV + (size_t)k * 64 + 16 * g);
+        const int8_t *v = (const int8_t *)&raw;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            lo[i] += pl * (int32_t)v[i];
+            hi[i] += ph * (int32_t)v[i];
+        }
+    }
+    int64_t acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        acc[i] = (int64_t)hi[i] * 65536 + lo[i];
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) acc[i] += __shfl_xor(acc[i], o, 64);
+    }
+    if (lane < 4) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) s_acc[w][16 * lane + i] = acc[i];
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int64_t o = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
+        a.out[(size_t)r * a.ldo + h * 64 + tid] = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
+    }
+}
+
 SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys) {
     // about 4096 waves over (row, head, chunk), chunks of a multiple of 64 keys
     SplitPlan p;
@@ -1341,6 +1506,7 @@ SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys) {
     p.chunk_keys = 64 * ((blocks64 + want - 1) / want);
     p.chunk_keys = p.chunk_keys > 4096 ? 4096 : p.chunk_keys;  // the p values of a chunk in LDS
     p.chunks = (max_keys + p.chunk_keys - 1) / p.chunk_keys;
+    p.max_keys = max_keys;
     return p;
 }
 
@@ -1354,9 +1520,31 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
                                hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
     if (!attend_split_ok(a.hd) || p.chunk_keys % 64 != 0 || p.chunk_keys > 4096) return hipErrorInvalidValue;
+    const int kmax = p.max_keys < a.ctx_cap ? p.max_keys : a.ctx_cap;
+    if (a.hd == 64 && kmax >= 1 && kmax <= 1024) {  // one launch, no scratch
+        const int kmax64 = (kmax + 63) & ~63;
+        const size_t dyn = (size_t)kmax64 * 64 + (size_t)kmax64 * 4;
+        static bool allowed[2];
+        const bool nc = attn_noclamp(a);
+        const void *fn = nc ? (const void *)k_attend_decode64<true> : (const void *)k_attend_decode64<false>;
+        if (!allowed[nc]) {
+            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024 + 4096);
+            if (e != hipSuccess) return e;
+            allowed[nc] = true;
+        }
+        if (nc) hipLaunchKernelGGL(k_attend_decode64<true>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
+        else hipLaunchKernelGGL(k_attend_decode64<false>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
+        return hipGetLastError();
+    }
     const dim3 grid(n_rows * a.n_head, p.chunks);
     const size_t lds = p.chunk_keys * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_split_dots, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
+    switch (a.hd) {
+    case 16: hipLaunchKernelGGL(k_split_dots<16>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 32: hipLaunchKernelGGL(k_split_dots<32>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 64: hipLaunchKernelGGL(k_split_dots<64>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 128: hipLaunchKernelGGL(k_split_dots<128>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    default: hipLaunchKernelGGL(k_split_dots<256>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    }
     if (attn_noclamp(a)) {
         hipLaunchKernelGGL(k_split_sum<true>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
         hipLaunchKernelGGL(k_split_pv<true>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);

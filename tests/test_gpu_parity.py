@@ -297,11 +297,14 @@ def _dev_buf(dev, arr):
     return p
 
 
-@pytest.mark.parametrize("ctx_cap,hd", [(320, 64), (1024, 64), (1024, 16), (700, 256), (320, 48)])
-def test_attend_decode_op(dev, ctx_cap, hd):
+@pytest.mark.parametrize("ctx_cap,hd,score_s", [
+    (320, 64, 33), (1024, 64, 33), (1024, 64, 8), (1100, 64, 33), (1024, 16, 33), (256, 32, 33),
+    (512, 128, 33), (700, 256, 33), (320, 48, 33)])
+def test_attend_decode_op(dev, ctx_cap, hd, score_s):
     """The decode attention op, smaller than GPT-2's: 8 streams x 12 heads over caches of
-    ctx_cap positions. Head dims that are powers of two take the split-key kernels, 48 the row
-    kernel."""
+    ctx_cap positions. head_dim 64 with at most 1,024 positions takes the one-launch kernel
+    (score shift 8: scores clamped at +-2^40), other powers of two and longer caches the
+    split-key kernels, 48 the row kernel."""
     import ctypes as C
     from taco_amd import hip
     r = np.random.default_rng(3 + hd)
@@ -311,7 +314,7 @@ def test_attend_decode_op(dev, ctx_cap, hd):
     vc = r.integers(-127, 128, (B, H, ctx_cap, hd)).astype(np.int8)
     ctx = np.array([1, 2, 63, 64, 65, 128, ctx_cap - 20, ctx_cap], np.uint32)
     table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
-    score_m, score_s, out_m, out_s = 1_400_000_000, 33, 1_300_000_000, 53
+    score_m, out_m, out_s = 1_400_000_000, 1_300_000_000, 53
     want = O.attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, 30)
     bufs = [_dev_buf(dev, a) for a in (q, kc, vc, ctx, table)]
     out = np.zeros((B, H * hd), np.int8)
