@@ -1370,10 +1370,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     uint32_t *s_p = (uint32_t *)(s_dyn + (size_t)kmax64 * 64);
     const size_t base = ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * 64;
     if (tid < 16) s_q[tid] = ((const int *)(a.q + (size_t)r * a.ldq + h * 64))[tid];
-    // K: four keys per thread (a key past the row reloads the row's last key)
-    v4i kk[4][4];
+    // K: up to four keys per thread; a round past the row (uniform) issues nothing, a key past the
+    // row in the last round reloads the row's last key
+    v4i kk[4][4] = {};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
+        if (256 * j >= keys) break;
         const int k = tid + 256 * j;
         const v4i *k16 = (const v4i *)(a.kc + base + (size_t)(k < keys ? k : keys - 1) * 64);
 #pragma unroll
