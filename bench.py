@@ -91,6 +91,67 @@ def traffic_summary(fetch_csv, write_csv, calib_mib, tokens_sha, command):
                         for k, (n, fb, wb) in sorted(agg.items())}}
 
 
+def calibration_copy(hip, dev, mib):
+    """One device-to-device copy of mib MiB: the counter runs scale FETCH_SIZE and WRITE_SIZE by
+    what they read for it."""
+    nb = mib << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(src)))
+    hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(dst)))
+    hip._check(hip.lib().hs_device_copy(dev.h, dst, src, nb))
+    hip.lib().hs_device_free(dev.h, src)
+    hip.lib().hs_device_free(dev.h, dst)
+    log(f"calibration copy: {mib} MiB device to device")
+
+
+ATTEND_CONTEXTS = ((128, 64), (512, 16), (1024, 8))  # (ctx, cache sets): two launches per set
+
+
+def attend_traffic_summary(fetch_csv, write_csv, calib_mib, command):
+    """HBM bytes per decode-attention launch at each context of the attend-decode workload, from
+    two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE), scaled by the calibration copy. The
+    workload launches the kernel 2 * sets times per context, contexts in order."""
+    import csv
+    import collections
+
+    def load(path):
+        per = collections.defaultdict(float)
+        for r in csv.DictReader(open(path)):
+            per[(r["Kernel_Name"], int(r["Dispatch_Id"]))] += float(r["Counter_Value"])
+        return per
+
+    fetch, write = load(fetch_csv), load(write_csv)
+    copy_kib = calib_mib * 1024.0
+    f_scale = copy_kib / max(v for (k, _), v in fetch.items() if "copyBuffer" in k)
+    w_scale = copy_kib / max(v for (k, _), v in write.items() if "copyBuffer" in k)
+    names = {k for (k, _) in fetch if "k_attend_decode64" in k or "k_split_pv" in k}
+    out = {}
+    for name in sorted(names):
+        fd = [v for (k, d), v in sorted(fetch.items(), key=lambda kv: kv[0][1]) if k == name]
+        wd = [v for (k, d), v in sorted(write.items(), key=lambda kv: kv[0][1]) if k == name]
+        if len(fd) != sum(2 * sets for _, sets in ATTEND_CONTEXTS) or len(wd) != len(fd):
+            continue
+        i = 0
+        for ctx, sets in ATTEND_CONTEXTS:
+            n = 2 * sets
+            out[str(ctx)] = {"kernel": name.split("(")[0].replace("void ", ""), "dispatches": n,
+                             "algorithmic_bytes": 2 * 64 * 12 * ctx * 64 + 2 * 64 * 12 * 64,
+                             "fetch_bytes": round(sum(fd[i:i + n]) / n * f_scale * 1024),
+                             "write_bytes": round(sum(wd[i:i + n]) / n * w_scale * 1024)}
+            i += n
+    return {"command": command, "calibration_mib": calib_mib, "fetch_scale": round(f_scale, 4),
+            "write_scale": round(w_scale, 4), "contexts": out}
+
+
+def committed_attend_traffic(ctx):
+    """HBM bytes per decode-attention launch at ctx from the committed summary, or None."""
+    path = os.path.join(HERE, "profiles", "attend_decode_traffic.json")
+    if not os.path.exists(path):
+        return None
+    c = json.load(open(path)).get("contexts", {}).get(str(ctx))
+    return c["fetch_bytes"] + c["write_bytes"] if c else None
+
+
 def committed_traffic(workload, tokens_sha):
     """The GEMM HBM bytes per launch of the committed traffic summary of this workload (the same
     token stream), or None."""
@@ -144,14 +205,7 @@ def run_fold(args):
 
     dev = hip.HipDevice.open(0)
     if args.calib_copy_mib:
-        nb = args.calib_copy_mib << 20
-        src, dst = C.c_void_p(), C.c_void_p()
-        hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(src)))
-        hip._check(hip.lib().hs_device_alloc(dev.h, nb, C.byref(dst)))
-        hip._check(hip.lib().hs_device_copy(dev.h, dst, src, nb))
-        hip.lib().hs_device_free(dev.h, src)
-        hip.lib().hs_device_free(dev.h, dst)
-        log(f"calibration copy: {args.calib_copy_mib} MiB device to device")
+        calibration_copy(hip, dev, args.calib_copy_mib)
     model = hip.HipModel.load(dev, model_bytes)
     batch = hip.HipBatch(model, W, W * n)
     log(f"device {dev.name()}, model {model.weight_bytes() / 1e6:.1f} MB, batch "
@@ -382,8 +436,10 @@ def run_attend(args):
     score_m, score_s, out_m, out_s = 1_400_000_000, 34, 1_300_000_000, 53
     dtab = _dev_buf(hip, dev, table)
     rows = []
-    for ctx in (128, 512, 1024):
-        sets = max(3, (768 << 20) // (2 * B * H * ctx * hd))  # >= 768 MB of caches
+    if args.calib_copy_mib:
+        calibration_copy(hip, dev, args.calib_copy_mib)
+    for ctx, sets in ATTEND_CONTEXTS:
+        assert sets == max(3, (768 << 20) // (2 * B * H * ctx * hd))  # >= 768 MB of caches
         q = rng.integers(-127, 128, (B, H, hd)).astype(np.int8)
         ctxs = np.full(B, ctx, np.uint32)
         dq, dctx = _dev_buf(hip, dev, q), _dev_buf(hip, dev, ctxs)
@@ -438,7 +494,10 @@ def run_attend(args):
                    "contexts": rows},
         "roofline": {"bound": "hbm", "kernel": "k_attend_decode64", "achieved": big["gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(big["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(big["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": committed_attend_traffic(big["ctx"]),
+                     "traffic_unit": "HBM bytes per launch at the largest context (FETCH_SIZE + "
+                                     "WRITE_SIZE, calibrated; profiles/attend_decode_traffic.json)"},
         "cpu_baseline": {"value": round(big["bytes"] / (big["cpu_ms"] * 1e6), 3), "unit": "GB/s",
                          "cores": 1, "kind": "port",
                          "sample": "the oracle's scalar decode attention of one cache set"},
@@ -450,6 +509,11 @@ def main_traffic(argv):
     two rocprofv3 counter runs of `bench.py --workload WORKLOAD --calib-copy-mib CALIB_MIB`."""
     from taco_amd import synth
     fetch_csv, write_csv, calib, workload = argv
+    if workload == "attend-decode":
+        cmd = ("rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -- python3 bench.py "
+               f"--workload attend-decode --steps 1 --warmup 0 --no-cpu --calib-copy-mib {calib}")
+        print(json.dumps(attend_traffic_summary(fetch_csv, write_csv, int(calib), cmd), indent=1))
+        return
     dims_name, W, n, _ = FOLDS[workload]
     tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
     cmd = (f"rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -- python3 bench.py "
