@@ -277,8 +277,24 @@ def run_fold(args):
         if not same:
             log("ROUND TRIP FAILURE: the unfolded tokens differ")
             sys.exit(1)
+        # the same round trip again with an event pair around every launch: GPU time per op
+        # for each decode pass (one row per slot), against the wall time of the timed run
+        hip._check(hip.lib().hs_batch_set_profiling(batch.h, 1))
+        hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
+        back2 = fold.unfold_blocks(batch, payloads, 0, cap=n)
+        hip._check(hip.lib().hs_batch_set_profiling(batch.h, 0))
+        uprof = read_profile(hip, batch)
+        if not all(np.array_equal(back2[w], blocks[w]) for w in range(W)):
+            log("ROUND TRIP FAILURE: the profiled unfold differs")
+            sys.exit(1)
+        passes = max(v["launches"] for kk, v in uprof.items() if kk == "embed")
+        u_ops = {kk: round(v["ns"] / 1e6 / passes, 4) for kk, v in sorted(uprof.items(), key=lambda x: -x[1]["ns"])}
+        log(f"unfold: {passes} passes; GPU ms per pass by op: {u_ops}; wall ms per pass "
+            f"{1e3 * u_s / passes:.3f}")
         unfold = {"tokens_per_s": round(W * n / u_s, 1), "seconds": round(u_s, 3),
-                  "round_trip_equal": same}
+                  "round_trip_equal": same, "passes": passes,
+                  "wall_ms_per_pass": round(1e3 * u_s / passes, 4),
+                  "gpu_ms_per_pass_by_op": u_ops}
 
     cpu = None
     if not args.no_cpu:

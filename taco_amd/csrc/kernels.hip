@@ -1012,7 +1012,12 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     // the vector forms need 4-aligned rows: d and ldo multiples of 4
     // the single-precision element rule: 8-bit outputs, integer beta with |beta| <= 256
     const bool f32 = a.bits == 8 && a.beta_frac == 0 && a.beta_small && a.s <= 126;
-    if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 768) {
+    // Fewer than 4,096 rows (decode passes): a wave per row, 4x the waves of the 16-lane form,
+    // which would leave most CUs idle (256 rows: 16 workgroups)
+    if (n_rows < 4096 && a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
+        if (a.d <= 1024) hipLaunchKernelGGL(k_layernorm_rows<4>, grid, dim3(256), 0, stream, a, n_rows);
+        else hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
+    } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 768) {
         if (f32) hipLaunchKernelGGL((k_layernorm_rows4<12, true>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
         else hipLaunchKernelGGL((k_layernorm_rows4<12, false>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 1024) {
