@@ -746,7 +746,7 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
 template <int NG>
 __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // no LDS, no barrier
     if (row >= n_rows) return;
     const int d = a.d;
     const int32_t *x = a.x + (size_t)(a.src ? a.src[row] : row) * d;
@@ -1012,11 +1012,11 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     // the vector forms need 4-aligned rows: d and ldo multiples of 4
     // the single-precision element rule: 8-bit outputs, integer beta with |beta| <= 256
     const bool f32 = a.bits == 8 && a.beta_frac == 0 && a.beta_small && a.s <= 126;
-    // Fewer than 4,096 rows (decode passes): a wave per row, 4x the waves of the 16-lane form,
-    // which would leave most CUs idle (256 rows: 16 workgroups)
+    // Fewer than 4,096 rows (decode passes): a one-wave workgroup per row, spread over the CUs;
+    // the 16-lane form would leave most of them idle (256 rows: 16 workgroups)
     if (n_rows < 4096 && a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
-        if (a.d <= 1024) hipLaunchKernelGGL(k_layernorm_rows<4>, grid, dim3(256), 0, stream, a, n_rows);
-        else hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
+        if (a.d <= 1024) hipLaunchKernelGGL(k_layernorm_rows<4>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
+        else hipLaunchKernelGGL(k_layernorm_rows<8>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 768) {
         if (f32) hipLaunchKernelGGL((k_layernorm_rows4<12, true>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
         else hipLaunchKernelGGL((k_layernorm_rows4<12, false>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
