@@ -90,15 +90,26 @@ class HsmWriter:
             header_len = len(js)
         v2 = self.ln_f_bits is not None or self.ln_beta_frac is not None or any(
             n.endswith(".mlp.gelu") and d.dtype == np.int16 for n, d, _ in self.tensors)
-        out = bytearray(b"HSHLMDL\0")
-        out += (2 if v2 else 1).to_bytes(4, "little") + header_len.to_bytes(4, "little")
-        out += js + b" " * (header_len - len(js))
-        out += b"\0" * (_align64(len(out)) - len(out))
-        out += vb
+        head = bytearray(b"HSHLMDL\0")
+        head += (2 if v2 else 1).to_bytes(4, "little") + header_len.to_bytes(4, "little")
+        head += js + b" " * (header_len - len(js))
+        # one zero-filled buffer, each section copied to its aligned offset (the padding is the
+        # zeros left between sections)
+        pos = _align64(len(head)) + len(vb)
         if mb:
-            out += b"\0" * (_align64(len(out)) - len(out))
-            out += mb
+            pos = _align64(pos) + len(mb)
+        offsets = []
         for _, data, _ in self.tensors:
-            out += b"\0" * (_align64(len(out)) - len(out))
-            out += data.tobytes()
-        return bytes(out)
+            pos = _align64(pos)
+            offsets.append(pos)
+            pos += data.nbytes
+        out = np.zeros(pos, np.uint8)
+        out[:len(head)] = np.frombuffer(bytes(head), np.uint8)
+        cur = _align64(len(head))
+        out[cur:cur + len(vb)] = np.frombuffer(bytes(vb), np.uint8)
+        if mb:
+            cur = _align64(cur + len(vb))
+            out[cur:cur + len(mb)] = np.frombuffer(bytes(mb), np.uint8)
+        for off, (_, data, _) in zip(offsets, self.tensors):
+            out[off:off + data.nbytes] = data.reshape(-1).view(np.uint8)
+        return out.tobytes()

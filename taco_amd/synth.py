@@ -16,6 +16,8 @@ library's pow.
 from __future__ import annotations
 
 import hashlib
+import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
 from fractions import Fraction
 from typing import List
@@ -46,12 +48,16 @@ GPT2_XL = Dims(48, 25, 1600, 6400)
 def splitmix_block(state0: int, start: int, n: int) -> np.ndarray:
     """Outputs start .. start+n of the splitmix64 stream whose state is `state0` before the
     first call (output i uses the state state0 + (i + 1) * GAMMA)."""
-    i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
+    z = np.arange(start + 1, start + n + 1, dtype=np.uint64)
     with np.errstate(over="ignore"):
-        z = np.uint64(state0 & MASK) + i * np.uint64(GAMMA)
-        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
-        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
-        return z ^ (z >> np.uint64(31))
+        z *= np.uint64(GAMMA)
+        z += np.uint64(state0 & MASK)
+        z ^= z >> np.uint64(30)
+        z *= np.uint64(0xBF58476D1CE4E5B9)
+        z ^= z >> np.uint64(27)
+        z *= np.uint64(0x94D049BB133111EB)
+        z ^= z >> np.uint64(31)
+    return z
 
 
 class Stream:
@@ -70,13 +76,31 @@ class Stream:
         return int(self.take(1)[0])
 
 
+_POOL = None
+
+
+def _pool():
+    global _POOL
+    if _POOL is None:
+        _POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1))
+    return _POOL
+
+
 def _uniform_i8(s: Stream, shape) -> np.ndarray:
+    """(next_u64 % 255) - 127 for each element, in stream order. Output i depends only on its
+    stream index, so chunks are generated on a thread pool (numpy releases the GIL)."""
     n = int(np.prod(shape))
     out = np.empty(n, np.int8)
-    step = 1 << 24
-    for i in range(0, n, step):
-        z = s.take(min(step, n - i))
-        out[i:i + len(z)] = ((z % np.uint64(255)).astype(np.int64) - 127).astype(np.int8)
+    step = 1 << 22
+    base = s.n
+
+    def fill(i):
+        z = splitmix_block(s.state0, base + i, min(step, n - i))
+        z %= np.uint64(255)
+        out[i:i + len(z)] = z.astype(np.int16) - 127
+
+    list(_pool().map(fill, range(0, n, step)))
+    s.n += n
     return out.reshape(shape)
 
 
@@ -173,12 +197,13 @@ SIGMA_ACT_SQ = Fraction(1600 * 1600)       # i8 model activations times weights
 
 
 def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_len: int = 8192,
-                score_target: int = 768) -> bytes:
+                score_target: int = 768, beta_max: int = 16) -> bytes:
     """The synthetic model. wide=True makes a model-file version 2 model: an i16 GELU table
     (output unit 1/10240), a 16-bit ln_f (target 10240) and ln_beta_frac = 8 (beta in units of
     2^-8, uniform in [-4096, 4096]); the shifts that read those activations are 8 larger.
     table_len sets the length of both exponent tables; score_target the typical attention score
-    (larger targets give smaller score shifts)."""
+    (larger targets give smaller score shifts); beta_max the LayerNorm beta range [-beta_max,
+    beta_max] in output units."""
     d, f, V, C, L, H = dims.d_model, dims.d_ff, dims.vocab, dims.n_ctx, dims.n_layer, dims.n_head
     hd = d // H
     s = Stream(seed)
@@ -202,7 +227,7 @@ def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_l
 
     def layernorm(prefix, target=40):
         w.add_tensor(prefix + ".g", _uniform_int(s, d, 1 << 13, 1 << 15, np.int16))
-        w.add_tensor(prefix + ".b", _uniform_int(s, d, -(16 << frac), (16 << frac) + 1, np.int32))
+        w.add_tensor(prefix + ".b", _uniform_int(s, d, -(beta_max << frac), (beta_max << frac) + 1, np.int32))
         w.add_tensor(prefix + ".rescale", mult(1), shift_for(Fraction(2) ** 80 * gamma_sq, target))
 
     def linear(prefix, rows, cols, target, in_scale=1):

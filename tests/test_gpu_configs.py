@@ -1,0 +1,163 @@
+"""The benchmark configurations at their full sizes on the GPU, and the LayerNorm forms each
+pass size and width selects, against the oracle (the C++ restatement of the reference CPU path).
+
+- GPT-2 medium shape (24 layers, d 1,024, 16 heads, d_ff 4,096): 256 windows of 256 Zipf(1.1)
+  tokens folded in one call, sampled payloads equal to the CPU fast path's, and every block
+  unfolded back to its tokens (crates/taco/src/gpu_fold.rs:205-306, gpu_unfold.rs:74-300).
+- GPT-2 XL shape (48 layers, d 1,600, 25 heads, d_ff 6,400): 512 windows of 512 tokens.
+- Decode attention at 64 streams x 12 heads x 64 over caches of 128, 512 and 1,024 positions.
+- One- and two-layer models at d 1,024 and 1,600, version-2 ("wide") models and a model with
+  |beta| > 256, each through a pass of fewer than 4,096 rows and one of at least 4,096 rows.
+"""
+
+import ctypes as C
+import time
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.conftest import splitmix_tokens
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from taco_amd import hip
+    return hip.HipDevice.open(0)
+
+
+def _windows(tokens, n, sel):
+    return [tokens[w * n:(w + 1) * n] for w in sel]
+
+
+def _cpu_payloads(om, blocks, n):
+    return O.fold_payloads(om, np.concatenate(blocks), len(blocks), n, chunk=32,
+                           threads=len(blocks))
+
+
+def test_gpt2_medium_fold_and_unfold_round_trip(dev):
+    from taco_amd import fold, hip, synth
+    t0 = time.time()
+    mb = synth.build_model(synth.GPT2_MEDIUM)
+    W, n = 256, 256
+    tokens = synth.zipf_tokens(W * n)
+    _log(f"medium: model {len(mb)} B and tokens built in {time.time() - t0:.1f}s")
+    hm = hip.HipModel.load(dev, mb)
+    batch = hip.HipBatch(hm, W, W * n)
+    blocks = _windows(tokens, n, range(W))
+    t0 = time.time()
+    got = fold.fold_blocks(batch, blocks)
+    _log(f"medium: fold of {W} x {n} in {time.time() - t0:.2f}s")
+    sel = [0, 1, 130, 255]
+    om = O.Model(mb)
+    want = _cpu_payloads(om, _windows(tokens, n, sel), n)
+    for i, w in enumerate(sel):
+        assert got[w] == want[i], f"window {w}: the GPU payload differs from the CPU's"
+    t0 = time.time()
+    back = fold.unfold_blocks(batch, got, 0, cap=n)
+    _log(f"medium: unfold of {W} blocks in {time.time() - t0:.2f}s")
+    bad = [w for w in range(W) if not np.array_equal(back[w], blocks[w])]
+    assert not bad, f"blocks {bad[:8]} did not round-trip"
+
+
+def test_gpt2_xl_fold_equals_the_cpu(dev):
+    from taco_amd import fold, hip, synth
+    t0 = time.time()
+    mb = synth.build_model(synth.GPT2_XL)
+    W, n = 512, 512
+    tokens = synth.zipf_tokens(W * n)
+    _log(f"xl: model {len(mb)} B and tokens built in {time.time() - t0:.1f}s")
+    hm = hip.HipModel.load(dev, mb)
+    batch = hip.HipBatch(hm, W, W * n)
+    t0 = time.time()
+    got = fold.fold_blocks(batch, _windows(tokens, n, range(W)))
+    _log(f"xl: fold of {W} x {n} in {time.time() - t0:.2f}s")
+    del batch
+    sel = [0, 511]
+    om = O.Model(mb)
+    want = _cpu_payloads(om, _windows(tokens, n, sel), n)
+    for i, w in enumerate(sel):
+        assert got[w] == want[i], f"window {w}: the GPU payload differs from the CPU's"
+
+
+def _dev_buf(dev, arr):
+    from taco_amd import hip
+    p = C.c_void_p()
+    hip._check(hip.lib().hs_device_alloc(dev.h, arr.nbytes, C.byref(p)))
+    hip._check(hip.lib().hs_device_upload(dev.h, p, arr.ctypes.data_as(C.c_void_p), arr.nbytes))
+    return p
+
+
+@pytest.mark.parametrize("ctx_len", [128, 512, 1024])
+def test_attend_decode_at_the_benchmark_shape(dev, ctx_len):
+    """64 streams x 12 heads x 64 with every stream at ctx_len positions (the decode attention
+    workload), plus a second call with ragged lengths, against the oracle."""
+    from taco_amd import hip
+    r = np.random.default_rng(ctx_len)
+    B, H, hd = 64, 12, 64
+    q = r.integers(-127, 128, (B, H, hd)).astype(np.int8)
+    kc = r.integers(-127, 128, (B, H, ctx_len, hd)).astype(np.int8)
+    vc = r.integers(-127, 128, (B, H, ctx_len, hd)).astype(np.int8)
+    table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
+    score_m, score_s, out_m, out_s = 1_400_000_000, 33, 1_300_000_000, 53
+    for ctx in (np.full(B, ctx_len, np.uint32),
+                r.integers(1, ctx_len + 1, B).astype(np.uint32)):
+        want = O.attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, 30)
+        bufs = [_dev_buf(dev, a) for a in (q, kc, vc, ctx, table)]
+        out = np.zeros((B, H * hd), np.int8)
+        dout = _dev_buf(dev, out)
+        try:
+            hip._check(hip.lib().hs_op_attend_decode_dev(
+                dev.h, bufs[0], bufs[1], bufs[2], bufs[3], B, H, hd, ctx_len, score_m, score_s,
+                out_m, out_s, bufs[4], len(table), 30, dout, None))
+            hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                    out.nbytes))
+        finally:
+            for p in bufs + [dout]:
+                hip.lib().hs_device_free(dev.h, p)
+        assert np.array_equal(out, want)
+
+
+# LayerNorm forms by pass size and width: fewer than 4,096 rows take a one-wave workgroup per
+# row (4 or 8 column groups per lane); at least 4,096 rows take the 16-lanes-per-row form for
+# d <= 1,024 (12 or 16 groups; single-precision element rule for 8-bit outputs with |beta| <=
+# 256, the integer rule otherwise, two planes for a 16-bit ln_f) and the 4-rows-per-workgroup
+# wave form for 1,024 < d <= 2,048.
+LN_MODELS = {
+    "d1024": dict(dims=(2, 16, 1024, 4096), kw={}),
+    "d1600": dict(dims=(1, 25, 1600, 6400), kw={}),
+    "d768_wide": dict(dims=(2, 12, 768, 3072), kw=dict(wide=True)),
+    "d1024_wide": dict(dims=(1, 16, 1024, 4096), kw=dict(wide=True)),
+    "d768_beta": dict(dims=(2, 12, 768, 3072), kw=dict(beta_max=1000)),
+    "d1024_beta": dict(dims=(1, 16, 1024, 4096), kw=dict(beta_max=1000)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(LN_MODELS))
+@pytest.mark.parametrize("windows", [8, 32])
+def test_layernorm_forms_equal_the_cpu(dev, name, windows):
+    """`windows` x 128-token windows in one pass: 1,024 rows (the decode-size form) or 4,096
+    rows (the prefill forms), every interval against the CPU fast path's."""
+    from taco_amd import hip, synth
+    L, H, d, f = LN_MODELS[name]["dims"]
+    V, n = 512, 128
+    mb = synth.build_model(synth.Dims(L, H, d, f, vocab=V, n_ctx=256), seed=0x1F00 + d,
+                           **LN_MODELS[name]["kw"])
+    hm, om = hip.HipModel.load(dev, mb), O.Model(mb)
+    blocks = [np.array(splitmix_tokens(0x5EED + w, n, V - 1), np.uint32) for w in range(windows)]
+    batch = hip.HipBatch(hm, windows, windows * n)
+    inputs, queries = [], []
+    for w, blk in enumerate(blocks):
+        inputs += [(w, V - 1)] + [(w, int(t)) for t in blk[:-1]]
+        queries += [(0, int(t)) for t in blk]
+    raw = batch.run_coded_raw(inputs, queries, 32).reshape(windows, n, 3)
+    for w in sorted({0, 3, windows - 1}):
+        want = O.fast_window_intervals(om, blocks[w], chunk=32)
+        bad = np.nonzero(np.any(raw[w] != want, axis=1))[0]
+        assert len(bad) == 0, f"{name}, window {w}: {len(bad)} rows differ, first {bad[:8].tolist()}"

@@ -401,6 +401,17 @@ def test_fast_engine_equals_reference(golden_model):
         assert np.array_equal(got, np.array(want)), chunk
 
 
+def test_fast_engine_equals_reference_version_2():
+    # the golden version-2 model (i16 GELU outputs, 16-bit ln_f, ln_beta_frac), whose reference
+    # session output is pinned by GOLDEN_V2_OUTPUT
+    m = O.Model(O.build_model(O.tiny_dims(), 0x7AC0_0001, 64, wide=True))
+    toks = splitmix_tokens(14, 60, 300)
+    s = O.Session(m)
+    want = [s.start_block()] + [s.step(t) for t in toks[:-1]]
+    for chunk in [1, 5, 32]:
+        assert np.array_equal(O.fast_window_weights(m, toks, chunk=chunk), np.array(want)), chunk
+
+
 @pytest.mark.parametrize("dims", [(1, 3, 60, 100, 300, 40), (2, 1, 33, 47, 270, 20),
                                   (1, 2, 40, 64, 260, 30)])
 def test_fast_engine_equals_reference_odd_dims(dims):
