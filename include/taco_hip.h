@@ -35,8 +35,11 @@ hs_status tc_fold_blocks(hs_batch *batch, uint32_t overlap, const uint32_t *toke
                          size_t cap, size_t *lens);
 
 /* Decodes `count` coded payloads (payload b is payloads[offsets[b] .. offsets[b + 1])) on
- * `batch` (one slot per block, in waves of hs_batch_slots blocks). Block b's tokens go to
- * tokens + b * cap; counts[b] is its token count. */
+ * `batch` with the context overlap `overlap` (set on the batch, as hs_batch_set_overlap; a
+ * value that does not fit the context is refused with its error). One slot per block: blocks
+ * take the slots in order, and a slot whose block is complete takes the next waiting block
+ * (crates/taco/src/gpu_unfold.rs:74-196). Block b's tokens go to tokens + b * cap; counts[b]
+ * is its token count. */
 hs_status tc_unfold_blocks(hs_batch *batch, uint32_t overlap, const uint8_t *payloads,
                            const size_t *offsets, size_t count, uint32_t *tokens, size_t cap,
                            size_t *counts);

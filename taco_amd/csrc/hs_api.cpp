@@ -87,6 +87,7 @@ struct hs_device {
     hipStream_t stream = nullptr;
 };
 
+
 namespace {
 
 struct DevLinear {
@@ -824,7 +825,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         split_plan = hs::attend_split_plan(n, m.H, max_keys);
         hs::AttnArgs probe;
         probe.n_head = m.H; probe.hd = m.hd; probe.ctx_cap = m.C;
-        const size_t need = hs::attend_split_bytes(probe, n, split_plan);
+        const size_t need = hs::attend_split_bytes(probe, n, split_plan);  // 0: one launch
         if (need <= (1ull << 30)) {
             if (need > b.split_bytes) {
                 if (b.split) {
@@ -1265,8 +1266,13 @@ extern "C" hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, co
     HIP_TRY(hipSetDevice(dev->ordinal));
     if (hs::attend_split_ok((int)hd)) {  // split over key chunks, scratch ordered on the stream
         const hs::SplitPlan plan = hs::attend_split_plan((int)b, (int)h, (int)ctx_cap);
+        const size_t bytes = hs::attend_split_bytes(at, (int)b, plan);
+        if (bytes == 0) {  // the one-launch kernel: no scratch
+            HIP_TRY(hs::launch_attend_split(at, (int)b, plan, nullptr, st));
+            return HS_OK;
+        }
         void *scratch = nullptr;
-        HIP_TRY(hipMallocAsync(&scratch, hs::attend_split_bytes(at, (int)b, plan), st));
+        HIP_TRY(hipMallocAsync(&scratch, bytes, st));
         const hipError_t e = hs::launch_attend_split(at, (int)b, plan, scratch, st);
         const hipError_t f = hipFreeAsync(scratch, st);
         HIP_TRY(e);
@@ -1379,12 +1385,13 @@ extern "C" hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q,
     HIP_TRY(hipSetDevice(dev->ordinal));
     if (hs::attend_split_ok((int)hd)) {
         const hs::SplitPlan plan = hs::attend_split_plan((int)b, (int)h, (int)ctx_cap);
+        const size_t bytes = hs::attend_split_bytes(at, (int)b, plan);
         void *scratch = nullptr;
-        HIP_TRY(hipMalloc(&scratch, hs::attend_split_bytes(at, (int)b, plan)));
+        if (bytes) HIP_TRY(hipMalloc(&scratch, bytes));
         const hs_status st = time_reps(dev, reps, ns, [&] {
             return hs::launch_attend_split(at, (int)b, plan, scratch, dev->stream);
         });
-        (void)hipFree(scratch);
+        if (scratch) (void)hipFree(scratch);
         return st;
     }
     return time_reps(dev, reps, ns, [&] { return hs::launch_attend(at, (int)b, dev->stream); });

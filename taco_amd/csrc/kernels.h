@@ -125,6 +125,9 @@ struct SplitPlan {
 };
 inline bool attend_split_ok(int hd) { return hd >= 16 && hd <= 256 && (hd & (hd - 1)) == 0; }
 SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys);
+// True when the plan takes the one-launch kernel (head_dim 64, at most 1,024 keys): no scratch.
+bool attend_split_one_launch(int hd, int ctx_cap, const SplitPlan &p);
+// The scratch bytes of the split launches (0 when the plan takes the one-launch kernel).
 size_t attend_split_bytes(const AttnArgs &a, int n_rows, const SplitPlan &p);
 hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p, void *scratch,
                                hipStream_t stream);

@@ -1517,7 +1517,13 @@ SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys) {
     return p;
 }
 
+bool attend_split_one_launch(int hd, int ctx_cap, const SplitPlan &p) {
+    const int kmax = p.max_keys < ctx_cap ? p.max_keys : ctx_cap;
+    return hd == 64 && kmax >= 1 && kmax <= 1024;
+}
+
 size_t attend_split_bytes(const AttnArgs &a, int n_rows, const SplitPlan &p) {
+    if (attend_split_one_launch(a.hd, a.ctx_cap, p)) return 0;
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
     const size_t rh = (size_t)n_rows * a.n_head;
     return al(rh * a.ctx_cap * 4) + 2 * al(rh * p.chunks * 8) + al(rh * p.chunks * a.hd * 8);
@@ -1528,7 +1534,7 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
     if (n_rows <= 0) return hipSuccess;
     if (!attend_split_ok(a.hd) || p.chunk_keys % 64 != 0 || p.chunk_keys > 4096) return hipErrorInvalidValue;
     const int kmax = p.max_keys < a.ctx_cap ? p.max_keys : a.ctx_cap;
-    if (a.hd == 64 && kmax >= 1 && kmax <= 1024) {  // one launch, no scratch
+    if (attend_split_one_launch(a.hd, a.ctx_cap, p)) {  // one launch, no scratch
         const int kmax64 = (kmax + 63) & ~63;
         const size_t dyn = (size_t)kmax64 * 64 + (size_t)kmax64 * 4;
         static bool allowed[2];

@@ -350,7 +350,10 @@ extern "C" hs_status tc_unfold_blocks(hs_batch *batch, uint32_t overlap, const u
                                       size_t cap, size_t *counts) {
     if (!batch || (count && (!payloads || !offsets || !tokens || !counts)))
         return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
-    (void)overlap;  // the batch applies its own overlap at each restart
+    // The lanes of gpu_unfold.rs run at the container's overlap: restarts inside the backend
+    // keep that many tokens (the batch refuses an overlap that does not fit its context).
+    hs_status s = hs_batch_set_overlap(batch, overlap);
+    if (s != HS_OK) return s;
     const size_t slots = hs_batch_slots(batch);
     const uint32_t eot = hs_model_eot(hs_batch_model(batch));
     std::vector<Decoder> dec(count);
@@ -364,37 +367,45 @@ extern "C" hs_status tc_unfold_blocks(hs_batch *batch, uint32_t overlap, const u
         dec[b].init(p + used, n - used);
         counts[b] = (size_t)total[b];
     }
+    // A job queue over the slots (decode_jobs, gpu_unfold.rs:74-196): a slot whose block is
+    // complete resets and takes the next waiting block, so a long block does not hold the
+    // slots of short ones idle. Blocks of no tokens need no rows.
+    std::vector<int64_t> job(slots, -1);
+    size_t next = 0;
+    auto take = [&](size_t slot) {
+        while (next < count && total[next] == 0) next++;
+        job[slot] = next < count ? (int64_t)next++ : -1;
+        if (job[slot] >= 0) hs_batch_reset(batch, slot);
+    };
+    for (size_t slot = 0; slot < slots; slot++) take(slot);
     std::vector<hs_input> inputs;
     std::vector<hs_query> queries;
-    std::vector<size_t> live;
+    std::vector<size_t> live;  // the slot of each row
     std::vector<hs_interval> answers;
-    for (size_t b0 = 0; b0 < count; b0 += slots) {
-        const size_t b1 = std::min(count, b0 + slots);
-        for (size_t b = b0; b < b1; b++) hs_batch_reset(batch, b - b0);
-        for (;;) {
-            inputs.clear();
-            queries.clear();
-            live.clear();
-            for (size_t b = b0; b < b1; b++) {
-                if (done[b] >= total[b]) continue;
-                const uint32_t prev = done[b] == 0 ? eot : tokens[b * cap + done[b] - 1];
-                inputs.push_back(hs_input{(uint32_t)(b - b0), prev});
-                queries.push_back(hs_query{1, (uint32_t)dec[b].target()});
-                live.push_back(b);
-            }
-            if (live.empty()) break;
-            answers.resize(inputs.size());
-            hs_status s = hs_batch_run_coded(batch, inputs.data(), queries.data(), inputs.size(),
-                                             TC_FREQ_BITS, answers.data());
-            if (s != HS_OK) return s;
-            for (size_t i = 0; i < live.size(); i++) {
-                const size_t b = live[i];
-                const hs_interval &a = answers[i];
-                if (!dec[b].decode(a.start, a.freq))
-                    return hs::fail(HS_DEVICE_ERROR, (int)b, "the coder op gave an interval that does not hold the target");
-                tokens[b * cap + done[b]] = (uint32_t)a.symbol;
-                done[b]++;
-            }
+    for (;;) {
+        inputs.clear();
+        queries.clear();
+        live.clear();
+        for (size_t slot = 0; slot < slots; slot++) {
+            if (job[slot] < 0) continue;
+            const size_t b = (size_t)job[slot];
+            const uint32_t prev = done[b] == 0 ? eot : tokens[b * cap + done[b] - 1];
+            inputs.push_back(hs_input{(uint32_t)slot, prev});
+            queries.push_back(hs_query{1, (uint32_t)dec[b].target()});
+            live.push_back(slot);
+        }
+        if (live.empty()) break;
+        answers.resize(inputs.size());
+        s = hs_batch_run_coded(batch, inputs.data(), queries.data(), inputs.size(), TC_FREQ_BITS,
+                               answers.data());
+        if (s != HS_OK) return s;
+        for (size_t i = 0; i < live.size(); i++) {
+            const size_t slot = live[i], b = (size_t)job[slot];
+            const hs_interval &a = answers[i];
+            if (!dec[b].decode(a.start, a.freq))
+                return hs::fail(HS_DEVICE_ERROR, (int)b, "the coder op gave an interval that does not hold the target");
+            tokens[b * cap + done[b]] = (uint32_t)a.symbol;
+            if (++done[b] == total[b]) take(slot);
         }
     }
     return HS_OK;

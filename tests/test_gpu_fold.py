@@ -38,6 +38,38 @@ def test_fold_and_unfold_equal_the_reference(dev, overlap):
         assert np.array_equal(back[i], blk), i
 
 
+def test_unfold_refills_slots_with_ragged_blocks(dev):
+    """Blocks of very different lengths (empty ones among them) on fewer slots than blocks:
+    each slot takes the next waiting block when its block ends (gpu_unfold.rs:74-196), with
+    restarts inside the backend (lengths past n_ctx = 64), and every block decodes back."""
+    from taco_amd import fold, hip
+    b = O.build_model(O.tiny_dims(), 0x7AC0_0001, 64)
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    lens = [200, 1, 0, 3, 130, 2, 64, 65, 1, 17, 0, 90]
+    blocks = [np.array(splitmix_tokens(1300 + i, n, 299), np.uint32) for i, n in enumerate(lens)]
+    for overlap in (0, 9):
+        payloads = [O.encode_block(om, blk, overlap=overlap) for blk in blocks]
+        batch = hip.HipBatch(hm, 3, 64)
+        back = fold.unfold_blocks(batch, payloads, overlap, cap=256)
+        for i, blk in enumerate(blocks):
+            assert np.array_equal(back[i], blk), (overlap, i)
+
+
+def test_unfold_applies_its_overlap(dev):
+    """The overlap argument is the batch's overlap for the decode (a batch left at another
+    overlap still decodes the container's blocks), and one that does not fit is refused."""
+    from taco_amd import fold, hip
+    b = O.build_model(O.tiny_dims(), 0x7AC0_0001, 64)
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    blk = np.array(splitmix_tokens(4242, 150, 299), np.uint32)
+    payload = O.encode_block(om, blk, overlap=32)
+    batch = hip.HipBatch(hm, 2, 64)
+    batch.set_overlap(0)
+    assert np.array_equal(fold.unfold_blocks(batch, [payload], 32, cap=256)[0], blk)
+    with pytest.raises(hip.HipError):
+        fold.unfold_blocks(batch, [payload], 63, cap=256)
+
+
 def test_stop_rule_equals_the_reference(dev):
     """codec.rs:105-112: the encoder stops when the varint plus the lower bound of the coder
     output reach `stop`; a payload of exactly `stop` bytes can still be made (it then loses to
