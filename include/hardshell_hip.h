@@ -237,6 +237,19 @@ hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, const int8_t 
                                   int32_t out_m, uint8_t out_s, const int32_t *attn_exp,
                                   size_t len, uint8_t softmax_p, int8_t *out, void *stream);
 
+/* hs_op_attend_decode_dev without any allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The split launches keep their partials in a fixed
+ * 64 MiB array per GPU (held until the process ends) instead of stream-ordered allocations;
+ * a shape that needs more (row-heads x ctx_cap x 4 bytes plus the chunk partials) is refused
+ * with HS_UNSUPPORTED. Calls that overlap on one GPU share that array and race. */
+hs_status hs_op_attend_decode_dev_noalloc(hs_device *dev, const int8_t *q, const int8_t *k_cache,
+                                          const int8_t *v_cache, const uint32_t *ctx, size_t b,
+                                          size_t h, size_t hd, size_t ctx_cap, int32_t score_m,
+                                          uint8_t score_s, int32_t out_m, uint8_t out_s,
+                                          const int32_t *attn_exp, size_t len, uint8_t softmax_p,
+                                          int8_t *out, void *stream);
+
 /* The coder op alone (the logits_weights + coder_interval kernels of
  * crates/hardshell-cuda/kernels/hardshell.cu:1393-1611, no public counterpart; for tests): for
  * each of `rows` rows of i64 logits [rows, vocab] (host pointers, each within +-2^40), the

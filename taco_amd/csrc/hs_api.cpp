@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <string>
 #include <unordered_map>
@@ -85,8 +86,37 @@ struct hs_device {
     int ordinal = 0;
     std::string name;
     hipStream_t stream = nullptr;
+    void *fixed_scratch = nullptr;  // this device's copy of `scratch` (below), a device address
 };
 
+// The scratch of hs_op_attend_decode_dev_noalloc: one array per GPU, loaded with the code
+// object and held until the process ends. In host code `scratch` names a host-side stand-in,
+// never the device memory: every use goes through the per-device address that
+// hipGetSymbolAddress gives at hs_device_open (fixed_scratch_of).
+constexpr size_t HS_FIXED_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[HS_FIXED_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_fixed_mu;
+std::vector<void *> g_fixed_scratch;  // by device ordinal
+
+// The device address of `scratch` on the current device `ordinal`, looked up once per device.
+hipError_t fixed_scratch_of(int ordinal, void **out) {
+    std::lock_guard<std::mutex> lock(g_fixed_mu);
+    if ((size_t)ordinal >= g_fixed_scratch.size()) g_fixed_scratch.resize((size_t)ordinal + 1, nullptr);
+    if (!g_fixed_scratch[ordinal]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_fixed_scratch[ordinal] = p;
+    }
+    *out = g_fixed_scratch[ordinal];
+    return hipSuccess;
+}
+
+}  // namespace
 
 namespace {
 
@@ -218,6 +248,7 @@ extern "C" hs_status hs_device_open(int ordinal, hs_device **out) {
     auto dev = std::make_unique<hs_device>();
     dev->ordinal = ordinal;
     dev->name = prop.name[0] ? std::string(prop.name) : "AMD " + arch;
+    HIP_TRY(fixed_scratch_of(ordinal, &dev->fixed_scratch));
     HIP_TRY(hipStreamCreate(&dev->stream));
     *out = dev.release();
     return HS_OK;
@@ -1280,6 +1311,47 @@ extern "C" hs_status hs_op_attend_decode_dev(hs_device *dev, const int8_t *q, co
         return HS_OK;
     }
     HIP_TRY(hs::launch_attend(at, (int)b, st));
+    return HS_OK;
+}
+
+// hs_op_attend_decode_dev without allocation: the split launches take their partials in this
+// device's fixed scratch array instead of hipMallocAsync memory. Calls that overlap on one GPU
+// share that array and race; every part a launch reads is written earlier in the same call, so
+// nothing has to be cleared between calls.
+extern "C" hs_status hs_op_attend_decode_dev_noalloc(hs_device *dev, const int8_t *q,
+                                                     const int8_t *k_cache, const int8_t *v_cache,
+                                                     const uint32_t *ctx, size_t b, size_t h,
+                                                     size_t hd, size_t ctx_cap, int32_t score_m,
+                                                     uint8_t score_s, int32_t out_m, uint8_t out_s,
+                                                     const int32_t *attn_exp, size_t len,
+                                                     uint8_t softmax_p, int8_t *out, void *stream) {
+    hs::clear_error();
+    if (!dev || !q || !k_cache || !v_cache || !ctx || !attn_exp || !out)
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (hd == 0 || hd % 4 != 0 || hd > 256 || h == 0 || len == 0 || softmax_p > 30 || ctx_cap == 0)
+        return hs::fail(HS_UNSUPPORTED, 0, "head_dim must be a multiple of 4 in 4..=256; h, len and ctx_cap >= 1; P <= 30");
+    if (b == 0) return HS_OK;
+    if (b * h > (size_t)INT32_MAX || ctx_cap > (size_t)INT32_MAX)
+        return hs::fail(HS_UNSUPPORTED, 0, "too many rows or keys");
+    hs::AttnArgs at;
+    at.rows = nullptr; at.keys = ctx; at.q = q; at.ldq = (int)(h * hd); at.kc = k_cache; at.vc = v_cache;
+    at.n_head = (int)h; at.hd = (int)hd; at.ctx_cap = (int)ctx_cap; at.score_m = score_m;
+    at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
+    at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
+    hipStream_t st = stream ? (hipStream_t)stream : dev->stream;
+    if (!hs::attend_split_ok((int)hd)) {  // the row kernel uses no scratch
+        HIP_TRY(hipSetDevice(dev->ordinal));
+        HIP_TRY(hs::launch_attend(at, (int)b, st));
+        return HS_OK;
+    }
+    const hs::SplitPlan plan = hs::attend_split_plan((int)b, (int)h, (int)ctx_cap);
+    const size_t bytes = hs::attend_split_bytes(at, (int)b, plan);
+    if (bytes > HS_FIXED_SCRATCH_BYTES)
+        return hs::fail(HS_UNSUPPORTED, 0, "the split attention needs " + std::to_string(bytes) +
+                                               " bytes of scratch; the fixed scratch holds " +
+                                               std::to_string(HS_FIXED_SCRATCH_BYTES));
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    HIP_TRY(hs::launch_attend_split(at, (int)b, plan, bytes ? dev->fixed_scratch : nullptr, st));
     return HS_OK;
 }
 

@@ -156,6 +156,7 @@ def lib() -> C.CDLL:
         L.hs_op_gemm_layout.restype = None
         L.hs_op_attend_decode_dev.argtypes = [P, P, P, P, P, S, S, S, S, C.c_int32, C.c_uint8,
                                               C.c_int32, C.c_uint8, P, S, C.c_uint8, P, P]
+        L.hs_op_attend_decode_dev_noalloc.argtypes = L.hs_op_attend_decode_dev.argtypes
         L.hs_device_alloc.argtypes = [P, S, C.POINTER(P)]
         L.hs_device_free.argtypes = [P, P]
         L.hs_device_upload.argtypes = [P, P, P, S]
