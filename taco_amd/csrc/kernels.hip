@@ -98,7 +98,108 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         mt = grp * G + in % gs;
     }
     const int m0 = mt * GEMM_BM, n0 = nt * BN;
-    const int K = g.k_pad, nk = K / GEMM_BK;
+    const int K = g.k_pad;
+
+    v4i acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    auto mfma_step = [&](const v4i *af, const v4i *bf) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
+                                 : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
+    if constexpr (BN == 256) {
+        // 256 x 256 tiles (8 waves, one workgroup per CU) stream stages of 128 k: each row's
+        // 128 bytes are one full cache line, eight lanes to a row (8 rows per instruction), which
+        // the memory path delivers at about 1.5 times the rate of the half lines of 64-k stages
+        // (measured). Row r's 16-byte chunk c sits at r * 128 + 16 (c ^ ((r >> 1) & 7)) of the
+        // stage, so the MFMA reads of 16 consecutive rows (one chunk) hit 16 distinct bank
+        // groups. Two stages of 64 KiB: the next stage loads while this one is multiplied.
+        // A k_pad that is an odd multiple of 64 ends with a half stage (chunks 0-3 only; the
+        // lanes of chunks 4-7 reload an in-row chunk that nothing reads).
+        constexpr int ROWS = GEMM_BM + BN, LD = ROWS / 8 / WAVES, SB = ROWS * 128;
+        const int nk2 = (K + 127) / 128;
+        const bool half = (K & 127) != 0;
+        // A wave's LD instructions all read one operand (waves 0-3 the A rows, 4-7 the W rows),
+        // rows 8 i + lane / 8 of its block; the chunk swizzle alternates with i, so two lane bases
+        // (even and odd i) and a uniform stride of 16 rows give every address.
+        static_assert(GEMM_BM / 8 % LD == 0, "a wave loads rows of one operand");
+        const int ld_r = lane >> 3, ld_s = lane & 7;
+        const int row0 = wave * LD * 8 + ld_r;  // the row of instruction 0 (row of i = row0 + 8 i)
+        const int c_even = ld_s ^ ((row0 >> 1) & 7), c_odd = c_even ^ 4;
+        const int8_t *base_row = row0 < GEMM_BM ? g.a + (size_t)(m0 + row0) * K
+                                                : g.w + (size_t)(n0 + row0 - GEMM_BM) * K;
+        const int8_t *p_even = base_row + c_even * 16, *p_odd = base_row + (size_t)8 * K + c_odd * 16;
+        const size_t stride16 = (size_t)16 * K;
+        // a half stage: the lanes whose chunk is 4-7 step back 64 bytes to an in-row chunk
+        const int h_even = c_even >= 4 ? -64 : 0, h_odd = c_odd >= 4 ? -64 : 0;
+        auto issue = [&](int kt, int stage) {
+            int8_t *base = gemm_lds + stage * SB + wave * LD * 1024;
+            const bool last_half = half && kt == nk2 - 1;
+            const int oe = kt * 128 + (last_half ? h_even : 0), oo = kt * 128 + (last_half ? h_odd : 0);
+#pragma unroll
+            for (int i = 0; i < LD; i++) {
+                const int8_t *p = (i & 1 ? p_odd + oo : p_even + oe) + (size_t)(i >> 1) * stride16;
+                __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + i * 1024), 16, 0, 0);
+            }
+        };
+        // lane l reads row l % 16 of each 16-row block (rows differ by multiples of 16, so the
+        // swizzle is the lane's) at chunk 4 h + l / 16 of the stage's k half h
+        const int rl = lane & 15, swz = (rl >> 1) & 7;
+        auto frag_ptr = [&](int stage, int h) {
+            return gemm_lds + stage * SB + rl * 128 + 16 * ((4 * h + (lane >> 4)) ^ swz);
+        };
+        auto read_a = [&](const int8_t *st, int i) { return *(const v4i *)(st + (wm * 128 + 16 * i) * 128); };
+        auto read_b = [&](const int8_t *st, int j) {
+            return *(const v4i *)(st + (GEMM_BM + wn * 64 + 16 * j) * 128);
+        };
+        issue(0, 0);
+        for (int kt = 0; kt < nk2; kt++) {
+            const int stage = kt & 1;
+            if (kt + 1 < nk2) {
+                // stage kt + 1 goes to the buffer read in step kt - 1 (free after its barrier)
+                issue(kt + 1, stage ^ 1);
+                wait_vmcnt<LD>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            asm volatile("s_barrier" ::: "memory");  // every wave's part of stage kt landed
+            const int8_t *s0 = frag_ptr(stage, 0), *s1 = frag_ptr(stage, 1);
+            v4i af[8], bf[4];
+#pragma unroll
+            for (int i = 0; i < 8; i++) af[i] = read_a(s0, i);
+#pragma unroll
+            for (int j = 0; j < 4; j++) bf[j] = read_b(s0, j);
+            // The second half's fragments load while the first half's MFMAs run: its W fragments
+            // first, then each A fragment into the registers of the one just used. A half stage
+            // multiplies its second half by zero W fragments (no branch around the MFMAs).
+            const bool zero_second = half && kt == nk2 - 1;
+            v4i bn[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const v4i b = read_b(s1, j);
+                bn[j] = zero_second ? v4i{0, 0, 0, 0} : b;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
+                                     : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                af[i] = read_a(s1, i);
+            }
+            mfma_step(af, bn);
+            // every wave finished reading this stage before step kt + 1 reloads it
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+    } else {
+    const int nk = K / GEMM_BK;
 
     // This wave loads fragments LOADS * wave .. +LOADS of each stage (0..15: A row blocks, then
     // the W row blocks, of 16 rows x 64 bytes). Each lane quad reads one row's 64
@@ -124,12 +225,6 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             __builtin_amdgcn_global_load_lds((const void *)(src[i] + kt * GEMM_BK),
                                              (lds_void *)(base + i * 1024), 16, 0, 0);
     };
-
-    v4i acc[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
     // The operand fragments of k-step kt + 1 are read from LDS while the MFMAs of k-step kt
     // run on registers read the step before. Of the three stages one is being read and two
@@ -169,16 +264,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         // compiler from sinking them into the next step (where they would wait at its barrier)
         read_frags(more ? kt + 1 : kt, an, bn);
         asm volatile("" ::: "memory");
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
-                                 : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        mfma_step(af, bf);
 #pragma unroll
         for (int i = 0; i < 8; i++) af[i] = an[i];
 #pragma unroll
         for (int j = 0; j < 4; j++) bf[j] = bn[j];
+    }
     }
 
     // Epilogue. Lane layout of each 16 x 16 tile (i, j) of the wave: with SWAP (the W fragment is
@@ -553,10 +644,13 @@ static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
     constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16;
     // the stages, and the epilogue's LDS: per-wave staging regions (18 KiB for the u16 logits
     // and the i16-plane epilogues, 10 KiB for i8 outputs), after the GELU table for Gelu
-    constexpr size_t stages = (size_t)GEMM_STAGES * FRAGS * 1024;
+    constexpr size_t stages = BN == 256 ? (size_t)2 * (GEMM_BM + BN) * 128 : (size_t)GEMM_STAGES * FRAGS * 1024;
     constexpr bool I8OUT = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
     constexpr size_t regions = (size_t)WAVES * (I8OUT ? 10240 : 18432);
-    constexpr size_t lds_max = (EPI == (int)Epi::Gelu ? 65536 : 0) + (stages > regions ? stages : regions);
+    // the largest request: the stages, or the 64 KiB GELU table and the staging regions after it
+    constexpr size_t after_table = (EPI == (int)Epi::Gelu ? 65536 : 0) + regions;
+    constexpr size_t lds_max = stages > after_table ? stages : after_table;
+    static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
     static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
     if (!ready) {
         hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC>,
@@ -575,10 +669,8 @@ static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
 }
 
 // 256 x 128 tiles (two workgroups per CU, so one's epilogue overlaps the other's main loop),
-// except for the i8 GELU epilogue of a wide product: each workgroup copies the 64 KiB table
-// into LDS, and 256 x 256 tiles halve those copies (measured: c_fc 5% faster; the other wide
-// products are slower with one workgroup per CU). Outputs whose rows are not 16-byte aligned
-// take the per-output store path.
+// or 256 x 256 (below). Outputs whose rows are not 16-byte aligned take the per-output store
+// path.
 template <int EPI, bool NARROW>
 static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
     constexpr bool WIDE = EPI == (int)Epi::ResidualWide || EPI == (int)Epi::LogitsWide ||
@@ -591,9 +683,13 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
                               : EPI == (int)Epi::Logits ? 8 : 1;
         const bool vec = ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0;
         if (!vec) return launch_gemm_t<EPI, NARROW, 128, false>(g, stream);
-        if constexpr (EPI == (int)Epi::Gelu) {
-            if (g.n > 1024) return launch_gemm_t<EPI, NARROW, 256, true>(g, stream);
-        }
+        // 256 x 256 tiles (one workgroup per CU, full-line 128-k stages) for long K, where their
+        // faster main loop outweighs the lost overlap of a second workgroup per CU and the
+        // coarser rounds (measured: GPT-2 small mlp.c_proj, K 3,072, 12% faster; c_attn and the
+        // LM head, K 768, 10% and 7% slower), and for the i8 GELU epilogue of a wide product
+        // (each workgroup copies the 64 KiB table into LDS; measured 4% faster)
+        if (g.n > 512 && (g.k_pad >= 2048 || (EPI == (int)Epi::Gelu && g.n > 1024)))
+            return launch_gemm_t<EPI, NARROW, 256, true>(g, stream);
         return launch_gemm_t<EPI, NARROW, 128, true>(g, stream);
     }
 }
