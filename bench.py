@@ -16,8 +16,10 @@ profiled steps, run right after the timed ones (events around every launch leave
 about 10 us between kernels, so the timed steps run without them).
 `cpu_baseline` is the oracle's C++ restatement of the reference CPU fast path (AVX2 products,
 prefill chunk 32, one window per thread) timed on a sample of the same windows in the same run,
-on up to 16 host threads and (`one_thread`) on one thread over the first window; its payloads
-must equal the GPU's.
+on every core the process may use within the GPU's CPU share (OMP_NUM_THREADS when set; the
+CPU model and core counts are recorded) and (`one_thread`) on one thread over the first window;
+its payloads must equal the GPU's. `sustained` is the same fold repeated for at least 3 s right
+after the timed steps.
 
 Other workloads (--workload) measure the other configurations of the path, each with its own
 line: the c_attn GEMM alone (gemm-qkv: M 256 and 16,384, K 768, N 2,304), decode attention over
@@ -168,6 +170,64 @@ def committed_traffic(workload, tokens_sha):
     return round(sum((v["fetch_bytes"] + v["write_bytes"]) * v["dispatches"] for v in g) / n)
 
 
+def mfma_summary(csv_path, tokens_sha, command):
+    """Per-kernel MFMA utilisation from one rocprofv3 --pmc run of SQ_INSTS_VALU_MFMA_MOPS_I8,
+    SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE and SQ_BUSY_CYCLES: MfmaUtil = busy cycles /
+    (GUI-active cycles of one XCD x 1,024 SIMDs), as rocprofv3's derived counter; int8 ops =
+    MOPS_I8 x 512 (the counter counts ops / 512)."""
+    import csv
+    import collections
+    per = collections.defaultdict(dict)
+    for r in csv.DictReader(open(csv_path)):
+        k = (int(r["Dispatch_Id"]), r["Kernel_Name"])
+        per[k][r["Counter_Name"]] = float(r["Counter_Value"])
+    agg = collections.defaultdict(lambda: collections.defaultdict(float))
+    for (_, name), c in per.items():
+        if not c.get("SQ_INSTS_VALU_MFMA_MOPS_I8"):
+            continue
+        a = agg[name.split("(")[0].replace("void ", "")]
+        a["dispatches"] += 1
+        for kk, v in c.items():
+            a[kk] += v
+    kernels, tot_busy, tot_gui, tot_ops = {}, 0.0, 0.0, 0.0
+    for name, a in sorted(agg.items()):
+        gui1 = a["GRBM_GUI_ACTIVE"] / 8  # GRBM_GUI_ACTIVE summed over the 8 XCDs
+        kernels[name] = {"dispatches": int(a["dispatches"]),
+                         "mfma_util": round(a["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui1 * 1024), 4),
+                         "int8_ops_per_dispatch": int(a["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512 / a["dispatches"]),
+                         "gui_cycles_per_dispatch": int(gui1 / a["dispatches"])}
+        if name.startswith("hs::k_gemm"):
+            tot_busy += a["SQ_VALU_MFMA_BUSY_CYCLES"]
+            tot_gui += gui1 * 1024
+            tot_ops += a["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
+    return {"tokens_sha256": tokens_sha, "command": command,
+            "gemm_mfma_util": round(tot_busy / tot_gui, 4) if tot_gui else None,
+            "gemm_int8_ops": int(tot_ops), "kernels": kernels}
+
+
+def committed_mfma(workload, tokens_sha):
+    """The GEMM MFMA utilisation of the committed counter summary of this workload, or None."""
+    path = os.path.join(HERE, "profiles", workload.replace("-", "_") + "_mfma.json")
+    if not os.path.exists(path):
+        return None
+    j = json.load(open(path))
+    return j["gemm_mfma_util"] if j.get("tokens_sha256") == tokens_sha else None
+
+
+def host_cpu():
+    """The host's CPU model, online cores and the cores this process may run on."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0))}
+
+
 def read_profile(hip, batch):
     cap = 32
     labels = C.create_string_buffer(32 * cap)
@@ -235,6 +295,24 @@ def run_fold(args):
         payloads, cont = step()
     elapsed = time.perf_counter() - ts
     timed_phase = dict(phase)
+    # Sustained: fold steps for at least args.sustain_s seconds right after the timed ones (the
+    # timed region is short enough to end before the clocks settle under a sustained MFMA load).
+    sustained = None
+    if args.sustain_s > 0:
+        ss, ts2 = 0, time.perf_counter()
+        while True:
+            spay, scont = step()
+            ss += 1
+            if time.perf_counter() - ts2 >= args.sustain_s:
+                break
+        s_el = time.perf_counter() - ts2
+        if scont != cont:
+            log("PARITY FAILURE: the sustained steps gave another container")
+            sys.exit(1)
+        sustained = {"seconds": round(s_el, 3), "steps": ss,
+                     "tokens_per_s": round(W * n * ss / s_el, 1),
+                     "ms_per_step": round(1e3 * s_el / ss, 3)}
+        log(f"sustained: {ss} steps in {s_el:.2f}s -> {W * n * ss / s_el:.0f} tokens/s")
     psteps = max(1, args.steps)
     hip._check(hip.lib().hs_batch_set_profiling(batch.h, 1))
     hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
@@ -299,7 +377,11 @@ def run_fold(args):
     cpu = None
     if not args.no_cpu:
         from oracle import oracle as O
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # every core this process may run on, within the GPU's CPU share when the environment
+        # states one (OMP_NUM_THREADS)
+        host = host_cpu()
+        share = int(os.environ.get("OMP_NUM_THREADS") or host["affinity"])
+        threads = args.cpu_threads or max(1, min(host["affinity"], share))
         cw = min(args.cpu_windows or cpu_per_thread * threads, W)
         om = O.Model(model_bytes)
         ts = time.perf_counter()
@@ -321,7 +403,7 @@ def run_fold(args):
             log("PARITY FAILURE: the one-thread CPU payload differs")
             sys.exit(1)
         cpu = {"value": round(cw * n / cpu_s, 2), "unit": "tokens/s", "cores": threads,
-               "kind": "port",
+               "kind": "port", "host": dict(host, cpu_share=share),
                "sample": f"the first {cw} of the {W} windows ({cw * n} tokens), {cpu_per_thread} "
                          f"window(s) per thread, AVX2 restatement of the reference CPU fast path, "
                          f"chunk 32",
@@ -356,12 +438,17 @@ def run_fold(args):
                      "traffic": committed_traffic(args.workload, synth.sha256_tokens(tokens)),
                      "traffic_unit": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated; "
                                      "profiles/" + args.workload.replace("-", "_") + "_traffic.json)",
+                     "mfma_util": committed_mfma(args.workload, synth.sha256_tokens(tokens)),
+                     "mfma_util_source": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1,024 "
+                                         "SIMDs) over the GEMM dispatches; profiles/" +
+                                         args.workload.replace("-", "_") + "_mfma.json",
                      "launches": gemm_launches,
                      "ops_per_launch": gemm_ops // max(1, gemm_launches),
                      "avg_launch_us": round(gemm_ns / max(1, gemm_launches) / 1e3, 2)},
         "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / psteps, 3) for kk, v in prof.items()},
         "profiled_steps": {"steps": psteps, "ms_per_step": round(1e3 * profiled_s / psteps, 3),
                            "kernel_ms_per_step": round(gpu_ms, 3)},
+        "sustained": sustained,
         "cpu_baseline": cpu,
     }
     if unfold:
@@ -499,6 +586,9 @@ def run_attend(args):
         for p in (dq, dctx, dout):
             hip.lib().hs_device_free(dev.h, p)
     hip.lib().hs_device_free(dev.h, dtab)
+    # the stream-read probe (read_gpu_ns, ops.rs:328-335): 2 GiB, well beyond the Infinity Cache
+    stream = hip.read_bw(dev, 2 << 30, 10) / 1e9
+    log(f"stream read: {stream:.0f} GB/s")
     big = rows[-1]
     print(json.dumps({
         "metric": "integer decode attention over an HBM KV cache on 1 MI355X (64 x 12 x 64)",
@@ -511,6 +601,8 @@ def run_attend(args):
         "roofline": {"bound": "hbm", "kernel": "k_attend_decode64", "achieved": big["gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(big["gbs"] / HBM_PEAK_GBS, 4),
+                     "stream_read_gbs": round(stream, 1),
+                     "frac_of_stream_read": round(big["gbs"] / stream, 4),
                      "traffic": committed_attend_traffic(big["ctx"]),
                      "traffic_unit": "HBM bytes per launch at the largest context (FETCH_SIZE + "
                                      "WRITE_SIZE, calibrated; profiles/attend_decode_traffic.json)"},
@@ -537,9 +629,24 @@ def main_traffic(argv):
     print(json.dumps(traffic_summary(fetch_csv, write_csv, int(calib), tokens_sha, cmd), indent=1))
 
 
+def main_mfma(argv):
+    """python bench.py --mfma-summary COUNTERS.csv WORKLOAD: the MFMA summary of one rocprofv3
+    --pmc run of `bench.py --workload WORKLOAD --steps 1 --warmup 0 --no-cpu --sustain-s 0`."""
+    from taco_amd import synth
+    csv_path, workload = argv
+    dims_name, W, n, _ = FOLDS[workload]
+    tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
+    cmd = ("rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE "
+           "SQ_BUSY_CYCLES --output-format csv -- python3 bench.py --workload " + workload +
+           " --steps 1 --warmup 0 --no-cpu --no-unfold --sustain-s 0")
+    print(json.dumps(mfma_summary(csv_path, tokens_sha, cmd), indent=1))
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--traffic-summary":
         return main_traffic(sys.argv[2:])
+    if len(sys.argv) > 1 and sys.argv[1] == "--mfma-summary":
+        return main_mfma(sys.argv[2:])
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
@@ -552,6 +659,8 @@ def main():
                     help="windows in the CPU-baseline sample (0: the workload's default)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sustain-s", type=float, default=3.0,
+                    help="seconds of fold steps after the timed ones for the sustained figure")
     ap.add_argument("--no-unfold", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (the known-size copy that "

@@ -273,6 +273,11 @@ hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8
                                      const int32_t *attn_exp, size_t len, uint8_t softmax_p,
                                      int8_t *out, size_t reps, uint64_t *ns);
 
+/* The GPU time of `reps` reads of a device buffer of `bytes` bytes (a multiple of 16) by a
+ * streaming kernel (hipEvents on the device stream): the HBM read bandwidth a kernel reaches,
+ * as read_gpu_ns (crates/hardshell-cuda/src/ops.rs:328-335). */
+hs_status hs_read_bw(hs_device *dev, size_t bytes, size_t reps, uint64_t *ns);
+
 /* ---- Batch profiling: CudaBatch::profile (crates/hardshell-cuda/src/batch.rs:493-498) ----- */
 /* With profiling on, every kernel launch of the batch is bracketed by hipEvents on the batch's
  * stream; hs_batch_profile gives, for each op label, the summed GPU nanoseconds, the launch

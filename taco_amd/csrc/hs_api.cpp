@@ -1438,6 +1438,29 @@ extern "C" hs_status hs_op_gemm_requant_gpu_ns(hs_device *dev, const int8_t *w, 
     return time_reps(dev, reps, ns, [&] { return hs::launch_gemm(Epi::Act, g, dev->stream); });
 }
 
+extern "C" hs_status hs_read_bw(hs_device *dev, size_t bytes, size_t reps, uint64_t *ns) {
+    hs::clear_error();
+    if (!dev || !ns) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (bytes == 0 || bytes % 16 != 0) return hs::fail(HS_UNSUPPORTED, 0, "bytes must be a positive multiple of 16");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    void *buf = nullptr;
+    int *sink = nullptr;
+    HIP_TRY(hipMalloc(&buf, bytes));
+    hipError_t e = hipMalloc((void **)&sink, (size_t)hs::READ_BW_GRID * 256 * sizeof(int));
+    if (e == hipSuccess) e = hipMemsetAsync(buf, 0x5A, bytes, dev->stream);  // a defined buffer
+    hs_status st = e == hipSuccess ? HS_OK : hip_fail("read probe buffers", e);
+    if (st == HS_OK) {  // one untimed read first (page mappings, clocks)
+        e = hs::launch_read_bw(buf, bytes / 16, sink, hs::READ_BW_GRID, dev->stream);
+        if (e != hipSuccess) st = hip_fail("read probe", e);
+    }
+    if (st == HS_OK)
+        st = time_reps(dev, reps, ns, [&] { return hs::launch_read_bw(buf, bytes / 16, sink, hs::READ_BW_GRID, dev->stream); });
+    (void)hipStreamSynchronize(dev->stream);
+    if (sink) (void)hipFree(sink);
+    (void)hipFree(buf);
+    return st;
+}
+
 extern "C" hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8_t *k_cache,
                                                 const int8_t *v_cache, const uint32_t *ctx, size_t b,
                                                 size_t h, size_t hd, size_t ctx_cap, int32_t score_m,

@@ -92,6 +92,11 @@ struct LnArgs {
 };
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream);
 
+// The stream-read probe: every 16-byte word of buf[0 .. n16) read once (one xor per word folded
+// into sink[grid x 256] so the loads are kept).
+hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipStream_t stream);
+constexpr int READ_BW_GRID = 2048;  // 8 workgroups of 256 threads per CU
+
 // K and V of each row into the caches [L][slots][H][n_ctx][hd] (layer base pointers given).
 hipError_t launch_kv_store(const RowInfo *rows, int n_rows, const int8_t *qkv, int d, int n_head,
                            int hd, int n_ctx, int8_t *kc, int8_t *vc, hipStream_t stream);

@@ -728,6 +728,31 @@ hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
 }
 
 // =============================================================================================
+// Stream read (the probe of crates/hardshell-cuda/src/ops.rs:328-335, read_gpu_ns): each thread
+// keeps 8 16-byte loads in flight per round and folds them with xor.
+// =============================================================================================
+
+__global__ __launch_bounds__(256) void k_read_bw(const v4i *p, size_t n16, int *sink) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    v4i acc = {0, 0, 0, 0};
+    for (; i + 7 * stride < n16; i += 8 * stride) {
+        v4i v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= v[u];
+    }
+    for (; i < n16; i += stride) acc ^= p[i];
+    sink[(size_t)blockIdx.x * 256 + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
+hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipStream_t stream) {
+    hipLaunchKernelGGL(k_read_bw, dim3(grid), dim3(256), 0, stream, (const v4i *)buf, n16, sink);
+    return hipGetLastError();
+}
+
+// =============================================================================================
 // Embedding (reference.rs:208-221): x = clamp(rescale(wte[tok]) + rescale(wpe[pos]), -R, R).
 // =============================================================================================
 

@@ -157,6 +157,7 @@ def lib() -> C.CDLL:
         L.hs_op_attend_decode_dev.argtypes = [P, P, P, P, P, S, S, S, S, C.c_int32, C.c_uint8,
                                               C.c_int32, C.c_uint8, P, S, C.c_uint8, P, P]
         L.hs_op_attend_decode_dev_noalloc.argtypes = L.hs_op_attend_decode_dev.argtypes
+        L.hs_read_bw.argtypes = [P, S, S, C.POINTER(C.c_uint64)]
         L.hs_device_alloc.argtypes = [P, S, C.POINTER(P)]
         L.hs_device_free.argtypes = [P, P]
         L.hs_device_upload.argtypes = [P, P, P, S]
@@ -439,6 +440,14 @@ def gemm_requant_i8(dev: HipDevice, w, a, bias, mult, shift: int) -> np.ndarray:
     _check(lib().hs_op_gemm_requant_i8(dev.h, _ptr(w), _ptr(a), _ptr(bias), _ptr(mult), shift,
                                        m, n, k, _ptr(out)))
     return out
+
+
+def read_bw(dev: HipDevice, nbytes: int, reps: int) -> float:
+    """read_gpu_ns (crates/hardshell-cuda/src/ops.rs:328-335) as bytes per second: a streaming
+    kernel reads a device buffer of nbytes, reps times."""
+    ns = C.c_uint64()
+    _check(lib().hs_read_bw(dev.h, nbytes, reps, C.byref(ns)))
+    return nbytes * reps / (ns.value * 1e-9)
 
 
 def gemm_layout(m: int, n: int, k: int) -> Tuple[int, int, int]:

@@ -456,3 +456,15 @@ def test_head_dim_64_long_contexts_equal_the_reference(dev, overlap):
     for i, blk in enumerate(blocks):
         print(f"block {i} ({len(blk)} tokens, K {overlap})", flush=True)
         assert got[i] == O.encode_block(om, blk, overlap=overlap), i
+
+
+def test_read_bw_probe(dev):
+    """hs_read_bw (read_gpu_ns, crates/hardshell-cuda/src/ops.rs:328-335): a streaming read of
+    256 MiB runs at a plausible HBM rate, and a size that is not a multiple of 16 is refused."""
+    import ctypes as C
+    from taco_amd import hip
+    gbs = hip.read_bw(dev, 256 << 20, 5) / 1e9
+    print(f"stream read {gbs:.0f} GB/s", flush=True)
+    assert 500 < gbs < 20000
+    ns = C.c_uint64()
+    assert hip.lib().hs_read_bw(dev.h, 1000, 1, C.byref(ns)) == hip.HS_UNSUPPORTED
