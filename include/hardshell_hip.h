@@ -211,6 +211,18 @@ hs_status hs_op_mixed_coder_logits(hs_device *dev, const int64_t *logits, size_t
  * values as hardshell::kernels::matvec_i8 (ops.rs:142-161 matmul_i8). */
 hs_status hs_op_gemm_i8(hs_device *dev, const int8_t *w, const int8_t *a, size_t m, size_t n,
                         size_t k, int32_t *out);
+/* As hs_op_gemm_i8 with the K dimension cut into `splits` slices (1..=16; a slice holds at
+ * least 64 of K, so fewer slices run when K is short) whose exact i32 partial products are
+ * summed on the GPU (ops.rs:163-184 matmul_i8_split). The forward pass uses the same split for
+ * decode-shaped products (at most 512 rows). */
+hs_status hs_op_gemm_i8_split(hs_device *dev, const int8_t *w, const int8_t *a, size_t m, size_t n,
+                              size_t k, uint32_t splits, int32_t *out);
+/* out[i * n + r] = w[r] . a[i] for i16 activations a [m, k] (host pointers), exact i64: the two
+ * i8 planes of each row (hi = v >> 8, lo = (v & 255) - 128), one i8 product of 2m rows in
+ * `splits` slices (1..=16), and 256 hi + lo + 128 sum(w[r]) per output, the result of
+ * hardshell::kernels::matvec_i8_i16 (ops.rs:220-282 matmul_i8_i16). */
+hs_status hs_op_gemm_i8_i16(hs_device *dev, const int8_t *w, const int16_t *a, size_t m, size_t n,
+                            size_t k, uint32_t splits, int64_t *out);
 /* The c_attn linear of the forward pass (gpt2/ops.rs:123-130): out[i * n + r] =
  * clamp(rescale(w[r] . a[i] + bias[r], mult[r], shift), -127, 127) as i8 (host pointers). */
 hs_status hs_op_gemm_requant_i8(hs_device *dev, const int8_t *w, const int8_t *a,

@@ -471,6 +471,8 @@ struct hs_batch {
     bool inflight = false;  // a pass returned with copies or kernels still queued on `st`
     void *split = nullptr;  // scratch of the split decode attention (grown on demand)
     size_t split_bytes = 0;
+    int32_t *gsplit = nullptr;  // i32 partials of the split-K decode products (grown on demand)
+    size_t gsplit_elems = 0;
     int8_t *d_a = nullptr, *d_qkv = nullptr, *d_att = nullptr, *d_g = nullptr, *d_af = nullptr;
     int64_t *d_logits = nullptr;
     uint16_t *d_d16 = nullptr;
@@ -504,6 +506,7 @@ struct hs_batch {
                         (void *)h_mix, (void *)h_stats, (void *)h_intervals2})
             if (p) (void)hipHostFree(p);
         if (split) (void)hipFree(split);
+        if (gsplit) (void)hipFree(gsplit);
         if (st) (void)hipStreamDestroy(st);
     }
     hipError_t event(hipEvent_t &e) {
@@ -842,10 +845,36 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
         g.fast32 = epi == Epi::ResidualWide ? 0 : lin.fast32;
         g.gelu = gelu; g.gelu16 = gelu16; g.gelu_off = gelu_off; g.wsum = lin.wsum;
+        g.partials = b.gsplit; g.partials_cap = b.gsplit_elems;
         const uint64_t ops = 2ull * (uint64_t)rows_n * (uint64_t)lin.n * (uint64_t)lin.k;
         return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
     };
     const bool kv_fused = m.hd % 16 == 0 && m.d % 16 == 0;
+    // Decode-shaped passes (at most two 256-row tiles): the layer products split K where the
+    // launcher's plan says so; their partials need a scratch, grown here before any launch.
+    if (n <= 2 * hs::GEMM_BM) {
+        size_t need = 0;
+        auto want = [&](Epi e, const DevLinear &lin) {
+            const int sp = hs::gemm_split_plan(e, n, lin.n, lin.k_pad, 0);
+            if (sp > 1) need = std::max(need, hs::gemm_split_elems(n, lin.n, sp));
+        };
+        for (const DevBlock &blk : m.blocks) {
+            want(Epi::Act, blk.c_attn);
+            want(Epi::Residual, blk.c_proj);
+            want(blk.gelu16 ? Epi::GeluWide : Epi::Gelu, blk.c_fc);
+            if (!blk.gelu16) want(Epi::Residual, blk.mlp_proj);
+        }
+        if (need > b.gsplit_elems) {
+            if (b.gsplit) {
+                HIP_TRY(hipStreamSynchronize(st));
+                HIP_TRY(hipFree(b.gsplit));
+                b.gsplit = nullptr;
+                b.gsplit_elems = 0;
+            }
+            HIP_TRY(hipMalloc((void **)&b.gsplit, need * sizeof(int32_t)));
+            b.gsplit_elems = need;
+        }
+    }
     // Decode-shaped passes (short runs): attention split over key chunks when the scratch fits
     // (at most 1 GiB), else the row kernel.
     bool split_attn = false;
@@ -881,6 +910,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             g.ldo = 3 * m.d; g.fast32 = blk.c_attn.fast32;
             g.kv_rows = b.d_rows; g.kc = b.kc[l]; g.vc = b.vc[l];
             g.kv_d = m.d; g.kv_hd = m.hd; g.kv_h = m.H; g.kv_ctx = m.C;
+            g.partials = b.gsplit; g.partials_cap = b.gsplit_elems;
             const uint64_t ops = 2ull * (uint64_t)n * (uint64_t)blk.c_attn.n * (uint64_t)blk.c_attn.k;
             HIP_TRY(b.launch("gemm_qkv", ops, [&] { return hs::launch_gemm(Epi::Act, g, st); }));
         } else {
@@ -1210,8 +1240,11 @@ extern "C" void hs_op_gemm_layout(size_t m, size_t n, size_t k, size_t *m_pad, s
 
 namespace {
 
+// `splits`: 0 lets the launcher choose the K slices (as the forward pass does), 1 runs one
+// workgroup per tile over all of K, 2..16 forces that many slices.
 hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, const int32_t *bias,
-                    const int32_t *mult, uint8_t shift, size_t m, size_t n, size_t k, void *out) {
+                    const int32_t *mult, uint8_t shift, size_t m, size_t n, size_t k, void *out,
+                    int splits = 0) {
     hs::clear_error();
     if (!dev || !w || !a || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
     if (m == 0 || n == 0 || k == 0) return HS_OK;
@@ -1240,6 +1273,12 @@ hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, c
     g.a = da; g.w = dw; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
     g.bias = db; g.mult = dm; g.shift = shift; g.out = dout; g.ldo = (int)n;
     g.fast32 = fits_i32(k, bias, bias ? n : 0);
+    g.splits = splits;
+    const int sp = hs::gemm_split_plan(epi, (int)m, (int)n, (int)kp, splits);
+    if (sp > 1) {
+        g.partials_cap = hs::gemm_split_elems((int)m, (int)n, sp);
+        if ((s = mem.alloc(g.partials, g.partials_cap)) != HS_OK) return s;
+    }
     HIP_TRY(hs::launch_gemm(epi, g, dev->stream));
     HIP_TRY(hipMemcpyAsync(out, dout, m * n * esz, hipMemcpyDeviceToHost, dev->stream));
     HIP_TRY(hipStreamSynchronize(dev->stream));
@@ -1251,6 +1290,63 @@ hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, c
 extern "C" hs_status hs_op_gemm_i8(hs_device *dev, const int8_t *w, const int8_t *a, size_t m, size_t n,
                                    size_t k, int32_t *out) {
     return gemm_host(dev, Epi::Raw, w, a, nullptr, nullptr, 0, m, n, k, out);
+}
+
+extern "C" hs_status hs_op_gemm_i8_split(hs_device *dev, const int8_t *w, const int8_t *a, size_t m,
+                                         size_t n, size_t k, uint32_t splits, int32_t *out) {
+    hs::clear_error();
+    if (splits == 0 || splits > 16) return hs::fail(HS_UNSUPPORTED, 0, "splits must be in 1..=16");
+    return gemm_host(dev, Epi::Raw, w, a, nullptr, nullptr, 0, m, n, k, out, (int)splits);
+}
+
+extern "C" hs_status hs_op_gemm_i8_i16(hs_device *dev, const int8_t *w, const int16_t *a, size_t m,
+                                       size_t n, size_t k, uint32_t splits, int64_t *out) {
+    hs::clear_error();
+    if (!dev || !w || !a || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (splits == 0 || splits > 16) return hs::fail(HS_UNSUPPORTED, 0, "splits must be in 1..=16");
+    if (m == 0 || n == 0 || k == 0) return HS_OK;
+    if (k > 65536) return hs::fail(HS_MODEL_ERROR, HS_MODEL_DOT_TOO_LONG, "a dot product is longer than 2^16");
+    if (m > (1u << 29) || n > (1u << 30)) return hs::fail(HS_UNSUPPORTED, 0, "the product is too large");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    // the i16 rows as two i8 plane rows (hi = v >> 8, lo = (v & 255) - 128), one i8 product of
+    // 2m rows, then 256 hi + lo + 128 wsum per output
+    size_t mp, np, kp;
+    hs_op_gemm_layout(2 * m, n, k, &mp, &np, &kp);
+    std::vector<int8_t> wp(np * kp, 0), ap(mp * kp, 0);
+    std::vector<int32_t> wsum(n, 0);
+    for (size_t r = 0; r < n; r++) {
+        std::memcpy(&wp[r * kp], w + r * k, k);
+        for (size_t j = 0; j < k; j++) wsum[r] += w[r * k + j];
+    }
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < k; j++) {
+            const int32_t v = a[i * k + j];
+            ap[(2 * i) * kp + j] = (int8_t)(v >> 8);
+            ap[(2 * i + 1) * kp + j] = (int8_t)((v & 255) - 128);
+        }
+    DevMem mem;
+    int8_t *dw, *da;
+    int32_t *dsum, *planes;
+    int64_t *dout;
+    hs_status s;
+    if ((s = mem.upload(dw, wp.data(), wp.size())) != HS_OK) return s;
+    if ((s = mem.upload(da, ap.data(), ap.size())) != HS_OK) return s;
+    if ((s = mem.upload(dsum, wsum.data(), n)) != HS_OK) return s;
+    if ((s = mem.alloc(planes, 2 * m * n)) != HS_OK) return s;
+    if ((s = mem.alloc(dout, m * n)) != HS_OK) return s;
+    hs::GemmArgs g;
+    g.a = da; g.w = dw; g.m = (int)(2 * m); g.n = (int)n; g.k_pad = (int)kp;
+    g.out = planes; g.ldo = (int)n; g.splits = (int)splits;
+    const int sp = hs::gemm_split_plan(Epi::Raw, g.m, g.n, g.k_pad, g.splits);
+    if (sp > 1) {
+        g.partials_cap = hs::gemm_split_elems(g.m, g.n, sp);
+        if ((s = mem.alloc(g.partials, g.partials_cap)) != HS_OK) return s;
+    }
+    HIP_TRY(hs::launch_gemm(Epi::Raw, g, dev->stream));
+    HIP_TRY(hs::launch_wide_combine(planes, dsum, (int)m, (int)n, dout, dev->stream));
+    HIP_TRY(hipMemcpyAsync(out, dout, m * n * sizeof(int64_t), hipMemcpyDeviceToHost, dev->stream));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    return HS_OK;
 }
 
 extern "C" hs_status hs_op_gemm_requant_i8(hs_device *dev, const int8_t *w, const int8_t *a,
@@ -1272,7 +1368,20 @@ extern "C" hs_status hs_op_gemm_requant_i8_dev(hs_device *dev, const int8_t *w, 
     hs::GemmArgs g;
     g.a = a; g.w = w; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
     g.bias = bias; g.mult = mult; g.shift = shift; g.out = out; g.ldo = (int)n;
-    HIP_TRY(hs::launch_gemm(Epi::Act, g, stream ? (hipStream_t)stream : dev->stream));
+    hipStream_t st = stream ? (hipStream_t)stream : dev->stream;
+    const int sp = hs::gemm_split_plan(Epi::Act, (int)m, (int)n, (int)kp, 0);
+    if (sp > 1) {  // the split-K partials in stream-ordered memory
+        g.partials_cap = hs::gemm_split_elems((int)m, (int)n, sp);
+        void *p = nullptr;
+        HIP_TRY(hipMallocAsync(&p, g.partials_cap * sizeof(int32_t), st));
+        g.partials = (int32_t *)p;
+        const hipError_t e = hs::launch_gemm(Epi::Act, g, st);
+        const hipError_t f = hipFreeAsync(p, st);
+        HIP_TRY(e);
+        HIP_TRY(f);
+        return HS_OK;
+    }
+    HIP_TRY(hs::launch_gemm(Epi::Act, g, st));
     return HS_OK;
 }
 
@@ -1435,6 +1544,15 @@ extern "C" hs_status hs_op_gemm_requant_gpu_ns(hs_device *dev, const int8_t *w, 
     g.a = a; g.w = w; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
     g.bias = bias; g.mult = mult; g.shift = shift; g.out = out; g.ldo = (int)n;
     g.fast32 = fits_i32(k, hb.data(), n);
+    // the split-K scratch of decode-shaped products, as the forward pass has it (outside the
+    // timed launches)
+    const int sp = hs::gemm_split_plan(Epi::Act, (int)m, (int)n, (int)kp, 0);
+    DevMem mem;
+    if (sp > 1) {
+        g.partials_cap = hs::gemm_split_elems((int)m, (int)n, sp);
+        hs_status s = mem.alloc(g.partials, g.partials_cap);
+        if (s != HS_OK) return s;
+    }
     return time_reps(dev, reps, ns, [&] { return hs::launch_gemm(Epi::Act, g, dev->stream); });
 }
 

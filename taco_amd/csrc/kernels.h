@@ -53,6 +53,14 @@ struct GemmArgs {
     const struct RowInfo *kv_rows = nullptr;
     int8_t *kc = nullptr, *vc = nullptr;
     int kv_d = 0, kv_hd = 0, kv_h = 0, kv_ctx = 0;
+    // Split-K (decode-shaped products: one or two M-tiles, few N tiles): when `partials` is set
+    // and the shape gains from it, the workgroups of a tile take slices of K and write exact i32
+    // partials, and an elementwise pass sums them and applies the epilogue. partials_cap is the
+    // scratch size in i32 elements (gemm_split_elems of the chosen split must fit).
+    int32_t *partials = nullptr;
+    size_t partials_cap = 0;
+    int splits = 0;  // 0: chosen by gemm_split_plan; 1: no split; 2..16: that many slices
+    int kslice = 0;  // set by the launcher: bytes of K per slice (a multiple of GEMM_BK)
 };
 
 
@@ -67,6 +75,14 @@ inline int gemm_group(int m) {
 }
 
 hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream);
+
+// The split-K plan of a product: the number of K slices (1 = no split) for m rows, n columns and
+// k_pad bytes of K with the given epilogue, and the i32 partial elements it needs.
+int gemm_split_plan(Epi epi, int m, int n, int k_pad, int splits_wanted);
+size_t gemm_split_elems(int m, int n, int splits);
+// out[i][r] = 256 planes[2i][r] + planes[2i + 1][r] + 128 wsum[r] (i64), planes [2m, n] i32.
+hipError_t launch_wide_combine(const int32_t *planes, const int32_t *wsum, int m, int n, int64_t *out,
+                               hipStream_t stream);
 
 hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_ld,
                         const int8_t *wpe, const int32_t *embed_m, int embed_s,

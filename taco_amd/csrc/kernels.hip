@@ -199,7 +199,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
     } else {
-    const int nk = K / GEMM_BK;
+    // Split-K: workgroup row blockIdx.y takes K bytes [kb0, kb0 + kslice) of a product whose
+    // partials go to out + blockIdx.y * m * ldo (Raw only).
+    const int kb0 = (int)blockIdx.y * g.kslice;
+    const int nk = (g.kslice ? min(g.kslice, K - kb0) : K) / GEMM_BK;
 
     // This wave loads fragments LOADS * wave .. +LOADS of each stage (0..15: A row blocks, then
     // the W row blocks, of 16 rows x 64 bytes). Each lane quad reads one row's 64
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         const int f = wave * LOADS + i;
         const int r = lane >> 2, c = (lane & 3) ^ sw(r);
         const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + r;
-        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) + c * 16;
+        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) + kb0 + c * 16;
     }
     const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ sw(lane & 15));
     auto issue = [&](int kt, int stage) {
@@ -397,7 +400,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                     const int m = rw + 16 * i + rl, n4 = cw + 16 * j + 4 * cg;
                     if (m >= g.m || n4 >= g.n) continue;
                     if (EPI == (int)Epi::Raw) {
-                        int32_t *o = (int32_t *)g.out + (size_t)m * g.ldo + n4;
+                        int32_t *o = (int32_t *)g.out + ((size_t)blockIdx.y * g.m + m) * g.ldo + n4;
                         if (vec && n4 + 4 <= g.n) *(v4i *)o = acc[i][j];
                         else
 #pragma unroll
@@ -701,13 +704,194 @@ static hipError_t launch_gemm_e(const GemmArgs &g, hipStream_t stream) {
     return launch_gemm_w<EPI, false>(g, stream);
 }
 
+// ---- Split-K for decode-shaped products ------------------------------------------------------
+// A pass of at most 512 rows has one or two 256-row M-tiles, so an N-tiled product launches
+// N / 128 workgroups, each walking all of K: a few dozen of the 256 CUs, each bound by the latency
+// of its k-steps (GPT-2 medium's mlp.c_proj: 8 workgroups x 64 k-steps). Here 64-column tiles
+// take slices of K (2 to 16 workgroups per tile), write exact i32 partials (|each| <= 2^30, and
+// i32 sums of them are exact in any order), and k_split_epi sums a tile's slices per output and
+// applies the epilogue's rule to the total: the epilogue is not linear, so it runs once, on the
+// exact product.
+
+constexpr int SPLIT_BN = 64;
+
+size_t gemm_split_elems(int m, int n, int splits) {
+    return (size_t)splits * (size_t)m * (size_t)((n + 3) & ~3);
+}
+
+int gemm_split_plan(Epi epi, int m, int n, int k_pad, int wanted) {
+    const bool ok = epi == Epi::Raw || epi == Epi::Act || epi == Epi::Residual || epi == Epi::Gelu ||
+                    epi == Epi::GeluWide;
+    if (!ok || m <= 0 || n <= 0 || k_pad < 2 * GEMM_BK) return 1;
+    const int nks = k_pad / GEMM_BK;
+    if (wanted >= 1) return wanted > nks ? nks : wanted;
+    const int gm = (m + GEMM_BM - 1) / GEMM_BM, tiles128 = gm * ((n + 127) / 128);
+    // enough workgroups without a split, or K too short for the partials to pay (measured: the
+    // c_attn product at M 256, K 768 takes 12.3 us whole and 13.5 us in three slices; at K 1,024
+    // and 4,096 the GPT-2-medium decode products take 1.9 instead of 3.2 ms per pass)
+    if (gm > 2 || tiles128 >= 96 || k_pad < 1024) return 1;
+    // about 256 workgroups of 64-column tiles, at least 4 k-steps each, and the partials
+    // (4 B per output and slice) at most about four times the weight bytes
+    const int tiles = gm * ((n + SPLIT_BN - 1) / SPLIT_BN);
+    int sp = (256 + tiles - 1) / tiles;
+    sp = sp < nks / 4 ? sp : nks / 4;
+    const int by_bytes = (int)((4ll * k_pad) / (4ll * gm * GEMM_BM));
+    sp = sp < by_bytes ? sp : by_bytes;
+    sp = sp > 16 ? 16 : sp;
+    return sp < 2 ? 1 : sp;
+}
+
+// Sums the `splits` partials of one output row x 4 columns and applies the epilogue rule of the
+// fused kernels to the exact product (Raw: the sum itself). A whole group of 4 columns whose
+// destination is 4-byte aligned (16-byte for the i32 outputs) is stored with one access.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_split_epi(GemmArgs g, int splits, int ldp) {
+    const int groups = ldp / 4;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int m = (int)(idx / groups), n4 = (int)(idx % groups) * 4;
+    if (m >= g.m || n4 >= g.n) return;
+    v4i acc = {0, 0, 0, 0};
+    for (int sl = 0; sl < splits; sl++) acc += *(const v4i *)(g.partials + ((size_t)sl * g.m + m) * ldp + n4);
+    const int cnt = g.n - n4 < 4 ? g.n - n4 : 4;
+    if (EPI == (int)Epi::Raw) {
+        int32_t *o = (int32_t *)g.out + (size_t)m * g.ldo + n4;
+        if (cnt == 4 && ((uintptr_t)o & 15) == 0) *(v4i *)o = acc;
+        else
+            for (int e = 0; e < cnt; e++) o[e] = acc[e];
+        return;
+    }
+    // rescale(a + bias, mult, shift) (int.rs:63-67): |a + bias| < 2^32, exact in i64
+    int64_t r[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        r[e] = e < cnt ? rescale_small((int64_t)acc[e] + g.bias[n4 + e], g.mult[n4 + e], (uint32_t)g.shift) : 0;
+    if (EPI == (int)Epi::Residual) {  // ops.rs:131-145: x = clamp(x + sat32(r), +-R)
+        int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n4;
+        if (cnt == 4 && ((uintptr_t)x & 15) == 0) {
+            v4i v = *(const v4i *)x;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = (int32_t)clamp64((int64_t)v[e] + clamp64(r[e], INT32_MIN, INT32_MAX), -RES, RES);
+            *(v4i *)x = v;
+        } else {
+            for (int e = 0; e < cnt; e++)
+                x[e] = (int32_t)clamp64((int64_t)x[e] + clamp64(r[e], INT32_MIN, INT32_MAX), -RES, RES);
+        }
+        return;
+    }
+    uint32_t b[4];  // the i8 outputs (GeluWide: the i16 values)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if (EPI == (int)Epi::Act) {  // ops.rs:123-130
+            b[e] = (uint32_t)clamp64(r[e], -127, 127);
+        } else {  // table[clamp(r, -off, off - 1) + off] (ops.rs:146-154, gelu.rs:58-62)
+            const int t = (int)clamp64(r[e], -g.gelu_off, g.gelu_off - 1) + g.gelu_off;
+            b[e] = EPI == (int)Epi::Gelu ? (uint32_t)g.gelu[t] : (uint32_t)g.gelu16[t];
+        }
+    }
+    auto store4 = [&](int8_t *o, auto byte) {
+        if (cnt == 4 && ((uintptr_t)o & 3) == 0) {
+            *(uint32_t *)o = (byte(0) & 255) | ((byte(1) & 255) << 8) | ((byte(2) & 255) << 16) | ((byte(3) & 255) << 24);
+        } else {
+            for (int e = 0; e < cnt; e++) o[e] = (int8_t)byte(e);
+        }
+    };
+    if (EPI == (int)Epi::Act) {
+        if (g.kv_rows && n4 >= g.kv_d) {
+            // K or V of the row into the cache: kv_d and kv_hd are multiples of 4, so the group
+            // lies in one head of one part; the columns past 3 kv_d are padding
+            if (n4 >= 3 * g.kv_d) return;
+            const RowInfo ri = g.kv_rows[m];
+            const int part = n4 >= 2 * g.kv_d, c = n4 - (part + 1) * g.kv_d;
+            const int hh = c / g.kv_hd, cc = c - hh * g.kv_hd;
+            store4((part ? g.vc : g.kc) + (((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc,
+                   [&](int e) { return b[e]; });
+        } else {
+            store4((int8_t *)g.out + (size_t)m * g.ldo + n4, [&](int e) { return b[e]; });
+        }
+    } else if (EPI == (int)Epi::Gelu) {
+        store4((int8_t *)g.out + (size_t)m * g.ldo + n4, [&](int e) { return b[e]; });
+    } else {  // GeluWide: the two planes of each i16 output, hi = v >> 8, lo = (v & 255) - 128
+        store4((int8_t *)g.out + (size_t)(2 * m) * g.ldo + n4, [&](int e) { return (uint32_t)((int32_t)(int16_t)b[e] >> 8); });
+        store4((int8_t *)g.out + (size_t)(2 * m + 1) * g.ldo + n4,
+               [&](int e) { return (uint32_t)(((int32_t)(int16_t)b[e] & 255) - 128); });
+    }
+}
+
+template <int EPI>
+static hipError_t launch_split_epi(const GemmArgs &g, int splits, int ldp, hipStream_t stream) {
+    const long long threads = (long long)g.m * (ldp / 4);
+    hipLaunchKernelGGL(k_split_epi<EPI>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, g,
+                       splits, ldp);
+    return hipGetLastError();
+}
+
+static hipError_t launch_gemm_split(Epi epi, const GemmArgs &ga, int splits, hipStream_t stream) {
+    if (ga.group < 1 || ga.group > (ga.m + GEMM_BM - 1) / GEMM_BM || splits < 2 || splits > 16)
+        return hipErrorInvalidValue;
+    GemmArgs p = ga;  // the partial products: Raw into the scratch, [splits][m][ldp]
+    const int ldp = (ga.n + 3) & ~3;
+    const int nks = ga.k_pad / GEMM_BK;
+    p.kslice = ((nks + splits - 1) / splits) * GEMM_BK;
+    splits = (ga.k_pad + p.kslice - 1) / p.kslice;  // every slice holds at least one k-step
+    p.out = ga.partials;
+    p.ldo = ldp;
+    constexpr int EPI_RAW = (int)Epi::Raw;
+    static bool ready = false;
+    constexpr size_t lds = (size_t)GEMM_STAGES * (GEMM_BM / 16 + SPLIT_BN / 16) * 1024;
+    if (!ready) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI_RAW, false, SPLIT_BN, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        ready = true;
+    }
+    const int gm = (ga.m + GEMM_BM - 1) / GEMM_BM, gn = (ga.n + SPLIT_BN - 1) / SPLIT_BN;
+    hipLaunchKernelGGL((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(2 * SPLIT_BN), lds,
+                       stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (epi) {
+        case Epi::Raw: return launch_split_epi<0>(ga, splits, ldp, stream);
+        case Epi::Act: return launch_split_epi<1>(ga, splits, ldp, stream);
+        case Epi::Residual: return launch_split_epi<2>(ga, splits, ldp, stream);
+        case Epi::Gelu: return launch_split_epi<3>(ga, splits, ldp, stream);
+        case Epi::GeluWide: return launch_split_epi<6>(ga, splits, ldp, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The i16-activation product from its plane rows (matvec_i8_i16, ADR 0004 addendum B):
+// out[i][r] = 256 p[2i][r] + p[2i + 1][r] + 128 wsum[r], exact in i64.
+__global__ void k_wide_combine(const int32_t *p, const int32_t *wsum, int m, int n, int64_t *out) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)m * n) return;
+    const int i = (int)(idx / n), r = (int)(idx % n);
+    out[idx] = 256 * (int64_t)p[(size_t)(2 * i) * n + r] + p[(size_t)(2 * i + 1) * n + r] + 128 * (int64_t)wsum[r];
+}
+
+hipError_t launch_wide_combine(const int32_t *planes, const int32_t *wsum, int m, int n, int64_t *out,
+                               hipStream_t stream) {
+    const long long t = (long long)m * n;
+    if (t == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_wide_combine, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, stream, planes, wsum, m, n, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
     GemmArgs g = ga;
     if (g.m <= 0 || g.n <= 0) return hipSuccess;
     if (g.k_pad % GEMM_BK != 0) return hipErrorInvalidValue;
+    // the tile order's M-tile group (the kernel divides by it): set and checked before any launch
     const int gm = (g.m + GEMM_BM - 1) / GEMM_BM;
     if (g.group == 0) g.group = gemm_group(g.m);
     if (g.group < 1 || g.group > gm) return hipErrorInvalidValue;
+    g.kslice = 0;
+    if (g.partials) {
+        const int sp = gemm_split_plan(epi, g.m, g.n, g.k_pad, g.splits);
+        if (sp > 1) {
+            if (gemm_split_elems(g.m, g.n, sp) > g.partials_cap) return hipErrorInvalidValue;
+            return launch_gemm_split(epi, g, sp, stream);
+        }
+    }
     switch (epi) {
         case Epi::Raw: return launch_gemm_w<0, false>(g, stream);
         case Epi::Act: return launch_gemm_e<1>(g, stream);
@@ -1624,6 +1808,158 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
 }
 
+// Decode attention for head_dim 64 and at most 64 KB keys (KB <= 4): one wave per (row, head),
+// four independent waves per workgroup, no barrier. Lane l holds the K rows of keys l + 64 j, and
+// the wave's V rows go to its own LDS region ([key][64 B], 16 keys per global_load_lds), all
+// loads issued at once; the lane later reads the 16-byte V chunk l % 4 of keys l / 4 + 16 i
+// back. The dots, the row
+// max (from the extreme dots), the table sum and p = floor(e 2^P / S) (the 2^64 / S reciprocal
+// with one correction) follow the rules of the kernels above. For sum p v the lane fetches the p
+// of its V keys from the lanes that formed them (the key of V slot i is l / 4 + 16 i, formed by
+// lane (l / 4 + 16 i) % 64 in its K round i / 4), splits p = 2^16 ph + pl so both halves sum in
+// i32 (at most 16 keys per lane, |v| <= 128: below 2^27), and the lanes of one chunk are summed
+// with xor shuffles.
+template <bool NOCLAMP, int KB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_decode_wave(AttnArgs a, int n_rh,
+                                                                                                     int kmax) {
+    const int lane = threadIdx.x & 63;
+    const int rh = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (rh >= n_rh) return;
+    const int r = rh / a.n_head, h = rh - r * a.n_head;
+    int keys = split_keys(a, r);
+    keys = keys < kmax ? keys : kmax;
+    const size_t base = ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * 64;
+    int qv[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) qv[t] = ((const int *)(a.q + (size_t)r * a.ldq + h * 64))[t];
+    extern __shared__ __attribute__((aligned(16))) int8_t s_v[];  // 4 waves x KB x 4 KiB
+    int8_t *sv = s_v + (threadIdx.x >> 6) * (KB * 4096);
+    v4i kk[KB][4];
+#pragma unroll
+    for (int j = 0; j < KB; j++) {
+        if (64 * j >= keys) break;  // uniform: the rounds past the row issue nothing
+        const int k = lane + 64 * j;
+        const v4i *k16 = (const v4i *)(a.kc + base + (size_t)(k < keys ? k : keys - 1) * 64);
+#pragma unroll
+        for (int t = 0; t < 4; t++) kk[j][t] = k16[t];
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * KB; i++) {
+        if (16 * i >= keys) break;
+        const int k = (lane >> 2) + 16 * i;
+        __builtin_amdgcn_global_load_lds((const void *)(a.vc + base + (size_t)(k < keys ? k : keys - 1) * 64 + 16 * (lane & 3)),
+                                         (lds_void *)(sv + i * 1024), 16, 0, 0);
+    }
+    int32_t d[KB];
+    int32_t dmin = INT32_MAX, dmax = INT32_MIN;
+#pragma unroll
+    for (int j = 0; j < KB; j++) {
+        int32_t x = 0;
+        if (64 * j < keys) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                x = __builtin_amdgcn_sdot4(qv[4 * t], kk[j][t][0], x, false);
+                x = __builtin_amdgcn_sdot4(qv[4 * t + 1], kk[j][t][1], x, false);
+                x = __builtin_amdgcn_sdot4(qv[4 * t + 2], kk[j][t][2], x, false);
+                x = __builtin_amdgcn_sdot4(qv[4 * t + 3], kk[j][t][3], x, false);
+            }
+        }
+        d[j] = x;
+        if (lane + 64 * j < keys) {
+            dmin = x < dmin ? x : dmin;
+            dmax = x > dmax ? x : dmax;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const int32_t u = __shfl_xor(dmin, o, 64), v = __shfl_xor(dmax, o, 64);
+        dmin = u < dmin ? u : dmin;
+        dmax = v > dmax ? v : dmax;
+    }
+    // the row max of the scores: the score is monotone in the dot (keys >= 1)
+    const int64_t s0 = attn_score<NOCLAMP>(a, dmin), s1 = attn_score<NOCLAMP>(a, dmax);
+    const int64_t M = s0 > s1 ? s0 : s1;
+    const int64_t last = a.exp_len - 1;
+    uint32_t e[KB];
+    uint64_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < KB; j++) {
+        e[j] = 0;
+        if (lane + 64 * j < keys) {
+            const int64_t dd = M - attn_score<NOCLAMP>(a, d[j]);
+            e[j] = (uint32_t)a.exp_table[dd < last ? dd : last];
+            sum += e[j];
+        }
+    }
+    sum = (uint64_t)wave_sum64((int64_t)sum);
+    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+    uint32_t p[KB];
+#pragma unroll
+    for (int j = 0; j < KB; j++) {
+        const uint64_t num = (uint64_t)e[j] << a.softmax_p;
+        uint64_t q = num;
+        if (sum >= 2) {
+            q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
+            if (num - q * sum >= sum) q++;
+        }
+        p[j] = (uint32_t)q;  // <= 2^P <= 2^30; 0 for keys past the row
+    }
+    wait_vmcnt<0>();  // this wave's V rows landed in its LDS region
+    int32_t lo[16], hi[16];
+#pragma unroll
+    for (int c = 0; c < 16; c++) lo[c] = hi[c] = 0;
+#pragma unroll
+    for (int i = 0; i < 4 * KB; i++) {
+        if (16 * i >= keys) break;
+        const uint32_t pk = (uint32_t)__shfl((int)p[i >> 2], 16 * (i & 3) + (lane >> 2), 64);
+        const int k = (lane >> 2) + 16 * i;
+        const uint32_t pv = k < keys ? pk : 0u;
+        const int32_t pl = (int32_t)(pv & 0xffffu), ph = (int32_t)(pv >> 16);
+        const v4i raw = *(const v4i *)(sv + i * 1024 + 16 * lane);
+        const int8_t *v = (const int8_t *)&raw;
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            lo[c] += pl * (int32_t)v[c];
+            hi[c] += ph * (int32_t)v[c];
+        }
+    }
+    int64_t acc[16];
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        acc[c] = (int64_t)hi[c] * 65536 + lo[c];
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) acc[c] += __shfl_xor(acc[c], o, 64);
+    }
+    if (lane < 4) {  // lane l holds channels 16 l .. 16 l + 15
+        uint32_t w4[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            const uint32_t b = (uint32_t)clamp128(rescale_full(acc[c], a.out_m, a.out_s), -127, 127) & 255;
+            w4[c >> 2] |= b << (8 * (c & 3));
+        }
+        int8_t *o = a.out + (size_t)r * a.ldo + h * 64 + 16 * lane;
+        if (((uintptr_t)o & 15) == 0) {
+            *(v4i *)o = v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
+        } else {
+#pragma unroll
+            for (int c = 0; c < 16; c++) o[c] = (int8_t)(w4[c >> 2] >> (8 * (c & 3)));
+        }
+    }
+}
+
+template <bool NOCLAMP>
+static hipError_t launch_decode_wave(const AttnArgs &a, int n_rows, int kmax, hipStream_t stream) {
+    const int n_rh = n_rows * a.n_head;
+    const dim3 grid((n_rh + 3) / 4);
+    const int kb = (kmax + 63) / 64;
+    const size_t lds = (size_t)4 * kb * 4096;  // 16 to 64 KiB
+    if (kb <= 1) hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 1>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    else if (kb == 2) hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 2>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    else if (kb == 3) hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 3>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    else hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 4>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    return hipGetLastError();
+}
+
 SplitPlan attend_split_plan(int n_rows, int n_head, int max_keys) {
     // about 4096 waves over (row, head, chunk), chunks of a multiple of 64 keys
     SplitPlan p;
@@ -1655,6 +1991,12 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
     if (n_rows <= 0) return hipSuccess;
     if (!attend_split_ok(a.hd) || p.chunk_keys % 64 != 0 || p.chunk_keys > 4096) return hipErrorInvalidValue;
     const int kmax = p.max_keys < a.ctx_cap ? p.max_keys : a.ctx_cap;
+    // a wave per (row, head) when there are enough of them to fill the CUs (measured: 4,096
+    // row-heads of a GPT-2-medium decode pass 42 -> 37 us per launch; 768 at 128 keys 12 -> 18 us,
+    // so those keep a workgroup per row-head)
+    if (a.hd == 64 && kmax >= 1 && kmax <= 256 && n_rows * a.n_head >= 2048)
+        return attn_noclamp(a) ? launch_decode_wave<true>(a, n_rows, kmax, stream)
+                               : launch_decode_wave<false>(a, n_rows, kmax, stream);
     if (attend_split_one_launch(a.hd, a.ctx_cap, p)) {  // one launch, no scratch
         const int kmax64 = (kmax + 63) & ~63;
         const size_t dyn = (size_t)kmax64 * 64 + (size_t)kmax64 * 4;

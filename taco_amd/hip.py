@@ -151,6 +151,8 @@ def lib() -> C.CDLL:
         L.hs_batch_truncate.argtypes = [P, S, S]
         L.hs_op_gemm_i8.argtypes = [P, P, P, S, S, S, P]
         L.hs_op_gemm_requant_i8.argtypes = [P, P, P, P, P, C.c_uint8, S, S, S, P]
+        L.hs_op_gemm_i8_split.argtypes = [P, P, P, S, S, S, C.c_uint32, P]
+        L.hs_op_gemm_i8_i16.argtypes = [P, P, P, S, S, S, C.c_uint32, P]
         L.hs_op_gemm_requant_i8_dev.argtypes = [P, P, P, P, P, C.c_uint8, S, S, S, P, P]
         L.hs_op_gemm_layout.argtypes = [S, S, S, C.POINTER(S), C.POINTER(S), C.POINTER(S)]
         L.hs_op_gemm_layout.restype = None
@@ -426,6 +428,28 @@ def matmul_i8(dev: HipDevice, w: np.ndarray, a: np.ndarray) -> np.ndarray:
     m = a.shape[0]
     out = np.zeros((m, n), np.int32)
     _check(lib().hs_op_gemm_i8(dev.h, _ptr(w), _ptr(a), m, n, k, _ptr(out)))
+    return out
+
+
+def matmul_i8_split(dev: HipDevice, w: np.ndarray, a: np.ndarray, splits: int) -> np.ndarray:
+    """ops.rs:163-184: matmul_i8 with K in `splits` slices whose partials are summed."""
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    n, k = w.shape
+    m = a.shape[0]
+    out = np.zeros((m, n), np.int32)
+    _check(lib().hs_op_gemm_i8_split(dev.h, _ptr(w), _ptr(a), m, n, k, splits, _ptr(out)))
+    return out
+
+
+def matmul_i8_i16(dev: HipDevice, w: np.ndarray, a: np.ndarray, splits: int = 1) -> np.ndarray:
+    """ops.rs:220-282: out[i][r] = w[r] . a[i] for i16 activations, exact i64."""
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    a = np.ascontiguousarray(a, dtype=np.int16)
+    n, k = w.shape
+    m = a.shape[0]
+    out = np.zeros((m, n), np.int64)
+    _check(lib().hs_op_gemm_i8_i16(dev.h, _ptr(w), _ptr(a), m, n, k, splits, _ptr(out)))
     return out
 
 

@@ -124,6 +124,38 @@ def test_attend_decode_at_the_benchmark_shape(dev, ctx_len):
         assert np.array_equal(out, want)
 
 
+@pytest.mark.parametrize("B,H,ctx_len", [(256, 12, 200), (200, 16, 64), (171, 12, 256)])
+def test_attend_decode_wave_per_head(dev, B, H, ctx_len):
+    """Decode attention with at least 2,048 row-heads and at most 256 keys (a GPT-2-medium
+    unfold pass: 256 slots x 16 heads) takes the wave-per-row-head kernel: full and ragged
+    contexts against the oracle."""
+    from taco_amd import hip
+    r = np.random.default_rng(B * H + ctx_len)
+    hd = 64
+    q = r.integers(-127, 128, (B, H, hd)).astype(np.int8)
+    kc = r.integers(-127, 128, (B, H, ctx_len, hd)).astype(np.int8)
+    vc = r.integers(-127, 128, (B, H, ctx_len, hd)).astype(np.int8)
+    table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
+    score_m, score_s, out_m, out_s = 1_400_000_000, 33, 1_300_000_000, 53
+    ragged = r.integers(1, ctx_len + 1, B).astype(np.uint32)
+    ragged[:3] = [1, ctx_len, min(65, ctx_len)]
+    for ctx in (np.full(B, ctx_len, np.uint32), ragged):
+        want = O.attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, 30)
+        bufs = [_dev_buf(dev, a) for a in (q, kc, vc, ctx, table)]
+        out = np.zeros((B, H * hd), np.int8)
+        dout = _dev_buf(dev, out)
+        try:
+            hip._check(hip.lib().hs_op_attend_decode_dev(
+                dev.h, bufs[0], bufs[1], bufs[2], bufs[3], B, H, hd, ctx_len, score_m, score_s,
+                out_m, out_s, bufs[4], len(table), 30, dout, None))
+            hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                    out.nbytes))
+        finally:
+            for p in bufs + [dout]:
+                hip.lib().hs_device_free(dev.h, p)
+        assert np.array_equal(out, want)
+
+
 # LayerNorm forms by pass size and width: fewer than 4,096 rows take a one-wave workgroup per
 # row (4 or 8 column groups per lane); at least 4,096 rows take the 16-lanes-per-row form for
 # d <= 1,024 (12 or 16 groups; single-precision element rule for 8-bit outputs with |beta| <=

@@ -58,6 +58,50 @@ def test_gemm_i8_worst_case_at_the_bound(dev):
     assert got[1].tolist() == [(k // 2) * (-128 * 127) + (k // 2) * (1 << 14)] * 3
 
 
+@pytest.mark.parametrize("n,k,m,splits", [
+    (2304, 768, 256, 3), (1024, 4096, 256, 16), (768, 3072, 100, 7), (65, 63, 7, 2),
+    (3, 1000, 2, 16), (300, 64 * 9 + 1, 17, 4), (2304, 768, 512, 2), (50, 3072, 33, 1)])
+def test_gemm_i8_split_is_the_exact_product(dev, n, k, m, splits):
+    """matmul_i8_split (crates/hardshell-cuda/src/ops.rs:163-184): K in `splits` slices, the
+    i32 partials summed on the GPU, equal to the exact product (slices of unequal length, K
+    below 64 per slice, the worst case of one slice)."""
+    from taco_amd import hip
+    print(f"gemm split n={n} k={k} m={m} splits={splits}", flush=True)
+    r = np.random.default_rng(n * 131 + k * 7 + m + splits)
+    w = r.integers(-128, 128, (n, k)).astype(np.int8)
+    a = r.integers(-128, 128, (m, k)).astype(np.int8)
+    got = hip.matmul_i8_split(dev, w, a, splits)
+    want = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(got, want)
+
+
+def test_gemm_i8_split_worst_case_at_the_bound(dev):
+    """kernels.rs:112-119: 2^16 products of (-128) * (-128) sum to exactly 2^30 in 16 slices."""
+    from taco_amd import hip
+    k = 1 << 16
+    w = np.full((70, k), -128, np.int8)
+    a = np.full((3, k), -128, np.int8)
+    a[1, ::2] = 127
+    got = hip.matmul_i8_split(dev, w, a, 16)
+    assert got[0].tolist() == [1 << 30] * 70
+    assert got[1].tolist() == [(k // 2) * (-128 * 127) + (k // 2) * (1 << 14)] * 70
+
+
+@pytest.mark.parametrize("n,k,m,splits", [(64, 64, 1, 1), (300, 768, 40, 1), (1024, 3072, 256, 8),
+                                          (77, 1000, 5, 3)])
+def test_gemm_i8_i16_is_the_exact_product(dev, n, k, m, splits):
+    """matmul_i8_i16 (ops.rs:220-282, kernels::matvec_i8_i16): i16 activations as two i8 planes,
+    one product of 2m rows, exact i64 (the i16 extremes included)."""
+    from taco_amd import hip
+    r = np.random.default_rng(n + 3 * k + m)
+    w = r.integers(-128, 128, (n, k)).astype(np.int8)
+    a = r.integers(-32768, 32768, (m, k)).astype(np.int16)
+    a[0, :3] = [-32768, 32767, -1]
+    got = hip.matmul_i8_i16(dev, w, a, splits)
+    want = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.array_equal(got, want)
+
+
 def test_gemm_requant_c1_shape(dev):
     # The c_attn linear at GPT-2-small shape: A [256, 768], W [2304, 768], per-channel m, one s.
     from taco_amd import hip
