@@ -87,11 +87,24 @@ void hs_device_close(hs_device *dev);
 /* The device name ("AMD Instinct MI355X" ...), NUL-terminated, truncated to cap bytes. */
 hs_status hs_device_name(const hs_device *dev, char *buf, size_t cap);
 hs_status hs_device_memory(const hs_device *dev, size_t *free_bytes, size_t *total_bytes);
+/* CudaDevice::kernel_resources (crates/hardshell-cuda/src/device.rs:65-74): for each of the main
+ * kernels, its name (NUL-terminated in 64-byte slots of `names`), vector registers per thread,
+ * private (spill) bytes per thread and static LDS bytes, as the compiler built them. Writes up
+ * to cap entries; *count is the number of kernels. For measurements. */
+hs_status hs_device_kernel_resources(hs_device *dev, char *names, int32_t *regs,
+                                     int32_t *private_bytes, int32_t *static_lds_bytes, size_t cap,
+                                     size_t *count);
 
 /* ---- Model: crates/hardshell-cuda/src/model.rs:242-398 ---------------------------------- */
 /* Loads a .hsm file with exactly the accept/reject rules of hardshell::gpt2::Model::load
  * (crates/hardshell/src/gpt2/model.rs:292-343, hsm/reader.rs:357-430) and uploads it. */
 hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t len, hs_model **out);
+/* CudaModel::load_with (crates/hardshell-cuda/src/model.rs:259-349): as hs_model_load, but when
+ * `bytes` hash to the file of `loaded` (a model this library already loaded, on any device),
+ * that model's parse is reused and the file's checks are not repeated; any other file (or
+ * loaded == NULL) gets the full hs_model_load. The result has the hash of `bytes`. */
+hs_status hs_model_load_with(hs_device *dev, const uint8_t *bytes, size_t len, const hs_model *loaded,
+                             hs_model **out);
 void hs_model_free(hs_model *model);
 /* Model::load on the host alone (gpt2/model.rs:292-343): validates the file with the same
  * rules as hs_model_load and gives its SHA-256, without a device. HS_OK or HS_MODEL_ERROR. */
@@ -142,6 +155,10 @@ void hs_batch_reset(hs_batch *batch, size_t slot);
 /* CudaBatch::run_weights: out holds n * vocab u64 values, in input order. A slot can occur many
  * times (prefill); a full context restarts with EOT and the last K tokens. */
 hs_status hs_batch_run_weights(hs_batch *batch, const hs_input *inputs, size_t n, uint64_t *out);
+/* CudaBatch::run_without_readback (crates/hardshell-cuda/src/batch.rs:478-484): runs the inputs
+ * as hs_batch_run_weights does (positions commit the same way), waits for the GPU and reads
+ * nothing back. For measurements. */
+hs_status hs_batch_run_without_readback(hs_batch *batch, const hs_input *inputs, size_t n);
 /* CudaBatch::run_coded: the interval of FreqTable::from_weights(weights, freq_bits) for each
  * input (queries[i] belongs to inputs[i]). 1 <= freq_bits <= 32 and 2^freq_bits >= vocab. */
 hs_status hs_batch_run_coded(hs_batch *batch, const hs_input *inputs, const hs_query *queries,

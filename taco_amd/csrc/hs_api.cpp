@@ -267,6 +267,27 @@ extern "C" hs_status hs_device_name(const hs_device *dev, char *buf, size_t cap)
     return HS_OK;
 }
 
+extern "C" hs_status hs_device_kernel_resources(hs_device *dev, char *names, int32_t *regs,
+                                                int32_t *private_bytes, int32_t *static_lds_bytes,
+                                                size_t cap, size_t *count) {
+    hs::clear_error();
+    if (!dev || !count || (cap && (!names || !regs || !private_bytes || !static_lds_bytes)))
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    std::vector<hs::KernelResource> r(64);
+    const int n = hs::kernel_resources(r.data(), (int)r.size());
+    if (n < 0) return hip_fail("hipFuncGetAttributes", (hipError_t)(-n));
+    for (int i = 0; i < n && (size_t)i < cap; i++) {
+        std::memset(names + 64 * (size_t)i, 0, 64);
+        std::strncpy(names + 64 * (size_t)i, r[i].name, 63);
+        regs[i] = r[i].regs;
+        private_bytes[i] = r[i].private_bytes;
+        static_lds_bytes[i] = r[i].static_lds_bytes;
+    }
+    *count = (size_t)n;
+    return HS_OK;
+}
+
 extern "C" hs_status hs_device_memory(const hs_device *dev, size_t *free_bytes, size_t *total_bytes) {
     if (!dev || !free_bytes || !total_bytes) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
     HIP_TRY(hipSetDevice(dev->ordinal));
@@ -278,6 +299,28 @@ extern "C" hs_status hs_device_memory(const hs_device *dev, size_t *free_bytes, 
 // Model: crates/hardshell-cuda/src/model.rs:242-349
 // ---------------------------------------------------------------------------------------------
 
+namespace {
+
+// A copy of a parsed model whose tensor pointers point into the copy's own file bytes.
+void copy_host_model(const hs::HostModel &src, hs::HostModel &dst) {
+    dst = src;
+    const int8_t *s0 = (const int8_t *)src.file.data();
+    const int8_t *d0 = (const int8_t *)dst.file.data();
+    auto rebase = [&](const int8_t *p) { return p ? d0 + (p - s0) : nullptr; };
+    dst.wte = rebase(src.wte);
+    dst.wpe = rebase(src.wpe);
+    for (size_t l = 0; l < dst.blocks.size(); l++) {
+        dst.blocks[l].c_attn.w = rebase(src.blocks[l].c_attn.w);
+        dst.blocks[l].c_proj.w = rebase(src.blocks[l].c_proj.w);
+        dst.blocks[l].c_fc.w = rebase(src.blocks[l].c_fc.w);
+        dst.blocks[l].mlp_proj.w = rebase(src.blocks[l].mlp_proj.w);
+    }
+}
+
+hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **out);
+
+}  // namespace
+
 extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t len, hs_model **out) {
     hs::clear_error();
     if (!dev || !bytes || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
@@ -285,6 +328,28 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
     auto m = std::make_unique<hs_model>();
     hs::ModelError err{};
     if (!hs::load_host_model(bytes, len, m->host, err)) return hs::fail(HS_MODEL_ERROR, err.kind, err.msg);
+    return upload_model(dev, m, out);
+}
+
+extern "C" hs_status hs_model_load_with(hs_device *dev, const uint8_t *bytes, size_t len,
+                                        const hs_model *loaded, hs_model **out) {
+    hs::clear_error();
+    if (!dev || !bytes || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    *out = nullptr;
+    if (!loaded) return hs_model_load(dev, bytes, len, out);
+    uint8_t hash[32];
+    hs::sha256(bytes, len, hash);
+    // the bytes of a model the library already parsed and checked: its parse is reused (the
+    // checks are not repeated); any other file gets its own full load (model.rs:259-274)
+    if (std::memcmp(hash, loaded->host.hash, 32) != 0) return hs_model_load(dev, bytes, len, out);
+    auto m = std::make_unique<hs_model>();
+    copy_host_model(loaded->host, m->host);
+    return upload_model(dev, m, out);
+}
+
+namespace {
+
+hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **out) {
     const hs::HostModel &h = m->host;
     if (h.head_dim % 4 != 0 || h.head_dim > 256)
         return hs::fail(HS_UNSUPPORTED, 0, "head_dim must be a multiple of 4 and at most 256");
@@ -347,6 +412,8 @@ extern "C" hs_status hs_model_load(hs_device *dev, const uint8_t *bytes, size_t 
     *out = m.release();
     return HS_OK;
 }
+
+}  // namespace
 
 extern "C" void hs_model_free(hs_model *model) { delete model; }
 
@@ -719,7 +786,7 @@ void commit(hs_batch &b, Plan &p) {
     for (auto &kv : p.prev) b.prev[kv.first] = std::move(kv.second);
 }
 
-enum class Out { Weights, Intervals };
+enum class Out { Weights, Intervals, Nothing };  // Nothing: the weights, not read back
 
 // The tables of a mixed call (batch/mixed.rs:23-33): the table word of each input
 // (HS_MIX_PLAIN, HS_MIX_NONE or the predicted token), the host mixer, and for a dual call the
@@ -956,7 +1023,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     DevLinear head;
     head.w = m.wte; head.m = m.logit_m; head.s = m.host.logit_s; head.n = m.V; head.k = m.d;
     head.n_pad = m.V_pad; head.k_pad = m.d_pad; head.wsum = m.wte_sum;
-    const size_t per_row = out == Out::Weights ? (size_t)m.V : 3;
+    const size_t per_row = out == Out::Intervals ? 3 : (size_t)m.V;
     std::vector<uint64_t> host(out == Out::Weights ? (size_t)n_out * per_row : 0);
     for (int c0 = 0; c0 < n_out; c0 += (int)b.chunk_rows) {
         const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
@@ -977,7 +1044,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
             ca.bits = (int)bits;
             ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
-            ca.weights = out == Out::Weights ? b.d_weights : nullptr;
+            ca.weights = out != Out::Intervals ? b.d_weights : nullptr;
             if (mx) {
                 ca.mix = b.d_mix + c0;
                 ca.stats = b.d_stats + 3 * (size_t)c0;
@@ -1003,7 +1070,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             ca.queries = out == Out::Intervals ? b.d_queries + 2 * c0 : nullptr;
             ca.bits = (int)bits;
             ca.intervals = out == Out::Intervals ? b.d_intervals + 3 * (size_t)c0 : nullptr;
-            ca.weights = out == Out::Weights ? b.d_weights : nullptr;
+            ca.weights = out != Out::Intervals ? b.d_weights : nullptr;
             if (mx) {
                 ca.mix = b.d_mix + c0;
                 ca.stats = b.d_stats + 3 * (size_t)c0;
@@ -1029,6 +1096,10 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     if (mx && mx->plain_sink)
         HIP_TRY(hipMemcpyAsync(b.h_intervals2, b.d_intervals2, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
+    if (out == Out::Nothing) {  // batch.rs:549: wait for the GPU, read nothing back
+        if (b.profiling && b.pending.size() > 8192) HIP_TRY(b.collect());
+        return HS_OK;
+    }
     const uint64_t *res = out == Out::Intervals ? b.h_intervals : host.data();
     // The event times are read back in bulk (hs_batch_profile), not inside every call.
     if (b.profiling && b.pending.size() > 8192) HIP_TRY(b.collect());
@@ -1068,6 +1139,13 @@ hs_status run(hs_batch *b, const hs_input *in, size_t n, Out out, const uint32_t
 }
 
 }  // namespace
+
+extern "C" hs_status hs_batch_run_without_readback(hs_batch *b, const hs_input *in, size_t n) {
+    hs::clear_error();
+    hs_status s = check_inputs(b, in, n);
+    if (s != HS_OK) return s;
+    return run(b, in, n, Out::Nothing, nullptr, 0, nullptr);
+}
 
 extern "C" hs_status hs_batch_run_weights(hs_batch *b, const hs_input *in, size_t n, uint64_t *out) {
     hs::clear_error();

@@ -76,6 +76,14 @@ inline int gemm_group(int m) {
 
 hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream);
 
+// The compiled resources of the main kernels: fills up to cap entries and returns the number of
+// kernels (or minus a hipError_t).
+struct KernelResource {
+    const char *name;
+    int regs, private_bytes, static_lds_bytes;
+};
+int kernel_resources(KernelResource *out, int cap);
+
 // The split-K plan of a product: the number of K slices (1 = no split) for m rows, n columns and
 // k_pad bytes of K with the given epilogue, and the i32 partial elements it needs.
 int gemm_split_plan(Epi epi, int m, int n, int k_pad, int splits_wanted);

@@ -3461,4 +3461,59 @@ hipError_t launch_coder_compact_mixed(const CompactCoderArgs &a, int n_rows, hip
     return launch_compact(k_coder_compact_mixed, a, n_rows, &allowed, stream);
 }
 
+// ---- kernel resources (CudaDevice::kernel_resources, crates/hardshell-cuda/src/device.rs:65-74) --
+// The main kernels of the path with the registers, spill (private) bytes and static LDS bytes
+// the compiler gave each.
+
+int kernel_resources(KernelResource *out, int cap) {
+    struct Entry {
+        const char *name;
+        const void *fn;
+    };
+    static const Entry table[] = {
+        {"k_gemm<Act, narrow, 256x128>", (const void *)k_gemm<1, true, 128, true>},
+        {"k_gemm<Residual, narrow, 256x128>", (const void *)k_gemm<2, true, 128, true>},
+        {"k_gemm<Residual, narrow, 256x256>", (const void *)k_gemm<2, true, 256, true>},
+        {"k_gemm<Gelu, narrow, 256x256>", (const void *)k_gemm<3, true, 256, true>},
+        {"k_gemm<LogitsCompact, narrow, 256x128>", (const void *)k_gemm<5, true, 128, true>},
+        {"k_gemm<Act, 256x128>", (const void *)k_gemm<1, false, 128, true>},
+        {"k_gemm<Residual, 256x128>", (const void *)k_gemm<2, false, 128, true>},
+        {"k_gemm<GeluWide, 256x128>", (const void *)k_gemm<6, false, 128, true>},
+        {"k_gemm<ResidualWide, 256x128>", (const void *)k_gemm<7, false, 128, true>},
+        {"k_gemm<LogitsCompactWide, 256x128>", (const void *)k_gemm<9, false, 128, true>},
+        {"k_gemm<Raw, split-K partials, 256x64>", (const void *)k_gemm<0, false, 64, true>},
+        {"k_split_epi<Act>", (const void *)k_split_epi<1>},
+        {"k_split_epi<Residual>", (const void *)k_split_epi<2>},
+        {"k_embed", (const void *)k_embed},
+        {"k_layernorm", (const void *)k_layernorm},
+        {"k_layernorm_rows<4>", (const void *)k_layernorm_rows<4>},
+        {"k_layernorm_rows<8>", (const void *)k_layernorm_rows<8>},
+        {"k_layernorm_rows4<12, f32>", (const void *)k_layernorm_rows4<12, true>},
+        {"k_layernorm_rows4<16, f32>", (const void *)k_layernorm_rows4<16, true>},
+        {"k_kv_store", (const void *)k_kv_store},
+        {"k_attend", (const void *)k_attend},
+        {"k_attend_short<4>", (const void *)k_attend_short<4>},
+        {"k_attend_short<8>", (const void *)k_attend_short<8>},
+        {"k_attend_mfma<noclamp, lds table>", (const void *)k_attend_mfma<true, true, false>},
+        {"k_attend_decode64<noclamp>", (const void *)k_attend_decode64<true>},
+        {"k_attend_decode_wave<noclamp, 4>", (const void *)k_attend_decode_wave<true, 4>},
+        {"k_split_dots<64>", (const void *)k_split_dots<64>},
+        {"k_split_pv<noclamp>", (const void *)k_split_pv<true>},
+        {"k_coder_compact", (const void *)k_coder_compact<false>},
+        {"k_coder_compact_mixed", (const void *)k_coder_compact_mixed},
+        {"k_read_bw", (const void *)k_read_bw},
+    };
+    const int n = (int)(sizeof(table) / sizeof(table[0]));
+    for (int i = 0; i < n && i < cap; i++) {
+        hipFuncAttributes at;
+        const hipError_t e = hipFuncGetAttributes(&at, table[i].fn);
+        if (e != hipSuccess) return -(int)e;
+        out[i].name = table[i].name;
+        out[i].regs = at.numRegs;
+        out[i].private_bytes = (int)at.localSizeBytes;
+        out[i].static_lds_bytes = (int)at.sharedSizeBytes;
+    }
+    return n;
+}
+
 }  // namespace hs

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 from dataclasses import dataclass
-from typing import Iterable, List, Sequence, Tuple
+from typing import Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -160,6 +160,9 @@ def lib() -> C.CDLL:
                                               C.c_int32, C.c_uint8, P, S, C.c_uint8, P, P]
         L.hs_op_attend_decode_dev_noalloc.argtypes = L.hs_op_attend_decode_dev.argtypes
         L.hs_read_bw.argtypes = [P, S, S, C.POINTER(C.c_uint64)]
+        L.hs_model_load_with.argtypes = [P, P, S, P, C.POINTER(P)]
+        L.hs_batch_run_without_readback.argtypes = [P, P, S]
+        L.hs_device_kernel_resources.argtypes = [P, P, P, P, P, S, C.POINTER(S)]
         L.hs_device_alloc.argtypes = [P, S, C.POINTER(P)]
         L.hs_device_free.argtypes = [P, P]
         L.hs_device_upload.argtypes = [P, P, P, S]
@@ -235,16 +238,25 @@ class HipDevice:
 class HipModel:
     """CudaModel (crates/hardshell-cuda/src/model.rs:242-398)."""
 
-    def __init__(self, dev: HipDevice, data: bytes):
+    def __init__(self, dev: HipDevice, data: bytes, loaded: Optional["HipModel"] = None):
         self.dev = dev  # the device outlives the model
         buf = np.frombuffer(data, dtype=np.uint8)
         h = C.c_void_p()
-        _check(lib().hs_model_load(dev.h, _ptr(buf), len(buf), C.byref(h)))
+        if loaded is None:
+            _check(lib().hs_model_load(dev.h, _ptr(buf), len(buf), C.byref(h)))
+        else:
+            _check(lib().hs_model_load_with(dev.h, _ptr(buf), len(buf), loaded.h, C.byref(h)))
         self.h = h
 
     @classmethod
     def load(cls, dev: HipDevice, data: bytes) -> "HipModel":
         return cls(dev, data)
+
+    @classmethod
+    def load_with(cls, dev: HipDevice, data: bytes, loaded: "HipModel") -> "HipModel":
+        """CudaModel::load_with (model.rs:259-349): reuses the parse of `loaded` when the bytes
+        are its file."""
+        return cls(dev, data, loaded)
 
     def hash(self) -> bytes:
         out = np.zeros(32, np.uint8)
@@ -322,6 +334,11 @@ class HipBatch:
 
     def reset(self, slot: int):
         lib().hs_batch_reset(self.h, slot)
+
+    def run_without_readback(self, inputs) -> None:
+        """CudaBatch::run_without_readback (batch.rs:478-484)."""
+        a = _inputs(inputs)
+        _check(lib().hs_batch_run_without_readback(self.h, _ptr(a), len(a)))
 
     def run_weights(self, inputs) -> np.ndarray:
         a = _inputs(inputs)
@@ -464,6 +481,20 @@ def gemm_requant_i8(dev: HipDevice, w, a, bias, mult, shift: int) -> np.ndarray:
     _check(lib().hs_op_gemm_requant_i8(dev.h, _ptr(w), _ptr(a), _ptr(bias), _ptr(mult), shift,
                                        m, n, k, _ptr(out)))
     return out
+
+
+def kernel_resources(dev: HipDevice):
+    """CudaDevice::kernel_resources (device.rs:65-74): (name, registers, private bytes, static
+    LDS bytes) of each main kernel."""
+    cap = 64
+    names = (C.c_char * (64 * cap))()
+    regs, priv, lds = (np.zeros(cap, np.int32) for _ in range(3))
+    n = C.c_size_t()
+    _check(lib().hs_device_kernel_resources(dev.h, names, _ptr(regs), _ptr(priv), _ptr(lds), cap,
+                                            C.byref(n)))
+    raw = bytes(names)
+    return [(raw[64 * i:64 * i + 64].split(b"\0")[0].decode(), int(regs[i]), int(priv[i]), int(lds[i]))
+            for i in range(min(n.value, cap))]
 
 
 def read_bw(dev: HipDevice, nbytes: int, reps: int) -> float:

@@ -512,3 +512,50 @@ def test_read_bw_probe(dev):
     assert 500 < gbs < 20000
     ns = C.c_uint64()
     assert hip.lib().hs_read_bw(dev.h, 1000, 1, C.byref(ns)) == hip.HS_UNSUPPORTED
+
+
+def test_model_load_with_reuses_a_loaded_parse(dev, golden):
+    """CudaModel::load_with (model.rs:259-349): the bytes of a loaded model give a model with the
+    same hash and the same weights; other bytes get their own full load (their hash, their
+    refusals)."""
+    from taco_amd import hip
+    b, hm, om = golden
+    again = hip.HipModel.load_with(dev, b, hm)
+    assert again.hash() == hm.hash()
+    eot = hm.eot_token()
+    inputs = [(0, eot), (0, 17), (0, 250)]
+    want = hip.HipBatch(hm, 1, 8).run_weights(inputs)
+    assert np.array_equal(hip.HipBatch(again, 1, 8).run_weights(inputs), want)
+    other = O.build_model(O.tiny_dims(), 0x7AC0_0002, 64)
+    m2 = hip.HipModel.load_with(dev, other, hm)
+    assert m2.hash() == hashlib.sha256(other).digest()
+    bad = bytearray(b)
+    bad[0] ^= 1  # the magic
+    with pytest.raises(hip.HipError):
+        hip.HipModel.load_with(dev, bytes(bad), hm)
+
+
+def test_run_without_readback_advances_like_run_weights(golden):
+    """CudaBatch::run_without_readback (batch.rs:478-484): the same passes and positions as
+    run_weights, nothing read back; the next weights equal those of a batch that read back."""
+    from taco_amd import hip
+    b, hm, om = golden
+    eot = hm.eot_token()
+    first = [(0, eot), (1, eot), (0, 5), (1, 77)]
+    nxt = [(0, 11), (1, 12)]
+    a, c = hip.HipBatch(hm, 2, 16), hip.HipBatch(hm, 2, 16)
+    a.run_weights(first)
+    c.run_without_readback(first)
+    assert [c.position(s) for s in range(2)] == [a.position(s) for s in range(2)] == [2, 2]
+    assert np.array_equal(c.run_weights(nxt), a.run_weights(nxt))
+
+
+def test_kernel_resources(dev):
+    """CudaDevice::kernel_resources (device.rs:65-74): every listed kernel has a name and
+    registers; the main GEMM loop does not spill."""
+    from taco_amd import hip
+    res = hip.kernel_resources(dev)
+    print(res, flush=True)
+    assert len(res) >= 20 and all(name and regs > 0 for name, regs, _, _ in res)
+    by = {name: (regs, priv) for name, regs, priv, _ in res}
+    assert by["k_gemm<Act, narrow, 256x128>"][1] == 0
