@@ -116,6 +116,13 @@ uint32_t hs_model_n_ctx(const hs_model *model);
 uint32_t hs_model_eot(const hs_model *model);
 /* 1 if the model uses a rule of model-file version 2 (gpt2/model.rs:379-384). */
 int hs_model_is_wide(const hs_model *model);
+/* Vocabulary::token (crates/hardshell/src/hsm/mod.rs): the bytes of token `id`, a pointer into
+ * the model's copy of its vocabulary (valid while the model lives; EOT's bytes are
+ * "<|endoftext|>"). */
+hs_status hs_model_token(const hs_model *model, uint32_t id, const uint8_t **bytes, size_t *len);
+/* Model::merges (crates/hardshell/src/hsm/merges.rs): the BPE merges of the file in rank order,
+ * as (left id, right id) pairs at *pairs (valid while the model lives); the count of merges. */
+size_t hs_model_merges(const hs_model *model, const uint32_t **pairs);
 uint64_t hs_model_weight_bytes(const hs_model *model);
 /* KV-cache bytes of one slot: 2 * n_layer * n_ctx * d_model (model.rs:392-398). */
 uint64_t hs_model_cache_bytes_per_slot(const hs_model *model);

@@ -44,6 +44,41 @@ hs_status tc_unfold_blocks(hs_batch *batch, uint32_t overlap, const uint8_t *pay
                            const size_t *offsets, size_t count, uint32_t *tokens, size_t cap,
                            size_t *counts);
 
+/* ---- The tokenizer (crates/taco/src/tokenizer): GPT-2 byte-level BPE ---------------------- */
+typedef struct tc_tokenizer tc_tokenizer;
+/* Tokenizer::new (tokenizer/mod.rs:87-147): token i has the bytes token_bytes[token_offsets[i]
+ * .. token_offsets[i + 1]) (count + 1 offsets); eot is the <|endoftext|> id (UINT32_MAX for
+ * none); merges are `n_merges` (left, right) id pairs in rank order. The EOT token and tokens
+ * with no bytes never appear in the output. Refused with HS_MODEL_ERROR (code
+ * HS_MODEL_VOCABULARY) when a byte value has no single-byte token or two, or a merge is not
+ * valid (a part out of range, EOT or empty; no token or two tokens with the joined bytes; a
+ * pair given twice). */
+hs_status tc_tokenizer_new(const uint8_t *token_bytes, const size_t *token_offsets, size_t count,
+                           uint32_t eot, const uint32_t *merges, size_t n_merges,
+                           tc_tokenizer **out);
+/* Tokenizer::for_vocabulary (tokenizer/mod.rs:150-160): the vocabulary and merges of a model. */
+hs_status tc_tokenizer_for_model(const hs_model *model, tc_tokenizer **out);
+void tc_tokenizer_free(tc_tokenizer *tokenizer);
+/* Tokenizer::encode (tokenizer/mod.rs:176-201): the token ids of data (maximal runs of
+ * well-formed UTF-8 through the GPT-2 pre-tokenizer and the merges; any other byte as its
+ * single-byte token). Writes up to cap ids; *count is the number of ids (HS_LENGTH_MISMATCH
+ * when it exceeds cap). */
+hs_status tc_tokenize(const tc_tokenizer *tokenizer, const uint8_t *data, size_t len, uint32_t *ids,
+                      size_t cap, size_t *count);
+/* The pieces of the GPT-2 pre-tokenizer (tokenizer/pretokenize.rs) of well-formed UTF-8 text:
+ * writes the byte end of each piece (up to cap) and returns the number of pieces, or SIZE_MAX
+ * when the text is not well-formed UTF-8. For tests. */
+size_t tc_pretokenize(const uint8_t *text, size_t len, size_t *ends, size_t cap);
+
+/* The byte-level fold of the text profile (crates/taco/src/fold.rs:502-565, code_segment):
+ * `data` cut into blocks of block_size bytes, each block tokenized (its tokens must restore its
+ * bytes), coded on `batch` with the context overlap, and each block stored as the smaller of
+ * its coded payload and its raw bytes (Block::choose_smallest without a zstd candidate), in a
+ * version-2 container. Writes the container to out when it fits cap; *out_len is its length. */
+hs_status tc_fold_bytes(hs_batch *batch, const tc_tokenizer *tokenizer, const uint8_t *data,
+                        size_t len, uint32_t block_size, uint32_t overlap, uint8_t *out, size_t cap,
+                        size_t *out_len);
+
 /* Container::build of format version 2 (crates/taco-format/src/writer.rs:245-288) for the text
  * profile: kinds[b] is 0 (raw) or 1 (coded); coded blocks are blocks[block_offsets[b] ..
  * block_offsets[b + 1]). Returns the container length (the bytes are written if cap allows),

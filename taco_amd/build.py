@@ -13,10 +13,10 @@ BUILD = os.path.join(ROOT, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
 # Host-only sources go through the host compiler; the HIP runtime calls and kernels through hipcc.
-HOST_SOURCES = {"common.cpp", "hsm.cpp", "taco/harness.cpp"}
+HOST_SOURCES = {"common.cpp", "hsm.cpp", "taco/harness.cpp", "taco/tokenizer.cpp"}
 
 BACKEND_SOURCES = ["common.cpp", "hsm.cpp", "hs_api.cpp", "kernels.hip"]
-HARNESS_SOURCES = ["taco/harness.cpp", "common.cpp"]
+HARNESS_SOURCES = ["taco/harness.cpp", "taco/tokenizer.cpp"]  # hs::fail, sha256: the backend's (one error state)
 
 LIB_BACKEND = os.path.join(HERE, "libhardshell_hip.so")
 LIB_HARNESS = os.path.join(HERE, "libtaco_hip.so")

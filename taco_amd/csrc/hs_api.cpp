@@ -417,6 +417,23 @@ hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **
 
 extern "C" void hs_model_free(hs_model *model) { delete model; }
 
+extern "C" hs_status hs_model_token(const hs_model *model, uint32_t id, const uint8_t **bytes, size_t *len) {
+    hs::clear_error();
+    if (!model || !bytes || !len) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    const hs::HostModel &h = model->host;
+    if (id >= h.vocab) return hs::fail(HS_MODEL_ERROR, HS_MODEL_TOKEN_OUT_OF_RANGE, "token " + std::to_string(id) + " is not in the vocabulary");
+    const uint32_t s = id == 0 ? 0 : h.vocab_ends[id - 1];
+    *bytes = h.vocab_bytes.data() + s;
+    *len = h.vocab_ends[id] - s;
+    return HS_OK;
+}
+
+extern "C" size_t hs_model_merges(const hs_model *model, const uint32_t **pairs) {
+    if (!model) return 0;
+    if (pairs) *pairs = model->host.merges.data();
+    return model->host.merges.size() / 2;
+}
+
 extern "C" hs_status hs_model_validate(const uint8_t *bytes, size_t len, uint8_t hash[32]) {
     hs::clear_error();
     if (!bytes && len) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");

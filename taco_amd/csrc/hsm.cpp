@@ -615,6 +615,8 @@ bool load_host_model(const uint8_t *bytes, size_t len, HostModel &out, ModelErro
             auto it = by_bytes.find(joined);
             if (it == by_bytes.end()) return bad(field, "the joined bytes are not a token");
             if (it->second < 0) return bad(field, "two tokens have the joined bytes");
+            out.merges.push_back(l);
+            out.merges.push_back(rr);
         }
         cursor = off + ml;
     }

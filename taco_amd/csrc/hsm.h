@@ -54,6 +54,7 @@ struct HostModel {
     std::vector<uint64_t> logits_exp;
     std::vector<uint32_t> vocab_ends;  // token i is file bytes [vocab_off + start_i, end_i)
     std::vector<uint8_t> vocab_bytes;
+    std::vector<uint32_t> merges;  // the BPE merges in rank order, (left, right) id pairs
     bool is_wide() const;
 };
 

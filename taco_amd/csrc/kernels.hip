@@ -1154,14 +1154,18 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
 // F32 (8-bit outputs, beta_frac 0, |beta| <= 256): each element takes the single-precision rule
 // (ln_elem_f32, with beta folded into the addend); declined groups take the integer rule, as in
 // the double-precision form.
+// Waves per workgroup of the four-rows-per-wave form: 16 (64 rows) so the beta and gamma staging
+// of a workgroup serves four times the rows of a 4-wave workgroup.
+constexpr int LN_WAVES = 16;
+
 template <int NG, bool F32>
-__global__ __launch_bounds__(256) void k_layernorm_rows4(LnArgs a, int n_rows) {
+__global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int n_rows) {
     __shared__ __attribute__((aligned(16))) int32_t s_beta[64 * NG];
     __shared__ __attribute__((aligned(16))) double s_gamma[F32 ? 1 : 64 * NG];
     __shared__ __attribute__((aligned(16))) float s_gammaf[F32 ? 64 * NG : 1];
     __shared__ __attribute__((aligned(16))) float s_betaf[F32 ? 64 * NG : 1];  // 1/2 + beta
     const int lane = threadIdx.x & 63, q = lane & 15;
-    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const int row = (blockIdx.x * LN_WAVES + (threadIdx.x >> 6)) * 4 + (lane >> 4);
     const bool live = row < n_rows;
     const int d = a.d;
     const int32_t *x = a.x + (size_t)(live ? (a.src ? a.src[row] : row) : 0) * d;
@@ -1171,7 +1175,7 @@ __global__ __launch_bounds__(256) void k_layernorm_rows4(LnArgs a, int n_rows) {
         const int j = 4 * (q + 16 * t);
         xv[t] = (live && j < d) ? *(const v4i *)(x + j) : v4i{0, 0, 0, 0};
     }
-    for (int c = threadIdx.x; c < d; c += 256) {  // gamma as doubles or floats (exact)
+    for (int c = threadIdx.x; c < d; c += 64 * LN_WAVES) {  // gamma as doubles or floats (exact)
         s_beta[c] = a.beta[c];
         if (F32) {
             s_gammaf[c] = (float)a.gamma[c];
@@ -1323,11 +1327,11 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
         if (a.d <= 1024) hipLaunchKernelGGL(k_layernorm_rows<4>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
         else hipLaunchKernelGGL(k_layernorm_rows<8>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 768) {
-        if (f32) hipLaunchKernelGGL((k_layernorm_rows4<12, true>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
-        else hipLaunchKernelGGL((k_layernorm_rows4<12, false>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
+        if (f32) hipLaunchKernelGGL((k_layernorm_rows4<12, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        else hipLaunchKernelGGL((k_layernorm_rows4<12, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 1024) {
-        if (f32) hipLaunchKernelGGL((k_layernorm_rows4<16, true>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
-        else hipLaunchKernelGGL((k_layernorm_rows4<16, false>), dim3((n_rows + 15) / 16), dim3(256), 0, stream, a, n_rows);
+        if (f32) hipLaunchKernelGGL((k_layernorm_rows4<16, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        else hipLaunchKernelGGL((k_layernorm_rows4<16, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
         hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
     } else {

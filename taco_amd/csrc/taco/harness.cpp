@@ -464,3 +464,67 @@ extern "C" size_t tc_container_build(const uint8_t model_hash[32], const uint8_t
     if (o.size() <= cap && out) std::memcpy(out, o.data(), o.size());
     return o.size();
 }
+
+// The byte-level fold of the text profile (crates/taco/src/fold.rs:502-565): tokenize each
+// block (its tokens must restore its bytes, tokens_restore), code the blocks on the batch with a
+// stop at the block's length, and store each block as the smaller of its payload and its bytes.
+extern "C" hs_status tc_fold_bytes(hs_batch *batch, const tc_tokenizer *tok, const uint8_t *data, size_t len,
+                                   uint32_t block_size, uint32_t overlap, uint8_t *out, size_t cap,
+                                   size_t *out_len) {
+    hs::clear_error();
+    if (!batch || !tok || !out_len || (len && !data)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (block_size == 0) return hs::fail(HS_UNSUPPORTED, 0, "the block size must be at least 1");
+    const hs_model *model = hs_batch_model(batch);
+    const size_t count = (len + block_size - 1) / block_size;
+    std::vector<uint32_t> tokens;
+    std::vector<size_t> offsets(count + 1, 0), stop(count);
+    std::vector<uint32_t> ids;
+    for (size_t b = 0; b < count; b++) {
+        const size_t b0 = b * block_size, bl = std::min<size_t>(block_size, len - b0);
+        size_t n = 0;
+        ids.resize(bl + 1);  // at most one token per byte
+        hs_status s = tc_tokenize(tok, data + b0, bl, ids.data(), ids.size(), &n);
+        if (s != HS_OK) return s;
+        // tokens_restore: the bytes of the tokens are the block's bytes
+        size_t at = 0;
+        for (size_t i = 0; i < n; i++) {
+            const uint8_t *p;
+            size_t tl;
+            if ((s = hs_model_token(model, ids[i], &p, &tl)) != HS_OK) return s;
+            if (at + tl > bl || std::memcmp(data + b0 + at, p, tl) != 0)
+                return hs::fail(HS_MODEL_ERROR, HS_MODEL_VOCABULARY,
+                                "block " + std::to_string(b) + ": the tokens do not restore the block's bytes");
+            at += tl;
+        }
+        if (at != bl)
+            return hs::fail(HS_MODEL_ERROR, HS_MODEL_VOCABULARY,
+                            "block " + std::to_string(b) + ": the tokens do not restore the block's bytes");
+        tokens.insert(tokens.end(), ids.begin(), ids.begin() + n);
+        offsets[b + 1] = tokens.size();
+        stop[b] = bl;
+    }
+    // payloads of at most the block's bytes (a longer one is never chosen)
+    const size_t pcap = block_size + 16;
+    std::vector<uint8_t> payloads(count * pcap);
+    std::vector<size_t> lens(count);
+    if (count) {
+        hs_status s = tc_fold_blocks(batch, overlap, tokens.data(), offsets.data(), count, stop.data(),
+                                     payloads.data(), pcap, lens.data());
+        if (s != HS_OK) return s;
+    }
+    std::vector<uint8_t> kinds(count), blocks;
+    std::vector<size_t> boffs(count + 1, 0);
+    for (size_t b = 0; b < count; b++) {
+        const size_t bl = std::min<size_t>(block_size, len - b * block_size);
+        kinds[b] = lens[b] != SIZE_MAX && lens[b] < bl;  // Block::choose_smallest (writer.rs:71-104)
+        if (kinds[b]) blocks.insert(blocks.end(), payloads.begin() + b * pcap, payloads.begin() + b * pcap + lens[b]);
+        boffs[b + 1] = blocks.size();
+    }
+    uint8_t hash[32];
+    hs_model_hash(model, hash);
+    const size_t n = tc_container_build(hash, data, len, block_size, overlap, kinds.data(), blocks.data(),
+                                        boffs.data(), out, cap);
+    if (n == 0) return hs::fail(HS_DEVICE_ERROR, 0, "the container could not be built");
+    *out_len = n;
+    return HS_OK;
+}

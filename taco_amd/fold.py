@@ -28,6 +28,14 @@ def lib() -> C.CDLL:
         L.tc_unfold_blocks.argtypes = [P, C.c_uint32, P, P, S, P, S, P]
         L.tc_container_build.restype = S
         L.tc_container_build.argtypes = [P, P, S, C.c_uint32, C.c_uint32, P, P, P, P, S]
+        L.tc_tokenizer_new.argtypes = [P, P, S, C.c_uint32, P, S, C.POINTER(P)]
+        L.tc_tokenizer_for_model.argtypes = [P, C.POINTER(P)]
+        L.tc_tokenizer_free.argtypes = [P]
+        L.tc_tokenizer_free.restype = None
+        L.tc_tokenize.argtypes = [P, P, S, P, S, C.POINTER(S)]
+        L.tc_pretokenize.argtypes = [P, S, P, S]
+        L.tc_pretokenize.restype = S
+        L.tc_fold_bytes.argtypes = [P, P, P, S, C.c_uint32, C.c_uint32, P, S, C.POINTER(S)]
         _lib = L
     return _lib
 
@@ -110,3 +118,67 @@ def container(model_hash: bytes, original: bytes, block_size: int, overlap: int,
 def token_bytes(tokens: np.ndarray) -> bytes:
     """The original bytes of a stream of fixed-width 4-byte tokens (id -> its LE u32)."""
     return np.ascontiguousarray(tokens, dtype="<u4").tobytes()
+
+
+class Tokenizer:
+    """crates/taco/src/tokenizer (Tokenizer::new / for_vocabulary / encode) over tc_tokenizer."""
+
+    def __init__(self, h):
+        self.h = h
+
+    @classmethod
+    def from_parts(cls, tokens: Sequence[bytes], eot: Optional[int], merges) -> "Tokenizer":
+        blob = np.frombuffer(b"".join(tokens) or b"\0", np.uint8).copy()
+        offs = np.zeros(len(tokens) + 1, np.uint64)
+        offs[1:] = np.cumsum([len(t) for t in tokens])
+        pairs = np.ascontiguousarray(np.asarray(merges, np.uint32).reshape(-1, 2)) if len(merges) else np.zeros((1, 2), np.uint32)
+        h = C.c_void_p()
+        hip._check(lib().tc_tokenizer_new(_p(blob), _p(offs), len(tokens),
+                                          0xFFFFFFFF if eot is None else eot, _p(pairs), len(merges),
+                                          C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def for_model(cls, model: hip.HipModel) -> "Tokenizer":
+        h = C.c_void_p()
+        hip._check(lib().tc_tokenizer_for_model(model.h, C.byref(h)))
+        return cls(h)
+
+    def encode(self, data: bytes) -> np.ndarray:
+        buf = np.frombuffer(data or b"\0", np.uint8)
+        out = np.zeros(max(1, len(data)), np.uint32)
+        n = C.c_size_t()
+        hip._check(lib().tc_tokenize(self.h, _p(buf), len(data), _p(out), len(out), C.byref(n)))
+        return out[:n.value].copy()
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.tc_tokenizer_free(self.h)
+            self.h = None
+
+
+def pieces(text: bytes) -> List[bytes]:
+    """The GPT-2 pre-tokenizer pieces of well-formed UTF-8 text (tokenizer/pretokenize.rs)."""
+    buf = np.frombuffer(text or b"\0", np.uint8)
+    ends = np.zeros(max(1, len(text)), np.uint64)
+    n = lib().tc_pretokenize(_p(buf), len(text), _p(ends), len(ends))
+    if n == (1 << 64) - 1:
+        raise ValueError("not well-formed UTF-8")
+    out, s = [], 0
+    for e in ends[:n]:
+        out.append(text[s:int(e)])
+        s = int(e)
+    return out
+
+
+def fold_bytes(batch: hip.HipBatch, tokenizer: Tokenizer, data: bytes, block_size: int,
+               overlap: int = 0) -> bytes:
+    """The byte-level fold of the text profile (crates/taco/src/fold.rs:502-565) without zstd
+    candidates: the .taco container of data."""
+    buf = np.frombuffer(data or b"\0", np.uint8)
+    cap = 256 + 6 * len(data)
+    out = np.zeros(cap, np.uint8)
+    n = C.c_size_t()
+    hip._check(lib().tc_fold_bytes(batch.h, tokenizer.h, _p(buf), len(data), block_size, overlap,
+                                   _p(out), cap, C.byref(n)))
+    return out[:n.value].tobytes()

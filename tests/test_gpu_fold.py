@@ -184,3 +184,21 @@ def test_bench_fold_payloads_equal_the_cpu(dev):
         one = _payload_from_intervals(O.fast_window_intervals(om, blocks[w], chunk=32))
         detail.append((w, len(gpu[w]), len(cpu[w]), len(one), one == gpu[w], one == cpu[w]))
     assert not bad, f"windows {bad} differ; (w, gpu, cpu16, cpu1, cpu1==gpu, cpu1==cpu16): {detail}"
+
+
+@pytest.mark.parametrize("name,k", [("predicted_text_k0", 0), ("predicted_text_k32", 32)])
+def test_byte_level_fold_rebuilds_the_conformance_container(dev, name, k):
+    """The byte-level fold of the text profile (crates/taco/src/fold.rs:502-565): the .in bytes
+    cut into 300-byte blocks, tokenized with tiny.hsm's vocabulary and merges, coded on the GPU
+    and stored as the smaller of payload and bytes: the container equals the reference's byte
+    for byte (every block of these containers is coded, so no zstd candidate would have won)."""
+    from taco_amd import fold, hip
+    hsm = open(os.path.join(GOLDEN, "tiny.hsm"), "rb").read()
+    original = open(os.path.join(GOLDEN, name + ".in"), "rb").read()
+    want = open(os.path.join(GOLDEN, name + ".taco"), "rb").read()
+    hm = hip.HipModel.load(dev, hsm)
+    tok = fold.Tokenizer.for_model(hm)
+    batch = hip.HipBatch(hm, 4, 512)
+    batch.set_overlap(k)
+    got = fold.fold_bytes(batch, tok, original, 300, k)
+    assert got == want
