@@ -478,10 +478,7 @@ def run_gemm(args):
     for M, reps in ((256, 2000), (16384, 50)):
         a = rng.integers(-127, 128, (M, K)).astype(np.int8)
         mp, np_, kp = hip.gemm_layout(M, N, K)
-        wp = np.zeros((np_, kp), np.int8)
-        wp[:N, :K] = w
-        ap = np.zeros((mp, kp), np.int8)
-        ap[:M, :K] = a
+        wp, ap = hip.gemm_pack(w, np_, kp), hip.gemm_pack(a, mp, kp)
         bufs = [_dev_buf(hip, dev, x) for x in (wp, ap, bias, mult)]
         out = np.zeros((M, N), np.int8)
         dout = _dev_buf(hip, dev, out)

@@ -253,12 +253,14 @@ hs_status hs_op_gemm_requant_i8(hs_device *dev, const int8_t *w, const int8_t *a
                                 const int32_t *bias, const int32_t *mult, uint8_t shift, size_t m,
                                 size_t n, size_t k, int8_t *out);
 /* The same product on device-resident operands (device pointers, `stream` a hipStream_t or
- * NULL), with w and a padded as hs_op_gemm_layout() states. For measurements. */
+ * NULL), with w and a in the operand layout of hs_op_gemm_layout(). For measurements. */
 hs_status hs_op_gemm_requant_i8_dev(hs_device *dev, const int8_t *w, const int8_t *a,
                                     const int32_t *bias, const int32_t *mult, uint8_t shift,
                                     size_t m, size_t n, size_t k, int8_t *out, void *stream);
-/* The padded row strides that the _dev entry points expect: w is [n_pad, k_pad], a is
- * [m_pad, k_pad] (zero padding), out is [m, n] dense. */
+/* The operand layout of the _dev and _gpu_ns entry points: an operand of R padded rows (w:
+ * R = n_pad, a: R = m_pad) and k_pad columns is stored as k_pad / 64 panels of R rows x 64 bytes,
+ * element (r, c) at byte ((c / 64) * R + r) * 64 + c % 64, zero beyond the real rows and
+ * columns; out is [m, n] dense. */
 void hs_op_gemm_layout(size_t m, size_t n, size_t k, size_t *m_pad, size_t *n_pad,
                        size_t *k_pad);
 /* Integer decode attention, one query row per stream (batch rows of the decode path):

@@ -121,12 +121,22 @@ hipError_t fixed_scratch_of(int ordinal, void **out) {
 namespace {
 
 struct DevLinear {
-    int8_t *w = nullptr;  // [n_pad, k_pad]
+    int8_t *w = nullptr;  // panels [k_pad / 64][n_pad][64] (hs::panel_off)
     int32_t *b = nullptr, *m = nullptr;
     int s = 0, n = 0, k = 0, n_pad = 0, k_pad = 0;
     int fast32 = 0;  // k * 2^14 + max|b| < 2^31: every acc + b fits i32
     int32_t *wsum = nullptr;  // sum_k w[n][k], for an i16 input as planes (|wsum| <= 2^23)
 };
+
+// A GEMM operand of `rows` dense rows of `cols` bytes as the kernels read it: panels of 64 bytes
+// of K, [k_pad / 64][rows_pad][64], zero beyond the rows and columns.
+std::vector<int8_t> pack_panels(const int8_t *src, size_t rows, size_t cols, size_t rows_pad, size_t k_pad) {
+    std::vector<int8_t> p(rows_pad * k_pad, 0);
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c0 = 0; c0 < cols; c0 += 64)
+            std::memcpy(&p[hs::panel_off(r, c0, rows_pad)], src + r * cols + c0, std::min<size_t>(64, cols - c0));
+    return p;
+}
 
 // The row sums of w [n, k] (i8), exact in i32 (|sum| <= k 2^7 <= 2^23).
 std::vector<int32_t> row_sums(const int8_t *w, size_t n, size_t k, size_t n_pad) {
@@ -173,7 +183,7 @@ struct hs_model {
     DevMem mem;
     int d = 0, f = 0, V = 0, C = 0, H = 0, hd = 0, L = 0;
     int d_pad = 0, f_pad = 0, V_pad = 0;
-    int8_t *wte = nullptr;  // [V_pad, d_pad]: the LM head operand; the embedding reads row tok
+    int8_t *wte = nullptr;  // the LM head operand, panels of V_pad rows; the embedding reads row tok
     int32_t *wte_sum = nullptr;  // row sums of wte, for a 16-bit ln_f (version 2)
     bool wide_ln_f = false, wide_gelu = false;
     int8_t *wpe = nullptr;  // [C, d]
@@ -196,8 +206,7 @@ hs_status upload_linear(DevMem &mem, const hs::HostLinear &l, DevLinear &o) {
     o.k = (int)l.cols;
     o.n_pad = (int)round_up(l.rows, hs::GEMM_NPAD);
     o.k_pad = (int)round_up(l.cols, hs::GEMM_BK);
-    std::vector<int8_t> w((size_t)o.n_pad * o.k_pad, 0);
-    for (uint32_t r = 0; r < l.rows; r++) std::memcpy(&w[(size_t)r * o.k_pad], l.w + (size_t)r * l.cols, l.cols);
+    const std::vector<int8_t> w = pack_panels(l.w, l.rows, l.cols, o.n_pad, o.k_pad);
     hs_status st = mem.upload(o.w, w.data(), w.size());
     if (st == HS_OK) st = mem.upload(o.b, l.b.data(), l.b.size(), o.n_pad);
     if (st == HS_OK) st = mem.upload(o.m, l.m.data(), l.m.size(), o.n_pad);
@@ -363,8 +372,7 @@ hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **
     DevMem &mem = m->mem;
     hs_status st;
     {
-        std::vector<int8_t> w((size_t)m->V_pad * m->d_pad, 0);
-        for (int v = 0; v < m->V; v++) std::memcpy(&w[(size_t)v * m->d_pad], h.wte + (size_t)v * m->d, m->d);
+        const std::vector<int8_t> w = pack_panels(h.wte, m->V, m->d, m->V_pad, m->d_pad);
         if ((st = mem.upload(m->wte, w.data(), w.size())) != HS_OK) return st;
     }
     m->wide_ln_f = h.ln_f_bits == 16;
@@ -669,8 +677,9 @@ extern "C" hs_status hs_batch_new(hs_model *model, size_t slots, size_t max_rows
     if ((s = mem.alloc(b->d_src, R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_groups, R)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_x, R * m.d)) != HS_OK) return s;
+    // the operands of the products (d_a, d_af, d_att, d_g) are panels of RP operand rows (2 RP
+    // for i16 activations: each row is two operand rows, its planes)
     if ((s = mem.alloc(b->d_a, RP * m.d_pad)) != HS_OK) return s;
-    // an i16 activation row is two operand rows (its planes)
     if ((s = mem.alloc(b->d_af, (m.wide_ln_f ? 2 : 1) * RP * m.d_pad)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_qkv, R * 3 * m.d)) != HS_OK) return s;
     if ((s = mem.alloc(b->d_att, RP * m.d_pad)) != HS_OK) return s;
@@ -906,27 +915,32 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     uint64_t attn_keys = 0;  // sum over rows of the keys each row reads
     for (int r = 0; r < n; r++) attn_keys += (uint64_t)rows[r].pos + 1;
     HIP_TRY(b.launch("embed", 0, [&] {
-        return hs::launch_embed(b.d_rows, n, m.wte, m.d_pad, m.wpe, m.embed_m, m.host.embed_s,
+        return hs::launch_embed(b.d_rows, n, m.wte, m.V_pad, m.wpe, m.embed_m, m.host.embed_s,
                                 m.pos_m, m.host.pos_s, m.d, b.d_x, st);
     }));
+    const int RP = (int)b.rows_pad;  // the panel rows of the operand buffers (per plane)
     auto ln = [&](const DevLn &l, const int32_t *src_rows, int rows_n, int8_t *dst, int out_bits = 8) {
         hs::LnArgs a;
         a.bits = out_bits;
         a.x = b.d_x; a.d = m.d; a.gamma = l.g; a.beta = l.b; a.m = l.m; a.s = l.s;
         a.beta_frac = m.host.ln_beta_frac; a.k = m.host.ln_k; a.j = m.host.ln_j; a.eps = m.host.ln_eps;
-        a.out = dst; a.ldo = m.d_pad; a.src = src_rows; a.gm = l.gm; a.beta_small = l.beta_small;
+        a.out = dst; a.out_rows = (out_bits == 16 ? 2 : 1) * RP;
+        a.src = src_rows; a.gm = l.gm; a.beta_small = l.beta_small;
         return b.launch("layer_norm", 0, [&] { return hs::launch_layernorm(a, rows_n, st); });
     };
     // The LM head: the rows of a chunk (at most a few MB of A) stay in every XCD's L2 while
     // each XCD streams its own slice of wte once (all M-tiles in one group, N outermost).
     auto head_group = [](int rows) { return (rows + hs::GEMM_BM - 1) / hs::GEMM_BM; };
-    auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int rows_n,
+    // `a` holds panels of a_rows rows; the GELU products write panels of the same row count (RP
+    // rows per plane)
+    auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int a_rows, int rows_n,
                     void *o, int ldo, const int8_t *gelu = nullptr, int gelu_off = 0,
                     const int16_t *gelu16 = nullptr, int group = 0) {
         hs::GemmArgs g;
         g.group = group;
-        g.a = a; g.w = lin.w; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
+        g.a = a; g.a_rows = a_rows; g.w = lin.w; g.w_rows = lin.n_pad; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
+        g.out_rows = (epi == Epi::GeluWide ? 2 : 1) * RP;
         g.fast32 = epi == Epi::ResidualWide ? 0 : lin.fast32;
         g.gelu = gelu; g.gelu16 = gelu16; g.gelu_off = gelu_off; g.wsum = lin.wsum;
         g.partials = b.gsplit; g.partials_cap = b.gsplit_elems;
@@ -989,7 +1003,8 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         HIP_TRY(ln(blk.ln1, nullptr, n, b.d_a));
         if (kv_fused) {  // K and V go from the c_attn epilogue straight into the caches
             hs::GemmArgs g;
-            g.a = b.d_a; g.w = blk.c_attn.w; g.m = n; g.n = blk.c_attn.n; g.k_pad = blk.c_attn.k_pad;
+            g.a = b.d_a; g.a_rows = RP; g.w = blk.c_attn.w; g.w_rows = blk.c_attn.n_pad;
+            g.m = n; g.n = blk.c_attn.n; g.k_pad = blk.c_attn.k_pad;
             g.bias = blk.c_attn.b; g.mult = blk.c_attn.m; g.shift = blk.c_attn.s; g.out = b.d_qkv;
             g.ldo = 3 * m.d; g.fast32 = blk.c_attn.fast32;
             g.kv_rows = b.d_rows; g.kc = b.kc[l]; g.vc = b.vc[l];
@@ -998,7 +1013,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             const uint64_t ops = 2ull * (uint64_t)n * (uint64_t)blk.c_attn.n * (uint64_t)blk.c_attn.k;
             HIP_TRY(b.launch("gemm_qkv", ops, [&] { return hs::launch_gemm(Epi::Act, g, st); }));
         } else {
-            HIP_TRY(gemm("gemm_qkv", Epi::Act, blk.c_attn, b.d_a, n, b.d_qkv, 3 * m.d));
+            HIP_TRY(gemm("gemm_qkv", Epi::Act, blk.c_attn, b.d_a, RP, n, b.d_qkv, 3 * m.d));
             HIP_TRY(b.launch("kv_store", 0, [&] {
                 return hs::launch_kv_store(b.d_rows, n, b.d_qkv, m.d, m.H, m.hd, m.C, b.kc[l], b.vc[l], st);
             }));
@@ -1008,21 +1023,21 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         at.n_head = m.H; at.hd = m.hd; at.ctx_cap = m.C; at.score_m = blk.score_m; at.score_s = blk.score_s;
         at.out_m = blk.out_m; at.out_s = blk.out_s; at.exp_table = m.attn_exp;
         at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
-        at.out = b.d_att; at.ldo = m.d_pad;
+        at.out = b.d_att; at.out_rows = RP;
         HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d, [&] {
             if (mfma_attn) return hs::launch_attend_groups(at, b.d_groups, n_groups, group_keys, st);
             if (split_attn) return hs::launch_attend_split(at, n, split_plan, b.split, st);
             return hs::launch_attend(at, n, st);
         }));
-        HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, n, b.d_x, m.d));
+        HIP_TRY(gemm("gemm_proj", Epi::Residual, blk.c_proj, b.d_att, RP, n, b.d_x, m.d));
         HIP_TRY(ln(blk.ln2, nullptr, n, b.d_a));
         if (blk.gelu16) {  // i16 GELU outputs as planes, mlp_proj over 2n operand rows
-            HIP_TRY(gemm("gemm_fc", Epi::GeluWide, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, nullptr, blk.gelu_off,
+            HIP_TRY(gemm("gemm_fc", Epi::GeluWide, blk.c_fc, b.d_a, RP, n, b.d_g, 0, nullptr, blk.gelu_off,
                          blk.gelu16));
-            HIP_TRY(gemm("gemm_mlp", Epi::ResidualWide, blk.mlp_proj, b.d_g, 2 * n, b.d_x, m.d));
+            HIP_TRY(gemm("gemm_mlp", Epi::ResidualWide, blk.mlp_proj, b.d_g, 2 * RP, 2 * n, b.d_x, m.d));
         } else {
-            HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, n, b.d_g, m.f_pad, blk.gelu, blk.gelu_off));
-            HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, n, b.d_x, m.d));
+            HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, RP, n, b.d_g, 0, blk.gelu, blk.gelu_off));
+            HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, RP, n, b.d_x, m.d));
         }
     }
     if (n_out == 0) {
@@ -1046,7 +1061,9 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         const int cn = std::min<int>((int)b.chunk_rows, n_out - c0);
         if (m.compact) {
             hs::GemmArgs g;
-            g.a = b.d_af + (size_t)pr * c0 * m.d_pad; g.w = m.wte; g.m = pr * cn; g.n = m.V; g.k_pad = m.d_pad;
+            // the chunk's operand rows start at row pr c0 of the panels of pr RP rows
+            g.a = b.d_af + (size_t)pr * c0 * 64; g.a_rows = pr * RP; g.w = m.wte; g.w_rows = m.V_pad;
+            g.m = pr * cn; g.n = m.V; g.k_pad = m.d_pad;
             g.mult = m.logit_m; g.shift = m.host.logit_s; g.out = b.d_d16; g.ldo = m.ld16;
             g.tmax = b.d_tmax; g.tmax_ld = m.ntiles; g.cap16 = (int)m.host.logits_exp.size() - 1;
             g.wsum = m.wte_sum;
@@ -1079,7 +1096,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             }
         } else {
             HIP_TRY(gemm("gemm_logits", m.wide_ln_f ? Epi::LogitsWide : Epi::Logits, head,
-                         b.d_af + (size_t)pr * c0 * m.d_pad, pr * cn, b.d_logits, m.V, nullptr, 0,
+                         b.d_af + (size_t)pr * c0 * 64, pr * RP, pr * cn, b.d_logits, m.V, nullptr, 0,
                          nullptr, head_group(pr * cn)));
             hs::CoderArgs ca;
             ca.logits = b.d_logits; ca.ld = m.V; ca.vocab = m.V; ca.table = m.logits_exp;
@@ -1348,9 +1365,7 @@ hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, c
     HIP_TRY(hipSetDevice(dev->ordinal));
     size_t mp, np, kp;
     hs_op_gemm_layout(m, n, k, &mp, &np, &kp);
-    std::vector<int8_t> wp(np * kp, 0), ap(mp * kp, 0);
-    for (size_t r = 0; r < n; r++) std::memcpy(&wp[r * kp], w + r * k, k);
-    for (size_t r = 0; r < m; r++) std::memcpy(&ap[r * kp], a + r * k, k);
+    const std::vector<int8_t> wp = pack_panels(w, n, k, np, kp), ap = pack_panels(a, m, k, mp, kp);
     DevMem mem;
     int8_t *dw, *da;
     int32_t *db = nullptr, *dm = nullptr;
@@ -1407,17 +1422,14 @@ extern "C" hs_status hs_op_gemm_i8_i16(hs_device *dev, const int8_t *w, const in
     // 2m rows, then 256 hi + lo + 128 wsum per output
     size_t mp, np, kp;
     hs_op_gemm_layout(2 * m, n, k, &mp, &np, &kp);
-    std::vector<int8_t> wp(np * kp, 0), ap(mp * kp, 0);
-    std::vector<int32_t> wsum(n, 0);
-    for (size_t r = 0; r < n; r++) {
-        std::memcpy(&wp[r * kp], w + r * k, k);
-        for (size_t j = 0; j < k; j++) wsum[r] += w[r * k + j];
-    }
+    const std::vector<int8_t> wp = pack_panels(w, n, k, np, kp);
+    const std::vector<int32_t> wsum = row_sums(w, n, k, n);
+    std::vector<int8_t> ap(mp * kp, 0);
     for (size_t i = 0; i < m; i++)
         for (size_t j = 0; j < k; j++) {
             const int32_t v = a[i * k + j];
-            ap[(2 * i) * kp + j] = (int8_t)(v >> 8);
-            ap[(2 * i + 1) * kp + j] = (int8_t)((v & 255) - 128);
+            ap[hs::panel_off(2 * i, j, mp)] = (int8_t)(v >> 8);
+            ap[hs::panel_off(2 * i + 1, j, mp)] = (int8_t)((v & 255) - 128);
         }
     DevMem mem;
     int8_t *dw, *da;

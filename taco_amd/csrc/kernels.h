@@ -25,15 +25,25 @@ enum class Epi : int {
     LogitsCompactWide = 9  // as LogitsCompact over planes
 };
 
+// GEMM operands are stored as panels of 64 bytes of K: an operand of R rows and K columns (a
+// multiple of 64) holds element (r, k) at ((k / 64) * R + r) * 64 + k % 64, so the 16 rows x 64
+// bytes of an MFMA fragment are 1 KiB of contiguous memory (full cache lines for the loads).
+// panel_off gives the byte offset; R is the operand's panel row count (its padded rows).
+__host__ __device__ inline size_t panel_off(size_t r, size_t k, size_t rows) {
+    return ((k >> 6) * rows + r) * 64 + (k & 63);
+}
+
 struct GemmArgs {
-    const int8_t *a = nullptr;  // [m_pad, k_pad]
-    const int8_t *w = nullptr;  // [n_pad, k_pad]
+    const int8_t *a = nullptr;  // panels [k_pad / 64][a_rows][64], rows m_pad and more
+    const int8_t *w = nullptr;  // panels [k_pad / 64][w_rows][64], w_rows >= n_pad
+    int a_rows = 0, w_rows = 0;  // the panel row counts (0: m_pad and n_pad)
     int m = 0, n = 0, k_pad = 0;
     const int32_t *bias = nullptr;  // [n] (Act, Residual, Gelu)
     const int32_t *mult = nullptr;  // [n]
     int shift = 0;
     void *out = nullptr;  // Raw: i32; Act/Gelu: i8; Residual: i32 x (read-modify-write); Logits: i64
     int ldo = 0;          // elements per output row
+    int out_rows = 0;     // Gelu/GeluWide: the output is an operand, in panels of out_rows rows
     const int8_t *gelu = nullptr;     // Gelu table, i8 entries
     const int16_t *gelu16 = nullptr;  // GeluWide table, i16 entries
     int gelu_off = 0;                 // half the table length (128 or 32768)
@@ -92,7 +102,7 @@ size_t gemm_split_elems(int m, int n, int splits);
 hipError_t launch_wide_combine(const int32_t *planes, const int32_t *wsum, int m, int n, int64_t *out,
                                hipStream_t stream);
 
-hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_ld,
+hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_rows,
                         const int8_t *wpe, const int32_t *embed_m, int embed_s,
                         const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream);
 
@@ -106,8 +116,8 @@ struct LnArgs {
     int beta_frac = 0;
     int k = 0, j = 0;
     uint64_t eps = 1;
-    int8_t *out = nullptr;  // [rows, ldo]
-    int ldo = 0;
+    int8_t *out = nullptr;  // the operand panels [d_pad / 64][out_rows][64]
+    int out_rows = 0;
     const int32_t *src = nullptr;  // optional: output row i reads x row src[i]
     const int64_t *gm = nullptr;   // gamma[j] * m, exact in i64 (|gamma m| < 2^46)
     int bits = 8;                  // 16: clamp to +-32767 and write the two i8 planes of each row
@@ -139,8 +149,9 @@ struct AttnArgs {
     const int32_t *exp_table = nullptr;
     int exp_len = 0;
     int softmax_p = 0;
-    int8_t *out = nullptr;  // row r, head h at out[r * ldo + h * hd]
+    int8_t *out = nullptr;  // row r, head h at out[r * ldo + h * hd] (out_rows 0)
     int ldo = 0;
+    int out_rows = 0;  // > 0: out is an operand in panels of out_rows rows (panel_off)
 };
 hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream);
 

@@ -37,8 +37,8 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 }
 
 // =============================================================================================
-// Int8 GEMM on MFMA: C[m][n] = sum_k A[m][k] * W[n][k] (both operands K-contiguous, "NT"),
-// exact int32 (|C| <= 2^30 for K <= 2^16, crates/hardshell/src/kernels.rs:24-29), with the
+// Int8 GEMM on MFMA: C[m][n] = sum_k A[m][k] * W[n][k] (both operands in panels of 64 bytes of
+// K, panel_off; "NT"), exact int32 (|C| <= 2^30 for K <= 2^16, crates/hardshell/src/kernels.rs:24-29), with the
 // requantize epilogue of the op fused (crates/hardshell/src/gpt2/ops.rs:107-176).
 //
 // Block tile 256 x 128 x 64, 256 threads = 4 waves in 2 x 2; each wave owns 128 x 64 = 8 x 4
@@ -115,14 +115,13 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     };
 
     if constexpr (BN == 256) {
-        // 256 x 256 tiles (8 waves, one workgroup per CU) stream stages of 128 k: each row's
-        // 128 bytes are one full cache line, eight lanes to a row (8 rows per instruction), which
-        // the memory path delivers at about 1.5 times the rate of the half lines of 64-k stages
-        // (measured). Row r's 16-byte chunk c sits at r * 128 + 16 (c ^ ((r >> 1) & 7)) of the
-        // stage, so the MFMA reads of 16 consecutive rows (one chunk) hit 16 distinct bank
-        // groups. Two stages of 64 KiB: the next stage loads while this one is multiplied.
-        // A k_pad that is an odd multiple of 64 ends with a half stage (chunks 0-3 only; the
-        // lanes of chunks 4-7 reload an in-row chunk that nothing reads).
+        // 256 x 256 tiles (8 waves, one workgroup per CU) stream stages of 128 k (two panels),
+        // eight lanes to a row (8 rows per instruction, 512 contiguous bytes of each panel).
+        // Row r's 16-byte chunk c sits at r * 128 + 16 (c ^ ((r >> 1) & 7)) of the stage, so the
+        // MFMA reads of 16 consecutive rows (one chunk) hit 16 distinct bank groups. Two stages
+        // of 64 KiB: the next stage loads while this one is multiplied. A k_pad that is an odd
+        // multiple of 64 ends with a half stage (chunks 0-3 only; the lanes of chunks 4-7 reload
+        // a chunk of the last panel that nothing reads).
         constexpr int ROWS = GEMM_BM + BN, LD = ROWS / 8 / WAVES, SB = ROWS * 128;
         const int nk2 = (K + 127) / 128;
         const bool half = (K & 127) != 0;
@@ -133,19 +132,21 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         const int ld_r = lane >> 3, ld_s = lane & 7;
         const int row0 = wave * LD * 8 + ld_r;  // the row of instruction 0 (row of i = row0 + 8 i)
         const int c_even = ld_s ^ ((row0 >> 1) & 7), c_odd = c_even ^ 4;
-        const int8_t *base_row = row0 < GEMM_BM ? g.a + (size_t)(m0 + row0) * K
-                                                : g.w + (size_t)(n0 + row0 - GEMM_BM) * K;
-        const int8_t *p_even = base_row + c_even * 16, *p_odd = base_row + (size_t)8 * K + c_odd * 16;
-        const size_t stride16 = (size_t)16 * K;
-        // a half stage: the lanes whose chunk is 4-7 step back 64 bytes to an in-row chunk
-        const int h_even = c_even >= 4 ? -64 : 0, h_odd = c_odd >= 4 ? -64 : 0;
+        const bool is_a = wave * LD * 8 < GEMM_BM;  // uniform per wave
+        const size_t pb = (size_t)(is_a ? g.a_rows : g.w_rows) * 64;  // bytes per panel
+        const int8_t *base_row = is_a ? g.a + (size_t)(m0 + row0) * 64 : g.w + (size_t)(n0 + row0 - GEMM_BM) * 64;
+        const int8_t *p_even = base_row + (c_even >> 2) * pb + (c_even & 3) * 16;
+        const int8_t *p_odd = base_row + 8 * 64 + (c_odd >> 2) * pb + (c_odd & 3) * 16;
+        // a half stage: the lanes whose chunk is 4-7 step back one panel
+        const long long h_even = c_even >= 4 ? -(long long)pb : 0, h_odd = c_odd >= 4 ? -(long long)pb : 0;
         auto issue = [&](int kt, int stage) {
             int8_t *base = gemm_lds + stage * SB + wave * LD * 1024;
             const bool last_half = half && kt == nk2 - 1;
-            const int oe = kt * 128 + (last_half ? h_even : 0), oo = kt * 128 + (last_half ? h_odd : 0);
+            const long long ok = (long long)kt * 2 * (long long)pb;
+            const long long oe = ok + (last_half ? h_even : 0), oo = ok + (last_half ? h_odd : 0);
 #pragma unroll
             for (int i = 0; i < LD; i++) {
-                const int8_t *p = (i & 1 ? p_odd + oo : p_even + oe) + (size_t)(i >> 1) * stride16;
+                const int8_t *p = (i & 1 ? p_odd + oo : p_even + oe) + (i >> 1) * 1024;
                 __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + i * 1024), 16, 0, 0);
             }
         };
@@ -205,28 +206,33 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int nk = (g.kslice ? min(g.kslice, K - kb0) : K) / GEMM_BK;
 
     // This wave loads fragments LOADS * wave .. +LOADS of each stage (0..15: A row blocks, then
-    // the W row blocks, of 16 rows x 64 bytes). Each lane quad reads one row's 64
-    // contiguous bytes (lane l: row l / 4, 16-byte chunk (l % 4) ^ sw(row)), so a load touches
-    // 16 lines, one per quad. The fragment lands in LDS in lane order, so chunk c of row r sits
-    // at 16-byte slot 4 r + (c ^ sw(r)); sw(r) = ((r >> 1) ^ (r >> 3)) % 4 makes the MFMA operand
-    // reads (lane l: row l % 16, chunk l / 16) of any 8 (and any 16) consecutive lanes hit
-    // distinct 16-byte bank groups.
+    // the W row blocks, of 16 rows x 64 bytes). Each lane quad reads one row's 64 bytes of the
+    // panel (lane l: row l / 4, 16-byte chunk (l % 4) ^ sw(row)); the 16 rows of a fragment are
+    // adjacent in the panel, so a load reads 1 KiB of contiguous memory, 8 whole 128-byte lines.
+    // The fragment lands in LDS in lane order, so chunk c of row r sits at 16-byte slot
+    // 4 r + (c ^ sw(r)); sw(r) = ((r >> 1) ^ (r >> 3)) % 4 makes the MFMA operand reads (lane l:
+    // row l % 16, chunk l / 16) of any 8 (and any 16) consecutive lanes hit distinct 16-byte
+    // bank groups.
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
+    const size_t pa = (size_t)g.a_rows * 64, pw = (size_t)g.w_rows * 64;  // bytes per panel
     const int8_t *src[LOADS];
 #pragma unroll
     for (int i = 0; i < LOADS; i++) {
         const int f = wave * LOADS + i;
         const int r = lane >> 2, c = (lane & 3) ^ sw(r);
         const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + r;
-        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(m0 + row) * K : g.w + (size_t)(n0 + row) * K) + kb0 + c * 16;
+        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(kb0 / GEMM_BK) * pa + (size_t)(m0 + row) * 64
+                                   : g.w + (size_t)(kb0 / GEMM_BK) * pw + (size_t)(n0 + row) * 64) + c * 16;
     }
     const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ sw(lane & 15));
     auto issue = [&](int kt, int stage) {
         int8_t *base = gemm_lds + stage * (FRAGS * 1024) + wave * LOADS * 1024;
 #pragma unroll
-        for (int i = 0; i < LOADS; i++)
-            __builtin_amdgcn_global_load_lds((const void *)(src[i] + kt * GEMM_BK),
+        for (int i = 0; i < LOADS; i++) {
+            const size_t step = wave * LOADS + i < GEMM_BM / 16 ? pa : pw;
+            __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)kt * step),
                                              (lds_void *)(base + i * 1024), 16, 0, 0);
+        }
     };
 
     // The operand fragments of k-step kt + 1 are read from LDS while the MFMAs of k-step kt
@@ -531,8 +537,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                                 (part ? g.vc : g.kc)[(((size_t)ri.slot * g.kv_h + hh) * g.kv_ctx + ri.pos) * g.kv_hd + cc] = v;
                                 continue;
                             }
-                            const size_t orow = EPI == (int)Epi::GeluWide ? 2 * (size_t)m + pl : (size_t)m;
-                            ((int8_t *)g.out)[orow * g.ldo + n] = v;
+                            if (EPI == (int)Epi::Act) {
+                                ((int8_t *)g.out)[(size_t)m * g.ldo + n] = v;
+                            } else {  // the operand of the next product, in panels
+                                const size_t orow = EPI == (int)Epi::GeluWide ? 2 * (size_t)m + pl : (size_t)m;
+                                ((int8_t *)g.out)[panel_off(orow, n, g.out_rows)] = v;
+                            }
                         }
                 continue;
             }
@@ -565,7 +575,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                     continue;
                 }
                 const size_t orow = EPI == (int)Epi::GeluWide ? 2 * (size_t)m + pl : (size_t)m;
-                int8_t *o = (int8_t *)g.out + orow * g.ldo + n;
+                // Gelu and GeluWide write the operand of the next product, in panels (16 columns
+                // from a multiple of 16 lie in one panel)
+                int8_t *o = (int8_t *)g.out + (EPI == (int)Epi::Act ? orow * g.ldo + n : panel_off(orow, n, g.out_rows));
                 if (n + 16 <= g.n) {
                     *(v4i *)o = v;
                 } else {
@@ -684,7 +696,9 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
         constexpr size_t ES = EPI == (int)Epi::Residual || EPI == (int)Epi::Raw ? 4
                               : EPI == (int)Epi::LogitsCompact ? 2
                               : EPI == (int)Epi::Logits ? 8 : 1;
-        const bool vec = ((uintptr_t)g.out & 15) == 0 && ((size_t)g.ldo * ES) % 16 == 0;
+        // (the GELU outputs are panels of 64-byte rows: aligned when the base is)
+        constexpr bool PANEL_OUT = EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
+        const bool vec = ((uintptr_t)g.out & 15) == 0 && (PANEL_OUT || ((size_t)g.ldo * ES) % 16 == 0);
         if (!vec) return launch_gemm_t<EPI, NARROW, 128, false>(g, stream);
         // 256 x 256 tiles (one workgroup per CU, full-line 128-k stages) for long K, where their
         // faster main loop outweighs the lost overlap of a second workgroup per CU and the
@@ -808,11 +822,12 @@ __global__ __launch_bounds__(256) void k_split_epi(GemmArgs g, int splits, int l
         } else {
             store4((int8_t *)g.out + (size_t)m * g.ldo + n4, [&](int e) { return b[e]; });
         }
-    } else if (EPI == (int)Epi::Gelu) {
-        store4((int8_t *)g.out + (size_t)m * g.ldo + n4, [&](int e) { return b[e]; });
+    } else if (EPI == (int)Epi::Gelu) {  // the operand of the next product, in panels
+        store4((int8_t *)g.out + panel_off(m, n4, g.out_rows), [&](int e) { return b[e]; });
     } else {  // GeluWide: the two planes of each i16 output, hi = v >> 8, lo = (v & 255) - 128
-        store4((int8_t *)g.out + (size_t)(2 * m) * g.ldo + n4, [&](int e) { return (uint32_t)((int32_t)(int16_t)b[e] >> 8); });
-        store4((int8_t *)g.out + (size_t)(2 * m + 1) * g.ldo + n4,
+        store4((int8_t *)g.out + panel_off(2 * (size_t)m, n4, g.out_rows),
+               [&](int e) { return (uint32_t)((int32_t)(int16_t)b[e] >> 8); });
+        store4((int8_t *)g.out + panel_off(2 * (size_t)m + 1, n4, g.out_rows),
                [&](int e) { return (uint32_t)(((int32_t)(int16_t)b[e] & 255) - 128); });
     }
 }
@@ -884,6 +899,13 @@ hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
     const int gm = (g.m + GEMM_BM - 1) / GEMM_BM;
     if (g.group == 0) g.group = gemm_group(g.m);
     if (g.group < 1 || g.group > gm) return hipErrorInvalidValue;
+    // the panel row counts cover every row a tile reads (whole 256-row tiles of A and of W)
+    const int n_pad = (g.n + GEMM_NPAD - 1) / GEMM_NPAD * GEMM_NPAD;
+    if (g.a_rows == 0) g.a_rows = gm * GEMM_BM;
+    if (g.w_rows == 0) g.w_rows = n_pad;
+    if (g.a_rows < gm * GEMM_BM || g.w_rows < n_pad) return hipErrorInvalidValue;
+    if ((epi == Epi::Gelu && g.out_rows < g.m) || (epi == Epi::GeluWide && g.out_rows < 2 * g.m))
+        return hipErrorInvalidValue;
     g.kslice = 0;
     if (g.partials) {
         const int sp = gemm_split_plan(epi, g.m, g.n, g.k_pad, g.splits);
@@ -940,22 +962,23 @@ hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipS
 // Embedding (reference.rs:208-221): x = clamp(rescale(wte[tok]) + rescale(wpe[pos]), -R, R).
 // =============================================================================================
 
-__global__ void k_embed(const RowInfo *rows, const int8_t *wte, int wte_ld, const int8_t *wpe,
+// wte is the LM head's operand: panels of wte_rows rows (panel_off).
+__global__ void k_embed(const RowInfo *rows, const int8_t *wte, int wte_rows, const int8_t *wpe,
                         const int32_t *embed_m, int embed_s, const int32_t *pos_m, int pos_s,
                         int d, int32_t *x) {
     const int r = blockIdx.x, j = blockIdx.y * blockDim.x + threadIdx.x;
     if (j >= d) return;
     const RowInfo ri = rows[r];
-    const int64_t v = rescale_small(wte[(size_t)ri.token * wte_ld + j], embed_m[ri.token], embed_s) +
+    const int64_t v = rescale_small(wte[panel_off(ri.token, j, wte_rows)], embed_m[ri.token], embed_s) +
                       rescale_small(wpe[(size_t)ri.pos * d + j], pos_m[ri.pos], pos_s);
     x[(size_t)r * d + j] = (int32_t)clamp64(v, -RES, RES);
 }
 
-hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_ld,
+hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_rows,
                         const int8_t *wpe, const int32_t *embed_m, int embed_s,
                         const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream) {
     dim3 grid(n_rows, (d + 255) / 256);
-    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_ld, wpe, embed_m,
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_rows, wpe, embed_m,
                        embed_s, pos_m, pos_s, d, x);
     return hipGetLastError();
 }
@@ -1009,15 +1032,17 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
     const bool wide = a.bits == 16;
-    int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+    // the operand rows of this row (two planes when wide), in panels (panel_off)
+    const size_t orow = (size_t)row * (wide ? 2 : 1);
+    auto at = [&](int pl, int j) { return a.out + panel_off(orow + pl, j, a.out_rows); };
     // clamp_act_i8, or clamp_act_i16 stored as the planes hi = v >> 8, lo = (v & 255) - 128
     auto put = [&](int j, int64_t y) {
         if (!wide) {
-            out[j] = (int8_t)clamp64(y, -127, 127);
+            *at(0, j) = (int8_t)clamp64(y, -127, 127);
         } else {
             const int32_t v = (int32_t)clamp64(y, -32767, 32767);
-            out[j] = (int8_t)(v >> 8);
-            out[a.ldo + j] = (int8_t)((v & 255) - 128);
+            *at(0, j) = (int8_t)(v >> 8);
+            *at(1, j) = (int8_t)((v & 255) - 128);
         }
     };
     if (small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126) {
@@ -1092,7 +1117,9 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
     const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
     const bool wide = a.bits == 16;
-    int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+    // the operand rows of this row (two planes when wide), in panels (panel_off)
+    const size_t orow = (size_t)row * (wide ? 2 : 1);
+    auto at = [&](int pl, int j) { return a.out + panel_off(orow + pl, j, a.out_rows); };
     // Each element first takes the double-precision form of the rule (ln_elem_f64), which gives
     // the exact integer or declines; a declined element takes the integer rule below.
     const bool fpath = a.beta_frac == 0 && a.s <= 126;
@@ -1140,8 +1167,8 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
                 packed_lo |= (uint32_t)(uint8_t)((v & 255) - 128) << (8 * e);
             }
         }
-        *(uint32_t *)(out + j) = packed;
-        if (wide) *(uint32_t *)(out + a.ldo + j) = packed_lo;
+        *(uint32_t *)at(0, j) = packed;  // 4 bytes from j % 4 == 0: one panel
+        if (wide) *(uint32_t *)at(1, j) = packed_lo;
     }
 }
 
@@ -1217,6 +1244,7 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
     }
     __syncthreads();  // beta and gamma are in LDS
     if (!live) return;
+    const bool wide = a.bits == 16;
     const u128 Q = ((u128)hi << 64) | lo;
     const int64_t mean = floor_div64(sum, d);
     const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
@@ -1225,8 +1253,10 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
     const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
     const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
-    const bool wide = a.bits == 16;
-    int8_t *out = a.out + (size_t)row * (wide ? 2 : 1) * a.ldo;
+    // the operand rows of this row (two planes when wide), in panels (panel_off); a wave's four
+    // rows are adjacent in every panel, so each store instruction writes 256 contiguous bytes
+    const size_t orow = (size_t)row * (wide ? 2 : 1);
+    auto at = [&](int pl, int j) { return (uint32_t *)(a.out + panel_off(orow + pl, j, a.out_rows)); };
     // Each element first takes the double-precision form of the rule (ln_elem_f64), which gives
     // the exact integer or declines. Every group is stored from it; the groups with a declined
     // element are then recomputed by the integer rule and stored again (the same lane rewrites
@@ -1246,8 +1276,8 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
                 packed_lo |= (uint32_t)(uint8_t)((y[e] & 255) - 128) << (8 * e);
             }
         }
-        *(uint32_t *)(out + j) = packed;
-        if (wide) *(uint32_t *)(out + a.ldo + j) = packed_lo;
+        *at(0, j) = packed;  // 4 bytes from j % 4 == 0: one panel
+        if (wide) *at(1, j) = packed_lo;
     };
     uint32_t redo = fpath ? 0u : ~0u;  // bit t: group t takes the integer rule
     if (F32) {
@@ -1318,21 +1348,21 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
 hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
     const dim3 grid((n_rows + 3) / 4);
-    // the vector forms need 4-aligned rows: d and ldo multiples of 4
+    // the vector forms need d a multiple of 4 (4-byte groups of a row lie in one panel)
     // the single-precision element rule: 8-bit outputs, integer beta with |beta| <= 256
     const bool f32 = a.bits == 8 && a.beta_frac == 0 && a.beta_small && a.s <= 126;
     // Fewer than 4,096 rows (decode passes): a one-wave workgroup per row, spread over the CUs;
     // the 16-lane form would leave most of them idle (256 rows: 16 workgroups)
-    if (n_rows < 4096 && a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
+    if (n_rows < 4096 && a.d % 4 == 0 && a.d <= 2048) {
         if (a.d <= 1024) hipLaunchKernelGGL(k_layernorm_rows<4>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
         else hipLaunchKernelGGL(k_layernorm_rows<8>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
-    } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 768) {
+    } else if (a.d % 4 == 0 && a.d <= 768) {
         if (f32) hipLaunchKernelGGL((k_layernorm_rows4<12, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
         else hipLaunchKernelGGL((k_layernorm_rows4<12, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
-    } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 1024) {
+    } else if (a.d % 4 == 0 && a.d <= 1024) {
         if (f32) hipLaunchKernelGGL((k_layernorm_rows4<16, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
         else hipLaunchKernelGGL((k_layernorm_rows4<16, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
-    } else if (a.d % 4 == 0 && a.ldo % 4 == 0 && a.d <= 2048) {
+    } else if (a.d % 4 == 0 && a.d <= 2048) {
         hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
     } else {
         hipLaunchKernelGGL(k_layernorm, dim3((n_rows + 3) / 4), dim3(256), 0, stream, a, n_rows);
@@ -1375,6 +1405,13 @@ __device__ __forceinline__ int32_t dot_key(const int *q4, const int8_t *k, int h
     const int *k4 = (const int *)k;
     for (int c = 0; c < hd / 4; c++) s = __builtin_amdgcn_sdot4(q4[c], k4[c], s, false);
     return s;
+}
+
+// The output of row r at column col: row-major (ldo) for the op entries, or the operand panels
+// of the next product (out_rows > 0). Groups of up to 16 columns from a multiple of 16 (of 4
+// for 4-byte groups) lie in one panel.
+__device__ __forceinline__ int8_t *attn_out(const AttnArgs &a, int r, int col) {
+    return a.out + (a.out_rows ? panel_off(r, col, a.out_rows) : (size_t)r * a.ldo + col);
 }
 
 __global__ __launch_bounds__(256) void k_attend(AttnArgs a, int n_tasks) {
@@ -1445,7 +1482,7 @@ __global__ __launch_bounds__(256) void k_attend(AttnArgs a, int n_tasks) {
     for (int t = 0; t < 4; t++) {
         const int c = lane + 64 * t;
         if (c < hd)
-            a.out[(size_t)r * a.ldo + h * hd + c] =
+            *attn_out(a, r, h * hd + c) =
                 (int8_t)clamp128(rescale_full(acc[t], a.out_m, a.out_s), -127, 127);
     }
 }
@@ -1659,7 +1696,7 @@ __global__ void k_split_out(AttnArgs a, int n_rows, SplitPlan pl, void *scratch)
     const int keys = split_keys(a, r), nch = (keys + pl.chunk_keys - 1) / pl.chunk_keys;
     int64_t o = 0;
     for (int cc = 0; cc < nch; cc++) o += S.part[((size_t)rh * pl.chunks + cc) * hd + t];
-    a.out[(size_t)r * a.ldo + h * hd + t] = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
+    *attn_out(a, r, h * hd + t) = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
 }
 
 // Decode attention for head_dim 64 and at most 1,024 keys in one launch: one workgroup (4 waves)
@@ -1808,7 +1845,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     __syncthreads();
     if (tid < 64) {
         const int64_t o = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
-        a.out[(size_t)r * a.ldo + h * 64 + tid] = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
+        *attn_out(a, r, h * 64 + tid) = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
     }
 }
 
@@ -1941,7 +1978,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             const uint32_t b = (uint32_t)clamp128(rescale_full(acc[c], a.out_m, a.out_s), -127, 127) & 255;
             w4[c >> 2] |= b << (8 * (c & 3));
         }
-        int8_t *o = a.out + (size_t)r * a.ldo + h * 64 + 16 * lane;
+        int8_t *o = attn_out(a, r, h * 64 + 16 * lane);
         if (((uintptr_t)o & 15) == 0) {
             *(v4i *)o = v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
         } else {
@@ -2363,7 +2400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         __syncthreads();  // V^T is read: sKV may take the next super-block
     }
     if (myrow < G.count) {
-        int8_t *o = a.out + (size_t)(G.first + myrow) * a.ldo + h * 64;
+        int8_t *o = attn_out(a, G.first + myrow, h * 64);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             uint32_t packed = 0;
@@ -2638,7 +2675,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
                 }
             }
         }
-        int8_t *o = a.out + (size_t)(G.first + myrow) * a.ldo + h * 64;
+        int8_t *o = attn_out(a, G.first + myrow, h * 64);
 #pragma unroll
         for (int c = 0; c < 4; c++) *(uint32_t *)(o + 16 * c + 4 * qg) = packed[c];
     }
@@ -2671,7 +2708,8 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
                                 hipStream_t stream) {
     if (n_groups <= 0) return hipSuccess;
     // the output of a row is four 4-byte stores per head
-    if (a.hd != 64 || a.ldo % 4 != 0 || ((uintptr_t)a.out & 3) != 0 || max_keys < 1) return hipErrorInvalidValue;
+    if (a.hd != 64 || (a.out_rows == 0 && a.ldo % 4 != 0) || ((uintptr_t)a.out & 3) != 0 || max_keys < 1)
+        return hipErrorInvalidValue;
     const bool noclamp = a.score_s >= 13, lds_table = a.exp_len <= ATTN_LDS_TABLE;
     if (lds_table && max_keys <= 8 * 64 && a.score_s >= 22 && a.softmax_p <= 30 && a.out_s >= 0) {
         const size_t lds = ((size_t)a.exp_len + 255) / 256 * 1024;  // whole 1 KiB chunks

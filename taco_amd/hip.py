@@ -511,6 +511,15 @@ def gemm_layout(m: int, n: int, k: int) -> Tuple[int, int, int]:
     return a.value, b.value, c.value
 
 
+def gemm_pack(x: np.ndarray, rows_pad: int, k_pad: int) -> np.ndarray:
+    """An i8 operand [rows, k] in the layout of the _dev GEMM entries: k_pad / 64 panels of
+    rows_pad rows x 64 bytes, zero padded (hs_op_gemm_layout)."""
+    rows, k = x.shape
+    p = np.zeros((rows_pad, k_pad), np.int8)
+    p[:rows, :k] = x
+    return np.ascontiguousarray(p.reshape(rows_pad, k_pad // 64, 64).transpose(1, 0, 2))
+
+
 def mixed_intervals_of_weights(dev: HipDevice, weights: np.ndarray, queries, predictions,
                                freq_bits: int, mixer):
     """mixed_intervals_of_weights (mixed.rs:160-233): the statistics [rows, 3] (total,
