@@ -72,10 +72,12 @@ struct DevMem {
         return HS_OK;
     }
     template <typename T>
+    // count entries from src, zero up to alloc_count
     hs_status upload(T *&p, const T *src, size_t count, size_t alloc_count = 0) {
         hs_status st = alloc(p, std::max(count, alloc_count));
         if (st != HS_OK) return st;
         if (count) HIP_TRY(hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice));
+        if (alloc_count > count) HIP_TRY(hipMemset(p + count, 0, (alloc_count - count) * sizeof(T)));
         return HS_OK;
     }
 };
@@ -940,6 +942,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         g.group = group;
         g.a = a; g.a_rows = a_rows; g.w = lin.w; g.w_rows = lin.n_pad; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
         g.bias = lin.b; g.mult = lin.m; g.shift = lin.s; g.out = o; g.ldo = ldo;
+        g.params_padded = 1;
         g.out_rows = (epi == Epi::GeluWide ? 2 : 1) * RP;
         g.fast32 = epi == Epi::ResidualWide ? 0 : lin.fast32;
         g.gelu = gelu; g.gelu16 = gelu16; g.gelu_off = gelu_off; g.wsum = lin.wsum;
@@ -1006,6 +1009,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             g.a = b.d_a; g.a_rows = RP; g.w = blk.c_attn.w; g.w_rows = blk.c_attn.n_pad;
             g.m = n; g.n = blk.c_attn.n; g.k_pad = blk.c_attn.k_pad;
             g.bias = blk.c_attn.b; g.mult = blk.c_attn.m; g.shift = blk.c_attn.s; g.out = b.d_qkv;
+            g.params_padded = 1;
             g.ldo = 3 * m.d; g.fast32 = blk.c_attn.fast32;
             g.kv_rows = b.d_rows; g.kc = b.kc[l]; g.vc = b.vc[l];
             g.kv_d = m.d; g.kv_hd = m.hd; g.kv_h = m.H; g.kv_ctx = m.C;
@@ -1065,6 +1069,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             g.a = b.d_af + (size_t)pr * c0 * 64; g.a_rows = pr * RP; g.w = m.wte; g.w_rows = m.V_pad;
             g.m = pr * cn; g.n = m.V; g.k_pad = m.d_pad;
             g.mult = m.logit_m; g.shift = m.host.logit_s; g.out = b.d_d16; g.ldo = m.ld16;
+            g.params_padded = 1;
             g.tmax = b.d_tmax; g.tmax_ld = m.ntiles; g.cap16 = (int)m.host.logits_exp.size() - 1;
             g.wsum = m.wte_sum;
             g.group = head_group(g.m);
@@ -1373,8 +1378,8 @@ hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, c
     hs_status s;
     if ((s = mem.upload(dw, wp.data(), wp.size())) != HS_OK) return s;
     if ((s = mem.upload(da, ap.data(), ap.size())) != HS_OK) return s;
-    if (bias && (s = mem.upload(db, bias, n)) != HS_OK) return s;
-    if (mult && (s = mem.upload(dm, mult, n)) != HS_OK) return s;
+    if (bias && (s = mem.upload(db, bias, n, np)) != HS_OK) return s;
+    if (mult && (s = mem.upload(dm, mult, n, np)) != HS_OK) return s;
     const size_t esz = epi == Epi::Raw ? 4 : 1;
     int8_t *o8;
     if ((s = mem.alloc(o8, m * n * esz)) != HS_OK) return s;
@@ -1382,6 +1387,7 @@ hs_status gemm_host(hs_device *dev, Epi epi, const int8_t *w, const int8_t *a, c
     hs::GemmArgs g;
     g.a = da; g.w = dw; g.m = (int)m; g.n = (int)n; g.k_pad = (int)kp;
     g.bias = db; g.mult = dm; g.shift = shift; g.out = dout; g.ldo = (int)n;
+    g.params_padded = 1;
     g.fast32 = fits_i32(k, bias, bias ? n : 0);
     g.splits = splits;
     const int sp = hs::gemm_split_plan(epi, (int)m, (int)n, (int)kp, splits);

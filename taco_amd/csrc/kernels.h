@@ -40,6 +40,7 @@ struct GemmArgs {
     int m = 0, n = 0, k_pad = 0;
     const int32_t *bias = nullptr;  // [n] (Act, Residual, Gelu)
     const int32_t *mult = nullptr;  // [n]
+    int params_padded = 0;          // 1: bias and mult hold round_up(n, 256) entries (zeros past n)
     int shift = 0;
     void *out = nullptr;  // Raw: i32; Act/Gelu: i8; Residual: i32 x (read-modify-write); Logits: i64
     int ldo = 0;          // elements per output row

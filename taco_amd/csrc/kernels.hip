@@ -303,9 +303,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         constexpr bool vec = VEC;
         // The rescale parameters of column group j of the lane (columns cw + 16 j + 4 cg + e).
         auto params = [&](int j, int32_t *bj, int32_t *mj) {
+            const int n4 = cw + 16 * j + 4 * cg;
+            if (g.params_padded) {  // every column of a tile is below n_pad: 16-byte loads
+                const v4i b4 = HAS_BIAS ? *(const v4i *)(g.bias + n4) : v4i{0, 0, 0, 0};
+                const v4i m4 = EPI != (int)Epi::Raw ? *(const v4i *)(g.mult + n4) : v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    bj[e] = b4[e];
+                    mj[e] = m4[e];
+                }
+                return;
+            }
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int n = cw + 16 * j + 4 * cg + e;
+                const int n = n4 + e;
                 const bool ok = n < g.n;
                 bj[e] = (HAS_BIAS && ok) ? g.bias[n] : 0;
                 mj[e] = (EPI != (int)Epi::Raw && ok) ? g.mult[n] : 0;
@@ -339,7 +350,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             }
         }
         if (EPI == (int)Epi::Residual) {  // ops.rs:131-145
-            // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R.
+            // clamp(x + clamp(r, +-2^40), +-R) == clamp(x + sat32(r), +-R) for |x| <= R, and
+            // == med3(sat32(x + sat32(r)), -R, R): a sum beyond i32 saturates to a value beyond R
+            // on the same side, so the i32 saturating add and one med3 give it exactly.
+            auto res = [](int32_t x, int32_t r) { return med3_i32(__builtin_elementwise_add_sat(x, r), -RES, RES); };
             if (!vec) {
 #pragma unroll
                 for (int i = 0; i < 8; i++)
@@ -350,7 +364,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                         int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n4;
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            if (n4 + e < g.n) x[e] = (int32_t)clamp64((int64_t)x[e] + acc[i][j][e], -RES, RES);
+                            if (n4 + e < g.n) x[e] = res(x[e], acc[i][j][e]);
                     }
                 return;
             }
@@ -385,12 +399,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                     if (n + 4 <= g.n) {
                         v4i o;
 #pragma unroll
-                        for (int t = 0; t < 4; t++) o[t] = (int32_t)clamp64((int64_t)xv[q][t] + rv[q][t], -RES, RES);
+                        for (int t = 0; t < 4; t++) o[t] = res(xv[q][t], rv[q][t]);
                         *(v4i *)x = o;
                     } else {
 #pragma unroll
                         for (int t = 0; t < 4; t++)
-                            if (n + t < g.n) x[t] = (int32_t)clamp64((int64_t)x[t] + rv[q][t], -RES, RES);
+                            if (n + t < g.n) x[t] = res(x[t], rv[q][t]);
                     }
                 }
             }
@@ -438,33 +452,39 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             }
             int8_t *wr = gemm_lds + wave * 18432;  // this wave's staging region: 128 rows x 144 B
             if (vec) __syncthreads();              // every wave finished reading the stages
+            // NARROW: every logit lies in [-2^31 + 1, 2^31 - 1] (no clamp), so the row max is an
+            // i32 max (INT32_MIN marks the columns past n) and tilemax - l < 2^32 a u32 difference.
+            using L = typename std::conditional<NARROW, int32_t, int64_t>::type;
+            using U = typename std::conditional<NARROW, uint32_t, int64_t>::type;
+            constexpr L LMIN = NARROW ? (L)INT32_MIN : (L)INT64_MIN;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                int64_t l[4][4], mx = INT64_MIN;
+                L l[4][4], mx = LMIN;
 #pragma unroll
                 for (int j = 0; j < 4; j++)
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int64_t r = rq(acc[i][j][e], 0, mult[j][e]);
                         const bool ok = cw + 16 * j + 4 * cg + e < g.n;
-                        l[j][e] = ok ? (NARROW ? r : clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : INT64_MIN;
+                        l[j][e] = ok ? (NARROW ? (L)r : (L)clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : LMIN;
                         mx = l[j][e] > mx ? l[j][e] : mx;
                     }
 #pragma unroll
                 for (int o = 16; o < 64; o <<= 1) {
-                    const int64_t u = __shfl_xor(mx, o, 64);
+                    const L u = __shfl_xor(mx, o, 64);
                     mx = u > mx ? u : mx;
                 }
                 const int m = rw + 16 * i + rl;
-                if (m < g.m && cg == 0 && cw < g.n) g.tmax[(size_t)m * g.tmax_ld + cw / 64] = mx;
+                if (m < g.m && cg == 0 && cw < g.n) g.tmax[(size_t)m * g.tmax_ld + cw / 64] = (int64_t)mx;
+                const U cap = (U)g.cap16;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     uint32_t w2[2];
 #pragma unroll
                     for (int p = 0; p < 2; p++) {
-                        const int64_t d0 = mx - l[j][2 * p], d1 = mx - l[j][2 * p + 1];
-                        const uint32_t u0 = (uint32_t)(d0 < g.cap16 ? d0 : g.cap16);
-                        const uint32_t u1 = (uint32_t)(d1 < g.cap16 ? d1 : g.cap16);
+                        const U d0 = (U)mx - (U)l[j][2 * p], d1 = (U)mx - (U)l[j][2 * p + 1];
+                        const uint32_t u0 = (uint32_t)(d0 < cap ? d0 : cap);
+                        const uint32_t u1 = (uint32_t)(d1 < cap ? d1 : cap);
                         w2[p] = (u0 & 0xFFFF) | (u1 << 16);
                     }
                     if (vec) {
