@@ -56,6 +56,7 @@ static_assert(GEMM_BM == 256 && GEMM_BK == 64 && GEMM_NPAD % 256 == 0, "tile sha
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef int v2i __attribute__((ext_vector_type(2)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 // s_waitcnt vmcnt(N) with the other counters left at their maximum (gfx9 encoding).
@@ -3102,11 +3103,22 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
             const bool whole = gq + 8 <= V, all_lo = gq + 8 <= (int)tok, none_lo = gq >= (int)tok;
             const bool top = base <= a.d0;
             if (packed && whole && (all_lo || none_lo) && !top) {
+                // two symbols per packed u16 add (saturating) and min: d = min(base + d16,
+                // zc + lane % 64), so the symbols of weight 0 (d >= zc) land in the 64 spare bins
+                // past the weighted ones (never read), each lane in its own, and no symbol needs
+                // a test (base < zc <= 16384)
                 const uint32_t inc = all_lo ? 0x10001u : 1u;
+                const us2 bb = {(unsigned short)base, (unsigned short)base};
+                const unsigned short zl = (unsigned short)(zc + (tid & 63));
+                const us2 zz = {zl, zl};
+                const uint32_t *wv = (const uint32_t *)&cur[u];
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const int dd = base + (int)dv[q];
-                    if (dd < zc) atomicAdd(&hist[dd], inc);  // then dd <= last: d = dd
+                for (int p = 0; p < 4; p++) {
+                    us2 v;
+                    __builtin_memcpy(&v, &wv[p], 4);
+                    v = __builtin_elementwise_min(__builtin_elementwise_add_sat(v, bb), zz);
+                    atomicAdd(&hist[v.x], inc);
+                    atomicAdd(&hist[v.y], inc);
                 }
                 continue;
             }
@@ -3129,10 +3141,22 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     __syncthreads();
     const int64_t largest = -block_max64w(-first, s_i, tid);
 
+    // The bins of this thread, 8 at a time: the counts from LDS first, then the table entries of
+    // the nonempty bins (up to 8 loads in flight), then the sums.
+    constexpr int BU = 8;
     uint64_t W = 0;
-    for (int d = tid; d < zc; d += 256) {
-        const uint32_t c = packed ? (hist[d] & 0xffffu) : hist[d];
-        W += (uint64_t)c * a.table[d];
+    for (int d0 = tid; d0 < zc; d0 += 256 * BU) {
+        uint32_t c[BU];
+        uint64_t t[BU];
+#pragma unroll
+        for (int u = 0; u < BU; u++) {
+            const int d = d0 + 256 * u;
+            c[u] = d < zc ? (packed ? (hist[d] & 0xffffu) : hist[d]) : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < BU; u++) t[u] = c[u] ? a.table[d0 + 256 * u] : 0;
+#pragma unroll
+        for (int u = 0; u < BU; u++) W += (uint64_t)c[u] * t[u];
     }
     W = block_sum64w(W, s_u, tid);
     if (STATS) {  // mixer.rs:278-288 (W >= table[0] >= 1, so top is the largest)
@@ -3160,24 +3184,35 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
     // nearest integer, the low word of the sum), else the exact quotient.
     const double Rq = (double)spare / (double)W;
     uint64_t S = 0, Slo = 0;
-    for (int d = tid; d < zc; d += 256) {
-        const uint32_t h = hist[d];
-        const uint32_t c = packed ? (h & 0xffffu) : h, clo = packed ? (h >> 16) : hist[zc + d];
-        if (!c) continue;
-        const uint64_t td = a.table[d];
-        const double v = (double)td * Rq;
-        const double t = v + 6755399441055744.0;
-        const double dl = v - (t - 6755399441055744.0);
-        uint64_t q;
-        if (fabs(dl) >= 0x1p-18) {
-            uint64_t bits;
-            __builtin_memcpy(&bits, &t, sizeof bits);
-            q = (uint64_t)(uint32_t)bits - (dl < 0.0 ? 1 : 0);
-        } else {
-            q = quotient(td, spare, W, frac);
+    for (int d0 = tid; d0 < zc; d0 += 256 * BU) {
+        uint32_t c[BU], clo[BU];
+        uint64_t td[BU];
+#pragma unroll
+        for (int u = 0; u < BU; u++) {
+            const int d = d0 + 256 * u;
+            const uint32_t h = d < zc ? hist[d] : 0;
+            c[u] = packed ? (h & 0xffffu) : h;
+            clo[u] = packed ? (h >> 16) : (c[u] ? hist[zc + d] : 0);
         }
-        S += (uint64_t)c * q;
-        Slo += (uint64_t)clo * q;
+#pragma unroll
+        for (int u = 0; u < BU; u++) td[u] = c[u] ? a.table[d0 + 256 * u] : 0;
+#pragma unroll
+        for (int u = 0; u < BU; u++) {
+            if (!c[u]) continue;
+            const double v = (double)td[u] * Rq;
+            const double t = v + 6755399441055744.0;
+            const double dl = v - (t - 6755399441055744.0);
+            uint64_t q;
+            if (fabs(dl) >= 0x1p-18) {
+                uint64_t bits;
+                __builtin_memcpy(&bits, &t, sizeof bits);
+                q = (uint64_t)(uint32_t)bits - (dl < 0.0 ? 1 : 0);
+            } else {
+                q = quotient(td[u], spare, W, frac);
+            }
+            S += (uint64_t)c[u] * q;
+            Slo += (uint64_t)clo[u] * q;
+        }
     }
     S = block_sum64w(S, s_u, tid);
     Slo = block_sum64w(Slo, s_u + 8, tid);
@@ -3496,7 +3531,8 @@ template <typename K>
 static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows, size_t *allowed,
                                  hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
-    const size_t lds = (a.vocab < 65536 ? 1 : 2) * sizeof(uint32_t) * (size_t)a.zcut;
+    // packed counts: zcut bins and 64 spare bins of the weight-0 symbols; else two arrays
+    const size_t lds = sizeof(uint32_t) * (a.vocab < 65536 ? (size_t)a.zcut + 64 : 2 * (size_t)a.zcut);
     if (lds > *allowed) {  // raise the dynamic LDS limit once per size
         hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
