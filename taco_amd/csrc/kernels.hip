@@ -72,10 +72,18 @@ __device__ __forceinline__ void wait_vmcnt() {
 // BN = 128 (4 waves, 2 x 2) or 256 (8 waves, 2 x 4); every wave computes 128 x 64.
 // VEC: the output rows are 16-byte aligned (checked by the launcher); the four-columns epilogues
 // then stage and store 16-byte pieces, else they store each output on its own.
-template <int EPI, bool NARROW, int BN, bool VEC>
-__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
-    constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16, LOADS = FRAGS / WAVES;
+// BM x BN tiles: 256 x 64 (2 x 1 waves), 256 x 128 (2 x 2), 256 x 256 (2 x 4, the full-line
+// loop) and 128 x 192 (2 x 2 waves of 64 x 96). Each wave computes a
+// (BM / 2) x (BN / WN) sub-tile: TI x TJ tiles of 16 x 16.
+constexpr int gemm_wn(int bn) { return bn == 192 ? 2 : bn / 64; }  // waves along N
+constexpr int gemm_waves(int bn) { return 2 * gemm_wn(bn); }
+
+template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM>
+__global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
+    constexpr int WN = gemm_wn(BN), WAVES = 2 * WN, TI = BM / 32, TJ = BN / WN / 16;
+    constexpr int FRAGS = BM / 16 + BN / 16, LOADS = FRAGS / WAVES;
     static_assert(FRAGS % WAVES == 0, "whole fragments per wave");
+    static_assert(TI * TJ <= 32 && (BM == GEMM_BM || (BM == 128 && BN == 192)), "tile shapes");
     // The i16-plane epilogues pair rows 2r and 2r + 1 in one lane and keep the W-as-columns
     // layout; every other epilogue takes four consecutive columns of a row per lane.
     constexpr bool SWAP = EPI != (int)Epi::ResidualWide && EPI != (int)Epi::LogitsWide &&
@@ -83,13 +91,13 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     extern __shared__ __attribute__((aligned(1024))) int8_t gemm_lds[];  // [stages][FRAGS][1024]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / (WAVES / 2), wn = wave % (WAVES / 2);
+    const int wm = wave / WN, wn = wave % WN;
     // XCD-aware tile order: workgroup L runs on XCD L % 8, and XCD x takes the x-th contiguous
     // chunk of a grouped order (groups of `group` M-tiles, N outermost inside a group), so an
     // A row-tile stays in one XCD's L2 while the W tiles stream past it.
     int mt, nt;
     {
-        const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + BN - 1) / BN;
+        const int gm = (g.m + BM - 1) / BM, gn = (g.n + BN - 1) / BN;
         const int T = gm * gn, L = blockIdx.x, x = L & 7, k = L >> 3;
         const int q = T >> 3, r = T & 7;
         const int p = x * q + (x < r ? x : r) + k;
@@ -98,19 +106,19 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         nt = in / gs;
         mt = grp * G + in % gs;
     }
-    const int m0 = mt * GEMM_BM, n0 = nt * BN;
+    const int m0 = mt * BM, n0 = nt * BN;
     const int K = g.k_pad;
 
-    v4i acc[8][4];
+    v4i acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < TJ; j++) acc[i][j] = v4i{0, 0, 0, 0};
     auto mfma_step = [&](const v4i *af, const v4i *bf) {
 #pragma unroll
-        for (int i = 0; i < 8; i++)
+        for (int i = 0; i < TI; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
+            for (int j = 0; j < TJ; j++)
                 acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
                                  : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     };
@@ -123,19 +131,19 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         // of 64 KiB: the next stage loads while this one is multiplied. A k_pad that is an odd
         // multiple of 64 ends with a half stage (chunks 0-3 only; the lanes of chunks 4-7 reload
         // a chunk of the last panel that nothing reads).
-        constexpr int ROWS = GEMM_BM + BN, LD = ROWS / 8 / WAVES, SB = ROWS * 128;
+        constexpr int ROWS = BM + BN, LD = ROWS / 8 / WAVES, SB = ROWS * 128;
         const int nk2 = (K + 127) / 128;
         const bool half = (K & 127) != 0;
         // A wave's LD instructions all read one operand (waves 0-3 the A rows, 4-7 the W rows),
         // rows 8 i + lane / 8 of its block; the chunk swizzle alternates with i, so two lane bases
         // (even and odd i) and a uniform stride of 16 rows give every address.
-        static_assert(GEMM_BM / 8 % LD == 0, "a wave loads rows of one operand");
+        static_assert(BM / 8 % LD == 0, "a wave loads rows of one operand");
         const int ld_r = lane >> 3, ld_s = lane & 7;
         const int row0 = wave * LD * 8 + ld_r;  // the row of instruction 0 (row of i = row0 + 8 i)
         const int c_even = ld_s ^ ((row0 >> 1) & 7), c_odd = c_even ^ 4;
-        const bool is_a = wave * LD * 8 < GEMM_BM;  // uniform per wave
+        const bool is_a = wave * LD * 8 < BM;  // uniform per wave
         const size_t pb = (size_t)(is_a ? g.a_rows : g.w_rows) * 64;  // bytes per panel
-        const int8_t *base_row = is_a ? g.a + (size_t)(m0 + row0) * 64 : g.w + (size_t)(n0 + row0 - GEMM_BM) * 64;
+        const int8_t *base_row = is_a ? g.a + (size_t)(m0 + row0) * 64 : g.w + (size_t)(n0 + row0 - BM) * 64;
         const int8_t *p_even = base_row + (c_even >> 2) * pb + (c_even & 3) * 16;
         const int8_t *p_odd = base_row + 8 * 64 + (c_odd >> 2) * pb + (c_odd & 3) * 16;
         // a half stage: the lanes whose chunk is 4-7 step back one panel
@@ -157,9 +165,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         auto frag_ptr = [&](int stage, int h) {
             return gemm_lds + stage * SB + rl * 128 + 16 * ((4 * h + (lane >> 4)) ^ swz);
         };
-        auto read_a = [&](const int8_t *st, int i) { return *(const v4i *)(st + (wm * 128 + 16 * i) * 128); };
+        auto read_a = [&](const int8_t *st, int i) { return *(const v4i *)(st + (wm * 16 * TI + 16 * i) * 128); };
         auto read_b = [&](const int8_t *st, int j) {
-            return *(const v4i *)(st + (GEMM_BM + wn * 64 + 16 * j) * 128);
+            return *(const v4i *)(st + (BM + wn * 16 * TJ + 16 * j) * 128);
         };
         issue(0, 0);
         for (int kt = 0; kt < nk2; kt++) {
@@ -173,25 +181,25 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             }
             asm volatile("s_barrier" ::: "memory");  // every wave's part of stage kt landed
             const int8_t *s0 = frag_ptr(stage, 0), *s1 = frag_ptr(stage, 1);
-            v4i af[8], bf[4];
+            v4i af[TI], bf[TJ];
 #pragma unroll
-            for (int i = 0; i < 8; i++) af[i] = read_a(s0, i);
+            for (int i = 0; i < TI; i++) af[i] = read_a(s0, i);
 #pragma unroll
-            for (int j = 0; j < 4; j++) bf[j] = read_b(s0, j);
+            for (int j = 0; j < TJ; j++) bf[j] = read_b(s0, j);
             // The second half's fragments load while the first half's MFMAs run: its W fragments
             // first, then each A fragment into the registers of the one just used. A half stage
             // multiplies its second half by zero W fragments (no branch around the MFMAs).
             const bool zero_second = half && kt == nk2 - 1;
-            v4i bn[4];
+            v4i bn[TJ];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < TJ; j++) {
                 const v4i b = read_b(s1, j);
                 bn[j] = zero_second ? v4i{0, 0, 0, 0} : b;
             }
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < TI; i++) {
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < TJ; j++)
                     acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
                                      : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
                 af[i] = read_a(s1, i);
@@ -221,8 +229,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int i = 0; i < LOADS; i++) {
         const int f = wave * LOADS + i;
         const int r = lane >> 2, c = (lane & 3) ^ sw(r);
-        const int row = (f < GEMM_BM / 16 ? f : f - GEMM_BM / 16) * 16 + r;
-        src[i] = (f < GEMM_BM / 16 ? g.a + (size_t)(kb0 / GEMM_BK) * pa + (size_t)(m0 + row) * 64
+        const int row = (f < BM / 16 ? f : f - BM / 16) * 16 + r;
+        src[i] = (f < BM / 16 ? g.a + (size_t)(kb0 / GEMM_BK) * pa + (size_t)(m0 + row) * 64
                                    : g.w + (size_t)(kb0 / GEMM_BK) * pw + (size_t)(n0 + row) * 64) + c * 16;
     }
     const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ sw(lane & 15));
@@ -230,7 +238,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         int8_t *base = gemm_lds + stage * (FRAGS * 1024) + wave * LOADS * 1024;
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
-            const size_t step = wave * LOADS + i < GEMM_BM / 16 ? pa : pw;
+            const size_t step = wave * LOADS + i < BM / 16 ? pa : pw;
             __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)kt * step),
                                              (lds_void *)(base + i * 1024), 16, 0, 0);
         }
@@ -242,9 +250,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     auto read_frags = [&](int kt, v4i *af, v4i *bf) {
         const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (FRAGS * 1024) + rd_slot * 16;
 #pragma unroll
-        for (int i = 0; i < 8; i++) af[i] = *(const v4i *)(st + (wm * 8 + i) * 1024);
+        for (int i = 0; i < TI; i++) af[i] = *(const v4i *)(st + (wm * TI + i) * 1024);
 #pragma unroll
-        for (int j = 0; j < 4; j++) bf[j] = *(const v4i *)(st + (GEMM_BM / 16 + wn * 4 + j) * 1024);
+        for (int j = 0; j < TJ; j++) bf[j] = *(const v4i *)(st + (BM / 16 + wn * TJ + j) * 1024);
     };
 #pragma unroll
     for (int s = 0; s < GEMM_STAGES; s++)
@@ -255,10 +263,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     else if (nk == 2) wait_vmcnt<LOADS>();
     else wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
-    v4i af[8], bf[4];
+    v4i af[TI], bf[TJ];
     read_frags(0, af, bf);
     for (int kt = 0; kt < nk; kt++) {
-        v4i an[8], bn[4];
+        v4i an[TI], bn[TJ];
         const bool more = kt + 1 < nk;
         if (more) {
             // stage kt + 1 landed (stage kt + 2's loads may be outstanding); this wave's reads of
@@ -276,9 +284,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         asm volatile("" ::: "memory");
         mfma_step(af, bf);
 #pragma unroll
-        for (int i = 0; i < 8; i++) af[i] = an[i];
+        for (int i = 0; i < TI; i++) af[i] = an[i];
 #pragma unroll
-        for (int j = 0; j < 4; j++) bf[j] = bn[j];
+        for (int j = 0; j < TJ; j++) bf[j] = bn[j];
     }
     }
 
@@ -296,8 +304,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         if (NARROW || fast) return ((int64_t)(a + bias) * mult + half) >> s_eff;
         return rescale_small((int64_t)a + bias, mult, g.shift);
     };
-    const int rw = m0 + wm * 128, cw = n0 + wn * 64;  // the wave's sub-tile origin
-    if (SWAP) {
+    const int rw = m0 + wm * 16 * TI, cw = n0 + wn * 16 * TJ;  // the wave's sub-tile origin
+    if constexpr (SWAP) {
         const int rl = lane & 15, cg = lane >> 4;
         constexpr bool HAS_BIAS = EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu ||
                                   EPI == (int)Epi::GeluWide;
@@ -326,11 +334,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         // Act, Gelu, GeluWide, Residual: the op's rule in place, one column group at a time.
         if (EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide || EPI == (int)Epi::Residual) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < TJ; j++) {
                 int32_t bj[4], mj[4];
                 params(j, bj, mj);
 #pragma unroll
-                for (int i = 0; i < 8; i++)
+                for (int i = 0; i < TI; i++)
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int64_t r = rq(acc[i][j][e], bj[e], mj[e]);
@@ -357,9 +365,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             auto res = [](int32_t x, int32_t r) { return med3_i32(__builtin_elementwise_add_sat(x, r), -RES, RES); };
             if (!vec) {
 #pragma unroll
-                for (int i = 0; i < 8; i++)
+                for (int i = 0; i < TI; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
+                    for (int j = 0; j < TJ; j++) {
                         const int m = rw + 16 * i + rl, n4 = cw + 16 * j + 4 * cg;
                         if (m >= g.m) continue;
                         int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n4;
@@ -369,32 +377,35 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                     }
                 return;
             }
-            // Staged in two halves of 64 rows through this wave's region (64 rows x 272 B): the
-            // lane's four outputs of a row are one 16-byte LDS write; the read-modify-write of x
-            // then covers 256 contiguous bytes of 4 rows per instruction, all 16 loads of a half
-            // in flight together.
+            // Staged in two halves of the wave's rows (64 rows of 64 columns, or 32 of 96) through
+            // this wave's region (row stride RS): the lane's four outputs of a row are one 16-byte
+            // LDS write; the read-modify-write of x then covers whole 16-byte pieces of rows (CPR
+            // per row), all Q loads of a half in flight together.
+            constexpr int HR = TJ == 4 ? 64 : 32, NH = 16 * TI / HR, RS = 64 * TJ + 16;
+            constexpr int CPR = 4 * TJ, Q = HR * CPR / 64;
+            static_assert(NH * HR == 16 * TI && HR * RS <= 18432 && Q * 64 == HR * CPR, "residual staging");
             __syncthreads();  // every wave finished reading the stages
             int8_t *wr = gemm_lds + wave * 18432;
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
+            for (int h = 0; h < NH; h++) {
 #pragma unroll
-                for (int ii = 0; ii < 4; ii++)
+                for (int ii = 0; ii < HR / 16; ii++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        *(v4i *)(wr + (16 * ii + rl) * 272 + (16 * j + 4 * cg) * 4) = acc[4 * h + ii][j];
-                v4i xv[16], rv[16];
+                    for (int j = 0; j < TJ; j++)
+                        *(v4i *)(wr + (16 * ii + rl) * RS + (16 * j + 4 * cg) * 4) = acc[(HR / 16) * h + ii][j];
+                v4i xv[Q], rv[Q];
 #pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const int rl2 = q * 4 + (lane >> 4), cl = (lane & 15) * 4;
-                    const int m = rw + 64 * h + rl2, n = cw + cl;
-                    rv[q] = *(const v4i *)(wr + rl2 * 272 + cl * 4);
+                for (int q = 0; q < Q; q++) {
+                    const int pc = q * 64 + lane, rl2 = pc / CPR, cl = (pc % CPR) * 4;
+                    const int m = rw + HR * h + rl2, n = cw + cl;
+                    rv[q] = *(const v4i *)(wr + rl2 * RS + cl * 4);
                     xv[q] = (m < g.m && n + 4 <= g.n) ? *(const v4i *)((const int32_t *)g.out + (size_t)m * g.ldo + n)
                                                        : v4i{0, 0, 0, 0};
                 }
 #pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const int rl2 = q * 4 + (lane >> 4), cl = (lane & 15) * 4;
-                    const int m = rw + 64 * h + rl2, n = cw + cl;
+                for (int q = 0; q < Q; q++) {
+                    const int pc = q * 64 + lane, rl2 = pc / CPR, cl = (pc % CPR) * 4;
+                    const int m = rw + HR * h + rl2, n = cw + cl;
                     if (m >= g.m) continue;
                     int32_t *x = (int32_t *)g.out + (size_t)m * g.ldo + n;
                     if (n + 4 <= g.n) {
@@ -413,11 +424,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
         if (EPI == (int)Epi::Raw || EPI == (int)Epi::Logits) {  // i32 products; ops.rs:229-234 (i64)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < TJ; j++) {
                 int32_t bj[4], mj[4];
                 params(j, bj, mj);
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
+                for (int i = 0; i < TI; i++) {
                     const int m = rw + 16 * i + rl, n4 = cw + 16 * j + 4 * cg;
                     if (m >= g.m || n4 >= g.n) continue;
                     if (EPI == (int)Epi::Raw) {
@@ -439,7 +450,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             }
             return;
         }
-        if (EPI == (int)Epi::LogitsCompact) {
+        if constexpr (EPI == (int)Epi::LogitsCompact) {
+            static_assert(TI == 8 && TJ == 4, "the compact logits keep 64-column tiles");
             // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the
             // largest logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16)
             // per logit; the table index min(max - l, len - 1) follows exactly from them, because
@@ -517,19 +529,21 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             return;
         }
         // Act, Gelu, GeluWide: i8 outputs (GeluWide: the two planes of each i16 output), staged
-        // per wave in LDS (128 rows x 80 B) and stored as 16-byte row pieces. Gelu copies its
+        // per wave in LDS (the wave's rows x RS8 bytes) and stored as 16-byte row pieces. Gelu copies its
         // table (256 or 65,536 entries) into LDS first; the staging regions follow it.
         int toff = 0;
         if (vec) {
             __syncthreads();  // every wave finished reading the stages
             if (EPI == (int)Epi::Gelu) {
                 const int T = 2 * g.gelu_off;
-                for (int c = threadIdx.x; c < T / 16; c += 2 * BN)
+                for (int c = threadIdx.x; c < T / 16; c += 64 * WAVES)
                     *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
                 __syncthreads();
                 toff = (T + 1023) & ~1023;
             }
         }
+        constexpr int RS8 = 16 * TJ + 16, Q8 = TI * TJ / 4;
+        static_assert(16 * TI * RS8 <= 10240 && Q8 * 64 == 16 * TI * TJ, "i8 staging");
         int8_t *wr = gemm_lds + toff + wave * 10240;
         // GeluWide: the hi plane of every row, then the lo plane (this wave's region is rewritten
         // only after its own reads: LDS operations of a wave stay in order)
@@ -542,9 +556,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
             };
             if (!vec) {  // unaligned output rows: one byte store per output
 #pragma unroll
-                for (int i = 0; i < 8; i++)
+                for (int i = 0; i < TI; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
+                    for (int j = 0; j < TJ; j++)
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
                             const int m = rw + 16 * i + rl, n = cw + 16 * j + 4 * cg + e;
@@ -568,20 +582,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
                 continue;
             }
 #pragma unroll
-            for (int i = 0; i < 8; i++)
+            for (int i = 0; i < TI; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
+                for (int j = 0; j < TJ; j++) {
                     uint32_t b[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++)
                         b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)gemm_lds[acc[i][j][e]] : byte_of(acc[i][j][e]);
-                    *(uint32_t *)(wr + (16 * i + rl) * 80 + 16 * j + 4 * cg) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-                    if (EPI == (int)Epi::Gelu && j == 3) asm volatile("" ::: "memory");  // 16 lookups in flight at most
+                    *(uint32_t *)(wr + (16 * i + rl) * RS8 + 16 * j + 4 * cg) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+                    if (EPI == (int)Epi::Gelu && j == TJ - 1) asm volatile("" ::: "memory");  // 4 TJ lookups in flight at most
                 }
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int rl2 = q * 16 + (lane >> 2), cl = (lane & 3) * 16;
-                const v4i v = *(const v4i *)(wr + rl2 * 80 + cl);
+            for (int q = 0; q < Q8; q++) {
+                const int pc = q * 64 + lane, rl2 = pc / TJ, cl = (pc % TJ) * 16;
+                const v4i v = *(const v4i *)(wr + rl2 * RS8 + cl);
                 const int m = rw + rl2, n = cw + cl;
                 if (m >= g.m) continue;
                 if (EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
@@ -611,7 +625,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
         return;
     }
     // The wide epilogues (no SWAP)
-    if (EPI == (int)Epi::ResidualWide || EPI == (int)Epi::LogitsWide || EPI == (int)Epi::LogitsCompactWide) {
+    if constexpr (EPI == (int)Epi::ResidualWide || EPI == (int)Epi::LogitsWide || EPI == (int)Epi::LogitsCompactWide) {
+        static_assert(TI == 8 && TJ == 4, "the plane epilogues keep 128 x 64 wave tiles");
         // i16 operand rows as planes (ops.rs:178-206,246-277): the lane holds plane rows
         // 4 (lane / 16) + e of each 16-row tile, so e = 0, 1 are the hi and lo planes of one row
         // and e = 2, 3 those of the next. dot(w, v) = 256 dot(w, hi) + dot(w, lo) + 128 wsum:
@@ -675,12 +690,16 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
 }
 
-template <int EPI, bool NARROW, int BN, bool VEC>
-static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
-    constexpr int WAVES = BN / 32, FRAGS = GEMM_BM / 16 + BN / 16;
+template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM>
+static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
+    constexpr int WAVES = gemm_waves(BN), FRAGS = BM / 16 + BN / 16;
+    GemmArgs g = ga;
+    const int gm = (g.m + BM - 1) / BM, gn = (g.n + BN - 1) / BN;
+    // the group of the tile order counts 256-row tiles: the same band of rows in BM-row tiles
+    if (BM != GEMM_BM) g.group = 2 * g.group < gm ? 2 * g.group : gm;
     // the stages, and the epilogue's LDS: per-wave staging regions (18 KiB for the u16 logits
     // and the i16-plane epilogues, 10 KiB for i8 outputs), after the GELU table for Gelu
-    constexpr size_t stages = BN == 256 ? (size_t)2 * (GEMM_BM + BN) * 128 : (size_t)GEMM_STAGES * FRAGS * 1024;
+    constexpr size_t stages = BN == 256 ? (size_t)2 * (BM + BN) * 128 : (size_t)GEMM_STAGES * FRAGS * 1024;
     constexpr bool I8OUT = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
     constexpr size_t regions = (size_t)WAVES * (I8OUT ? 10240 : 18432);
     // the largest request: the stages, or the 64 KiB GELU table and the staging regions after it
@@ -689,7 +708,7 @@ static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
     static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
     static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
     if (!ready) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC, BM>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
         if (e != hipSuccess) return e;
         ready = true;
@@ -699,8 +718,7 @@ static hipError_t launch_gemm_t(const GemmArgs &g, hipStream_t stream) {
         const size_t t = ((size_t)2 * g.gelu_off + 1023) & ~(size_t)1023;
         lds = stages > t + regions ? stages : t + regions;
     }
-    const int gm = (g.m + GEMM_BM - 1) / GEMM_BM, gn = (g.n + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC>), dim3(gm * gn), dim3(2 * BN), lds, stream, g);
+    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC, BM>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
     return hipGetLastError();
 }
 
@@ -726,8 +744,21 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
         // coarser rounds (measured: GPT-2 small mlp.c_proj, K 3,072, 12% faster; c_attn and the
         // LM head, K 768, 10% and 7% slower), and for the i8 GELU epilogue of a wide product
         // (each workgroup copies the 64 KiB table into LDS; measured 4% faster)
-        if (g.n > 512 && (g.k_pad >= 2048 || (EPI == (int)Epi::Gelu && g.n > 1024)))
-            return launch_gemm_t<EPI, NARROW, 256, true>(g, stream);
+        const bool wide = g.n > 512 && (g.k_pad >= 2048 || (EPI == (int)Epi::Gelu && g.n > 1024));
+        if constexpr (EPI == (int)Epi::Act || EPI == (int)Epi::Residual) {
+            // 128 x 192 tiles for a product that is one partial round of resident workgroups
+            // (at most 512 of 256 x 128, or 256 of 256 x 256) and one round of 128 x 192: the
+            // round then holds three quarters of the work per CU, spread over every CU
+            // (measured, GPT-2 small fold: c_proj 32.8 -> 29.6 us, mlp.c_proj 60.9 -> 52.8 us).
+            // Over several rounds the smaller tile's lower efficiency per output (its loads per
+            // output are 11% more) outweighs the fuller last round (c_attn, 1,152 tiles of
+            // 256 x 128: 47.0 us, 1,536 of 128 x 192: 47.8 us).
+            const long long gm2 = (g.m + 255) / 256, gm1 = (g.m + 127) / 128, gn3 = (g.n + 191) / 192;
+            const long long base_tiles = wide ? gm2 * ((g.n + 255) / 256) : gm2 * ((g.n + 127) / 128);
+            const bool one_round = base_tiles <= (wide ? 256 : 512) && gm1 * gn3 <= 512;
+            if (one_round && gn3 * 192 <= g.w_rows) return launch_gemm_t<EPI, NARROW, 192, true, 128>(g, stream);
+        }
+        if (wide) return launch_gemm_t<EPI, NARROW, 256, true>(g, stream);
         return launch_gemm_t<EPI, NARROW, 128, true>(g, stream);
     }
 }
@@ -881,7 +912,7 @@ static hipError_t launch_gemm_split(Epi epi, const GemmArgs &ga, int splits, hip
         ready = true;
     }
     const int gm = (ga.m + GEMM_BM - 1) / GEMM_BM, gn = (ga.n + SPLIT_BN - 1) / SPLIT_BN;
-    hipLaunchKernelGGL((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(2 * SPLIT_BN), lds,
+    hipLaunchKernelGGL((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(64 * gemm_waves(SPLIT_BN)), lds,
                        stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -3580,6 +3611,8 @@ int kernel_resources(KernelResource *out, int cap) {
         {"k_gemm<ResidualWide, 256x128>", (const void *)k_gemm<7, false, 128, true>},
         {"k_gemm<LogitsCompactWide, 256x128>", (const void *)k_gemm<9, false, 128, true>},
         {"k_gemm<Raw, split-K partials, 256x64>", (const void *)k_gemm<0, false, 64, true>},
+        {"k_gemm<Act, narrow, 128x192>", (const void *)k_gemm<1, true, 192, true, 128>},
+        {"k_gemm<Residual, narrow, 128x192>", (const void *)k_gemm<2, true, 192, true, 128>},
         {"k_split_epi<Act>", (const void *)k_split_epi<1>},
         {"k_split_epi<Residual>", (const void *)k_split_epi<2>},
         {"k_embed", (const void *)k_embed},

@@ -121,6 +121,24 @@ def test_gemm_requant_c1_shape(dev):
     assert np.array_equal(got, O.linear_act_ref(w, a, bias, mult2, 40))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 100, 64), (130, 700, 128), (700, 2304, 768), (16384, 768, 768),
+                                   (257, 1000, 192)])
+def test_gemm_requant_tile_shapes(dev, m, n, k):
+    # Shapes whose rounds favour the 128 x 192 tiles (partial tiles in M and N included) and the
+    # 256 x 128 ones, against the exact rule.
+    from taco_amd import hip
+    r = np.random.default_rng(m * 7 + n)
+    a = r.integers(-127, 128, (m, k)).astype(np.int8)
+    w = r.integers(-127, 128, (n, k)).astype(np.int8)
+    bias = r.integers(-(1 << 16), 1 << 16, n).astype(np.int32)
+    mult = r.integers(-(1 << 31), 1 << 31, n).astype(np.int64).astype(np.int32)
+    rows = min(m, 1024)  # the oracle's rows (the first 1,024)
+    got = hip.gemm_requant_i8(dev, w, a, bias, mult, 38)
+    assert np.array_equal(got[:rows], O.linear_act_ref(w, a[:rows], bias, mult, 38))
+    if m > rows:  # the last rows (the partial tiles) too
+        assert np.array_equal(got[-rows:], O.linear_act_ref(w, a[-rows:], bias, mult, 38))
+
+
 def test_gemm_requant_at_the_narrow_bound(dev):
     # The epilogue keeps rescaled values in i32 when the host shows |acc + bias| < 2^31 and the
     # shift is at least 31: operands at that bound (|acc| = 768 2^14, |bias| = 2^31 - 1 - 768 2^14)
