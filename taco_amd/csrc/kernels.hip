@@ -377,11 +377,11 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                     }
                 return;
             }
-            // Staged in two halves of the wave's rows (64 rows of 64 columns, or 32 of 96) through
-            // this wave's region (row stride RS): the lane's four outputs of a row are one 16-byte
-            // LDS write; the read-modify-write of x then covers whole 16-byte pieces of rows (CPR
-            // per row), all Q loads of a half in flight together.
-            constexpr int HR = TJ == 4 ? 64 : 32, NH = 16 * TI / HR, RS = 64 * TJ + 16;
+            // Staged in parts of 32 of the wave's rows through this wave's region (row stride RS):
+            // the lane's four outputs of a row are one 16-byte LDS write; the read-modify-write of
+            // x then covers whole 16-byte pieces of rows (CPR per row), all Q loads of a part in
+            // flight together (parts of 64 rows of 64 columns held 32 vectors per lane and spilled).
+            constexpr int HR = 32, NH = 16 * TI / HR, RS = 64 * TJ + 16;
             constexpr int CPR = 4 * TJ, Q = HR * CPR / 64;
             static_assert(NH * HR == 16 * TI && HR * RS <= 18432 && Q * 64 == HR * CPR, "residual staging");
             __syncthreads();  // every wave finished reading the stages
