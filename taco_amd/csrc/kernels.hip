@@ -1752,10 +1752,15 @@ __global__ void k_split_out(AttnArgs a, int n_rows, SplitPlan pl, void *scratch)
 }
 
 // Decode attention for head_dim 64 and at most 1,024 keys in one launch: one workgroup (4 waves)
-// per (row, head). The row's K rows go to registers (thread t: keys t + 256 j) and its V rows to
-// LDS (global_load_lds) in one round of loads; the dots, the row max, the table sum, the weights
-// p and the sums p v then come from registers and LDS with the rules of the split kernels above.
-// Dynamic LDS: kmax64 = 64 ceil(kmax / 64) V rows of 64 bytes, then kmax64 weights.
+// per (row, head). The row's K rows go to registers (thread t: keys t + 256 j), the V rows of its
+// first DEC_VLDS keys to LDS (global_load_lds) and those of the later keys to registers in the
+// layout the p v sums read them (thread t: keys DEC_VLDS + t / 4 + 64 i, chunk t % 4), all in one
+// round of loads; the dots, the row max, the table sum, the weights p and the sums p v then come
+// from registers and LDS with the rules of the split kernels above. Dynamic LDS:
+// min(kmax64, DEC_VLDS) V rows of 64 bytes, then kmax64 = 64 ceil(kmax / 64) weights: at most
+// 36 KiB, so four workgroups fit on a CU (a whole 1,024-key V in LDS, 68 KiB, allowed two;
+// measured at 1,024 keys and 768 row-heads: 34.2 -> 31.0 us).
+constexpr int DEC_VLDS = 512;
 template <bool NOCLAMP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_decode64(AttnArgs a,
                                                                                                   int kmax) {
@@ -1770,7 +1775,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     int keys = split_keys(a, r);
     keys = keys < kmax ? keys : kmax;  // the launch's bound holds every row's count
     int8_t *sV = s_dyn;
-    uint32_t *s_p = (uint32_t *)(s_dyn + (size_t)kmax64 * 64);
+    const int vl = kmax64 < DEC_VLDS ? kmax64 : DEC_VLDS;  // the V rows in LDS
+    uint32_t *s_p = (uint32_t *)(s_dyn + (size_t)vl * 64);
     const size_t base = ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * 64;
     if (tid < 16) s_q[tid] = ((const int *)(a.q + (size_t)r * a.ldq + h * 64))[tid];
     // K: up to four keys per thread; a round past the row (uniform) issues nothing, a key past the
@@ -1786,11 +1792,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
     // V: per round of 64 keys, wave w loads keys 16 w .. 16 w + 15 (lane l: key + l / 4, bytes
     // 16 (l % 4)); its 1 KiB lands contiguously, so sV is [key][64]
-    for (int k0 = 0; k0 < keys; k0 += 64) {
+    for (int k0 = 0; k0 < keys && k0 < DEC_VLDS; k0 += 64) {
         int key = k0 + 16 * w + (lane >> 2);
         key = key < keys ? key : keys - 1;
         __builtin_amdgcn_global_load_lds((const void *)(a.vc + base + (size_t)key * 64 + 16 * (lane & 3)),
                                          (lds_void *)(sV + (size_t)(k0 + 16 * w) * 64), 16, 0, 0);
+    }
+    // the V rows of keys DEC_VLDS + tid / 4 + 64 i (chunk tid % 4) into registers
+    constexpr int VR = (1024 - DEC_VLDS) / 64;
+    v4i vr[VR];
+#pragma unroll
+    for (int i = 0; i < VR; i++) {
+        const int k = DEC_VLDS + (tid >> 2) + 64 * i;
+        vr[i] = k < keys ? *(const v4i *)(a.vc + base + (size_t)k * 64 + 16 * (tid & 3)) : v4i{0, 0, 0, 0};
     }
     wait_vmcnt<0>();  // this wave's loads landed (the barrier shows the LDS ones to all)
     __syncthreads();
@@ -1872,16 +1886,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     int32_t lo[16], hi[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) lo[i] = hi[i] = 0;
-    for (int k = tid >> 2; k < keys; k += 64) {
+    auto pv = [&](int k, const v4i raw) {
         const uint32_t p = s_p[k];
         const int32_t pl = (int32_t)(p & 0xffffu), ph = (int32_t)(p >> 16);
-        const v4i raw = *(const v4i *)(sV + (size_t)k * 64 + 16 * g);
         const int8_t *v = (const int8_t *)&raw;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             lo[i] += pl * (int32_t)v[i];
             hi[i] += ph * (int32_t)v[i];
         }
+    };
+    for (int k = tid >> 2; k < keys && k < DEC_VLDS; k += 64) pv(k, *(const v4i *)(sV + (size_t)k * 64 + 16 * g));
+#pragma unroll
+    for (int i = 0; i < VR; i++) {
+        const int k = DEC_VLDS + (tid >> 2) + 64 * i;
+        if (k < keys) pv(k, vr[i]);
     }
     int64_t acc[16];
 #pragma unroll
@@ -2092,12 +2111,13 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
                                : launch_decode_wave<false>(a, n_rows, kmax, stream);
     if (attend_split_one_launch(a.hd, a.ctx_cap, p)) {  // one launch, no scratch
         const int kmax64 = (kmax + 63) & ~63;
-        const size_t dyn = (size_t)kmax64 * 64 + (size_t)kmax64 * 4;
+        if (kmax64 > 1024) return hipErrorInvalidValue;  // the kernel's register rows end at 1,024 keys
+        const size_t dyn = (size_t)(kmax64 < DEC_VLDS ? kmax64 : DEC_VLDS) * 64 + (size_t)kmax64 * 4;
         static bool allowed[2];
         const bool nc = attn_noclamp(a);
         const void *fn = nc ? (const void *)k_attend_decode64<true> : (const void *)k_attend_decode64<false>;
         if (!allowed[nc]) {
-            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024 + 4096);
+            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, DEC_VLDS * 64 + 4096);
             if (e != hipSuccess) return e;
             allowed[nc] = true;
         }
