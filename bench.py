@@ -524,6 +524,41 @@ def run_gemm(args):
     }), flush=True)
 
 
+ISSUE_OPS = (("v_add_u32", 8, None), ("v_mad_i64_i32", 8, None), ("v_fma_f64", 8, None),
+             ("v_mfma_i32_16x16x64_i8", 8, 16), ("v_mfma_i32_32x32x32_i8", 4, 32))
+
+
+def run_issue(args):
+    """Issue rates (hs_probe_issue): clocks per instruction per SIMD at the nominal 2.4 GHz for
+    three VALU forms and the two int8 MFMA forms, at 1, 2 and 4 waves per SIMD. An MFMA form's
+    peak is 16 (16 x 16 x 64) or 32 (32 x 32 x 32) clocks per instruction: 5.0 POPS over 1,024
+    SIMDs at 2.4 GHz is 2,035 int8 ops per clock and SIMD."""
+    from taco_amd import hip
+    dev = hip.HipDevice.open(0)
+    iters = 4096
+    rows = []
+    for op, (name, per_round, peak_clk) in enumerate(ISSUE_OPS):
+        for wps in (1, 2, 4):
+            ns = min(hip.probe_issue(dev, op, wps, iters) for _ in range(3))
+            inst = wps * iters * per_round  # per SIMD
+            clk = ns * 1e-9 * 2.4e9 / inst
+            row = {"op": name, "waves_per_simd": wps, "ns": ns, "clocks_per_instruction": round(clk, 2)}
+            if peak_clk:
+                row["frac_of_peak_rate"] = round(peak_clk / clk, 3)
+            rows.append(row)
+            log(f"{name:24s} {wps} waves/SIMD: {clk:6.2f} clocks per instruction"
+                + (f" ({peak_clk / clk:.3f} of the peak rate)" if peak_clk else ""))
+    big = [r for r in rows if r["op"] == "v_mfma_i32_16x16x64_i8" and r["waves_per_simd"] == 2][0]
+    line = {"metric": "int8 MFMA issue rate on 1 MI355X (v_mfma_i32_16x16x64_i8, 2 waves per SIMD)",
+            "value": big["frac_of_peak_rate"], "unit": "fraction of the peak rate", "n_gpus": 1,
+            "steps": 3, "warmup": 1, "ms_per_step": round(big["ns"] / 1e6, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": "issue-rate probe: 4,096 rounds per wave, 256 x waves workgroups",
+                       "rows": rows},
+            "roofline": None, "cpu_baseline": None}
+    print(json.dumps(line), flush=True)
+
+
 def run_attend(args):
     """Decode attention, one query row per stream: 64 streams x 12 heads x 64 over caches of
     ctx positions, rotating over cache sets that together exceed the 256 MB Infinity Cache."""
@@ -649,7 +684,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="fold-gpt2-small",
-                    choices=sorted(FOLDS) + ["gemm-qkv", "attend-decode"])
+                    choices=sorted(FOLDS) + ["gemm-qkv", "attend-decode", "issue-rates"])
     ap.add_argument("--windows", type=int, default=0)
     ap.add_argument("--window-tokens", type=int, default=0)
     ap.add_argument("--cpu-windows", type=int, default=0,
@@ -672,6 +707,8 @@ def main():
         run_fold(args)
     elif args.workload == "gemm-qkv":
         run_gemm(args)
+    elif args.workload == "issue-rates":
+        run_issue(args)
     else:
         run_attend(args)
 

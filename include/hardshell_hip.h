@@ -315,6 +315,14 @@ hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8
  * streaming kernel (hipEvents on the device stream): the HBM read bandwidth a kernel reaches,
  * as read_gpu_ns (crates/hardshell-cuda/src/ops.rs:328-335). */
 hs_status hs_read_bw(hs_device *dev, size_t bytes, size_t reps, uint64_t *ns);
+/* The GPU time of one launch of `iters` rounds of independent instructions of one kind on every
+ * SIMD (256 x waves_per_simd workgroups of 4 waves, one wave on each SIMD of a CU): op 0 v_add_u32, 1 v_mad_i64_i32,
+ * 2 v_fma_f64 (8 chains per wave), 3 v_mfma_i32_16x16x64_i8 (8 accumulators per wave), 4
+ * v_mfma_i32_32x32x32_i8 (4 accumulators). No counterpart in the reference: it measures the issue
+ * rates that bound the kernels here (clocks per instruction = ns x clock / instructions per SIMD).
+ * Allocates a 1 KiB sink for the call. */
+hs_status hs_probe_issue(hs_device *dev, uint32_t op, uint32_t waves_per_simd, uint32_t iters,
+                         uint64_t *ns);
 
 /* ---- Batch profiling: CudaBatch::profile (crates/hardshell-cuda/src/batch.rs:493-498) ----- */
 /* With profiling on, every kernel launch of the batch is bracketed by hipEvents on the batch's

@@ -1692,6 +1692,24 @@ extern "C" hs_status hs_read_bw(hs_device *dev, size_t bytes, size_t reps, uint6
     return st;
 }
 
+extern "C" hs_status hs_probe_issue(hs_device *dev, uint32_t op, uint32_t waves_per_simd, uint32_t iters,
+                                    uint64_t *ns) {
+    hs::clear_error();
+    if (!dev || !ns) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (op > 4 || waves_per_simd < 1 || waves_per_simd > 8 || iters < 1 || iters > (1u << 20))
+        return hs::fail(HS_UNSUPPORTED, 0, "op must be 0..4, waves_per_simd 1..8, iters 1..2^20");
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    int *sink = nullptr;
+    HIP_TRY(hipMalloc((void **)&sink, 256 * sizeof(int)));
+    hipError_t e = hs::launch_issue_probe((int)op, (int)waves_per_simd, (int)iters, sink, dev->stream);  // untimed
+    hs_status st = e == hipSuccess ? HS_OK : hip_fail("issue probe", e);
+    if (st == HS_OK)
+        st = time_reps(dev, 1, ns, [&] { return hs::launch_issue_probe((int)op, (int)waves_per_simd, (int)iters, sink, dev->stream); });
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipFree(sink);
+    return st;
+}
+
 extern "C" hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8_t *k_cache,
                                                 const int8_t *v_cache, const uint32_t *ctx, size_t b,
                                                 size_t h, size_t hd, size_t ctx_cap, int32_t score_m,

@@ -130,6 +130,10 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream);
 // The stream-read probe: every 16-byte word of buf[0 .. n16) read once (one xor per word folded
 // into sink[grid x 256] so the loads are kept).
 hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipStream_t stream);
+// op: 0 v_add_u32, 1 v_mad_i64_i32, 2 v_fma_f64 (8 chains each), 3 v_mfma_i32_16x16x64_i8 (8
+// accumulators), 4 v_mfma_i32_32x32x32_i8 (4); 256 x waves_per_simd workgroups of 4 waves; sink
+// holds 256 ints.
+hipError_t launch_issue_probe(int op, int waves_per_simd, int iters, int *sink, hipStream_t stream);
 constexpr int READ_BW_GRID = 2048;  // 8 workgroups of 256 threads per CU
 
 // K and V of each row into the caches [L][slots][H][n_ctx][hd] (layer base pointers given).

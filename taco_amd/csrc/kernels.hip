@@ -1011,6 +1011,67 @@ hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipS
 }
 
 // =============================================================================================
+// Issue-rate probe: `iters` rounds of independent instructions of one kind per wave (8 chains of
+// a VALU form, or 8 accumulators of 16 x 16 x 64 / 4 of 32 x 32 x 32 MFMAs), workgroups of 4
+// waves (one per SIMD of a CU), 256 x `waves_per_simd` workgroups; the time over the instruction count gives the
+// clocks per instruction per SIMD (hs_probe_issue). The results go to `sink` only when a lane
+// sees an impossible value, so nothing is folded away.
+// =============================================================================================
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+template <int OP>
+__global__ __launch_bounds__(256) void k_issue_probe(int *sink, int iters, int seed) {
+    const int t = threadIdx.x;
+    int32_t a[8];
+    int64_t b[8];
+    double c[8];
+    v4i x[8];
+    v16i y[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = seed + i + t;
+        b[i] = (int64_t)a[i] * 3;
+        c[i] = a[i];
+        x[i] = v4i{a[i], i, t, seed};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = v16i{};
+    const v4i fa = {seed, t, 7, 9}, fb = {t, seed, 3, 5};
+    const int m = seed | 1;
+    const double md = 1.000001;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (OP == 0) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a[i]) : "s"(m));
+            if (OP == 1) asm volatile("v_mad_i64_i32 %0, vcc, %1, %2, %0" : "+v"(b[i]) : "v"(a[i]), "s"(m) : "vcc");
+            if (OP == 2) asm volatile("v_fma_f64 %0, %0, %1, %1" : "+v"(c[i]) : "s"(md));
+            if (OP == 3) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(x[i]) : "v"(fa), "v"(fb));
+            if (OP == 4 && i < 4) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(y[i]) : "v"(fa), "v"(fb));
+        }
+    }
+    int64_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc += a[i] + b[i] + (int64_t)c[i] + x[i][0] + x[i][3];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc += y[i][0] + y[i][15];
+    if (acc == 0x7fffffffffffll) sink[t] = (int)acc;
+}
+
+hipError_t launch_issue_probe(int op, int waves_per_simd, int iters, int *sink, hipStream_t stream) {
+    const dim3 grid(256 * waves_per_simd), block(256);
+    switch (op) {
+        case 0: hipLaunchKernelGGL(k_issue_probe<0>, grid, block, 0, stream, sink, iters, 7); break;
+        case 1: hipLaunchKernelGGL(k_issue_probe<1>, grid, block, 0, stream, sink, iters, 7); break;
+        case 2: hipLaunchKernelGGL(k_issue_probe<2>, grid, block, 0, stream, sink, iters, 7); break;
+        case 3: hipLaunchKernelGGL(k_issue_probe<3>, grid, block, 0, stream, sink, iters, 7); break;
+        case 4: hipLaunchKernelGGL(k_issue_probe<4>, grid, block, 0, stream, sink, iters, 7); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// =============================================================================================
 // Embedding (reference.rs:208-221): x = clamp(rescale(wte[tok]) + rescale(wpe[pos]), -R, R).
 // =============================================================================================
 

@@ -160,6 +160,7 @@ def lib() -> C.CDLL:
                                               C.c_int32, C.c_uint8, P, S, C.c_uint8, P, P]
         L.hs_op_attend_decode_dev_noalloc.argtypes = L.hs_op_attend_decode_dev.argtypes
         L.hs_read_bw.argtypes = [P, S, S, C.POINTER(C.c_uint64)]
+        L.hs_probe_issue.argtypes = [P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]
         L.hs_model_load_with.argtypes = [P, P, S, P, C.POINTER(P)]
         L.hs_batch_run_without_readback.argtypes = [P, P, S]
         L.hs_device_kernel_resources.argtypes = [P, P, P, P, P, S, C.POINTER(S)]
@@ -503,6 +504,13 @@ def read_bw(dev: HipDevice, nbytes: int, reps: int) -> float:
     ns = C.c_uint64()
     _check(lib().hs_read_bw(dev.h, nbytes, reps, C.byref(ns)))
     return nbytes * reps / (ns.value * 1e-9)
+
+
+def probe_issue(dev: HipDevice, op: int, waves_per_simd: int, iters: int) -> int:
+    """hs_probe_issue: the GPU ns of one launch of `iters` rounds of op on every SIMD."""
+    ns = C.c_uint64()
+    _check(lib().hs_probe_issue(dev.h, op, waves_per_simd, iters, C.byref(ns)))
+    return ns.value
 
 
 def gemm_layout(m: int, n: int, k: int) -> Tuple[int, int, int]:

@@ -568,6 +568,17 @@ def test_run_without_readback_advances_like_run_weights(golden):
     assert np.array_equal(c.run_weights(nxt), a.run_weights(nxt))
 
 
+def test_probe_issue(dev):
+    """hs_probe_issue times every op and refuses the ones it does not have."""
+    from taco_amd import hip
+    for op in range(5):
+        assert hip.probe_issue(dev, op, 1, 64) > 0
+    with pytest.raises(hip.HipError):
+        hip.probe_issue(dev, 5, 1, 64)
+    with pytest.raises(hip.HipError):
+        hip.probe_issue(dev, 0, 9, 64)
+
+
 def test_kernel_resources(dev):
     """CudaDevice::kernel_resources (device.rs:65-74): every listed kernel has a name and
     registers; the main GEMM loop does not spill."""
