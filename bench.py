@@ -205,6 +205,53 @@ def mfma_summary(csv_path, tokens_sha, command):
             "gemm_int8_ops": int(tot_ops), "kernels": kernels}
 
 
+SQ_PASSES = (
+    ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA",
+     "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "SQ_WAVE_CYCLES"),
+    ("SQ_WAVE_CYCLES", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_WAIT_INST_ANY",
+     "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE"),
+)
+
+
+def sq_summary(csv_paths, tokens_sha, command):
+    """Per-kernel instruction mix from the two rocprofv3 --pmc runs of SQ_PASSES: instructions
+    per wave by kind, and, as fractions of the waves' lifetime (SQ_WAVE_CYCLES, quad-cycles like
+    the ACTIVE and WAIT counters), the cycles spent issuing VALU and LDS instructions and waiting
+    to issue; LDS bank-conflict cycles per LDS-active cycle."""
+    import csv
+    import collections
+    agg = collections.defaultdict(lambda: collections.defaultdict(float))
+    for pi, path in enumerate(csv_paths):
+        per = collections.defaultdict(dict)
+        for r in csv.DictReader(open(path)):
+            per[(int(r["Dispatch_Id"]), r["Kernel_Name"])][r["Counter_Name"]] = float(r["Counter_Value"])
+        for (_, name), c in per.items():
+            a = agg[name.split("(")[0].replace("void ", "")]
+            a[f"dispatches{pi}"] += 1
+            for kk, v in c.items():
+                a[f"{kk}#{pi}"] += v
+    kernels = {}
+    for name, a in sorted(agg.items()):
+        n0, n1 = a["dispatches0"], a["dispatches1"]
+        if not n0 or not n1 or not a["SQ_WAVES#0"]:
+            continue
+        waves = a["SQ_WAVES#0"] / n0
+        per_wave = lambda k: round(a[k + "#0"] / n0 / waves, 1)
+        wc = a["SQ_WAVE_CYCLES#1"]
+        kernels[name] = {
+            "dispatches": int(n0), "waves_per_dispatch": int(waves),
+            "valu_per_wave": per_wave("SQ_INSTS_VALU"), "salu_per_wave": per_wave("SQ_INSTS_SALU"),
+            "lds_per_wave": per_wave("SQ_INSTS_LDS"), "mfma_per_wave": per_wave("SQ_INSTS_MFMA"),
+            "vmem_rd_per_wave": per_wave("SQ_INSTS_VMEM_RD"), "vmem_wr_per_wave": per_wave("SQ_INSTS_VMEM_WR"),
+            "valu_active_frac": round(a["SQ_ACTIVE_INST_VALU#1"] / wc, 3) if wc else None,
+            "lds_active_frac": round(a["SQ_ACTIVE_INST_LDS#1"] / wc, 3) if wc else None,
+            "wait_frac": round(a["SQ_WAIT_INST_ANY#1"] / wc, 3) if wc else None,
+            "lds_conflict_per_active": (round(a["SQ_LDS_BANK_CONFLICT#1"] / a["SQ_LDS_IDX_ACTIVE#1"], 3)
+                                        if a["SQ_LDS_IDX_ACTIVE#1"] else None),
+            "gui_cycles_per_dispatch": int(a["GRBM_GUI_ACTIVE#1"] / 8 / n1)}
+    return {"tokens_sha256": tokens_sha, "command": command, "kernels": kernels}
+
+
 def committed_mfma(workload, tokens_sha):
     """The GEMM MFMA utilisation of the committed counter summary of this workload, or None."""
     path = os.path.join(HERE, "profiles", workload.replace("-", "_") + "_mfma.json")
@@ -674,7 +721,22 @@ def main_mfma(argv):
     print(json.dumps(mfma_summary(csv_path, tokens_sha, cmd), indent=1))
 
 
+def main_sq(argv):
+    """python bench.py --sq-summary PASS1.csv PASS2.csv WORKLOAD: the instruction-mix summary of
+    the two rocprofv3 --pmc runs of SQ_PASSES over `bench.py --workload WORKLOAD --steps 1
+    --warmup 0 --no-cpu --no-unfold --sustain-s 0`."""
+    from taco_amd import synth
+    a_csv, b_csv, workload = argv
+    dims_name, W, n, _ = FOLDS[workload]
+    tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
+    cmd = " ; ".join("rocprofv3 --pmc " + " ".join(p) + " --output-format csv -- python3 bench.py --workload "
+                     + workload + " --steps 1 --warmup 0 --no-cpu --no-unfold --sustain-s 0" for p in SQ_PASSES)
+    print(json.dumps(sq_summary([a_csv, b_csv], tokens_sha, cmd), indent=1))
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--sq-summary":
+        return main_sq(sys.argv[2:])
     if len(sys.argv) > 1 and sys.argv[1] == "--traffic-summary":
         return main_traffic(sys.argv[2:])
     if len(sys.argv) > 1 and sys.argv[1] == "--mfma-summary":

@@ -66,6 +66,12 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// A compile-time flag for the steps of an unrolled loop (the first k-step differs).
+template <bool B>
+struct Flag {
+    static constexpr bool value = B;
+};
+
 // NARROW: g.fast32 holds and the shift is at least 31, so every rescaled value fits i32: with
 // |a + bias| <= 2^31 - 1 and -2^31 <= mult < 2^31, |(a + bias) mult| <= (2^31 - 1) 2^31, so
 // ((a + bias) mult + 2^30) >> 31 lies in [-2^31 + 1, 2^31 - 1] (larger shifts shrink it).
@@ -109,18 +115,43 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
     const int m0 = mt * BM, n0 = nt * BN;
     const int K = g.k_pad;
 
+    // The first k-step's MFMAs take the accumulators' start values as their C operand (no
+    // zeroing moves): 0, or, for the NARROW epilogues with a bias, the bias of the lane's columns
+    // (SWAP: columns cw + 16 j + 4 (lane / 16) + e). fast32 bounds every partial sum plus the
+    // bias by k 2^14 + max|b| < 2^31, so the i32 accumulation stays exact and the epilogue adds
+    // no bias.
+    constexpr bool FOLD_BIAS = NARROW && SWAP && (EPI == (int)Epi::Act || EPI == (int)Epi::Residual ||
+                                                  EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide);
     v4i acc[TI][TJ];
+    v4i init[TJ];
 #pragma unroll
-    for (int i = 0; i < TI; i++)
+    for (int j = 0; j < TJ; j++) {
+        init[j] = v4i{0, 0, 0, 0};
+        if constexpr (FOLD_BIAS) {
+            const int n4 = n0 + wn * 16 * TJ + 16 * j + 4 * (lane >> 4);
+            if (g.params_padded) {
+                init[j] = *(const v4i *)(g.bias + n4);
+            } else {
 #pragma unroll
-        for (int j = 0; j < TJ; j++) acc[i][j] = v4i{0, 0, 0, 0};
+                for (int e = 0; e < 4; e++) init[j][e] = n4 + e < g.n ? g.bias[n4 + e] : 0;
+            }
+        }
+    }
+    auto mfma_ij = [&](const v4i &a, const v4i &b, const v4i &c) {
+        return SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a, c, 0, 0, 0)
+                    : __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+    };
     auto mfma_step = [&](const v4i *af, const v4i *bf) {
 #pragma unroll
         for (int i = 0; i < TI; i++)
 #pragma unroll
-            for (int j = 0; j < TJ; j++)
-                acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
-                                 : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < TJ; j++) acc[i][j] = mfma_ij(af[i], bf[j], acc[i][j]);
+    };
+    auto mfma_first = [&](const v4i *af, const v4i *bf) {
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+            for (int j = 0; j < TJ; j++) acc[i][j] = mfma_ij(af[i], bf[j], init[j]);
     };
 
     if constexpr (BN == 256) {
@@ -170,7 +201,8 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
             return *(const v4i *)(st + (BM + wn * 16 * TJ + 16 * j) * 128);
         };
         issue(0, 0);
-        for (int kt = 0; kt < nk2; kt++) {
+        auto body = [&](int kt, auto first_tag) {
+            constexpr bool FIRST = decltype(first_tag)::value;
             const int stage = kt & 1;
             if (kt + 1 < nk2) {
                 // stage kt + 1 goes to the buffer read in step kt - 1 (free after its barrier)
@@ -199,15 +231,15 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
 #pragma unroll
             for (int i = 0; i < TI; i++) {
 #pragma unroll
-                for (int j = 0; j < TJ; j++)
-                    acc[i][j] = SWAP ? __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0)
-                                     : __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TJ; j++) acc[i][j] = mfma_ij(af[i], bf[j], FIRST ? init[j] : acc[i][j]);
                 af[i] = read_a(s1, i);
             }
             mfma_step(af, bn);
             // every wave finished reading this stage before step kt + 1 reloads it
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        }
+        };
+        body(0, Flag<true>{});
+        for (int kt = 1; kt < nk2; kt++) body(kt, Flag<false>{});
     } else {
     // Split-K: workgroup row blockIdx.y takes K bytes [kb0, kb0 + kslice) of a product whose
     // partials go to out + blockIdx.y * m * ldo (Raw only).
@@ -263,10 +295,10 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
     else if (nk == 2) wait_vmcnt<LOADS>();
     else wait_vmcnt<0>();
     asm volatile("s_barrier" ::: "memory");
-    v4i af[TI], bf[TJ];
-    read_frags(0, af, bf);
-    for (int kt = 0; kt < nk; kt++) {
-        v4i an[TI], bn[TJ];
+    // One k-step: the MFMAs of step kt on (ca, cb) while step kt + 1's fragments are read into
+    // (na, nb). Two register sets alternate (the loop is unrolled by two), so no fragment moves
+    // between registers.
+    auto step = [&](int kt, const v4i *ca, const v4i *cb, v4i *na, v4i *nb, auto first_tag) {
         const bool more = kt + 1 < nk;
         if (more) {
             // stage kt + 1 landed (stage kt + 2's loads may be outstanding); this wave's reads of
@@ -280,14 +312,20 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         // unconditional (the last step re-reads its own stage), so the reads share the MFMAs'
         // basic block and no wait for them lands before the MFMAs; the empty asm keeps the
         // compiler from sinking them into the next step (where they would wait at its barrier)
-        read_frags(more ? kt + 1 : kt, an, bn);
+        read_frags(more ? kt + 1 : kt, na, nb);
         asm volatile("" ::: "memory");
-        mfma_step(af, bf);
-#pragma unroll
-        for (int i = 0; i < TI; i++) af[i] = an[i];
-#pragma unroll
-        for (int j = 0; j < TJ; j++) bf[j] = bn[j];
+        if constexpr (decltype(first_tag)::value) mfma_first(ca, cb);
+        else mfma_step(ca, cb);
+    };
+    v4i fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    read_frags(0, fa0, fb0);
+    step(0, fa0, fb0, fa1, fb1, Flag<true>{});
+    int kt = 1;
+    for (; kt + 1 < nk; kt += 2) {
+        step(kt, fa1, fb1, fa0, fb0, Flag<false>{});
+        step(kt + 1, fa0, fb0, fa1, fb1, Flag<false>{});
     }
+    if (kt < nk) step(kt, fa1, fb1, fa0, fb0, Flag<false>{});
     }
 
     // Epilogue. Lane layout of each 16 x 16 tile (i, j) of the wave: with SWAP (the W fragment is
@@ -314,7 +352,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         auto params = [&](int j, int32_t *bj, int32_t *mj) {
             const int n4 = cw + 16 * j + 4 * cg;
             if (g.params_padded) {  // every column of a tile is below n_pad: 16-byte loads
-                const v4i b4 = HAS_BIAS ? *(const v4i *)(g.bias + n4) : v4i{0, 0, 0, 0};
+                const v4i b4 = HAS_BIAS && !FOLD_BIAS ? *(const v4i *)(g.bias + n4) : v4i{0, 0, 0, 0};
                 const v4i m4 = EPI != (int)Epi::Raw ? *(const v4i *)(g.mult + n4) : v4i{0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -327,7 +365,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
             for (int e = 0; e < 4; e++) {
                 const int n = n4 + e;
                 const bool ok = n < g.n;
-                bj[e] = (HAS_BIAS && ok) ? g.bias[n] : 0;
+                bj[e] = (HAS_BIAS && !FOLD_BIAS && ok) ? g.bias[n] : 0;
                 mj[e] = (EPI != (int)Epi::Raw && ok) ? g.mult[n] : 0;
             }
         };
@@ -946,7 +984,8 @@ hipError_t launch_wide_combine(const int32_t *planes, const int32_t *wsum, int m
 hipError_t launch_gemm(Epi epi, const GemmArgs &ga, hipStream_t stream) {
     GemmArgs g = ga;
     if (g.m <= 0 || g.n <= 0) return hipSuccess;
-    if (g.k_pad % GEMM_BK != 0) return hipErrorInvalidValue;
+    // at least one k-step: the loop's first step runs unconditionally
+    if (g.k_pad < GEMM_BK || g.k_pad % GEMM_BK != 0) return hipErrorInvalidValue;
     // the tile order's M-tile group (the kernel divides by it): set and checked before any launch
     const int gm = (g.m + GEMM_BM - 1) / GEMM_BM;
     if (g.group == 0) g.group = gemm_group(g.m);
