@@ -8,6 +8,10 @@
  *
  * The bytes are those of crates/taco/src/codec.rs (encode_block), crates/taco-coder (the
  * range coder) and crates/taco-format/src/writer.rs:245-288 (Container::build).
+ *
+ * Calls on different batches may run on different host threads at once (each batch has its own
+ * stream; the range coders' worker pool takes their jobs one after another). One batch serves
+ * one call at a time.
  */
 #ifndef TACO_HIP_H
 #define TACO_HIP_H

@@ -149,7 +149,8 @@ bool read_varint(const uint8_t *b, size_t len, uint64_t &value, size_t &used) { 
 // A persistent pool of host threads: run(n, f) calls f(0) .. f(n - 1) on the workers and the
 // calling thread and returns when all are done. Blocks are independent streams, so their range
 // coders run in parallel (the reference codes blocks in parallel too, crates/taco/src/parallel.rs).
-// The pool is never destroyed: its threads wait for work until the process ends.
+// The pool is never destroyed: its threads wait for work until the process ends. run() may be
+// called from several host threads; their jobs run one after another.
 class Pool {
   public:
     static Pool &get() {
@@ -161,6 +162,8 @@ class Pool {
             for (size_t i = 0; i < n; i++) f(i);
             return;
         }
+        // one job at a time: callers on several host threads (one per batch) take turns
+        std::lock_guard<std::mutex> one(run_mu_);
         std::unique_lock<std::mutex> lk(mu_);
         job_ = &f;
         n_ = n;
@@ -208,7 +211,7 @@ class Pool {
         }
     }
     unsigned workers_ = 0;
-    std::mutex mu_;
+    std::mutex run_mu_, mu_;
     std::condition_variable cv_, done_cv_;
     const std::function<void(size_t)> *job_ = nullptr;
     size_t n_ = 0, next_ = 0, done_ = 0;
