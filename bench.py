@@ -24,8 +24,9 @@ after the timed steps.
 Other workloads (--workload) measure the other configurations of the path, each with its own
 line: the c_attn GEMM alone (gemm-qkv: M 256 and 16,384, K 768, N 2,304), decode attention over
 HBM-resident caches (attend-decode: 64 streams x 12 heads x 64, contexts 128 / 512 / 1,024),
-the GPT-2-medium fold with the full unfold round trip (fold-gpt2-medium: 256 x 256 tokens) and
-the GPT-2-XL fold (fold-gpt2-xl: 512 x 512 tokens).
+the GPT-2-medium fold with the full unfold round trip (fold-gpt2-medium: 256 x 256 tokens),
+the GPT-2-XL fold (fold-gpt2-xl: 512 x 512 tokens), and the fold's GEMM shapes beside the vendor
+library's int8 product (gemm-vendor: hipBLASLt through torch._int_mm, i32 outputs, no epilogue).
 """
 
 import argparse
@@ -571,6 +572,95 @@ def run_gemm(args):
     }), flush=True)
 
 
+VENDOR_SHAPES = (  # (name, M, K, N): the GPT-2-small fold's products, and one decode pass's c_attn
+    ("c_attn", 16384, 768, 2304), ("c_proj", 16384, 768, 768), ("c_fc", 16384, 768, 3072),
+    ("mlp.c_proj", 16384, 3072, 768), ("lm_head (N padded to 50,304)", 2048, 768, 50304),
+    ("c_attn, decode pass", 256, 768, 2304))
+
+
+def run_gemm_vendor(args):
+    """The fold's GEMM shapes on this build's k_gemm (i8 x i8 -> i32, bias, per-channel rescale,
+    clamp to +-127: the Act epilogue, i8 outputs) and on the vendor library's int8 product
+    (hipBLASLt through torch._int_mm: i8 x i8 -> i32, no epilogue, 4 B written per output).
+    Both on the same operands, timed with hipEvents over 20 launches (the best of 3 runs); rows
+    0..63 of each are checked against the oracle's exact product. torch is only the comparator
+    here: the fold path never calls it."""
+    import torch
+    from oracle import oracle as O
+    from taco_amd import hip
+    dev = hip.HipDevice.open(0)
+    rng = np.random.default_rng(0xBEEF)
+    rows, total_ops, ours_us, lib_us = [], 0, 0.0, 0.0
+    for name, M, K, N in VENDOR_SHAPES:
+        w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+        bias = rng.integers(-(1 << 16), (1 << 16) + 1, N).astype(np.int32)
+        mult = rng.integers(1 << 30, 1 << 31, N).astype(np.int64).astype(np.int32)
+        shift = 42
+        mp, np_, kp = hip.gemm_layout(M, N, K)
+        bufs = [_dev_buf(hip, dev, x) for x in (hip.gemm_pack(w, np_, kp), hip.gemm_pack(a, mp, kp), bias, mult)]
+        out = np.zeros((M, N), np.int8)
+        dout = _dev_buf(hip, dev, out)
+        ns = C.c_uint64()
+        hip._check(hip.lib().hs_op_gemm_requant_gpu_ns(dev.h, bufs[0], bufs[1], bufs[2], bufs[3], shift,
+                                                         M, N, K, dout, 5, C.byref(ns)))
+        best = float("inf")
+        for _ in range(3):
+            hip._check(hip.lib().hs_op_gemm_requant_gpu_ns(dev.h, bufs[0], bufs[1], bufs[2], bufs[3], shift,
+                                                             M, N, K, dout, 20, C.byref(ns)))
+            best = min(best, ns.value / 20 / 1e3)
+        hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout, out.nbytes))
+        for p in bufs + [dout]:
+            hip.lib().hs_device_free(dev.h, p)
+        ours_ok = bool(np.array_equal(out[:64], O.linear_act_ref(w, a[:64], bias, mult, shift)))
+        ta = torch.from_numpy(a).cuda()
+        tb = torch.from_numpy(w).cuda().t()  # [K, N], column-major: the NT product
+        for _ in range(5):
+            tc = torch._int_mm(ta, tb)
+        torch.cuda.synchronize()
+        lbest = float("inf")
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(20):
+                tc = torch._int_mm(ta, tb)
+            e1.record()
+            torch.cuda.synchronize()
+            lbest = min(lbest, e0.elapsed_time(e1) * 1e3 / 20)
+        lib_ok = bool(np.array_equal(tc[:64].cpu().numpy().astype(np.int64), O.matmul_i8(w, a[:64])))
+        del ta, tb, tc
+        ops = 2 * M * N * K
+        total_ops += ops
+        ours_us += best
+        lib_us += lbest
+        log(f"{name:30s} M {M:5d} K {K:4d} N {N:5d}: k_gemm {best:8.2f} us {ops / best / 1e6:7.1f} TOPS "
+            f"(rows 0..63 exact: {ours_ok}); hipBLASLt {lbest:8.2f} us {ops / lbest / 1e6:7.1f} TOPS "
+            f"(rows 0..63 exact: {lib_ok}); {lbest / best:.2f}x")
+        if not (ours_ok and lib_ok):
+            log("PARITY FAILURE")
+            sys.exit(1)
+        rows.append(dict(name=name, M=M, K=K, N=N, k_gemm_us=round(best, 3),
+                         k_gemm_tops=round(ops / best / 1e6, 1), hipblaslt_us=round(lbest, 3),
+                         hipblaslt_tops=round(ops / lbest / 1e6, 1), speedup=round(lbest / best, 3)))
+    agg = total_ops / ours_us / 1e6
+    print(json.dumps({
+        "metric": "int8 GEMM of the fold's shapes on 1 MI355X: fused requantize kernel vs hipBLASLt",
+        "value": round(agg, 1), "unit": "TOPS", "n_gpus": 1, "steps": 20, "warmup": 5,
+        "ms_per_step": round(ours_us / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "the GPT-2-small fold's GEMM shapes (M 16,384; the LM head at 2,048 "
+                               "rows) and the decode c_attn (M 256), Act epilogue vs torch._int_mm",
+                   "shapes": rows},
+        "vendor": {"library": "hipBLASLt through torch._int_mm (i32 outputs, no epilogue)",
+                   "tops": round(total_ops / lib_us / 1e6, 1),
+                   "time_ratio": round(lib_us / ours_us, 3)},
+        "roofline": {"bound": "mfma", "kernel": "k_gemm<Act>", "achieved": round(agg, 1),
+                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(agg / INT8_PEAK_TOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 ISSUE_OPS = (("v_add_u32", 8, None), ("v_mad_i64_i32", 8, None), ("v_fma_f64", 8, None),
              ("v_mfma_i32_16x16x64_i8", 8, 16), ("v_mfma_i32_32x32x32_i8", 4, 32))
 
@@ -746,7 +836,7 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="fold-gpt2-small",
-                    choices=sorted(FOLDS) + ["gemm-qkv", "attend-decode", "issue-rates"])
+                    choices=sorted(FOLDS) + ["gemm-qkv", "gemm-vendor", "attend-decode", "issue-rates"])
     ap.add_argument("--windows", type=int, default=0)
     ap.add_argument("--window-tokens", type=int, default=0)
     ap.add_argument("--cpu-windows", type=int, default=0,
@@ -769,6 +859,8 @@ def main():
         run_fold(args)
     elif args.workload == "gemm-qkv":
         run_gemm(args)
+    elif args.workload == "gemm-vendor":
+        run_gemm_vendor(args)
     elif args.workload == "issue-rates":
         run_issue(args)
     else:

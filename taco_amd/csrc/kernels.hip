@@ -79,8 +79,8 @@ struct Flag {
 // VEC: the output rows are 16-byte aligned (checked by the launcher); the four-columns epilogues
 // then stage and store 16-byte pieces, else they store each output on its own.
 // BM x BN tiles: 256 x 64 (2 x 1 waves), 256 x 128 (2 x 2), 256 x 256 (2 x 4, the full-line
-// loop) and 128 x 192 (2 x 2 waves of 64 x 96). Each wave computes a
-// (BM / 2) x (BN / WN) sub-tile: TI x TJ tiles of 16 x 16.
+// loop), 128 x 192 (2 x 2 waves of 64 x 96) and 64 x 64 (2 x 1 waves of 32 x 64, decode
+// passes). Each wave computes a (BM / 2) x (BN / WN) sub-tile: TI x TJ tiles of 16 x 16.
 constexpr int gemm_wn(int bn) { return bn == 192 ? 2 : bn / 64; }  // waves along N
 constexpr int gemm_waves(int bn) { return 2 * gemm_wn(bn); }
 
@@ -89,7 +89,8 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
     constexpr int WN = gemm_wn(BN), WAVES = 2 * WN, TI = BM / 32, TJ = BN / WN / 16;
     constexpr int FRAGS = BM / 16 + BN / 16, LOADS = FRAGS / WAVES;
     static_assert(FRAGS % WAVES == 0, "whole fragments per wave");
-    static_assert(TI * TJ <= 32 && (BM == GEMM_BM || (BM == 128 && BN == 192)), "tile shapes");
+    static_assert(TI * TJ <= 32 && (BM == GEMM_BM || (BM == 128 && BN == 192) || (BM == 64 && BN == 64)),
+                  "tile shapes");
     // The i16-plane epilogues pair rows 2r and 2r + 1 in one lane and keep the W-as-columns
     // layout; every other epilogue takes four consecutive columns of a row per lane.
     constexpr bool SWAP = EPI != (int)Epi::ResidualWide && EPI != (int)Epi::LogitsWide &&
@@ -568,11 +569,14 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         }
         // Act, Gelu, GeluWide: i8 outputs (GeluWide: the two planes of each i16 output), staged
         // per wave in LDS (the wave's rows x RS8 bytes) and stored as 16-byte row pieces. Gelu copies its
-        // table (256 or 65,536 entries) into LDS first; the staging regions follow it.
+        // table (256 or 65,536 entries) into LDS first; the staging regions follow it. The 64 x 64
+        // tiles of decode passes read the table through the caches instead (a 64 KiB copy per
+        // workgroup would outweigh the 4,096 lookups of its tile).
+        constexpr bool GELU_LDS = BM != 64;
         int toff = 0;
         if (vec) {
             __syncthreads();  // every wave finished reading the stages
-            if (EPI == (int)Epi::Gelu) {
+            if (EPI == (int)Epi::Gelu && GELU_LDS) {
                 const int T = 2 * g.gelu_off;
                 for (int c = threadIdx.x; c < T / 16; c += 64 * WAVES)
                     *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
@@ -626,7 +630,8 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                     uint32_t b[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)gemm_lds[acc[i][j][e]] : byte_of(acc[i][j][e]);
+                        b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)(GELU_LDS ? gemm_lds[acc[i][j][e]] : g.gelu[acc[i][j][e]])
+                                                     : byte_of(acc[i][j][e]);
                     *(uint32_t *)(wr + (16 * i + rl) * RS8 + 16 * j + 4 * cg) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
                     if (EPI == (int)Epi::Gelu && j == TJ - 1) asm volatile("" ::: "memory");  // 4 TJ lookups in flight at most
                 }
@@ -734,14 +739,15 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     GemmArgs g = ga;
     const int gm = (g.m + BM - 1) / BM, gn = (g.n + BN - 1) / BN;
     // the group of the tile order counts 256-row tiles: the same band of rows in BM-row tiles
-    if (BM != GEMM_BM) g.group = 2 * g.group < gm ? 2 * g.group : gm;
+    if (BM != GEMM_BM) g.group = (GEMM_BM / BM) * g.group < gm ? (GEMM_BM / BM) * g.group : gm;
     // the stages, and the epilogue's LDS: per-wave staging regions (18 KiB for the u16 logits
     // and the i16-plane epilogues, 10 KiB for i8 outputs), after the GELU table for Gelu
     constexpr size_t stages = BN == 256 ? (size_t)2 * (BM + BN) * 128 : (size_t)GEMM_STAGES * FRAGS * 1024;
     constexpr bool I8OUT = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
     constexpr size_t regions = (size_t)WAVES * (I8OUT ? 10240 : 18432);
     // the largest request: the stages, or the 64 KiB GELU table and the staging regions after it
-    constexpr size_t after_table = (EPI == (int)Epi::Gelu ? 65536 : 0) + regions;
+    constexpr bool GELU_LDS = EPI == (int)Epi::Gelu && BM != 64;  // the 64 x 64 tiles read it from memory
+    constexpr size_t after_table = (GELU_LDS ? 65536 : 0) + regions;
     constexpr size_t lds_max = stages > after_table ? stages : after_table;
     static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
     static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
@@ -752,13 +758,17 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
         ready = true;
     }
     size_t lds = stages > regions ? stages : regions;
-    if (EPI == (int)Epi::Gelu && VEC) {
+    if (GELU_LDS && VEC) {
         const size_t t = ((size_t)2 * g.gelu_off + 1023) & ~(size_t)1023;
         lds = stages > t + regions ? stages : t + regions;
     }
     hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC, BM>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
     return hipGetLastError();
 }
+
+// Decode-shaped products (at most two 256-row tiles of rows, K at most 4,096) take 64 x 64 tiles
+// over the whole of K (more workgroups than 128 x 192 tiles, no partials); longer K splits.
+static bool gemm_decode_tiles(int m, int k_pad) { return m <= 2 * GEMM_BM && k_pad <= 4096; }
 
 // 256 x 128 tiles (two workgroups per CU, so one's epilogue overlaps the other's main loop),
 // or 256 x 256 (below). Outputs whose rows are not 16-byte aligned take the per-output store
@@ -777,6 +787,14 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
         constexpr bool PANEL_OUT = EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
         const bool vec = ((uintptr_t)g.out & 15) == 0 && (PANEL_OUT || ((size_t)g.ldo * ES) % 16 == 0);
         if (!vec) return launch_gemm_t<EPI, NARROW, 128, false>(g, stream);
+        // Decode passes (at most two 256-row tiles of rows) with K up to 4,096: 64 x 64 tiles,
+        // two waves each (a 256-row pass of GPT-2 medium's c_attn: 192 workgroups instead of 24
+        // of 128 x 192 or 288 split-K slices and their summing pass; measured 16.0 -> 7.0 us,
+        // mlp.c_proj (K 4,096) 19.4 -> 16.1 us, the M 256 c_attn of GPT-2 small 10.2 -> 6.1 us).
+        if constexpr (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu ||
+                      EPI == (int)Epi::GeluWide || EPI == (int)Epi::Raw) {
+            if (gemm_decode_tiles(g.m, g.k_pad)) return launch_gemm_t<EPI, NARROW, 64, true, 64>(g, stream);
+        }
         // 256 x 256 tiles (one workgroup per CU, full-line 128-k stages) for long K, where their
         // faster main loop outweighs the lost overlap of a second workgroup per CU and the
         // coarser rounds (measured: GPT-2 small mlp.c_proj, K 3,072, 12% faster; c_attn and the
@@ -819,6 +837,7 @@ static hipError_t launch_gemm_e(const GemmArgs &g, hipStream_t stream) {
 
 constexpr int SPLIT_BN = 64;
 
+
 size_t gemm_split_elems(int m, int n, int splits) {
     return (size_t)splits * (size_t)m * (size_t)((n + 3) & ~3);
 }
@@ -829,6 +848,7 @@ int gemm_split_plan(Epi epi, int m, int n, int k_pad, int wanted) {
     if (!ok || m <= 0 || n <= 0 || k_pad < 2 * GEMM_BK) return 1;
     const int nks = k_pad / GEMM_BK;
     if (wanted >= 1) return wanted > nks ? nks : wanted;
+    if (gemm_decode_tiles(m, k_pad)) return 1;  // the 64 x 64 tiles take the whole of K
     const int gm = (m + GEMM_BM - 1) / GEMM_BM, tiles128 = gm * ((n + 127) / 128);
     // enough workgroups without a split, or K too short for the partials to pay (measured: the
     // c_attn product at M 256, K 768 takes 12.3 us whole and 13.5 us in three slices; at K 1,024
@@ -3733,6 +3753,9 @@ int kernel_resources(KernelResource *out, int cap) {
         {"k_gemm<Raw, split-K partials, 256x64>", (const void *)k_gemm<0, false, 64, true>},
         {"k_gemm<Act, narrow, 128x192>", (const void *)k_gemm<1, true, 192, true, 128>},
         {"k_gemm<Residual, narrow, 128x192>", (const void *)k_gemm<2, true, 192, true, 128>},
+        {"k_gemm<Act, narrow, 64x64 decode>", (const void *)k_gemm<1, true, 64, true, 64>},
+        {"k_gemm<Residual, narrow, 64x64 decode>", (const void *)k_gemm<2, true, 64, true, 64>},
+        {"k_gemm<Gelu, narrow, 64x64 decode>", (const void *)k_gemm<3, true, 64, true, 64>},
         {"k_split_epi<Act>", (const void *)k_split_epi<1>},
         {"k_split_epi<Residual>", (const void *)k_split_epi<2>},
         {"k_embed", (const void *)k_embed},

@@ -122,10 +122,12 @@ def test_gemm_requant_c1_shape(dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 100, 64), (130, 700, 128), (700, 2304, 768), (16384, 768, 768),
-                                   (257, 1000, 192)])
+                                   (257, 1000, 192), (512, 3072, 1024), (511, 1000, 4096),
+                                   (300, 1030, 4100)])
 def test_gemm_requant_tile_shapes(dev, m, n, k):
     # Shapes whose rounds favour the 128 x 192 tiles (partial tiles in M and N included) and the
-    # 256 x 128 ones, against the exact rule.
+    # 256 x 128 ones, the 64 x 64 tiles of passes of at most 512 rows (K up to 4,096, partial
+    # tiles in M and N), and a K just past them (split into slices), against the exact rule.
     from taco_amd import hip
     r = np.random.default_rng(m * 7 + n)
     a = r.integers(-127, 128, (m, k)).astype(np.int8)
