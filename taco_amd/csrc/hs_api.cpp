@@ -908,6 +908,12 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         r += c;
     }
     const bool mfma_attn = m.hd == 64 && n >= 16 * n_groups;
+    // the largest key counts first: the persistent prefill kernel pairs long and short groups
+    // in its rounds (every group writes only its own rows, so the order changes no output)
+    if (mfma_attn)
+        std::stable_sort(b.h_groups, b.h_groups + n_groups, [](const hs::AttnGroup &x, const hs::AttnGroup &y) {
+            return x.pos0 + x.count > y.pos0 + y.count;
+        });
     if (mfma_attn)
         HIP_TRY(hipMemcpyAsync(b.d_groups, b.h_groups, n_groups * sizeof(hs::AttnGroup), hipMemcpyHostToDevice, st));
     if (n_out) HIP_TRY(hipMemcpyAsync(b.d_src, src, n_out * sizeof(int32_t), hipMemcpyHostToDevice, st));

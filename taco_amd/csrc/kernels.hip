@@ -2627,6 +2627,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 //    from an integer floor(y) is exact, else the element takes the i128 rule.
 //  - the Q fragment is read straight from global memory (each lane's 16 bytes of its row).
 // =============================================================================================
+// x, hidden from the optimizer (a value it cannot prove invariant in a loop)
+__device__ __forceinline__ int opaque_vgpr(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // v_med3_i32(x, 0, hi) for a wave-uniform hi (the compiler forms med3 only for constant bounds)
 __device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
     int32_t r;
@@ -2635,44 +2641,66 @@ __device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
 }
 
 // NB: key blocks of 64 (4: three workgroups per CU with a 32 KiB table; 8: two).
+// Persistent: the grid holds the resident workgroups (at most n_tasks), and workgroup i takes
+// the tasks (group, head), task = group n_head + head, of rounds r = 0, 1, .. in snake order:
+// task r P + i for even r and r P + P - 1 - i for odd r (P workgroups). The host orders the
+// groups by key count, largest first, so the rounds pair long tasks with short ones. The table
+// is copied once per workgroup; the next task's group loads under the current task's softmax,
+// its K rows and Q fragment as soon as every wave has read the current V rows.
 template <int NB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3 : 2))) void k_attend_short(AttnArgs a, const AttnGroup *groups) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3 : 2))) void k_attend_short(AttnArgs a, const AttnGroup *groups, int n_tasks) {
     // the K rows, then the V rows (as loaded)
     __shared__ __attribute__((aligned(1024))) int8_t sKV[NB * 64 * 64];
     extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];  // attn_exp
-    const AttnGroup G = groups[blockIdx.x];
-    const int h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ql = lane & 15, qg = lane >> 4;
-    const int nk = G.pos0 + G.count < a.ctx_cap ? G.pos0 + G.count : a.ctx_cap;
-    const int nkb = (nk + 63) / 64;  // 1 .. NB (checked by the launcher)
-    const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
     const int last = a.exp_len - 1;
+    const int P = gridDim.x, wg = blockIdx.x;
+    auto task_at = [&](int r) { return r * P + ((r & 1) ? P - 1 - wg : wg); };
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
+    auto key_blocks = [&](const AttnGroup &g) {
+        const int nk = g.pos0 + g.count < a.ctx_cap ? g.pos0 + g.count : a.ctx_cap;
+        return (nk + 63) / 64;  // 1 .. NB (checked by the launcher)
+    };
     // the K (then V) rows of the group's blocks straight into LDS (dense rows, 16-byte chunk c of
     // row r at slot 4 r + (c ^ sw(r % 16))); rows past the cache read its last row (their keys
     // are masked)
-    auto rows_to_lds = [&](const int8_t *cache) {
-        const int r = 16 * w + (lane >> 2), c = (lane & 3) ^ sw(r & 15);
+    auto rows_to_lds = [&](const int8_t *cache, size_t base_, int nkb_) {
+        const int ln = opaque_vgpr(lane);
+        const int r = 16 * w + (ln >> 2), c = (ln & 3) ^ sw(r & 15);
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            if (b >= nkb) break;
+            if (b >= nkb_) break;
             int key = b * 64 + r;
             key = key < a.ctx_cap ? key : a.ctx_cap - 1;
-            const size_t off = base + (size_t)key * 64 + 16 * c;
+            const size_t off = base_ + (size_t)key * 64 + 16 * c;
             __builtin_amdgcn_global_load_lds((const void *)(cache + off), (lds_void *)(sKV + (b * 64 + 16 * w) * 64), 16, 0, 0);
         }
     };
-    {
-        rows_to_lds(a.kc);
-        for (int ch = w; ch < (a.exp_len + 255) / 256; ch += 4)  // whole 1 KiB chunks
-            __builtin_amdgcn_global_load_lds((const void *)(a.exp_table + ch * 256 + 4 * lane),
-                                             (lds_void *)(s_exp + ch * 256), 16, 0, 0);
-    }
-    const int myrow = 16 * w + ql, mypos = G.pos0 + myrow;  // this lane's row and its position
-    v4i qf = {0, 0, 0, 0};
-    if (myrow < G.count) qf = *(const v4i *)(a.q + (size_t)(G.first + myrow) * a.ldq + h * 64 + 16 * qg);
+    auto q_frag = [&](const AttnGroup &g, int hh) -> v4i {  // this lane's row is 16 w + ql
+        const int ln = opaque_vgpr(lane), row = 16 * w + (ln & 15);
+        if (row < g.count) return *(const v4i *)(a.q + (size_t)(g.first + row) * a.ldq + hh * 64 + 16 * (ln >> 4));
+        return v4i{0, 0, 0, 0};
+    };
+    int t = task_at(0);  // below n_tasks: the launcher takes P <= n_tasks
+    AttnGroup G = groups[t / a.n_head];
+    int h = t % a.n_head;
+    rows_to_lds(a.kc, ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64, key_blocks(G));
+    for (int ch = w; ch < (a.exp_len + 255) / 256; ch += 4)  // whole 1 KiB chunks
+        __builtin_amdgcn_global_load_lds((const void *)(a.exp_table + ch * 256 + 4 * lane),
+                                         (lds_void *)(s_exp + ch * 256), 16, 0, 0);
+    v4i qf = q_frag(G, h);
+    for (int round = 0;; round++) {
+    // the lane's indexes, recomputed each round from an opaque copy of the lane: the compiler
+    // then derives the LDS addresses at their use instead of keeping them in registers across
+    // the loop
+    const int lane_r = opaque_vgpr(lane);
+    const int ql = lane_r & 15, qg = lane_r >> 4;
+    const int myrow = 16 * w + ql;
+    const int nk = G.pos0 + G.count < a.ctx_cap ? G.pos0 + G.count : a.ctx_cap;
+    const int nkb = key_blocks(G);
+    const size_t base = ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64;
+    const int mypos = G.pos0 + myrow;  // this lane's position
     wait_vmcnt<0>();  // this wave's direct loads landed (the barrier shows them to all)
     __syncthreads();
     // S[b][t][e]: the dot (then the table entry) of this lane's row with key 64 b + 16 t + 4 qg + e
@@ -2690,7 +2718,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
             }
         }
     __syncthreads();  // every K row is read: the V rows load in their place during passes 1 and 2
-    rows_to_lds(a.vc);
+    rows_to_lds(a.vc, base, nkb);
+    // the next task's group, loading under passes 1 .. 3
+    const int tn = task_at(round + 1);
+    const bool more = tn < n_tasks;  // uniform
+    AttnGroup Gn = G;
+    if (more) Gn = groups[tn / a.n_head];
     // key 64 b + 16 t + 4 qg + e is visible to this lane's row iff 16 t + e <= lim - 64 b - 4 qg;
     // block b is visible to every row of the wave iff 64 b + 63 <= wlim (uniform)
     const int lim = mypos < nk - 1 ? mypos : nk - 1;
@@ -2871,6 +2904,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
 #pragma unroll
         for (int c = 0; c < 4; c++) *(uint32_t *)(o + 16 * c + 4 * qg) = packed[c];
     }
+    if (!more) break;
+    __syncthreads();  // every wave read the V rows: sKV takes the next task's K rows
+    G = Gn;
+    h = tn % a.n_head;
+    rows_to_lds(a.kc, ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64, key_blocks(G));
+    qf = q_frag(G, h);
+    }
 }
 
 template <bool NOCLAMP, bool LDS_TABLE, bool MULTI>
@@ -2913,8 +2953,27 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
             if (e != hipSuccess) return e;
             allowed[four] = lds;
         }
-        if (four) hipLaunchKernelGGL(k_attend_short<4>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
-        else hipLaunchKernelGGL(k_attend_short<8>, dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+        // the resident workgroups: CUs x workgroups per CU at this LDS size (cached per form and
+        // LDS size on the current device), at most one per task
+        static int cached_dev[2] = {-1, -1}, cached_p[2] = {0, 0};
+        static size_t cached_lds[2] = {0, 0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (cached_dev[four] != dev || cached_lds[four] != lds) {
+            int cus = 0, per_cu = 0;
+            e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+            if (e != hipSuccess) return e;
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds);
+            if (e != hipSuccess) return e;
+            cached_p[four] = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+            cached_dev[four] = dev;
+            cached_lds[four] = lds;
+        }
+        const int n_tasks = n_groups * a.n_head;
+        const int P = cached_p[four] < n_tasks ? cached_p[four] : n_tasks;
+        if (four) hipLaunchKernelGGL(k_attend_short<4>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
+        else hipLaunchKernelGGL(k_attend_short<8>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
         return hipGetLastError();
     }
     if (noclamp && lds_table) return launch_attend_groups_m<true, true>(a, groups, n_groups, max_keys, stream);
