@@ -175,18 +175,19 @@ HS_HD int64_t shift_round_hi(int64_t t, int64_t g, uint32_t s) {
 // The LayerNorm element rule in single precision for 8-bit outputs with |beta| <= 256:
 // clamp(floor(X + 1/2) + beta, +-127) for X = c inv m gamma 2^-s, from y = c k + b with
 // k = float(inv m 2^-s) gamma (two roundings) and b = 1/2 + beta (exact), one fused
-// multiply-add. |y - (X + b)| <= 3.0001 2^-24 |X| + 2^-24 |y|. y is clamped to +-200.25: inside,
-// |X| < 458 and the error is below 1575 2^-24 < 2^-13, so floor(y) is exact when y lies at
-// least 2^-13 from an integer; outside, y has the sign and size of X + b, the output clamp
-// decides, and +-200.25 lie 1/4 from an integer. |k| <= 2^110 keeps y finite or an infinity of
-// the sign of c k (never NaN). Returns false (declines) near an integer; *out is then unused.
+// multiply-add. |y - (X + b)| <= 3.0001 2^-24 |X| + 2^-24 |y|. y is clamped to [-126.5, 127.5]:
+// inside, |X| < 458 and the error is below 1575 2^-24 < 2^-13, so floor(y) is exact when y lies
+// at least 2^-13 from an integer, and it lies in [-127, 127] (no output clamp); outside, y has
+// the sign and size of X + b (relative error below 2^-21), so floor(X + b) is at least 127 or at
+// most -127 and the output clamp gives the floor of the clamped y, whose fraction is 1/2.
+// |k| <= 2^110 keeps y finite or an infinity of the sign of c k (never NaN). Returns false
+// (declines) near an integer; *out is then unused.
 HS_HD bool ln_elem_f32(int32_t c, float k, float b, int32_t *out) {
     const float y = fmaf((float)c, k, b);
-    const float yc = fminf(fmaxf(y, -200.25f), 200.25f);
+    const float yc = fminf(fmaxf(y, -126.5f), 127.5f);
     const float fl = floorf(yc);
     const float f = yc - fl;
-    const int32_t r = (int32_t)fl;
-    *out = r < -127 ? -127 : (r > 127 ? 127 : r);
+    *out = (int32_t)fl;
     return fabsf(f - 0.5f) <= 0.5f - 0x1p-13f;
 }
 
@@ -209,12 +210,56 @@ HS_HD bool ln_elem_f64(int32_t c, double kr, double gamma, int32_t *f) {
     return true;
 }
 
+// floor(a / d) for d >= 1 and |a| < 2^52, from inv_d = 1.0 / d (rounded to double). For d >= 2
+// the product a inv_d lies within |a / d| 2^-51 < 1/2 of a / d (d = 1 is exact), so its floor is
+// within one of the quotient; the exact remainder a - q d then corrects it (|q d| <= |a| + d).
+HS_HD int64_t floor_div_est(int64_t a, int64_t d, double inv_d) {
+    int64_t q = (int64_t)__builtin_floor((double)a * inv_d);
+    const int64_t r = a - q * d;
+    if (r < 0) q--;
+    else if (r >= d) q++;
+    return q;
+}
+
+// floor(x / n) for n >= 1 when the quotient is below 2^62, from inv_n = 1.0 / n. The double
+// estimate of x / n carries a relative error below 2^-50 (x to double, the product), so it is
+// within 2^12 of the quotient; the remainder x - q1 n then has |x - q1 n| < 2^13 n < 2^45 and is
+// exact in 64-bit two's complement arithmetic, and floor_div_est finishes the quotient.
+HS_HD uint64_t div_u128_est(u128 x, uint32_t n, double inv_n) {
+    const double dx = (double)(uint64_t)(x >> 64) * 18446744073709551616.0 + (double)(uint64_t)x;
+    const uint64_t q1 = (uint64_t)(dx * inv_n);
+    const int64_t r = (int64_t)((uint64_t)x - q1 * (uint64_t)n);
+    return (uint64_t)((int64_t)q1 + floor_div_est(r, n, inv_n));
+}
+
+// floor(2^k / r) for k <= 62 and 1 <= r < 2^53: the correctly rounded double quotient is within
+// 2^k 2^-53 of 2^k / r, so for k <= 52 its truncation is within one of the quotient, and the
+// exact remainder corrects it; larger k take the integer division.
+HS_HD uint64_t pow2_div_est(uint32_t k, uint64_t r) {
+    const int64_t num = (int64_t)1 << k;
+    if (k > 52) return (uint64_t)num / r;
+    int64_t q = (int64_t)((double)num / (double)r);
+    const int64_t rem = num - q * (int64_t)r;
+    if (rem < 0) q--;
+    else if (rem >= (int64_t)r) q++;
+    return (uint64_t)q;
+}
+
 // The LayerNorm scale of a row (layernorm.rs:188-256): inv = floor(2^k / isqrt(var 2^(2j) + eps))
 // with var = floor(sq / n). k <= 48 and the root is below 2^64, so the division is in u64.
 HS_HD uint64_t ln_inv(u128 sq, uint32_t n, uint32_t k, uint32_t j, uint64_t eps) {
     const u128 var = div_u128_u32(sq, n);
     const uint64_t r = isqrt_est((var << (2 * j)) + (u128)eps);
     return ((uint64_t)1 << k) / (r > 0 ? r : 1);
+}
+
+// ln_inv for rows of the residual stream: sq < n 2^62 (every |x - mean| < 2^31), so var < 2^62,
+// var 2^(2j) + eps < 2^100 for j <= 18, and the root is below 2^50; the divisions take the
+// estimate-and-correct forms above (inv_n = 1.0 / n). Equal to ln_inv on that domain.
+HS_HD uint64_t ln_inv_est(u128 sq, uint32_t n, uint32_t k, uint32_t j, uint64_t eps, double inv_n) {
+    const uint64_t var = div_u128_est(sq, n, inv_n);
+    const uint64_t r = isqrt_est(((u128)var << (2 * j)) + (u128)eps);
+    return pow2_div_est(k, r > 0 ? r : 1);
 }
 
 }  // namespace hs

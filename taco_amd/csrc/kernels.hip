@@ -1189,7 +1189,8 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     int64_t sum = 0;
     for (int j = lane; j < d; j += 64) sum += x[j];
     sum = wave_sum64(sum);
-    const int64_t mean = floor_div64(sum, d);
+    const double inv_d = 1.0 / (double)d;  // |sum| <= d RES < 2^52, sq < d 2^62: the estimate forms
+    const int64_t mean = floor_div_est(sum, d, inv_d);
     uint64_t lo = 0, hi = 0, cmax = 0;
     for (int j = lane; j < d; j += 64) {
         const int64_t c = (int64_t)x[j] - mean;
@@ -1201,7 +1202,7 @@ __global__ __launch_bounds__(256) void k_layernorm(LnArgs a, int n_rows) {
     }
     const u128 sq = wave_sum128(((u128)hi << 64) | lo);
     cmax = (uint64_t)wave_max64((int64_t)cmax);
-    const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
+    const uint64_t inv = ln_inv_est(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps, inv_d);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
     const bool wide = a.bits == 16;
     // the operand rows of this row (two planes when wide), in panels (panel_off)
@@ -1281,9 +1282,10 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
     const u128 Q = wave_sum128(((u128)hi << 64) | lo);
     mx = (int32_t)wave_max64(mx);
     mn = (int32_t)-wave_max64(-(int64_t)mn);
-    const int64_t mean = floor_div64(sum, d);
+    const double inv_d = 1.0 / (double)d;  // |sum| <= d RES < 2^52, sq < d 2^62: the estimate forms
+    const int64_t mean = floor_div_est(sum, d, inv_d);
     const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
-    const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
+    const uint64_t inv = ln_inv_est(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps, inv_d);
     const int64_t c1 = (int64_t)mx - mean, c2 = mean - (int64_t)mn;
     const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);
@@ -1418,9 +1420,10 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
     if (!live) return;
     const bool wide = a.bits == 16;
     const u128 Q = ((u128)hi << 64) | lo;
-    const int64_t mean = floor_div64(sum, d);
+    const double inv_d = 1.0 / (double)d;  // |sum| <= d RES < 2^52, sq < d 2^62: the estimate forms
+    const int64_t mean = floor_div_est(sum, d, inv_d);
     const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
-    const uint64_t inv = ln_inv(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps);
+    const uint64_t inv = ln_inv_est(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps, inv_d);
     const int64_t c1 = (int64_t)mx - mean, c2 = mean - (int64_t)mn;
     const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
     const bool small = (u128)cmax * inv < ((u128)1 << 63);

@@ -155,6 +155,47 @@ int main(int argc, char **argv) {
         CHECK(hs::ln_inv(sq, nn, k, j, eps) == want, "ln_inv");
         count++;
     }
+    // the estimate-and-correct divisions of the LayerNorm row scale against exact division
+    auto floor_ref = [](int64_t a, int64_t d) { return a >= 0 ? a / d : -((-a + d - 1) / d); };
+    for (long i = 0; i < n; i++) {
+        int64_t a = (int64_t)(next() >> (12 + next() % 52));  // |a| < 2^52
+        if (next() & 1) a = -a;
+        const int64_t d = (next() & 3) == 0 ? 1 + (int64_t)(next() % 8) : 1 + (int64_t)(next() % (1u << 22));
+        const int64_t near = (next() & 1) ? (a / d) * d + (int64_t)(next() % 3) - 1 : a;  // next to multiples
+        for (int64_t v : {a, near}) {
+            if (v >= ((int64_t)1 << 52) || v <= -((int64_t)1 << 52)) continue;
+            CHECK(hs::floor_div_est(v, d, 1.0 / (double)d) == floor_ref(v, d), "floor_div_est %lld %lld",
+                  (long long)v, (long long)d);
+            count++;
+        }
+    }
+    for (long i = 0; i < n; i++) {  // x < n 2^62, the quotient below 2^62
+        const uint32_t nn = (next() & 3) == 0 ? 1 + (uint32_t)(next() % 4) : 1 + (uint32_t)(next() % 4096);
+        const u128 lim = (u128)nn << 62;
+        u128 x = (((u128)next() << 64) | next()) % lim;
+        if ((next() & 7) == 0) x = lim - 1 - (u128)(next() % 4);
+        if ((next() & 7) == 1) x = (x / nn) * nn + (next() % 2);  // exact multiples and one past
+        if (x >= lim) x = lim - 1;
+        CHECK((u128)hs::div_u128_est(x, nn, 1.0 / (double)nn) == x / nn, "div_u128_est");
+        count++;
+    }
+    for (long i = 0; i < n; i++) {
+        const uint32_t k = (uint32_t)(next() % 63);
+        uint64_t r = 1 + (next() >> (11 + next() % 53));  // 1 .. 2^53
+        if ((next() & 7) == 0) r = (uint64_t)1 << (next() % 53);
+        if (r >= ((uint64_t)1 << 53)) r = ((uint64_t)1 << 53) - 1;
+        CHECK(hs::pow2_div_est(k, r) == ((uint64_t)1 << k) / r, "pow2_div_est %u %llu", k, (unsigned long long)r);
+        count++;
+    }
+    for (long i = 0; i < n / 4; i++) {  // ln_inv_est equals ln_inv on rows of the residual stream
+        const uint32_t nn = 1 + (uint32_t)(next() % 4096), k = (uint32_t)(next() % 49), j = (uint32_t)(next() % 17);
+        const u128 lim = (u128)nn << 62;
+        u128 sq = ((((u128)next() << 64) | next()) >> (next() % 128)) % lim;
+        if ((next() & 7) == 0) sq = lim - 1;
+        const uint64_t eps = (next() & 3) == 0 ? 0 : 1 + (next() >> (2 + next() % 62));
+        CHECK(hs::ln_inv_est(sq, nn, k, j, eps, 1.0 / (double)nn) == hs::ln_inv(sq, nn, k, j, eps), "ln_inv_est");
+        count++;
+    }
     // ln_elem_f64 against floor((c inv gamma m + 2^(s-1)) / 2^s) in i128 (|product| < 2^126):
     // every value it returns is exact; it may only decline.
     auto exact_ln = [](int32_t c, uint64_t inv, int32_t g, int32_t m, uint32_t s) -> i128 {
