@@ -175,6 +175,8 @@ struct DevBlock {
     int8_t *gelu = nullptr;
     int16_t *gelu16 = nullptr;  // an i16 table (version 2): c_fc writes planes, mlp_proj reads them
     int gelu_off = 0;
+    // the span of the i8 table past whose ends the entries repeat (GemmArgs::gelu_lo ..)
+    int gelu_lo = 0, gelu_clo = 0, gelu_chi = 0, gelu_shift = 0, gelu_copy = 0;
 };
 
 }  // namespace
@@ -407,6 +409,21 @@ hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **
             return st;
         }
         b.gelu_off = (int)hb.gelu_len / 2;
+        if (!hb.gelu_wide && hb.gelu8.size() >= 16 && hb.gelu8.size() % 16 == 0) {
+            // the span [lo, hi] outside which every entry equals the end entry it lies beyond: the
+            // epilogue clamps its index to it and copies only entries lo16 .. (16-byte aligned)
+            const std::vector<int8_t> &t = hb.gelu8;
+            const int len = (int)t.size();
+            int lo = 0, hi = len - 1;
+            while (lo + 1 < len && t[lo + 1] == t[0]) lo++;
+            while (hi - 1 > lo && t[hi - 1] == t[len - 1]) hi--;
+            const int lo16 = lo & ~15, end16 = std::min(len, (hi + 16) & ~15);
+            b.gelu_lo = lo16;
+            b.gelu_clo = lo - b.gelu_off;
+            b.gelu_chi = hi - b.gelu_off;
+            b.gelu_shift = b.gelu_off - lo16;
+            b.gelu_copy = end16 - lo16;
+        }
     }
     if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
     // padded to a multiple of 256 entries: the prefill attention loads it in 1 KiB chunks
@@ -943,7 +960,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     // rows per plane)
     auto gemm = [&](const char *label, Epi epi, const DevLinear &lin, const int8_t *a, int a_rows, int rows_n,
                     void *o, int ldo, const int8_t *gelu = nullptr, int gelu_off = 0,
-                    const int16_t *gelu16 = nullptr, int group = 0) {
+                    const int16_t *gelu16 = nullptr, int group = 0, const DevBlock *gspan = nullptr) {
         hs::GemmArgs g;
         g.group = group;
         g.a = a; g.a_rows = a_rows; g.w = lin.w; g.w_rows = lin.n_pad; g.m = rows_n; g.n = lin.n; g.k_pad = lin.k_pad;
@@ -952,6 +969,10 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         g.out_rows = (epi == Epi::GeluWide ? 2 : 1) * RP;
         g.fast32 = epi == Epi::ResidualWide ? 0 : lin.fast32;
         g.gelu = gelu; g.gelu16 = gelu16; g.gelu_off = gelu_off; g.wsum = lin.wsum;
+        if (gspan && gspan->gelu_copy > 0) {
+            g.gelu_lo = gspan->gelu_lo; g.gelu_clo = gspan->gelu_clo; g.gelu_chi = gspan->gelu_chi;
+            g.gelu_shift = gspan->gelu_shift; g.gelu_copy = gspan->gelu_copy;
+        }
         g.partials = b.gsplit; g.partials_cap = b.gsplit_elems;
         const uint64_t ops = 2ull * (uint64_t)rows_n * (uint64_t)lin.n * (uint64_t)lin.k;
         return b.launch(label, ops, [&] { return hs::launch_gemm(epi, g, st); });
@@ -1046,7 +1067,8 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
                          blk.gelu16));
             HIP_TRY(gemm("gemm_mlp", Epi::ResidualWide, blk.mlp_proj, b.d_g, 2 * RP, 2 * n, b.d_x, m.d));
         } else {
-            HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, RP, n, b.d_g, 0, blk.gelu, blk.gelu_off));
+            HIP_TRY(gemm("gemm_fc", Epi::Gelu, blk.c_fc, b.d_a, RP, n, b.d_g, 0, blk.gelu, blk.gelu_off, nullptr, 0,
+                         &blk));
             HIP_TRY(gemm("gemm_mlp", Epi::Residual, blk.mlp_proj, b.d_g, RP, n, b.d_x, m.d));
         }
     }

@@ -48,6 +48,13 @@ struct GemmArgs {
     const int8_t *gelu = nullptr;     // Gelu table, i8 entries
     const int16_t *gelu16 = nullptr;  // GeluWide table, i16 entries
     int gelu_off = 0;                 // half the table length (128 or 32768)
+    // Gelu: the span of the i8 table the epilogue reads. Every entry below gelu_clo + gelu_off
+    // equals that one and every entry above gelu_chi + gelu_off equals that one, so clamping the
+    // rescaled value to [gelu_clo, gelu_chi] (inside [-gelu_off, gelu_off - 1]) changes no output;
+    // entries gelu_lo .. gelu_lo + gelu_copy - 1 (gelu_lo and gelu_copy multiples of 16) hold the
+    // span, and value r reads entry gelu_lo + (clamp(r) + gelu_shift), gelu_shift = gelu_off -
+    // gelu_lo. gelu_copy 0: the whole table (the launcher fills the fields).
+    int gelu_lo = 0, gelu_clo = 0, gelu_chi = 0, gelu_shift = 0, gelu_copy = 0;
     const int32_t *wsum = nullptr;    // the wide epilogues: sum_k w[n][k] per output column
     // LogitsCompact: out is u16 [m, ldo] = min(tilemax - logit, cap16) and tmax [m, tmax_ld] is
     // the largest logit of each 64-column tile.

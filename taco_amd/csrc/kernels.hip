@@ -386,11 +386,16 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                             v = NARROW ? med3_i32((int32_t)r, -127, 127) : (int32_t)clamp64(r, -127, 127);
                         } else if (EPI == (int)Epi::Residual) {
                             v = NARROW ? (int32_t)r : (int32_t)clamp64(r, INT32_MIN, INT32_MAX);
-                        } else {  // ops.rs:146-154, gelu.rs:58-62: table[clamp(r) + off]
+                        } else if (EPI == (int)Epi::Gelu) {  // ops.rs:146-154, gelu.rs:58-62: table[clamp(r) + off]
+                            // clamped to the table's span (the same entry), as an index from gelu_lo
+                            v = (NARROW ? med3_i32((int32_t)r, g.gelu_clo, g.gelu_chi)
+                                        : (int32_t)clamp64(r, g.gelu_clo, g.gelu_chi)) +
+                                g.gelu_shift;
+                        } else {
                             v = (NARROW ? med3_i32((int32_t)r, -g.gelu_off, g.gelu_off - 1)
                                         : (int32_t)clamp64(r, -g.gelu_off, g.gelu_off - 1)) +
                                 g.gelu_off;
-                            if (EPI == (int)Epi::GeluWide) v = g.gelu16[v];  // the i16 table through the caches
+                            v = g.gelu16[v];  // the i16 table through the caches
                         }
                         acc[i][j][e] = v;
                     }
@@ -569,17 +574,18 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         }
         // Act, Gelu, GeluWide: i8 outputs (GeluWide: the two planes of each i16 output), staged
         // per wave in LDS (the wave's rows x RS8 bytes) and stored as 16-byte row pieces. Gelu copies its
-        // table (256 or 65,536 entries) into LDS first; the staging regions follow it. The 64 x 64
-        // tiles of decode passes read the table through the caches instead (a 64 KiB copy per
-        // workgroup would outweigh the 4,096 lookups of its tile).
+        // table's span (gelu_copy bytes from entry gelu_lo) into LDS first; the staging regions
+        // follow it. The 64 x 64 tiles of decode passes read the table through the caches instead
+        // (a copy per workgroup would outweigh the 4,096 lookups of its tile).
         constexpr bool GELU_LDS = BM != 64;
+        const int8_t *gspan = g.gelu + g.gelu_lo;  // entry gelu_lo: index 0 of the lookups
         int toff = 0;
         if (vec) {
             __syncthreads();  // every wave finished reading the stages
             if (EPI == (int)Epi::Gelu && GELU_LDS) {
-                const int T = 2 * g.gelu_off;
+                const int T = g.gelu_copy;
                 for (int c = threadIdx.x; c < T / 16; c += 64 * WAVES)
-                    *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(g.gelu + 16 * c);
+                    *(v4i *)(gemm_lds + 16 * c) = *(const v4i *)(gspan + 16 * c);
                 __syncthreads();
                 toff = (T + 1023) & ~1023;
             }
@@ -605,7 +611,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                         for (int e = 0; e < 4; e++) {
                             const int m = rw + 16 * i + rl, n = cw + 16 * j + 4 * cg + e;
                             if (m >= g.m || n >= g.n) continue;
-                            const int32_t a = EPI == (int)Epi::Gelu ? (int32_t)g.gelu[acc[i][j][e]] : acc[i][j][e];
+                            const int32_t a = EPI == (int)Epi::Gelu ? (int32_t)gspan[acc[i][j][e]] : acc[i][j][e];
                             const int8_t v = (int8_t)byte_of(a);
                             if (EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
                                 const RowInfo ri = g.kv_rows[m];
@@ -630,7 +636,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                     uint32_t b[4];
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)(GELU_LDS ? gemm_lds[acc[i][j][e]] : g.gelu[acc[i][j][e]])
+                        b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)(GELU_LDS ? gemm_lds[acc[i][j][e]] : gspan[acc[i][j][e]])
                                                      : byte_of(acc[i][j][e]);
                     *(uint32_t *)(wr + (16 * i + rl) * RS8 + 16 * j + 4 * cg) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
                     if (EPI == (int)Epi::Gelu && j == TJ - 1) asm volatile("" ::: "memory");  // 4 TJ lookups in flight at most
@@ -737,6 +743,13 @@ template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM>
 static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     constexpr int WAVES = gemm_waves(BN), FRAGS = BM / 16 + BN / 16;
     GemmArgs g = ga;
+    if (EPI == (int)Epi::Gelu && g.gelu_copy <= 0) {  // the whole table
+        g.gelu_lo = 0;
+        g.gelu_clo = -g.gelu_off;
+        g.gelu_chi = g.gelu_off - 1;
+        g.gelu_shift = g.gelu_off;
+        g.gelu_copy = 2 * g.gelu_off;
+    }
     const int gm = (g.m + BM - 1) / BM, gn = (g.n + BN - 1) / BN;
     // the group of the tile order counts 256-row tiles: the same band of rows in BM-row tiles
     if (BM != GEMM_BM) g.group = (GEMM_BM / BM) * g.group < gm ? (GEMM_BM / BM) * g.group : gm;
@@ -759,7 +772,7 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     }
     size_t lds = stages > regions ? stages : regions;
     if (GELU_LDS && VEC) {
-        const size_t t = ((size_t)2 * g.gelu_off + 1023) & ~(size_t)1023;
+        const size_t t = ((size_t)g.gelu_copy + 1023) & ~(size_t)1023;
         lds = stages > t + regions ? stages : t + regions;
     }
     hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC, BM>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
@@ -799,8 +812,12 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
         // faster main loop outweighs the lost overlap of a second workgroup per CU and the
         // coarser rounds (measured: GPT-2 small mlp.c_proj, K 3,072, 12% faster; c_attn and the
         // LM head, K 768, 10% and 7% slower), and for the i8 GELU epilogue of a wide product
-        // (each workgroup copies the 64 KiB table into LDS; measured 4% faster)
-        const bool wide = g.n > 512 && (g.k_pad >= 2048 || (EPI == (int)Epi::Gelu && g.n > 1024));
+        // whose table span exceeds 32 KiB (each workgroup copies it into LDS, and beside the
+        // staging regions of 256 x 128 tiles it would leave room for one workgroup per CU; the
+        // full 64 KiB table measured 4% faster in 256 x 256 tiles). A span of at most 32 KiB fits
+        // in the 256 x 128 tiles' stages: two workgroups per CU.
+        const int gcopy = g.gelu_copy > 0 ? g.gelu_copy : 2 * g.gelu_off;
+        const bool wide = g.n > 512 && (g.k_pad >= 2048 || (EPI == (int)Epi::Gelu && g.n > 1024 && gcopy > 32768));
         if constexpr (EPI == (int)Epi::Act || EPI == (int)Epi::Residual) {
             // 128 x 192 tiles for a product that is one partial round of resident workgroups
             // (at most 512 of 256 x 128, or 256 of 256 x 256) and one round of 128 x 192: the
