@@ -814,10 +814,14 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
         // LM head, K 768, 10% and 7% slower), and for the i8 GELU epilogue of a wide product
         // whose table span exceeds 32 KiB (each workgroup copies it into LDS, and beside the
         // staging regions of 256 x 128 tiles it would leave room for one workgroup per CU; the
-        // full 64 KiB table measured 4% faster in 256 x 256 tiles). A span of at most 32 KiB fits
-        // in the 256 x 128 tiles' stages: two workgroups per CU.
+        // full 64 KiB table measured 4% faster in 256 x 256 tiles) or whose K is 1,536 or more.
+        // A span of at most 32 KiB fits in the 256 x 128 tiles' stages: two workgroups per CU
+        // (measured, c_fc with a 23 KiB span: GPT-2 small, K 768, 66 -> 58 us; GPT-2 medium,
+        // K 1,024, 10.4 -> 9.3 ms per step; GPT-2 XL, K 1,600, 190 -> 214 ms per step, so it
+        // keeps 256 x 256).
         const int gcopy = g.gelu_copy > 0 ? g.gelu_copy : 2 * g.gelu_off;
-        const bool wide = g.n > 512 && (g.k_pad >= 2048 || (EPI == (int)Epi::Gelu && g.n > 1024 && gcopy > 32768));
+        const bool wide = g.n > 512 && (g.k_pad >= 2048 ||
+                                        (EPI == (int)Epi::Gelu && g.n > 1024 && (gcopy > 32768 || g.k_pad >= 1536)));
         if constexpr (EPI == (int)Epi::Act || EPI == (int)Epi::Residual) {
             // 128 x 192 tiles for a product that is one partial round of resident workgroups
             // (at most 512 of 256 x 128, or 256 of 256 x 256) and one round of 128 x 192: the
