@@ -82,13 +82,19 @@ struct Flag {
 // loop), 128 x 192 (2 x 2 waves of 64 x 96) and 64 x 64 (2 x 1 waves of 32 x 64, decode
 // passes). Each wave computes a (BM / 2) x (BN / WN) sub-tile: TI x TJ tiles of 16 x 16.
 constexpr int gemm_wn(int bn) { return bn == 192 ? 2 : bn / 64; }  // waves along N
+// The ring's stages: 3, or 6 for the 64 x 64 tiles of decode passes with K >= 1,024 (DEEP: their
+// k-steps hold little MFMA work, so more k-steps of loads stay in flight; one workgroup per CU at
+// most there). Measured, GPT-2-medium unfold passes: c_attn and c_fc (K 1,024) 7-10% and
+// mlp.c_proj (K 4,096) 18% faster; the GPT-2-small c_attn (K 768) 6.0 -> 6.4 us, so it keeps 3.
+constexpr int gemm_stages(int bm, bool deep) { return bm == 64 && deep ? 6 : GEMM_STAGES; }
 constexpr int gemm_waves(int bn) { return 2 * gemm_wn(bn); }
 
-template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM>
+template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM, bool DEEP = false>
 __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
     constexpr int WN = gemm_wn(BN), WAVES = 2 * WN, TI = BM / 32, TJ = BN / WN / 16;
-    constexpr int FRAGS = BM / 16 + BN / 16, LOADS = FRAGS / WAVES;
+    constexpr int FRAGS = BM / 16 + BN / 16, LOADS = FRAGS / WAVES, NST = gemm_stages(BM, DEEP);
     static_assert(FRAGS % WAVES == 0, "whole fragments per wave");
+    static_assert(NST <= 6 && (NST - 1) * LOADS < 64, "ring depth");
     static_assert(TI * TJ <= 32 && (BM == GEMM_BM || (BM == 128 && BN == 192) || (BM == 64 && BN == 64)),
                   "tile shapes");
     // The i16-plane epilogues pair rows 2r and 2r + 1 in one lane and keep the W-as-columns
@@ -278,23 +284,36 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
     };
 
     // The operand fragments of k-step kt + 1 are read from LDS while the MFMAs of k-step kt
-    // run on registers read the step before. Of the three stages one is being read and two
-    // are in flight.
+    // run on registers read the step before. Of the NST stages (3, or 6 for the 64 x 64 tiles)
+    // one is being read and the others are in flight.
     auto read_frags = [&](int kt, v4i *af, v4i *bf) {
-        const int8_t *st = gemm_lds + (kt % GEMM_STAGES) * (FRAGS * 1024) + rd_slot * 16;
+        const int8_t *st = gemm_lds + (kt % NST) * (FRAGS * 1024) + rd_slot * 16;
 #pragma unroll
         for (int i = 0; i < TI; i++) af[i] = *(const v4i *)(st + (wm * TI + i) * 1024);
 #pragma unroll
         for (int j = 0; j < TJ; j++) bf[j] = *(const v4i *)(st + (BM / 16 + wn * TJ + j) * 1024);
     };
+    // wait until at most n stages' loads are in flight (n <= NST - 1)
+    auto wait_stages = [&](int n) {
+        if (NST > 5 && n >= 5) wait_vmcnt<(NST > 5 ? 5 * LOADS : 0)>();
+        else if (NST > 4 && n == 4) wait_vmcnt<(NST > 4 ? 4 * LOADS : 0)>();
+        else if (NST > 3 && n == 3) wait_vmcnt<(NST > 3 ? 3 * LOADS : 0)>();
+        else if (n == 2) wait_vmcnt<2 * LOADS>();
+        else if (n == 1) wait_vmcnt<LOADS>();
+        else wait_vmcnt<0>();
+    };
 #pragma unroll
-    for (int s = 0; s < GEMM_STAGES; s++)
+    for (int s = 0; s < NST; s++)
         if (s < nk) issue(s, s);
     // stage 0 landed (the later stages' loads may be outstanding); a bare s_barrier (a compiler
     // memory barrier, no fence: a fence would also wait for the stages in flight)
-    if (nk >= 3) wait_vmcnt<2 * LOADS>();
-    else if (nk == 2) wait_vmcnt<LOADS>();
-    else wait_vmcnt<0>();
+    if constexpr (NST == 3) {
+        if (nk >= 3) wait_vmcnt<2 * LOADS>();
+        else if (nk == 2) wait_vmcnt<LOADS>();
+        else wait_vmcnt<0>();
+    } else {
+        wait_stages((nk < NST ? nk : NST) - 1);
+    }
     asm volatile("s_barrier" ::: "memory");
     // One k-step: the MFMAs of step kt on (ca, cb) while step kt + 1's fragments are read into
     // (na, nb). Two register sets alternate (the loop is unrolled by two), so no fragment moves
@@ -305,10 +324,15 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
             // stage kt + 1 landed (stage kt + 2's loads may be outstanding); this wave's reads of
             // stage kt % 3 (issued the step before) completed, so after the barrier no wave
             // reads it and it takes k-step kt + 3
-            if (kt + 2 < nk) wait_vmcnt<LOADS>();
-            else wait_vmcnt<0>();
+            if constexpr (NST == 3) {
+                if (kt + 2 < nk) wait_vmcnt<LOADS>();
+                else wait_vmcnt<0>();
+            } else {  // the stages after kt + 1 that were issued: kt + 2 .. min(kt + NST - 1, nk - 1)
+                const int ahead = nk - kt - 2;
+                wait_stages(ahead < NST - 2 ? ahead : NST - 2);
+            }
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (kt + GEMM_STAGES < nk) issue(kt + GEMM_STAGES, kt % GEMM_STAGES);
+            if (kt + NST < nk) issue(kt + NST, kt % NST);
         }
         // unconditional (the last step re-reads its own stage), so the reads share the MFMAs'
         // basic block and no wait for them lands before the MFMAs; the empty asm keeps the
@@ -739,7 +763,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
     }
 }
 
-template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM>
+template <int EPI, bool NARROW, int BN, bool VEC, int BM = GEMM_BM, bool DEEP = false>
 static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     constexpr int WAVES = gemm_waves(BN), FRAGS = BM / 16 + BN / 16;
     GemmArgs g = ga;
@@ -755,7 +779,7 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     if (BM != GEMM_BM) g.group = (GEMM_BM / BM) * g.group < gm ? (GEMM_BM / BM) * g.group : gm;
     // the stages, and the epilogue's LDS: per-wave staging regions (18 KiB for the u16 logits
     // and the i16-plane epilogues, 10 KiB for i8 outputs), after the GELU table for Gelu
-    constexpr size_t stages = BN == 256 ? (size_t)2 * (BM + BN) * 128 : (size_t)GEMM_STAGES * FRAGS * 1024;
+    constexpr size_t stages = BN == 256 ? (size_t)2 * (BM + BN) * 128 : (size_t)gemm_stages(BM, DEEP) * FRAGS * 1024;
     constexpr bool I8OUT = EPI == (int)Epi::Act || EPI == (int)Epi::Gelu || EPI == (int)Epi::GeluWide;
     constexpr size_t regions = (size_t)WAVES * (I8OUT ? 10240 : 18432);
     // the largest request: the stages, or the 64 KiB GELU table and the staging regions after it
@@ -765,7 +789,7 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
     static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
     if (!ready) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC, BM>,
+        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC, BM, DEEP>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
         if (e != hipSuccess) return e;
         ready = true;
@@ -775,7 +799,7 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
         const size_t t = ((size_t)g.gelu_copy + 1023) & ~(size_t)1023;
         lds = stages > t + regions ? stages : t + regions;
     }
-    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC, BM>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
+    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC, BM, DEEP>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
     return hipGetLastError();
 }
 
@@ -806,7 +830,10 @@ static hipError_t launch_gemm_w(const GemmArgs &g, hipStream_t stream) {
         // mlp.c_proj (K 4,096) 19.4 -> 16.1 us, the M 256 c_attn of GPT-2 small 10.2 -> 6.1 us).
         if constexpr (EPI == (int)Epi::Act || EPI == (int)Epi::Residual || EPI == (int)Epi::Gelu ||
                       EPI == (int)Epi::GeluWide || EPI == (int)Epi::Raw) {
-            if (gemm_decode_tiles(g.m, g.k_pad)) return launch_gemm_t<EPI, NARROW, 64, true, 64>(g, stream);
+            if (gemm_decode_tiles(g.m, g.k_pad)) {
+                if (g.k_pad >= 1024) return launch_gemm_t<EPI, NARROW, 64, true, 64, true>(g, stream);
+                return launch_gemm_t<EPI, NARROW, 64, true, 64>(g, stream);
+            }
         }
         // 256 x 256 tiles (one workgroup per CU, full-line 128-k stages) for long K, where their
         // faster main loop outweighs the lost overlap of a second workgroup per CU and the
