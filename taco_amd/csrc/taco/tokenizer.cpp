@@ -8,7 +8,6 @@
 #include <cstring>
 #include <functional>
 #include <memory>
-#include <queue>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -126,77 +125,132 @@ size_t first_piece(const Chars &t, size_t i) {
     return count - 1;
 }
 
-// ---- BPE merges of one piece (bpe.rs:41-116) ---------------------------------------------------
-// The lowest-ranked adjacent pair is joined at every position, left to right, skipping pairs an
-// earlier join of the same step used; repeated until no pair has a merge. Each step is one
-// round over a min-heap of (rank, position): a round takes every entry of the lowest rank, in
-// position order, joins those still valid, and pushes the at most two new pairs of each join
-// for later rounds (a joined token is longer than its parts, so a new pair never has the
-// round's rank).
+// ---- BPE merges of one piece (the semantics of bpe.rs:41-116) ---------------------------------
+// The rule: the adjacent pair that comes first in the merge list is joined at each of its
+// occurrences, scanning left to right and leaving out an occurrence that overlaps one just
+// joined; this repeats until no adjacent pair is in the list.
+//
+// A piece of n symbols is a row of n slots. A live slot holds a symbol and, when it has a live
+// right neighbour, the list order of the pair it starts (NO_RULE otherwise). A min-tournament
+// over the slots' orders names the round's pair at its root. The round then asks the tournament
+// for the leftmost slot at or after a cursor whose order is at most the round's, joins there and
+// moves the cursor one slot past the join. A join changes only the orders of its own slot and of
+// its live left neighbour, both left of the cursor, and at the round's start no slot holds a
+// smaller order, so the search meets exactly the occurrences of the round's pair, in order.
+// Each join retires a slot, so a piece costs O(n log n) tournament steps.
 
-struct Merge {
-    uint32_t rank, merged;
+struct PairRule {
+    uint32_t order;   // position of the pair in the merge list
+    uint32_t result;  // the token of the joined bytes
 };
 
-using MergeMap = std::unordered_map<uint64_t, Merge>;
+using PairRules = std::unordered_map<uint64_t, PairRule>;
 
-inline uint64_t pair_key(uint32_t a, uint32_t b) { return ((uint64_t)a << 32) | b; }
+inline uint64_t pair_code(uint32_t left, uint32_t right) { return ((uint64_t)left << 32) | right; }
 
-void merge_into(const std::vector<uint32_t> &symbols, const MergeMap &merges, std::vector<uint32_t> &out) {
-    const size_t n = symbols.size();
-    if (n < 2) {
-        out.insert(out.end(), symbols.begin(), symbols.end());
-        return;
-    }
-    constexpr size_t NONE = SIZE_MAX;
-    std::vector<uint32_t> sym = symbols;
-    std::vector<size_t> next(n), prev(n);
-    std::vector<char> alive(n, 1);
-    for (size_t i = 0; i < n; i++) {
-        next[i] = i + 1 < n ? i + 1 : NONE;
-        prev[i] = i > 0 ? i - 1 : NONE;
-    }
-    auto merge_at = [&](size_t i, Merge &m) -> bool {
-        if (i == NONE || next[i] == NONE) return false;
-        const auto it = merges.find(pair_key(sym[i], sym[next[i]]));
-        if (it == merges.end()) return false;
-        m = it->second;
-        return true;
-    };
-    using Entry = std::pair<uint32_t, size_t>;  // (rank, position)
-    std::priority_queue<Entry, std::vector<Entry>, std::greater<Entry>> heap;
-    Merge m;
-    for (size_t i = 0; i + 1 < n; i++)
-        if (merge_at(i, m)) heap.push({m.rank, i});
-    std::vector<size_t> batch;
-    while (!heap.empty()) {
-        const uint32_t rank = heap.top().first;
-        batch.clear();
-        while (!heap.empty() && heap.top().first == rank) {
-            batch.push_back(heap.top().second);
-            heap.pop();
+class PieceJoiner {
+  public:
+    explicit PieceJoiner(const PairRules &rules) : rules_(rules) {}
+
+    // Appends the tokens of `piece` after every join to `out`.
+    void run(const std::vector<uint32_t> &piece, std::vector<uint32_t> &out) {
+        const size_t n = piece.size();
+        if (n < 2) {
+            out.insert(out.end(), piece.begin(), piece.end());
+            return;
         }
-        std::sort(batch.begin(), batch.end());
-        batch.erase(std::unique(batch.begin(), batch.end()), batch.end());
-        for (size_t i : batch) {
-            if (!alive[i] || !merge_at(i, m) || m.rank != rank) continue;
-            const size_t j = next[i], after = next[j];
-            sym[i] = m.merged;
-            alive[j] = 0;
-            next[i] = after;
-            if (after != NONE) prev[after] = i;
-            for (size_t k : {prev[i], i})
-                if (merge_at(k, m)) heap.push({m.rank, k});
+        tok_ = piece;
+        made_.assign(n, 0);
+        right_.resize(n);
+        left_.resize(n);
+        for (size_t i = 0; i < n; i++) {
+            right_[i] = i + 1;  // n: no right neighbour
+            left_[i] = i;       // i: no left neighbour (only slot 0)
+            if (i) left_[i] = i - 1;
+        }
+        leaves_ = 1;
+        while (leaves_ < n) leaves_ <<= 1;
+        min_.assign(2 * leaves_, NO_RULE);
+        for (size_t i = 0; i + 1 < n; i++) min_[leaves_ + i] = order_of(i);
+        for (size_t k = leaves_ - 1; k >= 1; k--) min_[k] = std::min(min_[2 * k], min_[2 * k + 1]);
+
+        while (min_[1] != NO_RULE) {
+            const uint32_t round = min_[1];
+            for (size_t at = 0;;) {
+                const size_t p = leftmost_at_most(at, round);
+                if (p == NONE) break;
+                join(p);
+                at = p + 1;
+            }
+        }
+        for (size_t i = 0; i < n; i = right_[i]) out.push_back(tok_[i]);
+    }
+
+  private:
+    static constexpr uint32_t NO_RULE = UINT32_MAX;
+    static constexpr size_t NONE = SIZE_MAX;
+
+    // The order of the pair that slot i starts (its result kept in made_[i]).
+    uint32_t order_of(size_t i) {
+        const size_t r = right_[i];
+        if (r >= tok_.size()) return NO_RULE;
+        const auto it = rules_.find(pair_code(tok_[i], tok_[r]));
+        if (it == rules_.end()) return NO_RULE;
+        made_[i] = it->second.result;
+        return it->second.order;
+    }
+
+    void set(size_t i, uint32_t v) {
+        size_t k = leaves_ + i;
+        min_[k] = v;
+        for (k >>= 1; k; k >>= 1) min_[k] = std::min(min_[2 * k], min_[2 * k + 1]);
+    }
+
+    // The leftmost slot >= lo whose order is <= bound, or NONE: test the subtrees right of lo in
+    // order (climb while the node is a right child, then step to its right sibling) and descend
+    // into the first whose minimum qualifies.
+    size_t leftmost_at_most(size_t lo, uint32_t bound) const {
+        if (lo >= leaves_) return NONE;
+        size_t k = leaves_ + lo;
+        for (;;) {
+            if (min_[k] <= bound) {
+                while (k < leaves_) {
+                    k = 2 * k;
+                    if (min_[k] > bound) k++;
+                }
+                return k - leaves_;
+            }
+            while (k & 1) k >>= 1;
+            if (k == 0) return NONE;
+            k++;
         }
     }
-    for (size_t i = 0; i != NONE; i = next[i]) out.push_back(sym[i]);
-}
+
+    // Joins slot p with its right neighbour: p takes the result, the neighbour retires, and the
+    // orders of p and of p's left neighbour are taken again.
+    void join(size_t p) {
+        const size_t n = tok_.size();
+        const size_t gone = right_[p];
+        tok_[p] = made_[p];
+        const size_t after = right_[gone];
+        right_[p] = after;
+        if (after < n) left_[after] = p;
+        set(gone, NO_RULE);
+        set(p, order_of(p));
+        if (left_[p] != p) set(left_[p], order_of(left_[p]));
+    }
+
+    const PairRules &rules_;
+    std::vector<uint32_t> tok_, made_, min_;
+    std::vector<size_t> right_, left_;
+    size_t leaves_ = 0;
+};
 
 }  // namespace
 
 struct tc_tokenizer {
     uint32_t byte_tokens[256];
-    MergeMap merges;
+    PairRules rules;
     size_t vocab_size = 0;
 };
 
@@ -227,7 +281,7 @@ hs_status make_tokenizer(size_t count, const std::function<std::pair<const uint8
                             "byte " + std::to_string(c) + " has no single-byte token, or two");
         t->byte_tokens[c] = (uint32_t)it->second;
     }
-    t->merges.reserve(n_merges);
+    t->rules.reserve(n_merges);
     for (size_t r = 0; r < n_merges; r++) {
         const uint32_t l = merges[2 * r], rr = merges[2 * r + 1];
         auto fault = [&](const char *why) {
@@ -241,7 +295,7 @@ hs_status make_tokenizer(size_t count, const std::function<std::pair<const uint8
         const auto it = owners.find(joined);
         if (it == owners.end()) return fault("no token has the joined bytes");
         if (it->second < 0) return fault("two or more tokens have the joined bytes");
-        if (!t->merges.emplace(pair_key(l, rr), Merge{(uint32_t)r, (uint32_t)it->second}).second)
+        if (!t->rules.emplace(pair_code(l, rr), PairRule{(uint32_t)r, (uint32_t)it->second}).second)
             return fault("the pair occurs two times");
     }
     *out = t.release();
@@ -252,6 +306,7 @@ hs_status make_tokenizer(size_t count, const std::function<std::pair<const uint8
 void encode(const tc_tokenizer &t, const uint8_t *data, size_t len, std::vector<uint32_t> &ids) {
     Chars run;
     std::vector<uint32_t> symbols;
+    PieceJoiner joiner(t.rules);
     size_t i = 0;
     while (i < len) {
         // the maximal well-formed run at i
@@ -270,7 +325,7 @@ void encode(const tc_tokenizer &t, const uint8_t *data, size_t len, std::vector<
             const size_t nc = first_piece(run, c);
             symbols.clear();
             for (size_t b = run.off[c]; b < run.off[c + nc]; b++) symbols.push_back(t.byte_tokens[data[i + b]]);
-            merge_into(symbols, t.merges, ids);
+            joiner.run(symbols, ids);
             c += nc;
         }
         if (j < len) {  // a byte outside well-formed UTF-8 is its single-byte token

@@ -176,6 +176,38 @@ def test_merge_rounds_equal_the_quadratic_algorithm():
             assert t.encode(bytes(word)).tolist() == want, (case, pairs, word)
 
 
+def test_long_pieces_equal_the_quadratic_algorithm():
+    """Pieces of 200-3,000 letters over two letters (runs of one letter, where the pair (a, a)
+    overlaps itself, and mixed runs), with merge lists that build up to 8-letter tokens in
+    shuffled order."""
+    rng = random.Random(0x5EED)
+    a, b = ord("a"), ord("b")
+    for case in range(12):
+        vocab = list(BYTES)
+        by_bytes = {bytes([x]): x for x in range(256)}
+        ids = [a, b]
+        pairs = []
+        while len(pairs) < 20:
+            x, y = rng.choice(ids), rng.choice(ids)
+            joined = vocab[x] + vocab[y]
+            if len(joined) > 8 or joined in by_bytes or (x, y) in [p for p, _ in pairs]:
+                continue
+            by_bytes[joined] = len(vocab)
+            vocab.append(joined)
+            ids.append(len(vocab) - 1)
+            pairs.append(((x, y), len(vocab) - 1))
+        if case % 2:
+            rng.shuffle(pairs)
+        merges = {p: (rank, m) for rank, (p, m) in enumerate(pairs)}
+        t = tok(vocab, None, [p for p, _ in pairs])
+        n = rng.randint(200, 3000)
+        if case % 3 == 0:
+            word = [a] * n
+        else:
+            word = [rng.choice((a, a, b)) for _ in range(n)]
+        assert t.encode(bytes(word)).tolist() == bpe_quadratic(word, merges), case
+
+
 # ---- the conformance blocks -------------------------------------------------------------------
 
 @pytest.mark.parametrize("name", ["predicted_text_k0", "predicted_text_k32", "all_kinds_text"])
