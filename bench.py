@@ -46,7 +46,7 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
 HBM_PEAK_GBS = 8000.0
 
 FOLDS = {  # workload -> (dims name, windows, tokens per window, CPU-baseline windows per thread)
-    "fold-gpt2-small": ("GPT2_SMALL", 64, 256, 2),
+    "fold-gpt2-small": ("GPT2_SMALL", 64, 256, 4),
     "fold-gpt2-medium": ("GPT2_MEDIUM", 256, 256, 2),
     "fold-gpt2-xl": ("GPT2_XL", 512, 512, 1),
 }
@@ -88,7 +88,8 @@ def traffic_summary(fetch_csv, write_csv, calib_mib, tokens_sha, command):
         if "rocclr" in k:
             continue
         agg[k][2] += v * w_scale * 1024
-    return {"tokens_sha256": tokens_sha, "command": command, "calibration_mib": calib_mib,
+    return {"library": library_version(), "tokens_sha256": tokens_sha, "command": command,
+            "calibration_mib": calib_mib,
             "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
             "kernels": {k: {"dispatches": n, "fetch_bytes": round(fb / n), "write_bytes": round(wb / n)}
                         for k, (n, fb, wb) in sorted(agg.items())}}
@@ -142,16 +143,31 @@ def attend_traffic_summary(fetch_csv, write_csv, calib_mib, command):
                              "fetch_bytes": round(sum(fd[i:i + n]) / n * f_scale * 1024),
                              "write_bytes": round(sum(wd[i:i + n]) / n * w_scale * 1024)}
             i += n
-    return {"command": command, "calibration_mib": calib_mib, "fetch_scale": round(f_scale, 4),
-            "write_scale": round(w_scale, 4), "contexts": out}
+    return {"library": library_version(), "command": command, "calibration_mib": calib_mib,
+            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "contexts": out}
+
+
+def library_version():
+    """hs_version() of the loaded library: the SHA-256 prefix of the kernel sources it was built
+    from. Counter summaries record it, and a summary of another build is not reported."""
+    from taco_amd import hip
+    return hip.version()
+
+
+def _same_build(summary):
+    return summary.get("library") == library_version()
 
 
 def committed_attend_traffic(ctx):
-    """HBM bytes per decode-attention launch at ctx from the committed summary, or None."""
+    """HBM bytes per decode-attention launch at ctx from the committed summary of this build, or
+    None."""
     path = os.path.join(HERE, "profiles", "attend_decode_traffic.json")
     if not os.path.exists(path):
         return None
-    c = json.load(open(path)).get("contexts", {}).get(str(ctx))
+    j = json.load(open(path))
+    if not _same_build(j):
+        return None
+    c = j.get("contexts", {}).get(str(ctx))
     return c["fetch_bytes"] + c["write_bytes"] if c else None
 
 
@@ -162,7 +178,7 @@ def committed_traffic(workload, tokens_sha):
     if not os.path.exists(path):
         return None
     t = json.load(open(path))
-    if t.get("tokens_sha256") != tokens_sha:
+    if t.get("tokens_sha256") != tokens_sha or not _same_build(t):
         return None
     g = [v for k, v in t["kernels"].items() if "k_gemm" in k]
     n = sum(v["dispatches"] for v in g)
@@ -201,7 +217,7 @@ def mfma_summary(csv_path, tokens_sha, command):
             tot_busy += a["SQ_VALU_MFMA_BUSY_CYCLES"]
             tot_gui += gui1 * 1024
             tot_ops += a["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
-    return {"tokens_sha256": tokens_sha, "command": command,
+    return {"library": library_version(), "tokens_sha256": tokens_sha, "command": command,
             "gemm_mfma_util": round(tot_busy / tot_gui, 4) if tot_gui else None,
             "gemm_int8_ops": int(tot_ops), "kernels": kernels}
 
@@ -250,7 +266,7 @@ def sq_summary(csv_paths, tokens_sha, command):
             "lds_conflict_per_active": (round(a["SQ_LDS_BANK_CONFLICT#1"] / a["SQ_LDS_IDX_ACTIVE#1"], 3)
                                         if a["SQ_LDS_IDX_ACTIVE#1"] else None),
             "gui_cycles_per_dispatch": int(a["GRBM_GUI_ACTIVE#1"] / 8 / n1)}
-    return {"tokens_sha256": tokens_sha, "command": command, "kernels": kernels}
+    return {"library": library_version(), "tokens_sha256": tokens_sha, "command": command, "kernels": kernels}
 
 
 def committed_mfma(workload, tokens_sha):
@@ -259,7 +275,7 @@ def committed_mfma(workload, tokens_sha):
     if not os.path.exists(path):
         return None
     j = json.load(open(path))
-    return j["gemm_mfma_util"] if j.get("tokens_sha256") == tokens_sha else None
+    return j["gemm_mfma_util"] if j.get("tokens_sha256") == tokens_sha and _same_build(j) else None
 
 
 def host_cpu():
@@ -337,11 +353,21 @@ def run_fold(args):
     # The timed steps run without per-launch events (an event pair around every launch costs
     # about 10 us of idle GPU between kernels); the per-op times and the roofline come from the
     # same number of profiled steps right after them.
+    # The timed steps record one event pair per forward pass (no per-launch events): the GPU
+    # span of the passes, so the host's share of a step is the wall time minus the span.
     phase.update(fold=0.0, container=0.0)
+    hip._check(hip.lib().hs_batch_set_profiling(batch.h, 2))
+    hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
     ts = time.perf_counter()
     for i in range(args.steps):
         payloads, cont = step()
     elapsed = time.perf_counter() - ts
+    span = read_profile(hip, batch).get("pass_span", {"ns": 0, "launches": 0})
+    hip._check(hip.lib().hs_batch_set_profiling(batch.h, 0))
+    span_ms = span["ns"] / 1e6 / max(1, args.steps)
+    host_ms = 1e3 * elapsed / max(1, args.steps) - span_ms
+    log(f"timed steps: GPU span of the passes {span_ms:.3f} ms per step ({span['launches']} passes), "
+        f"host share {host_ms:.3f} ms per step")
     timed_phase = dict(phase)
     # Sustained: fold steps for at least args.sustain_s seconds right after the timed ones (the
     # timed region is short enough to end before the clocks settle under a sustained MFMA load).
@@ -496,6 +522,8 @@ def run_fold(args):
         "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / psteps, 3) for kk, v in prof.items()},
         "profiled_steps": {"steps": psteps, "ms_per_step": round(1e3 * profiled_s / psteps, 3),
                            "kernel_ms_per_step": round(gpu_ms, 3)},
+        "gpu_span_ms_per_step": round(span_ms, 3),
+        "host_ms_per_step": round(host_ms, 3),
         "sustained": sustained,
         "cpu_baseline": cpu,
     }

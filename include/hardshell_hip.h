@@ -325,9 +325,12 @@ hs_status hs_probe_issue(hs_device *dev, uint32_t op, uint32_t waves_per_simd, u
                          uint64_t *ns);
 
 /* ---- Batch profiling: CudaBatch::profile (crates/hardshell-cuda/src/batch.rs:493-498) ----- */
-/* With profiling on, every kernel launch of the batch is bracketed by hipEvents on the batch's
- * stream; hs_batch_profile gives, for each op label, the summed GPU nanoseconds, the launch
- * count and the algorithmic int8 operations (2 per multiply-accumulate of the GEMMs). */
+/* With profiling on (on = 1), every kernel launch of the batch is bracketed by hipEvents on the
+ * batch's stream; hs_batch_profile gives, for each op label, the summed GPU nanoseconds, the
+ * launch count and the algorithmic int8 operations (2 per multiply-accumulate of the GEMMs).
+ * With on = 2 only each forward pass is bracketed (one pair from before its first input copy to
+ * after its last launch, label "pass_span"), so the timed calls keep their launch rhythm and the
+ * span gives their GPU time with the gaps between kernels. */
 hs_status hs_batch_set_profiling(hs_batch *batch, int on);
 /* Writes up to cap entries (labels are NUL-terminated in 32-byte slots); returns the number of
  * labels. Clears the counters when `clear` is nonzero. The event times of the calls since the

@@ -602,7 +602,7 @@ struct hs_batch {
         hipEvent_t e0, e1;
         uint64_t ops;
     };
-    bool profiling = false;
+    int profiling = 0;  // 1: an event pair around every launch; 2: one pair around each pass
     std::vector<ProfEntry> prof;
     std::vector<Pending> pending;
     std::vector<hipEvent_t> event_pool;
@@ -611,6 +611,7 @@ struct hs_batch {
             event_pool.push_back(p.e0);
             event_pool.push_back(p.e1);
         }
+        if (span0) event_pool.push_back(span0);
         for (auto e : event_pool) (void)hipEventDestroy(e);
         if (st) (void)hipStreamSynchronize(st);
         for (void *p : {(void *)h_rows, (void *)h_groups, (void *)h_src, (void *)h_queries, (void *)h_intervals,
@@ -637,7 +638,7 @@ struct hs_batch {
     // Runs `fn` (a launch on the batch stream), bracketed by events when profiling.
     template <typename F>
     hipError_t launch(const char *label, uint64_t ops, F &&fn) {
-        if (!profiling) return fn();
+        if (profiling != 1) return fn();
         hipEvent_t e0, e1;
         hipError_t e = event(e0);
         if (e == hipSuccess) e = event(e1);
@@ -646,6 +647,26 @@ struct hs_batch {
         if ((e = fn()) != hipSuccess) return e;
         if ((e = hipEventRecord(e1, st)) != hipSuccess) return e;
         pending.push_back(Pending{entry(label), e0, e1, ops});
+        return hipSuccess;
+    }
+    // Span profiling: an event before the pass's first copy and one after its last launch, so
+    // "pass_span" sums the GPU time of the passes, gaps between kernels included.
+    hipEvent_t span0 = nullptr;
+    hipError_t span_begin() {
+        if (profiling != 2) return hipSuccess;
+        if (span0) event_pool.push_back(span0);  // a pass that failed after its first event
+        hipError_t e = event(span0);
+        if (e != hipSuccess) return e;
+        return hipEventRecord(span0, st);
+    }
+    hipError_t span_end() {
+        if (profiling != 2 || !span0) return hipSuccess;
+        hipEvent_t e1;
+        hipError_t e = event(e1);
+        if (e != hipSuccess) return e;
+        if ((e = hipEventRecord(e1, st)) != hipSuccess) return e;
+        pending.push_back(Pending{entry("pass_span"), span0, e1, 0});
+        span0 = nullptr;
         return hipSuccess;
     }
     // After a stream synchronisation: adds the event times of the finished launches.
@@ -913,6 +934,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             n_out++;
         }
     }
+    HIP_TRY(b.span_begin());
     HIP_TRY(hipMemcpyAsync(b.d_rows, info, n * sizeof(RowInfo), hipMemcpyHostToDevice, st));
     // Attention groups (runs of one slot at consecutive positions, at most 64 rows each) for
     // the MFMA prefill kernel; decode-shaped passes (short runs) use the row kernel.
@@ -1073,6 +1095,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         }
     }
     if (n_out == 0) {
+        HIP_TRY(b.span_end());
         b.inflight = true;
         if (b.profiling && b.pending.size() > 8192) {
             HIP_TRY(hipStreamSynchronize(st));
@@ -1158,6 +1181,7 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
             HIP_TRY(hipMemcpyAsync(host.data() + (size_t)c0 * m.V, b.d_weights, (size_t)cn * m.V * 8,
                                    hipMemcpyDeviceToHost, st));
     }
+    HIP_TRY(b.span_end());
     if (out == Out::Intervals)
         HIP_TRY(hipMemcpyAsync(b.h_intervals, b.d_intervals, (size_t)n_out * 24, hipMemcpyDeviceToHost, st));
     if (mx && mx->plain_sink)
@@ -1620,7 +1644,8 @@ extern "C" hs_status hs_batch_set_profiling(hs_batch *b, int on) {
             b->event_pool.push_back(e);
         }
     }
-    b->profiling = on != 0;
+    if (on < 0 || on > 2) return hs::fail(HS_INVALID_ARGUMENT, 0, "profiling mode must be 0, 1 or 2");
+    b->profiling = on;
     return HS_OK;
 }
 

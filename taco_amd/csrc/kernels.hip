@@ -6,10 +6,59 @@
 // scheduling.
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "intmath.h"
 #include "kernels.h"
 
 namespace hs {
+
+// ---- launch attributes, per kernel and device ---------------------------------------------------
+// A kernel's dynamic-LDS limit is raised on the current device before its first launch that needs
+// more than the default, and the resident-workgroup count of the persistent kernels is taken
+// from the occupancy query once per (kernel, device, LDS size). Launchers may run on several
+// host threads at once (one batch per thread), so both caches sit behind one mutex.
+static std::mutex g_attr_mutex;
+
+static hipError_t allow_dynamic_lds(const void *fn, size_t bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    static std::map<std::pair<const void *, int>, size_t> raised;
+    std::lock_guard<std::mutex> lock(g_attr_mutex);
+    size_t &have = raised[{fn, dev}];
+    if (bytes <= have) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return e;
+    have = bytes;
+    return hipSuccess;
+}
+
+// CUs x workgroups per CU of `fn` at `threads` threads and `lds` bytes of dynamic LDS.
+static hipError_t resident_workgroups(const void *fn, int threads, size_t lds, int *out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    static std::map<std::tuple<const void *, int, size_t>, int> known;
+    std::lock_guard<std::mutex> lock(g_attr_mutex);
+    const auto key = std::make_tuple(fn, dev, lds);
+    const auto it = known.find(key);
+    if (it != known.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    int cus = 0, per_cu = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds);
+    if (e != hipSuccess) return e;
+    const int p = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    known.emplace(key, p);
+    *out = p;
+    return hipSuccess;
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int32_t RES = (1 << 30) - 1;             // gpt2/mod.rs:116
@@ -787,12 +836,9 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
     constexpr size_t after_table = (GELU_LDS ? 65536 : 0) + regions;
     constexpr size_t lds_max = stages > after_table ? stages : after_table;
     static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
-    static bool ready = false;  // the dynamic LDS limit, raised once per instantiation
-    if (!ready) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI, NARROW, BN, VEC, BM, DEEP>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
+    {
+        const hipError_t e = allow_dynamic_lds((const void *)k_gemm<EPI, NARROW, BN, VEC, BM, DEEP>, lds_max);
         if (e != hipSuccess) return e;
-        ready = true;
     }
     size_t lds = stages > regions ? stages : regions;
     if (GELU_LDS && VEC) {
@@ -1009,13 +1055,10 @@ static hipError_t launch_gemm_split(Epi epi, const GemmArgs &ga, int splits, hip
     p.out = ga.partials;
     p.ldo = ldp;
     constexpr int EPI_RAW = (int)Epi::Raw;
-    static bool ready = false;
     constexpr size_t lds = (size_t)GEMM_STAGES * (GEMM_BM / 16 + SPLIT_BN / 16) * 1024;
-    if (!ready) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_gemm<EPI_RAW, false, SPLIT_BN, true>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    {
+        const hipError_t e = allow_dynamic_lds((const void *)k_gemm<EPI_RAW, false, SPLIT_BN, true>, lds);
         if (e != hipSuccess) return e;
-        ready = true;
     }
     const int gm = (ga.m + GEMM_BM - 1) / GEMM_BM, gn = (ga.n + SPLIT_BN - 1) / SPLIT_BN;
     hipLaunchKernelGGL((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(64 * gemm_waves(SPLIT_BN)), lds,
@@ -2284,13 +2327,11 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
         const int kmax64 = (kmax + 63) & ~63;
         if (kmax64 > 1024) return hipErrorInvalidValue;  // the kernel's register rows end at 1,024 keys
         const size_t dyn = (size_t)(kmax64 < DEC_VLDS ? kmax64 : DEC_VLDS) * 64 + (size_t)kmax64 * 4;
-        static bool allowed[2];
         const bool nc = attn_noclamp(a);
         const void *fn = nc ? (const void *)k_attend_decode64<true> : (const void *)k_attend_decode64<false>;
-        if (!allowed[nc]) {
-            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, DEC_VLDS * 64 + 4096);
+        {
+            const hipError_t e = allow_dynamic_lds(fn, DEC_VLDS * 64 + 4096);
             if (e != hipSuccess) return e;
-            allowed[nc] = true;
         }
         if (nc) hipLaunchKernelGGL(k_attend_decode64<true>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
         else hipLaunchKernelGGL(k_attend_decode64<false>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
@@ -2969,12 +3010,9 @@ static hipError_t launch_attend_groups_t(const AttnArgs &a, const AttnGroup *gro
                                          hipStream_t stream) {
     // without MULTI the table lands in whole 1 KiB chunks
     const size_t lds = LDS_TABLE ? (MULTI ? sizeof(int32_t) * (size_t)a.exp_len : ((size_t)a.exp_len + 255) / 256 * 1024) : 0;
-    static size_t allowed = 0;  // the dynamic LDS limit, raised once per variant
-    if (lds > allowed) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    {
+        const hipError_t e = allow_dynamic_lds((const void *)k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>, lds);
         if (e != hipSuccess) return e;
-        allowed = lds;
     }
     hipLaunchKernelGGL((k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>), dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
     return hipGetLastError();
@@ -2998,31 +3036,14 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
         const size_t lds = ((size_t)a.exp_len + 255) / 256 * 1024;  // whole 1 KiB chunks
         const bool four = max_keys <= 4 * 64;
         const void *fn = four ? (const void *)k_attend_short<4> : (const void *)k_attend_short<8>;
-        static size_t allowed[2] = {0, 0};  // the dynamic LDS limit, raised once per form
-        if (lds > allowed[four]) {
-            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return e;
-            allowed[four] = lds;
-        }
-        // the resident workgroups: CUs x workgroups per CU at this LDS size (cached per form and
-        // LDS size on the current device), at most one per task
-        static int cached_dev[2] = {-1, -1}, cached_p[2] = {0, 0};
-        static size_t cached_lds[2] = {0, 0};
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
+        hipError_t e = allow_dynamic_lds(fn, lds);
         if (e != hipSuccess) return e;
-        if (cached_dev[four] != dev || cached_lds[four] != lds) {
-            int cus = 0, per_cu = 0;
-            e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-            if (e != hipSuccess) return e;
-            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds);
-            if (e != hipSuccess) return e;
-            cached_p[four] = (cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
-            cached_dev[four] = dev;
-            cached_lds[four] = lds;
-        }
+        // the resident workgroups (CUs x workgroups per CU at this LDS size), at most one per task
+        int resident = 0;
+        e = resident_workgroups(fn, 256, lds, &resident);
+        if (e != hipSuccess) return e;
         const int n_tasks = n_groups * a.n_head;
-        const int P = cached_p[four] < n_tasks ? cached_p[four] : n_tasks;
+        const int P = resident < n_tasks ? resident : n_tasks;
         if (four) hipLaunchKernelGGL(k_attend_short<4>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
         else hipLaunchKernelGGL(k_attend_short<8>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
         return hipGetLastError();
@@ -3809,35 +3830,30 @@ __global__ __launch_bounds__(256) void k_coder_compact_mixed(CompactCoderArgs a)
 }
 
 template <typename K>
-static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows, size_t *allowed,
-                                 hipStream_t stream) {
+static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
     // packed counts: zcut bins and 64 spare bins of the weight-0 symbols; else two arrays
     const size_t lds = sizeof(uint32_t) * (a.vocab < 65536 ? (size_t)a.zcut + 64 : 2 * (size_t)a.zcut);
-    if (lds > *allowed) {  // raise the dynamic LDS limit once per size
-        hipError_t e = hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    {
+        const hipError_t e = allow_dynamic_lds((const void *)kernel, lds);
         if (e != hipSuccess) return e;
-        *allowed = lds;
     }
     hipLaunchKernelGGL(kernel, dim3(n_rows), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
-    static size_t allowed = 0;
-    return launch_compact(k_coder_compact<false>, a, n_rows, &allowed, stream);
+    return launch_compact(k_coder_compact<false>, a, n_rows, stream);
 }
 
 hipError_t launch_mix_stats_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
-    static size_t allowed = 0;
     if (!a.mix || !a.stats) return hipErrorInvalidValue;
-    return launch_compact(k_coder_compact<true>, a, n_rows, &allowed, stream);
+    return launch_compact(k_coder_compact<true>, a, n_rows, stream);
 }
 
 hipError_t launch_coder_compact_mixed(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
-    static size_t allowed = 0;
     if (!a.mix) return hipErrorInvalidValue;
-    return launch_compact(k_coder_compact_mixed, a, n_rows, &allowed, stream);
+    return launch_compact(k_coder_compact_mixed, a, n_rows, stream);
 }
 
 // ---- kernel resources (CudaDevice::kernel_resources, crates/hardshell-cuda/src/device.rs:65-74) --

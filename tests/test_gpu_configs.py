@@ -2,9 +2,11 @@
 pass size and width selects, against the oracle (the C++ restatement of the reference CPU path).
 
 - GPT-2 medium shape (24 layers, d 1,024, 16 heads, d_ff 4,096): 256 windows of 256 Zipf(1.1)
-  tokens folded in one call, sampled payloads equal to the CPU fast path's, and every block
+  tokens folded in one call, 32 payloads spread over the slots equal to the CPU fast path's,
+  and every block
   unfolded back to its tokens (crates/taco/src/gpu_fold.rs:205-306, gpu_unfold.rs:74-300).
-- GPT-2 XL shape (48 layers, d 1,600, 25 heads, d_ff 6,400): 512 windows of 512 tokens.
+- GPT-2 XL shape (48 layers, d 1,600, 25 heads, d_ff 6,400): 512 windows of 512 tokens, 16
+  payloads spread over the slots equal to the CPU's.
 - Decode attention at 64 streams x 12 heads x 64 over caches of 128, 512 and 1,024 positions.
 - One- and two-layer models at d 1,024 and 1,600, version-2 ("wide") models and a model with
   |beta| > 256, each through a pass of fewer than 4,096 rows and one of at least 4,096 rows.
@@ -38,7 +40,16 @@ def _windows(tokens, n, sel):
 
 def _cpu_payloads(om, blocks, n):
     return O.fold_payloads(om, np.concatenate(blocks), len(blocks), n, chunk=32,
-                           threads=len(blocks))
+                           threads=min(16, len(blocks)))
+
+
+def _spread(total, count, seed):
+    """count window indices over 0..total-1: evenly spaced (the first and the last included)
+    plus seeded random ones, so slot-, group-order- and offset-dependent errors show."""
+    even = np.linspace(0, total - 1, count // 2).round().astype(int).tolist()
+    rng = np.random.default_rng(seed)
+    rest = [int(x) for x in rng.permutation(total) if int(x) not in even][:count - len(even)]
+    return sorted(even + rest)
 
 
 def test_gpt2_medium_fold_and_unfold_round_trip(dev):
@@ -54,7 +65,7 @@ def test_gpt2_medium_fold_and_unfold_round_trip(dev):
     t0 = time.time()
     got = fold.fold_blocks(batch, blocks)
     _log(f"medium: fold of {W} x {n} in {time.time() - t0:.2f}s")
-    sel = [0, 1, 130, 255]
+    sel = _spread(W, 32, 4)
     om = O.Model(mb)
     want = _cpu_payloads(om, _windows(tokens, n, sel), n)
     for i, w in enumerate(sel):
@@ -79,7 +90,7 @@ def test_gpt2_xl_fold_equals_the_cpu(dev):
     got = fold.fold_blocks(batch, _windows(tokens, n, range(W)))
     _log(f"xl: fold of {W} x {n} in {time.time() - t0:.2f}s")
     del batch
-    sel = [0, 511]
+    sel = _spread(W, 16, 5)
     om = O.Model(mb)
     want = _cpu_payloads(om, _windows(tokens, n, sel), n)
     for i, w in enumerate(sel):
@@ -192,4 +203,43 @@ def test_layernorm_forms_equal_the_cpu(dev, name, windows):
     for w in sorted({0, 3, windows - 1}):
         want = O.fast_window_intervals(om, blocks[w], chunk=32)
         bad = np.nonzero(np.any(raw[w] != want, axis=1))[0]
+        assert len(bad) == 0, f"{name}, window {w}: {len(bad)} rows differ, first {bad[:8].tolist()}"
+
+
+# Split-K products in decode-shaped passes: passes of at most 512 rows whose mlp.c_proj has
+# K = d_ff > 4,096 run k_gemm<Raw> partials over K slices and the summing pass k_split_epi with
+# the Residual rule (GPT-2 XL's mlp.c_proj, K 6,400, in every unfold pass).
+SPLIT_MODELS = {"d256_f6400": (1, 4, 256, 6400), "d1600_f6400": (1, 25, 1600, 6400)}
+
+
+@pytest.mark.parametrize("name", sorted(SPLIT_MODELS))
+def test_split_k_residual_passes_equal_the_cpu(dev, name):
+    """4 windows of 128 tokens: a first pass of 4 x 96 rows (384 rows, 12 or more K slices),
+    then one row per slot per pass (4-row passes, 16 slices), every interval against the CPU
+    fast path's."""
+    from taco_amd import hip, synth
+    L, H, d, f = SPLIT_MODELS[name]
+    V, n, W, first = 512, 128, 4, 96
+    mb = synth.build_model(synth.Dims(L, H, d, f, vocab=V, n_ctx=256), seed=0x5B11 + d)
+    hm, om = hip.HipModel.load(dev, mb), O.Model(mb)
+    blocks = [np.array(splitmix_tokens(0x7E57 + w, n, V - 1), np.uint32) for w in range(W)]
+    feed = [[V - 1] + [int(t) for t in blk[:-1]] for blk in blocks]
+    batch = hip.HipBatch(hm, W, 512)
+    got = [[] for _ in range(W)]
+    inputs, queries = [], []
+    for w in range(W):
+        inputs += [(w, t) for t in feed[w][:first]]
+        queries += [(0, int(t)) for t in blocks[w][:first]]
+    raw = batch.run_coded_raw(inputs, queries, 32).reshape(W, first, 3)
+    for w in range(W):
+        got[w].extend(raw[w])
+    for pos in range(first, n):
+        raw = batch.run_coded_raw([(w, feed[w][pos]) for w in range(W)],
+                                  [(0, int(blocks[w][pos])) for w in range(W)], 32)
+        for w in range(W):
+            got[w].append(raw[w])
+    for w in range(W):
+        want = O.fast_window_intervals(om, blocks[w], chunk=32)
+        g = np.array(got[w])
+        bad = np.nonzero(np.any(g != want, axis=1))[0]
         assert len(bad) == 0, f"{name}, window {w}: {len(bad)} rows differ, first {bad[:8].tolist()}"

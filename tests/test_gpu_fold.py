@@ -20,6 +20,38 @@ def dev():
     return hip.HipDevice.open(0)
 
 
+def test_two_host_threads_fold_on_two_batches(dev):
+    """Two batches of one model folded from two host threads at once (ctypes drops the GIL for
+    the call), three rounds each: the kernels' launch-attribute and occupancy caches are shared
+    across threads, and every payload must equal the single-threaded fold's."""
+    import threading
+    from taco_amd import fold, hip, synth
+    mb = synth.build_model(synth.Dims(2, 12, 768, 3072, vocab=4096, n_ctx=256), seed=0x2720)
+    hm = hip.HipModel.load(dev, mb)
+    blocks = [np.array(splitmix_tokens(0x7A1 + w, 200, 4095), np.uint32) for w in range(32)]
+    halves = (blocks[:16], blocks[16:])
+    want = [fold.fold_blocks(hip.HipBatch(hm, 16, 16 * 200), h) for h in halves]
+    batches = [hip.HipBatch(hm, 16, 16 * 200), hip.HipBatch(hm, 8, 1024)]
+    got, errors = [[], []], []
+
+    def run(i):
+        try:
+            for _ in range(3):
+                got[i].append(fold.fold_blocks(batches[i], halves[i]))
+        except Exception as e:  # surfaced below, on the test's thread
+            errors.append((i, e))
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for r in range(3):
+            assert got[i][r] == want[i], f"thread {i}, round {r}: payloads differ"
+
+
 @pytest.mark.parametrize("overlap", [0, 5, 32])
 def test_fold_and_unfold_equal_the_reference(dev, overlap):
     from taco_amd import fold, hip
@@ -168,8 +200,9 @@ def _payload_from_intervals(iv):
 
 
 def test_bench_fold_payloads_equal_the_cpu(dev):
-    """The benchmark's fold step exactly (64 windows x 256 tokens through the harness), against
-    the threaded CPU baseline and, for any disagreement, a single-window CPU recomputation."""
+    """The benchmark's fold step exactly (64 windows x 256 tokens through the harness): every
+    window's payload against the threaded CPU baseline and, for any disagreement, a
+    single-window CPU recomputation."""
     from taco_amd import fold, hip, synth
     mb = synth.build_model(synth.GPT2_SMALL)
     tokens = synth.zipf_tokens(64 * 256)
@@ -177,8 +210,8 @@ def test_bench_fold_payloads_equal_the_cpu(dev):
     batch = hip.HipBatch(hm, 64, 64 * 256)
     blocks = [tokens[w * 256:(w + 1) * 256] for w in range(64)]
     gpu = fold.fold_blocks(batch, blocks)
-    cpu = O.fold_payloads(om, tokens[:32 * 256], 32, 256, chunk=32, threads=16)
-    bad = [w for w in range(32) if gpu[w] != cpu[w]]
+    cpu = O.fold_payloads(om, tokens, 64, 256, chunk=32, threads=16)
+    bad = [w for w in range(64) if gpu[w] != cpu[w]]
     detail = []
     for w in bad[:3]:
         one = _payload_from_intervals(O.fast_window_intervals(om, blocks[w], chunk=32))
