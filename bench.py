@@ -690,7 +690,11 @@ def run_gemm_vendor(args):
 
 
 ISSUE_OPS = (("v_add_u32", 8, None), ("v_mad_i64_i32", 8, None), ("v_fma_f64", 8, None),
-             ("v_mfma_i32_16x16x64_i8", 8, 16), ("v_mfma_i32_32x32x32_i8", 4, 32))
+             ("v_mfma_i32_16x16x64_i8", 8, 16), ("v_mfma_i32_32x32x32_i8", 4, 32),
+             ("v_ashrrev_i64", 8, None), ("v_mul_hi_i32", 8, None))
+# ops 7 and 8: MFMA chains on waves 0-3 of an 8-wave workgroup, VALU chains (3x the rounds) on
+# waves 4-7
+MIXED_OPS = ((7, "mfma + v_add_u32"), (8, "mfma + v_mad_i64_i32"))
 
 
 def run_issue(args):
@@ -713,13 +717,25 @@ def run_issue(args):
             rows.append(row)
             log(f"{name:24s} {wps} waves/SIMD: {clk:6.2f} clocks per instruction"
                 + (f" ({peak_clk / clk:.3f} of the peak rate)" if peak_clk else ""))
+    # Mixed: alone, the MFMA waves take T_m (op 3 at one wave per SIMD) and the VALU waves T_v
+    # (the VALU op at one wave per SIMD, 3x the rounds); the mixed time against max and sum
+    # tells whether the two kinds issue side by side on a SIMD.
+    mixed = []
+    for op, name in MIXED_OPS:
+        ns = min(hip.probe_issue(dev, op, 2, iters) for _ in range(3))
+        t_m = min(hip.probe_issue(dev, 3, 1, iters) for _ in range(3))
+        t_v = min(hip.probe_issue(dev, 0 if op == 7 else 1, 1, 3 * iters) for _ in range(3))
+        mixed.append({"ops": name, "ns": ns, "mfma_alone_ns": t_m, "valu_alone_ns": t_v,
+                      "overlap": round((t_m + t_v - ns) / min(t_m, t_v), 3)})
+        log(f"{name}: {ns} ns; alone {t_m} and {t_v} ns; overlap {mixed[-1]['overlap']} "
+            "(1: fully side by side, 0: one after the other)")
     big = [r for r in rows if r["op"] == "v_mfma_i32_16x16x64_i8" and r["waves_per_simd"] == 2][0]
     line = {"metric": "int8 MFMA issue rate on 1 MI355X (v_mfma_i32_16x16x64_i8, 2 waves per SIMD)",
             "value": big["frac_of_peak_rate"], "unit": "fraction of the peak rate", "n_gpus": 1,
             "steps": 3, "warmup": 1, "ms_per_step": round(big["ns"] / 1e6, 4), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
             "config": {"workload": "issue-rate probe: 4,096 rounds per wave, 256 x waves workgroups",
-                       "rows": rows},
+                       "rows": rows, "mixed": mixed},
             "roofline": None, "cpu_baseline": None}
     print(json.dumps(line), flush=True)
 

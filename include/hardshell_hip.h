@@ -318,7 +318,10 @@ hs_status hs_read_bw(hs_device *dev, size_t bytes, size_t reps, uint64_t *ns);
 /* The GPU time of one launch of `iters` rounds of independent instructions of one kind on every
  * SIMD (256 x waves_per_simd workgroups of 4 waves, one wave on each SIMD of a CU): op 0 v_add_u32, 1 v_mad_i64_i32,
  * 2 v_fma_f64 (8 chains per wave), 3 v_mfma_i32_16x16x64_i8 (8 accumulators per wave), 4
- * v_mfma_i32_32x32x32_i8 (4 accumulators). No counterpart in the reference: it measures the issue
+ * v_mfma_i32_32x32x32_i8 (4 accumulators), 5 v_ashrrev_i64, 6 v_mul_hi_i32 (8 chains); 7 and 8
+ * run workgroups of 8 waves (waves_per_simd even) in which waves 0-3 run op 3's MFMA chains and
+ * waves 4-7 three times as many rounds of v_add_u32 (7) or v_mad_i64_i32 (8), which shows whether
+ * one wave's VALU work issues beside another wave's MFMAs. No counterpart in the reference: it measures the issue
  * rates that bound the kernels here (clocks per instruction = ns x clock / instructions per SIMD).
  * Allocates a 1 KiB sink for the call. */
 hs_status hs_probe_issue(hs_device *dev, uint32_t op, uint32_t waves_per_simd, uint32_t iters,

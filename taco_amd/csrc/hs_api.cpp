@@ -1749,8 +1749,10 @@ extern "C" hs_status hs_probe_issue(hs_device *dev, uint32_t op, uint32_t waves_
                                     uint64_t *ns) {
     hs::clear_error();
     if (!dev || !ns) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
-    if (op > 4 || waves_per_simd < 1 || waves_per_simd > 8 || iters < 1 || iters > (1u << 20))
-        return hs::fail(HS_UNSUPPORTED, 0, "op must be 0..4, waves_per_simd 1..8, iters 1..2^20");
+    if (op > 8 || waves_per_simd < 1 || waves_per_simd > 8 || iters < 1 || iters > (1u << 20) ||
+        ((op == 7 || op == 8) && waves_per_simd % 2))
+        return hs::fail(HS_UNSUPPORTED, 0, "op must be 0..8, waves_per_simd 1..8 (even for the mixed ops 7 "
+                                           "and 8), iters 1..2^20");
     HIP_TRY(hipSetDevice(dev->ordinal));
     int *sink = nullptr;
     HIP_TRY(hipMalloc((void **)&sink, 256 * sizeof(int)));

@@ -1170,9 +1170,15 @@ hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipS
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// OP 5 v_ashrrev_i64 and 6 v_mul_hi_i32 (8 chains each); OP 7 and 8: workgroups of 8 waves
+// (two per SIMD), waves 0-3 the 16 x 16 x 64 MFMA chains and waves 4-7 three times as many
+// rounds of v_add_u32 (7) or v_mad_i64_i32 (8), so the time shows whether a SIMD issues one
+// wave's VALU work while another wave's MFMAs run.
 template <int OP>
-__global__ __launch_bounds__(256) void k_issue_probe(int *sink, int iters, int seed) {
+__global__ __launch_bounds__(512) void k_issue_probe(int *sink, int iters, int seed) {
     const int t = threadIdx.x;
+    constexpr bool MIX = OP == 7 || OP == 8;
+    const bool mfma_wave = MIX && __builtin_amdgcn_readfirstlane(t >> 6) < 4;
     int32_t a[8];
     int64_t b[8];
     double c[8];
@@ -1190,14 +1196,32 @@ __global__ __launch_bounds__(256) void k_issue_probe(int *sink, int iters, int s
     const v4i fa = {seed, t, 7, 9}, fb = {t, seed, 3, 5};
     const int m = seed | 1;
     const double md = 1.000001;
-    for (int it = 0; it < iters; it++) {
+    if (MIX && mfma_wave) {
+        for (int it = 0; it < iters; it++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (OP == 0) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a[i]) : "s"(m));
-            if (OP == 1) asm volatile("v_mad_i64_i32 %0, vcc, %1, %2, %0" : "+v"(b[i]) : "v"(a[i]), "s"(m) : "vcc");
-            if (OP == 2) asm volatile("v_fma_f64 %0, %0, %1, %1" : "+v"(c[i]) : "s"(md));
-            if (OP == 3) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(x[i]) : "v"(fa), "v"(fb));
-            if (OP == 4 && i < 4) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(y[i]) : "v"(fa), "v"(fb));
+            for (int i = 0; i < 8; i++)
+                asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(x[i]) : "v"(fa), "v"(fb));
+        }
+    } else if (MIX) {
+        for (int it = 0; it < 3 * iters; it++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (OP == 7) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a[i]) : "s"(m));
+                if (OP == 8) asm volatile("v_mad_i64_i32 %0, vcc, %1, %2, %0" : "+v"(b[i]) : "v"(a[i]), "s"(m) : "vcc");
+            }
+        }
+    } else {
+        for (int it = 0; it < iters; it++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (OP == 0) asm volatile("v_add_u32 %0, %0, %1" : "+v"(a[i]) : "s"(m));
+                if (OP == 1) asm volatile("v_mad_i64_i32 %0, vcc, %1, %2, %0" : "+v"(b[i]) : "v"(a[i]), "s"(m) : "vcc");
+                if (OP == 2) asm volatile("v_fma_f64 %0, %0, %1, %1" : "+v"(c[i]) : "s"(md));
+                if (OP == 3) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(x[i]) : "v"(fa), "v"(fb));
+                if (OP == 4 && i < 4) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(y[i]) : "v"(fa), "v"(fb));
+                if (OP == 5) asm volatile("v_ashrrev_i64 %0, %1, %0" : "+v"(b[i]) : "s"(m & 31));
+                if (OP == 6) asm volatile("v_mul_hi_i32 %0, %0, %1" : "+v"(a[i]) : "s"(m));
+            }
         }
     }
     int64_t acc = 0;
@@ -1209,6 +1233,13 @@ __global__ __launch_bounds__(256) void k_issue_probe(int *sink, int iters, int s
 }
 
 hipError_t launch_issue_probe(int op, int waves_per_simd, int iters, int *sink, hipStream_t stream) {
+    if (op == 7 || op == 8) {  // 8 waves per workgroup: waves_per_simd counts both kinds
+        if (waves_per_simd % 2) return hipErrorInvalidValue;
+        const dim3 grid(256 * waves_per_simd / 2), block(512);
+        if (op == 7) hipLaunchKernelGGL(k_issue_probe<7>, grid, block, 0, stream, sink, iters, 7);
+        else hipLaunchKernelGGL(k_issue_probe<8>, grid, block, 0, stream, sink, iters, 7);
+        return hipGetLastError();
+    }
     const dim3 grid(256 * waves_per_simd), block(256);
     switch (op) {
         case 0: hipLaunchKernelGGL(k_issue_probe<0>, grid, block, 0, stream, sink, iters, 7); break;
@@ -1216,6 +1247,8 @@ hipError_t launch_issue_probe(int op, int waves_per_simd, int iters, int *sink, 
         case 2: hipLaunchKernelGGL(k_issue_probe<2>, grid, block, 0, stream, sink, iters, 7); break;
         case 3: hipLaunchKernelGGL(k_issue_probe<3>, grid, block, 0, stream, sink, iters, 7); break;
         case 4: hipLaunchKernelGGL(k_issue_probe<4>, grid, block, 0, stream, sink, iters, 7); break;
+        case 5: hipLaunchKernelGGL(k_issue_probe<5>, grid, block, 0, stream, sink, iters, 7); break;
+        case 6: hipLaunchKernelGGL(k_issue_probe<6>, grid, block, 0, stream, sink, iters, 7); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
