@@ -573,10 +573,14 @@ def test_run_without_readback_advances_like_run_weights(golden):
 def test_probe_issue(dev):
     """hs_probe_issue times every op and refuses the ones it does not have."""
     from taco_amd import hip
-    for op in range(5):
+    for op in range(7):
         assert hip.probe_issue(dev, op, 1, 64) > 0
+    for op in (7, 8):  # the mixed forms run two waves per SIMD
+        assert hip.probe_issue(dev, op, 2, 64) > 0
     with pytest.raises(hip.HipError):
-        hip.probe_issue(dev, 5, 1, 64)
+        hip.probe_issue(dev, 9, 1, 64)
+    with pytest.raises(hip.HipError):
+        hip.probe_issue(dev, 7, 1, 64)
     with pytest.raises(hip.HipError):
         hip.probe_issue(dev, 0, 9, 64)
 
