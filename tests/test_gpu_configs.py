@@ -243,3 +243,34 @@ def test_split_k_residual_passes_equal_the_cpu(dev, name):
         g = np.array(got[w])
         bad = np.nonzero(np.any(g != want, axis=1))[0]
         assert len(bad) == 0, f"{name}, window {w}: {len(bad)} rows differ, first {bad[:8].tolist()}"
+
+
+# Passes of more than 12,288 rows at d 768 (a last 64-row tile partly filled) through both forms
+# of the residual epilogue and both LayerNorm element rules.
+LARGE_PASS_MODELS = {
+    "narrow": {},                                # shifts >= 31: the i32 rescale form
+    "general": dict(residual_target=1 << 18),    # shifts below 31: the general rescale form
+    "beta_1000": dict(beta_max=1000),            # |beta| > 256: the integer LayerNorm element rule
+}
+
+
+@pytest.mark.parametrize("name", sorted(LARGE_PASS_MODELS))
+def test_large_pass_residual_forms_equal_the_cpu(dev, name):
+    """97 windows of 127 tokens in one pass (12,319 rows), every interval of sampled windows
+    against the CPU fast path's."""
+    from taco_amd import hip, synth
+    V, n, W = 512, 127, 97
+    mb = synth.build_model(synth.Dims(2, 12, 768, 3072, vocab=V, n_ctx=256), seed=0xF05E,
+                           **LARGE_PASS_MODELS[name])
+    hm, om = hip.HipModel.load(dev, mb), O.Model(mb)
+    blocks = [np.array(splitmix_tokens(0xAB00 + w, n, V - 1), np.uint32) for w in range(W)]
+    batch = hip.HipBatch(hm, W, W * n)
+    inputs, queries = [], []
+    for w, blk in enumerate(blocks):
+        inputs += [(w, V - 1)] + [(w, int(t)) for t in blk[:-1]]
+        queries += [(0, int(t)) for t in blk]
+    raw = batch.run_coded_raw(inputs, queries, 32).reshape(W, n, 3)
+    for w in (0, 1, 48, 95, 96):
+        want = O.fast_window_intervals(om, blocks[w], chunk=32)
+        bad = np.nonzero(np.any(raw[w] != want, axis=1))[0]
+        assert len(bad) == 0, f"{name}, window {w}: {len(bad)} rows differ, first {bad[:8].tolist()}"
