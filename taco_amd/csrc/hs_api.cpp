@@ -788,46 +788,63 @@ namespace {
 // The plan of a call (batch/plan.rs:60-117): inputs -> rows -> passes of <= max_rows rows; a
 // restart of a slot that already has rows in the current pass starts a new pass.
 struct Plan {
-    std::vector<std::vector<PassRow>> passes;
+    std::vector<std::vector<PassRow>> passes;  // the first n_passes hold this call's passes
+    size_t n_passes = 0;
     std::vector<size_t> pos;
-    std::vector<size_t> touched;               // the slots of the call, in first-use order
-    std::vector<std::vector<uint32_t>> hist;   // their token histories after the call
+    std::vector<size_t> touched;  // the slots of the call, in first-use order
+    std::vector<uint32_t> hist;   // their token histories after the call, n_ctx entries each
     std::vector<StreamState> streams;
     std::unordered_map<size_t, std::vector<uint32_t>> prev;
 };
 
-Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
-    Plan p;
+// Builds the plan into `p`, whose vectors keep their capacity from call to call (a fold step's
+// 16k rows would otherwise touch fresh pages of host memory on every call).
+void make_plan(const hs_batch &b, const hs_input *in, size_t n, Plan &p) {
     const size_t C = b.model->host.n_ctx;
     const size_t k = std::min<size_t>(b.overlap, C - 2);
     const uint32_t eot = b.model->host.eot;
+    p.n_passes = 0;
     p.pos = b.pos;
     p.streams = b.streams;
-    std::vector<PassRow> cur;
+    p.touched.clear();
+    p.hist.clear();
+    p.prev.clear();
+    auto open_pass = [&]() -> std::vector<PassRow> & {
+        if (p.passes.size() <= p.n_passes) p.passes.emplace_back();
+        std::vector<PassRow> &v = p.passes[p.n_passes];
+        v.clear();
+        v.reserve(std::min(n + b.slots, b.max_rows));
+        return v;
+    };
+    std::vector<PassRow> *cur = &open_pass();
     std::vector<char> in_pass(b.slots, 0);
     auto flush = [&]() {
-        if (!cur.empty()) p.passes.push_back(std::move(cur));
-        cur.clear();
+        if (!cur->empty()) {
+            p.n_passes++;
+            cur = &open_pass();
+        }
         std::fill(in_pass.begin(), in_pass.end(), 0);
     };
     auto push = [&](PassRow r) {
-        if (cur.size() >= b.max_rows) flush();
+        if (cur->size() >= b.max_rows) flush();
         in_pass[r.slot] = 1;
-        cur.push_back(r);
+        cur->push_back(r);
     };
     std::vector<int32_t> index(b.slots, -1);  // slot -> its entry in p.touched / p.hist
+    p.touched.reserve(std::min(n, b.slots));
+    p.hist.reserve(std::min(n, b.slots) * C);
     for (size_t i = 0; i < n; i++) {
         const size_t slot = in[i].slot;
         if (index[slot] < 0) {
             index[slot] = (int32_t)p.touched.size();
             p.touched.push_back(slot);
-            p.hist.emplace_back(b.hist.begin() + slot * C, b.hist.begin() + (slot + 1) * C);
+            p.hist.insert(p.hist.end(), b.hist.begin() + slot * C, b.hist.begin() + (slot + 1) * C);
         }
-        std::vector<uint32_t> &h = p.hist[index[slot]];
+        uint32_t *h = p.hist.data() + (size_t)index[slot] * C;
         size_t at = p.pos[slot];
         if (at >= C) {
             if (in_pass[slot]) flush();
-            p.prev[slot] = h;  // the full context before the restart, for a truncation
+            p.prev[slot].assign(h, h + C);  // the full context before the restart, for a truncation
             p.streams[slot].restart(k);
             if (k > 0) std::memmove(&h[1], &h[C - k], k * sizeof(uint32_t));
             h[0] = eot;
@@ -839,8 +856,7 @@ Plan make_plan(const hs_batch &b, const hs_input *in, size_t n) {
         push(PassRow{(uint32_t)slot, in[i].token, (uint32_t)at, (int64_t)i});
         p.pos[slot] = at + 1;
     }
-    flush();
-    return p;
+    if (!cur->empty()) p.n_passes++;
 }
 
 void commit(hs_batch &b, Plan &p) {
@@ -848,7 +864,7 @@ void commit(hs_batch &b, Plan &p) {
     b.pos = p.pos;
     b.streams = p.streams;
     for (size_t t = 0; t < p.touched.size(); t++)
-        std::memcpy(&b.hist[p.touched[t] * C], p.hist[t].data(), C * sizeof(uint32_t));
+        std::memcpy(&b.hist[p.touched[t] * C], p.hist.data() + t * C, C * sizeof(uint32_t));
     for (auto &kv : p.prev) b.prev[kv.first] = std::move(kv.second);
 }
 
@@ -918,7 +934,8 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
     RowInfo *info = b.h_rows;
     int32_t *src = b.h_src;
     uint32_t *q = b.h_queries;
-    std::vector<int64_t> owner;
+    static thread_local std::vector<int64_t> owner;
+    owner.clear();
     owner.reserve(n);
     int n_out = 0;
     for (int r = 0; r < n; r++) {
@@ -1220,9 +1237,10 @@ hs_status check_inputs(const hs_batch *b, const hs_input *in, size_t n) {
 hs_status run(hs_batch *b, const hs_input *in, size_t n, Out out, const uint32_t *queries,
               uint32_t bits, uint64_t *sink, const Mixing *mx = nullptr) {
     HIP_TRY(hipSetDevice(b->model->dev->ordinal));
-    Plan plan = make_plan(*b, in, n);
-    for (auto &pass : plan.passes) {
-        hs_status s = run_pass(*b, pass, out, queries, bits, sink, mx);
+    static thread_local Plan plan;  // host scratch kept from call to call (one call per thread at a time)
+    make_plan(*b, in, n, plan);
+    for (size_t i = 0; i < plan.n_passes; i++) {
+        hs_status s = run_pass(*b, plan.passes[i], out, queries, bits, sink, mx);
         if (s != HS_OK) return s;  // no position changes after an error
     }
     commit(*b, plan);
@@ -1289,7 +1307,7 @@ extern "C" hs_status hs_batch_run_coded(hs_batch *b, const hs_input *in, const h
     hs_status s = check_inputs(b, in, n);
     if (s != HS_OK) return s;
     if (n && (!queries || !out)) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
-    std::vector<uint32_t> words;
+    static thread_local std::vector<uint32_t> words;
     HS_TRY(coder_words(queries, n, b->model->host.vocab, freq_bits, words));
     return run(b, in, n, Out::Intervals, words.data(), freq_bits, (uint64_t *)out);
 }

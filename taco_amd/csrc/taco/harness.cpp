@@ -157,6 +157,9 @@ class Pool {
         static Pool *p = new Pool();
         return *p;
     }
+    // Runs f(0) .. f(n - 1) on the calling thread and the workers; returns when all are done.
+    // Tasks are claimed from one word holding (job number, next index), so a worker still
+    // leaving an earlier job can never claim a task of this one.
     void run(size_t n, const std::function<void(size_t)> &f) {
         if (n <= 1 || workers_ == 0) {
             for (size_t i = 0; i < n; i++) f(i);
@@ -164,18 +167,18 @@ class Pool {
         }
         // one job at a time: callers on several host threads (one per batch) take turns
         std::lock_guard<std::mutex> one(run_mu_);
-        std::unique_lock<std::mutex> lk(mu_);
-        job_ = &f;
+        const uint64_t job = (word_.load(std::memory_order_relaxed) >> 32) + 1;
+        fn_ = &f;
         n_ = n;
-        next_ = 0;
-        done_ = 0;
-        gen_++;
-        lk.unlock();
+        done_.store(0, std::memory_order_relaxed);
+        word_.store(job << 32, std::memory_order_release);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            posted_ = job;
+        }
         cv_.notify_all();
-        work();
-        lk.lock();
-        done_cv_.wait(lk, [&] { return done_ == n_; });
-        job_ = nullptr;
+        work(job);
+        while (done_.load(std::memory_order_acquire) != n) __builtin_ia32_pause();
     }
 
   private:
@@ -187,35 +190,37 @@ class Pool {
     void loop() {
         uint64_t seen = 0;
         for (;;) {
+            uint64_t job;
             {
                 std::unique_lock<std::mutex> lk(mu_);
-                cv_.wait(lk, [&] { return gen_ != seen; });
-                seen = gen_;
+                cv_.wait(lk, [&] { return posted_ != seen; });
+                job = seen = posted_;
             }
-            work();
+            work(job);
         }
     }
-    void work() {
+    void work(uint64_t job) {
         for (;;) {
-            const std::function<void(size_t)> *fn;
+            uint64_t w = word_.load(std::memory_order_acquire);
             size_t i;
-            {
-                std::lock_guard<std::mutex> lk(mu_);
-                if (!job_ || next_ >= n_) return;
-                fn = job_;
-                i = next_++;
+            for (;;) {
+                if ((w >> 32) != job) return;
+                i = (size_t)(w & 0xffffffffu);
+                if (i >= n_) return;
+                if (word_.compare_exchange_weak(w, w + 1, std::memory_order_acq_rel)) break;
             }
-            (*fn)(i);
-            std::lock_guard<std::mutex> lk(mu_);
-            if (++done_ == n_) done_cv_.notify_all();
+            (*fn_)(i);
+            done_.fetch_add(1, std::memory_order_release);
         }
     }
     unsigned workers_ = 0;
     std::mutex run_mu_, mu_;
-    std::condition_variable cv_, done_cv_;
-    const std::function<void(size_t)> *job_ = nullptr;
-    size_t n_ = 0, next_ = 0, done_ = 0;
-    uint64_t gen_ = 0;
+    std::condition_variable cv_;
+    uint64_t posted_ = 0;            // the last job posted to the workers
+    std::atomic<uint64_t> word_{0};  // job number << 32 | next task index
+    std::atomic<size_t> done_{0};
+    const std::function<void(size_t)> *fn_ = nullptr;
+    size_t n_ = 0;
 };
 
 // A context window of a block (gpu_fold.rs:128-134).
@@ -270,10 +275,33 @@ extern "C" hs_status tc_fold_blocks(hs_batch *batch, uint32_t overlap, const uin
             size = std::max<size_t>(1, std::max<size_t>(n_ctx, 2) - std::min(std::max<size_t>(n_ctx, 2), 1 + k));
         }
     }
-    std::vector<hs_input> inputs;
-    std::vector<hs_query> queries;
-    std::vector<int64_t> owner;  // the block of each coded row, -1 for a row that codes nothing
-    std::vector<hs_interval> answers;
+    // Host scratch kept from call to call on this thread (fresh vectors of a fold step's 16k
+    // rows would touch new pages of memory on every call). The names below are references to
+    // the calling thread's instances, so the range-coder tasks on the pool's threads (which
+    // capture them) see this call's rows.
+    struct Scratch {
+        std::vector<hs_input> inputs;
+        std::vector<hs_query> queries;
+        std::vector<int64_t> owner;
+        std::vector<hs_interval> answers;
+    };
+    static thread_local Scratch scratch;
+    std::vector<hs_input> &inputs = scratch.inputs;
+    std::vector<hs_query> &queries = scratch.queries;
+    std::vector<int64_t> &owner = scratch.owner;  // the block of each coded row, -1 for a row that codes nothing
+    std::vector<hs_interval> &answers = scratch.answers;
+    {
+        size_t most = 0;  // rows of the largest wave of windows
+        for (size_t w0 = 0; w0 < windows.size(); w0 += slots) {
+            size_t r = 0;
+            for (size_t wi = w0; wi < std::min(windows.size(), w0 + slots); wi++) r += windows[wi].len + k + 1;
+            most = std::max(most, r);
+        }
+        inputs.reserve(most);
+        queries.reserve(most);
+        owner.reserve(most);
+        answers.reserve(most);
+    }
     for (size_t w0 = 0; w0 < windows.size(); w0 += slots) {
         const size_t w1 = std::min(windows.size(), w0 + slots);
         inputs.clear();
