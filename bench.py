@@ -420,10 +420,15 @@ def run_fold(args):
 
     unfold = None
     if args.workload == "fold-gpt2-medium" and not args.no_unfold:
-        # the full round trip: every block decoded on the GPU (one row per slot per call)
+        # the full round trip: every block decoded on the GPU (one row per slot per call), with
+        # one event pair per pass (the GPU span of the passes, gaps between kernels included)
+        hip._check(hip.lib().hs_batch_set_profiling(batch.h, 2))
+        hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
         ts = time.perf_counter()
         back = fold.unfold_blocks(batch, payloads, 0, cap=n)
         u_s = time.perf_counter() - ts
+        uspan = read_profile(hip, batch).get("pass_span", {"ns": 0, "launches": 0})
+        hip._check(hip.lib().hs_batch_set_profiling(batch.h, 0))
         same = all(np.array_equal(back[w], blocks[w]) for w in range(W))
         log(f"unfold: {W} blocks in {u_s:.3f}s -> {W * n / u_s:.0f} tokens/s; round trip equal: {same}")
         if not same:
@@ -443,9 +448,13 @@ def run_fold(args):
         u_ops = {kk: round(v["ns"] / 1e6 / passes, 4) for kk, v in sorted(uprof.items(), key=lambda x: -x[1]["ns"])}
         log(f"unfold: {passes} passes; GPU ms per pass by op: {u_ops}; wall ms per pass "
             f"{1e3 * u_s / passes:.3f}")
+        span_pass = uspan["ns"] / 1e6 / max(1, uspan["launches"])
+        log(f"unfold: GPU span {span_pass:.3f} ms per pass over {uspan['launches']} passes; wall "
+            f"{1e3 * u_s / max(1, uspan['launches']):.3f} ms per pass")
         unfold = {"tokens_per_s": round(W * n / u_s, 1), "seconds": round(u_s, 3),
                   "round_trip_equal": same, "passes": passes,
                   "wall_ms_per_pass": round(1e3 * u_s / passes, 4),
+                  "gpu_span_ms_per_pass": round(span_pass, 4),
                   "gpu_ms_per_pass_by_op": u_ops}
 
     cpu = None

@@ -636,6 +636,9 @@ struct hs_batch {
         return prof.size() - 1;
     }
     // Runs `fn` (a launch on the batch stream), bracketed by events when profiling.
+    // The op's kernels carry the events on their dispatches (hs::set_op_events): the first one
+    // records e0 as it starts, each one e1 as it ends. An op that launched no kernel is timed
+    // by a pair recorded around it.
     template <typename F>
     hipError_t launch(const char *label, uint64_t ops, F &&fn) {
         if (profiling != 1) return fn();
@@ -643,9 +646,15 @@ struct hs_batch {
         hipError_t e = event(e0);
         if (e == hipSuccess) e = event(e1);
         if (e != hipSuccess) return e;
-        if ((e = hipEventRecord(e0, st)) != hipSuccess) return e;
-        if ((e = fn()) != hipSuccess) return e;
-        if ((e = hipEventRecord(e1, st)) != hipSuccess) return e;
+        hs::set_op_events(e0, e1);
+        e = fn();
+        const int launched = hs::op_launches();
+        hs::set_op_events(nullptr, nullptr);
+        if (e != hipSuccess) return e;
+        if (launched == 0) {
+            if ((e = hipEventRecord(e0, st)) != hipSuccess) return e;
+            if ((e = hipEventRecord(e1, st)) != hipSuccess) return e;
+        }
         pending.push_back(Pending{entry(label), e0, e1, ops});
         return hipSuccess;
     }

@@ -94,6 +94,12 @@ inline int gemm_group(int m) {
 
 hipError_t launch_gemm(Epi epi, const GemmArgs &g, hipStream_t stream);
 
+// Profiling: the kernels launched on this host thread until the next call record `start` (the
+// first one, as it begins) and `stop` (each one, as it ends) on their dispatches; null stops
+// it. op_launches counts the kernels launched since the events were set.
+void set_op_events(hipEvent_t start, hipEvent_t stop);
+int op_launches();
+
 // The compiled resources of the main kernels: fills up to cap entries and returns the number of
 // kernels (or minus a hipError_t).
 struct KernelResource {

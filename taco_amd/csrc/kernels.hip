@@ -4,6 +4,7 @@
 // Reductions are fixed-order wave/LDS trees, and the only atomics are the coder op's integer
 // histogram counts in LDS, whose sums do not depend on order: results do not depend on
 // scheduling.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -14,6 +15,33 @@
 #include "kernels.h"
 
 namespace hs {
+
+// ---- kernel launches and their profiling events -------------------------------------------------
+// The caller of an op may hand it a pair of events (set_op_events): the first kernel the op
+// launches then records `start` as it begins and every one records `stop` as it ends (the
+// events ride on the dispatches, hipExtLaunchKernelGGL), so stop - start is the op's GPU time
+// with no event packets between its kernels.
+static thread_local hipEvent_t t_op_start = nullptr, t_op_stop = nullptr;
+static thread_local int t_op_launches = 0;
+
+void set_op_events(hipEvent_t start, hipEvent_t stop) {
+    t_op_start = start;
+    t_op_stop = stop;
+    t_op_launches = 0;
+}
+
+int op_launches() { return t_op_launches; }
+
+template <typename K, typename... Args>
+static inline void launch_k(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+    if (t_op_stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, t_op_launches == 0 ? t_op_start : nullptr,
+                              t_op_stop, 0u, args...);
+        t_op_launches++;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    }
+}
 
 // ---- launch attributes, per kernel and device ---------------------------------------------------
 // A kernel's dynamic-LDS limit is raised on the current device before its first launch that needs
@@ -845,7 +873,7 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
         const size_t t = ((size_t)g.gelu_copy + 1023) & ~(size_t)1023;
         lds = stages > t + regions ? stages : t + regions;
     }
-    hipLaunchKernelGGL((k_gemm<EPI, NARROW, BN, VEC, BM, DEEP>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
+    launch_k((k_gemm<EPI, NARROW, BN, VEC, BM, DEEP>), dim3(gm * gn), dim3(64 * WAVES), lds, stream, g);
     return hipGetLastError();
 }
 
@@ -1039,7 +1067,7 @@ __global__ __launch_bounds__(256) void k_split_epi(GemmArgs g, int splits, int l
 template <int EPI>
 static hipError_t launch_split_epi(const GemmArgs &g, int splits, int ldp, hipStream_t stream) {
     const long long threads = (long long)g.m * (ldp / 4);
-    hipLaunchKernelGGL(k_split_epi<EPI>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, g,
+    launch_k(k_split_epi<EPI>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, g,
                        splits, ldp);
     return hipGetLastError();
 }
@@ -1061,7 +1089,7 @@ static hipError_t launch_gemm_split(Epi epi, const GemmArgs &ga, int splits, hip
         if (e != hipSuccess) return e;
     }
     const int gm = (ga.m + GEMM_BM - 1) / GEMM_BM, gn = (ga.n + SPLIT_BN - 1) / SPLIT_BN;
-    hipLaunchKernelGGL((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(64 * gemm_waves(SPLIT_BN)), lds,
+    launch_k((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(64 * gemm_waves(SPLIT_BN)), lds,
                        stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1088,7 +1116,7 @@ hipError_t launch_wide_combine(const int32_t *planes, const int32_t *wsum, int m
                                hipStream_t stream) {
     const long long t = (long long)m * n;
     if (t == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_wide_combine, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, stream, planes, wsum, m, n, out);
+    launch_k(k_wide_combine, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, stream, planes, wsum, m, n, out);
     return hipGetLastError();
 }
 
@@ -1156,7 +1184,7 @@ __global__ __launch_bounds__(256) void k_read_bw(const v4i *p, size_t n16, int *
 }
 
 hipError_t launch_read_bw(const void *buf, size_t n16, int *sink, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL(k_read_bw, dim3(grid), dim3(256), 0, stream, (const v4i *)buf, n16, sink);
+    launch_k(k_read_bw, dim3(grid), dim3(256), 0, stream, (const v4i *)buf, n16, sink);
     return hipGetLastError();
 }
 
@@ -1236,19 +1264,19 @@ hipError_t launch_issue_probe(int op, int waves_per_simd, int iters, int *sink, 
     if (op == 7 || op == 8) {  // 8 waves per workgroup: waves_per_simd counts both kinds
         if (waves_per_simd % 2) return hipErrorInvalidValue;
         const dim3 grid(256 * waves_per_simd / 2), block(512);
-        if (op == 7) hipLaunchKernelGGL(k_issue_probe<7>, grid, block, 0, stream, sink, iters, 7);
-        else hipLaunchKernelGGL(k_issue_probe<8>, grid, block, 0, stream, sink, iters, 7);
+        if (op == 7) launch_k(k_issue_probe<7>, grid, block, 0, stream, sink, iters, 7);
+        else launch_k(k_issue_probe<8>, grid, block, 0, stream, sink, iters, 7);
         return hipGetLastError();
     }
     const dim3 grid(256 * waves_per_simd), block(256);
     switch (op) {
-        case 0: hipLaunchKernelGGL(k_issue_probe<0>, grid, block, 0, stream, sink, iters, 7); break;
-        case 1: hipLaunchKernelGGL(k_issue_probe<1>, grid, block, 0, stream, sink, iters, 7); break;
-        case 2: hipLaunchKernelGGL(k_issue_probe<2>, grid, block, 0, stream, sink, iters, 7); break;
-        case 3: hipLaunchKernelGGL(k_issue_probe<3>, grid, block, 0, stream, sink, iters, 7); break;
-        case 4: hipLaunchKernelGGL(k_issue_probe<4>, grid, block, 0, stream, sink, iters, 7); break;
-        case 5: hipLaunchKernelGGL(k_issue_probe<5>, grid, block, 0, stream, sink, iters, 7); break;
-        case 6: hipLaunchKernelGGL(k_issue_probe<6>, grid, block, 0, stream, sink, iters, 7); break;
+        case 0: launch_k(k_issue_probe<0>, grid, block, 0, stream, sink, iters, 7); break;
+        case 1: launch_k(k_issue_probe<1>, grid, block, 0, stream, sink, iters, 7); break;
+        case 2: launch_k(k_issue_probe<2>, grid, block, 0, stream, sink, iters, 7); break;
+        case 3: launch_k(k_issue_probe<3>, grid, block, 0, stream, sink, iters, 7); break;
+        case 4: launch_k(k_issue_probe<4>, grid, block, 0, stream, sink, iters, 7); break;
+        case 5: launch_k(k_issue_probe<5>, grid, block, 0, stream, sink, iters, 7); break;
+        case 6: launch_k(k_issue_probe<6>, grid, block, 0, stream, sink, iters, 7); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1274,7 +1302,7 @@ hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int 
                         const int8_t *wpe, const int32_t *embed_m, int embed_s,
                         const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream) {
     dim3 grid(n_rows, (d + 255) / 256);
-    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_rows, wpe, embed_m,
+    launch_k(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_rows, wpe, embed_m,
                        embed_s, pos_m, pos_s, d, x);
     return hipGetLastError();
 }
@@ -1653,18 +1681,18 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     // Fewer than 4,096 rows (decode passes): a one-wave workgroup per row, spread over the CUs;
     // the 16-lane form would leave most of them idle (256 rows: 16 workgroups)
     if (n_rows < 4096 && a.d % 4 == 0 && a.d <= 2048) {
-        if (a.d <= 1024) hipLaunchKernelGGL(k_layernorm_rows<4>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
-        else hipLaunchKernelGGL(k_layernorm_rows<8>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
+        if (a.d <= 1024) launch_k(k_layernorm_rows<4>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
+        else launch_k(k_layernorm_rows<8>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.d <= 768) {
-        if (f32) hipLaunchKernelGGL((k_layernorm_rows4<12, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
-        else hipLaunchKernelGGL((k_layernorm_rows4<12, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        if (f32) launch_k((k_layernorm_rows4<12, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        else launch_k((k_layernorm_rows4<12, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.d <= 1024) {
-        if (f32) hipLaunchKernelGGL((k_layernorm_rows4<16, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
-        else hipLaunchKernelGGL((k_layernorm_rows4<16, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        if (f32) launch_k((k_layernorm_rows4<16, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        else launch_k((k_layernorm_rows4<16, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.d <= 2048) {
-        hipLaunchKernelGGL(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
+        launch_k(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
     } else {
-        hipLaunchKernelGGL(k_layernorm, dim3((n_rows + 3) / 4), dim3(256), 0, stream, a, n_rows);
+        launch_k(k_layernorm, dim3((n_rows + 3) / 4), dim3(256), 0, stream, a, n_rows);
     }
     return hipGetLastError();
 }
@@ -1688,7 +1716,7 @@ __global__ void k_kv_store(const RowInfo *rows, const int8_t *qkv, int d, int n_
 hipError_t launch_kv_store(const RowInfo *rows, int n_rows, const int8_t *qkv, int d, int n_head,
                            int hd, int n_ctx, int8_t *kc, int8_t *vc, hipStream_t stream) {
     dim3 grid(n_rows, (d + 255) / 256);
-    hipLaunchKernelGGL(k_kv_store, grid, dim3(256), 0, stream, rows, qkv, d, n_head, hd, n_ctx,
+    launch_k(k_kv_store, grid, dim3(256), 0, stream, rows, qkv, d, n_head, hd, n_ctx,
                        kc, vc);
     return hipGetLastError();
 }
@@ -1789,7 +1817,7 @@ __global__ __launch_bounds__(256) void k_attend(AttnArgs a, int n_tasks) {
 hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
     const int tasks = n_rows * a.n_head;
     if (tasks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_attend, dim3((tasks + 3) / 4), dim3(256), 0, stream, a, tasks);
+    launch_k(k_attend, dim3((tasks + 3) / 4), dim3(256), 0, stream, a, tasks);
     return hipGetLastError();
 }
 
@@ -2312,10 +2340,10 @@ static hipError_t launch_decode_wave(const AttnArgs &a, int n_rows, int kmax, hi
     const dim3 grid((n_rh + 3) / 4);
     const int kb = (kmax + 63) / 64;
     const size_t lds = (size_t)4 * kb * 4096;  // 16 to 64 KiB
-    if (kb <= 1) hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 1>), grid, dim3(256), lds, stream, a, n_rh, kmax);
-    else if (kb == 2) hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 2>), grid, dim3(256), lds, stream, a, n_rh, kmax);
-    else if (kb == 3) hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 3>), grid, dim3(256), lds, stream, a, n_rh, kmax);
-    else hipLaunchKernelGGL((k_attend_decode_wave<NOCLAMP, 4>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    if (kb <= 1) launch_k((k_attend_decode_wave<NOCLAMP, 1>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    else if (kb == 2) launch_k((k_attend_decode_wave<NOCLAMP, 2>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    else if (kb == 3) launch_k((k_attend_decode_wave<NOCLAMP, 3>), grid, dim3(256), lds, stream, a, n_rh, kmax);
+    else launch_k((k_attend_decode_wave<NOCLAMP, 4>), grid, dim3(256), lds, stream, a, n_rh, kmax);
     return hipGetLastError();
 }
 
@@ -2366,27 +2394,27 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
             const hipError_t e = allow_dynamic_lds(fn, DEC_VLDS * 64 + 4096);
             if (e != hipSuccess) return e;
         }
-        if (nc) hipLaunchKernelGGL(k_attend_decode64<true>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
-        else hipLaunchKernelGGL(k_attend_decode64<false>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
+        if (nc) launch_k(k_attend_decode64<true>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
+        else launch_k(k_attend_decode64<false>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
         return hipGetLastError();
     }
     const dim3 grid(n_rows * a.n_head, p.chunks);
     const size_t lds = p.chunk_keys * sizeof(uint32_t);
     switch (a.hd) {
-    case 16: hipLaunchKernelGGL(k_split_dots<16>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
-    case 32: hipLaunchKernelGGL(k_split_dots<32>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
-    case 64: hipLaunchKernelGGL(k_split_dots<64>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
-    case 128: hipLaunchKernelGGL(k_split_dots<128>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
-    default: hipLaunchKernelGGL(k_split_dots<256>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 16: launch_k(k_split_dots<16>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 32: launch_k(k_split_dots<32>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 64: launch_k(k_split_dots<64>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    case 128: launch_k(k_split_dots<128>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
+    default: launch_k(k_split_dots<256>, grid, dim3(64), 0, stream, a, n_rows, p, scratch); break;
     }
     if (attn_noclamp(a)) {
-        hipLaunchKernelGGL(k_split_sum<true>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
-        hipLaunchKernelGGL(k_split_pv<true>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);
+        launch_k(k_split_sum<true>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
+        launch_k(k_split_pv<true>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);
     } else {
-        hipLaunchKernelGGL(k_split_sum<false>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
-        hipLaunchKernelGGL(k_split_pv<false>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);
+        launch_k(k_split_sum<false>, grid, dim3(64), 0, stream, a, n_rows, p, scratch);
+        launch_k(k_split_pv<false>, grid, dim3(64), lds, stream, a, n_rows, p, scratch);
     }
-    hipLaunchKernelGGL(k_split_out, dim3(n_rows * a.n_head), dim3(a.hd), 0, stream, a, n_rows, p, scratch);
+    launch_k(k_split_out, dim3(n_rows * a.n_head), dim3(a.hd), 0, stream, a, n_rows, p, scratch);
     return hipGetLastError();
 }
 
@@ -3047,7 +3075,7 @@ static hipError_t launch_attend_groups_t(const AttnArgs &a, const AttnGroup *gro
         const hipError_t e = allow_dynamic_lds((const void *)k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>, lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>), dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
+    launch_k((k_attend_mfma<NOCLAMP, LDS_TABLE, MULTI>), dim3(n_groups, a.n_head), dim3(256), lds, stream, a, groups);
     return hipGetLastError();
 }
 
@@ -3077,8 +3105,8 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
         if (e != hipSuccess) return e;
         const int n_tasks = n_groups * a.n_head;
         const int P = resident < n_tasks ? resident : n_tasks;
-        if (four) hipLaunchKernelGGL(k_attend_short<4>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
-        else hipLaunchKernelGGL(k_attend_short<8>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
+        if (four) launch_k(k_attend_short<4>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
+        else launch_k(k_attend_short<8>, dim3(P), dim3(256), lds, stream, a, groups, n_tasks);
         return hipGetLastError();
     }
     if (noclamp && lds_table) return launch_attend_groups_m<true, true>(a, groups, n_groups, max_keys, stream);
@@ -3292,9 +3320,9 @@ static hipError_t launch_coder_mode(const CoderArgs &a, int n_rows, hipStream_t 
     if (n_rows <= 0) return hipSuccess;
     if (MODE != 0 && !a.mix) return hipErrorInvalidValue;
     if (a.wsrc)
-        hipLaunchKernelGGL((k_coder<1, MODE>), dim3(n_rows), dim3(256), 0, stream, a);
+        launch_k((k_coder<1, MODE>), dim3(n_rows), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((k_coder<0, MODE>), dim3(n_rows), dim3(256), 0, stream, a);
+        launch_k((k_coder<0, MODE>), dim3(n_rows), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -3871,7 +3899,7 @@ static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows
         const hipError_t e = allow_dynamic_lds((const void *)kernel, lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(n_rows), dim3(256), lds, stream, a);
+    launch_k(kernel, dim3(n_rows), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
