@@ -428,7 +428,11 @@ hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **
     if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
     // padded to a multiple of 256 entries: the prefill attention loads it in 1 KiB chunks
     if ((st = mem.upload(m->attn_exp, h.attn_exp.data(), h.attn_exp.size(), (h.attn_exp.size() + 255) / 256 * 256)) != HS_OK) return st;
-    if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size())) != HS_OK) return st;
+    // zero-padded to at least CODER_TABLE_READ entries: the compact coder loads its first bins'
+    // entries without bounds tests
+    if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size(),
+                         std::max<size_t>(h.logits_exp.size(), hs::CODER_TABLE_READ))) != HS_OK)
+        return st;
     m->compact = h.logits_exp.size() <= (size_t)hs::CODER_MAX_TABLE;
     while ((size_t)m->d0 + 1 < h.logits_exp.size() && h.logits_exp[m->d0 + 1] == h.logits_exp[0]) m->d0++;
     m->zcut = (int)h.logits_exp.size();
@@ -1953,7 +1957,7 @@ hs_status coder_on_logits(hs_device *dev, const int64_t *logits, size_t rows, si
     hs::MixRec *dm = nullptr;
     std::vector<hs::MixRec> rec(predictions ? rows : 0);
     for (size_t r = 0; r < rec.size(); r++) rec[r] = hs::MixRec{predictions[r], 0, 0, 0, 0, 0};
-    HS_TRY(mem.upload(dt, table, len));
+    HS_TRY(mem.upload(dt, table, len, std::max<size_t>(len, hs::CODER_TABLE_READ)));  // as the model's
     HS_TRY(mem.upload(dq, q.data(), q.size()));
     HS_TRY(mem.alloc(di, 3 * rows));
     if (predictions) {

@@ -235,13 +235,15 @@ hipError_t launch_coder_mixed(const CoderArgs &a, int n_rows, hipStream_t stream
 // The coder op over compact logits (the LogitsCompact GEMM epilogue): d16 [rows, ld16] u16 and
 // tmax [rows, ntiles] i64, with a non-increasing table of table_len <= CODER_MAX_TABLE entries.
 constexpr int CODER_MAX_TABLE = 16384;
+// The table buffer of the compact coder holds at least this many entries (zeros past table_len).
+constexpr int CODER_TABLE_READ = 8192;
 struct CompactCoderArgs {
     const uint16_t *d16 = nullptr;
     int ld16 = 0;
     const int64_t *tmax = nullptr;
     int ntiles = 0;
     int vocab = 0;
-    const uint64_t *table = nullptr;
+    const uint64_t *table = nullptr;  // max(table_len, CODER_TABLE_READ) entries readable
     int table_len = 0;
     int d0 = 0;    // the largest d with table[d] == table[0]
     int zcut = 0;  // every table[d] with d >= zcut is 0 (1 <= zcut <= table_len)

@@ -3392,96 +3392,154 @@ __device__ __forceinline__ uint64_t block_sum64w(uint64_t v, uint64_t *s4, int t
     return r;
 }
 
+// Exclusive prefix sum over a 256-thread block in thread order, and the block total: wave scans
+// through shuffles, then the four wave totals through one LDS slot per wave.
+__device__ __forceinline__ uint64_t block_scan64w(uint64_t v, uint64_t *s4, int tid, uint64_t &total) {
+    const int lane = tid & 63, w = tid >> 6;
+    int64_t x = (int64_t)v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int64_t u = __shfl_up(x, o, 64);
+        if (lane >= o) x += u;
+    }
+    if (lane == 63) s4[w] = (uint64_t)x;
+    __syncthreads();
+    uint64_t before = 0, all = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint64_t t = s4[k];
+        before += k < w ? t : 0;
+        all += t;
+    }
+    __syncthreads();
+    total = all;
+    return before + (uint64_t)x - v;
+}
+
 // One row per workgroup. The histogram counts the symbols of each table index d < zcut (the
 // bins with a nonzero weight); with V < 2^16 the count and the count below the Encode token
 // share one u32 (low and high half), else they are two arrays. Symbols with d >= zcut have
 // weight 0, f = 1 and no share of the spare, and need no count.
 // STATS: the mixer statistics of the row (sum w, w[p] for the record's p, the top token = the
 // largest) instead of the coder interval.
-template <bool STATS>
-__global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
-    extern __shared__ uint32_t hist[];
-    __shared__ int64_t s_i[256];
-    __shared__ uint64_t s_u[256];
-    __shared__ uint64_t s_frac;
-    const int row = blockIdx.x, tid = threadIdx.x;
+// PACKED: V < 2^16 (the launch picks the form). The histogram is the only sizeable LDS of the
+// workgroup (4 (zcut + 64) bytes); with at most 128 registers four rows share a CU, so a chunk
+// of 2,048 rows runs in two full rounds of 1,024.
+template <bool STATS, bool PACKED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_coder_compact(CompactCoderArgs a) {
+    // LDS: the histogram from address 0 (a bin's byte address is 4 d), then the reduction slots
+    extern __shared__ uint4 lds4[];
+    uint32_t *hist = (uint32_t *)lds4;
     const int V = a.vocab, len = a.table_len, last = len - 1;
     const int zc = a.zcut;
-    const bool packed = V < 65536;
+    constexpr bool packed = PACKED;
+    const int n4 = ((packed ? zc + 64 : 2 * zc) + 3) >> 2;  // histogram words in uint4
+    int64_t *s_i = (int64_t *)(lds4 + n4);
+    uint64_t *s_u = (uint64_t *)(lds4 + n4 + 2);
+    const int row = blockIdx.x, tid = threadIdx.x;
     const uint16_t *d16 = a.d16 + (size_t)row * a.ld16;
     const int64_t *tm = a.tmax + (size_t)row * a.ntiles;
     const uint32_t kind = a.queries ? a.queries[2 * row] : 0;
     const uint32_t value = a.queries ? a.queries[2 * row + 1] : 0;
     const uint32_t tok = kind == 0 && !STATS ? value : 0;  // Encode token (0: no symbol below)
+    // thread 0 of an Encode row needs the token's weight last: its tile max and offset are
+    // loaded first, its table entry as soon as the row max is known
+    const bool tok_lead = !STATS && tid == 0 && kind == 0 && a.intervals;
+    int64_t tok_tm = 0;
+    uint32_t tok_off = 0;
+    if (tok_lead) {
+        tok_tm = tm[tok >> 6];
+        tok_off = d16[tok];
+    }
 
     // The symbol pass reads 8 consecutive symbols per thread and group (one 16-byte load of d16;
     // the 8 share a 64-column tile), four groups per step, and the tile maxes of those groups:
-    // d16 rows are padded to whole tiles, so every load is in range. The loads of a step are
-    // issued one step ahead (the first before the row max), so none waits on another.
+    // d16 rows are padded to whole tiles, so every load is in range. Two register sets take the
+    // steps in turn, each step's loads issued one step ahead (the first before the row max). A
+    // group past the row loads the row's last group instead (no branch around the loads, so a
+    // step waits only for its own loads).
     constexpr int STEP = 4 * 256 * 8;
-    uint4 raw[4];
-    int64_t tmv[4];
-    auto fetch = [&](int g0) {
+    const int last_group = (V - 1) & ~7;
+    auto fetch = [&](uint4 (&raw)[4], int64_t (&tmv)[4], int g0) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int gq = g0 + u * 256 * 8;
-            if (gq < V) {
-                raw[u] = *(const uint4 *)(d16 + gq);
-                tmv[u] = tm[gq >> 6];
-            }
+            const int gc = gq < V ? gq : last_group;
+            raw[u] = *(const uint4 *)(d16 + gc);
+            tmv[u] = tm[gc >> 6];
         }
     };
-    fetch(tid * 8);
+    uint4 ra[4], rb[4];
+    int64_t ta[4], tb[4];
+    // The row max: the tile maxes are loaded first (four per thread at a time, clamped indexes,
+    // no branch), so the max waits for them alone while the first step's groups arrive; the
+    // histogram is cleared meanwhile (the barriers of the max order it before the symbol pass).
     int64_t mx = INT64_MIN;
-    for (int t = tid; t < a.ntiles; t += 256) mx = tm[t] > mx ? tm[t] : mx;
+    for (int t = tid; t < a.ntiles; t += 1024) {
+        int64_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = tm[min(t + 256 * u, a.ntiles - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) mx = v[u] > mx ? v[u] : mx;
+    }
+    fetch(ra, ta, tid * 8);
+    for (int k = tid; k < n4; k += 256) lds4[k] = make_uint4(0, 0, 0, 0);
     const int64_t M = block_max64w(mx, s_i, tid);
-    for (int d = tid; d < (packed ? zc : 2 * zc); d += 256) hist[d] = 0;
+    uint64_t tok_w = 0;
+    if (tok_lead) {
+        const int64_t dt = M - tok_tm + tok_off;
+        tok_w = a.table[dt < last ? dt : last];
+    }
     if (!STATS && a.weights) {  // the weights themselves (run_weights)
         for (int j = tid; j < V; j += 256) {
             const int64_t dd = M - tm[j >> 6] + d16[j];
             a.weights[(size_t)row * V + j] = a.table[dd < last ? dd : last];
         }
     }
-    __syncthreads();
 
-    // A group whose tile max is zcut or more below M has only weight-0 symbols.
     int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0 < zcut)
-    for (int g0 = tid * 8; g0 < V; g0 += STEP) {
-        uint4 cur[4];
-        int64_t b64[4];
+    const unsigned short zl = (unsigned short)(zc + (tid & 63));
+    auto process = [&](const uint4 (&cur)[4], const int64_t (&tmv)[4], int g0) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int gq = g0 + u * 256 * 8;
-            cur[u] = raw[u];
-            b64[u] = gq < V ? M - tmv[u] : (int64_t)zc;
-        }
-        if (g0 + STEP < V) fetch(g0 + STEP);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            if (b64[u] >= zc) continue;
-            const int gq = g0 + u * 256 * 8, base = (int)b64[u];
+            // a group whose tile max is zcut or more below M has only weight-0 symbols
+            const int64_t b64 = gq < V ? M - tmv[u] : (int64_t)zc;
+            if (b64 >= zc) continue;
+            const int base = (int)b64;
             const uint16_t *dv = (const uint16_t *)&cur[u];
-            // per group: all 8 symbols below the Encode token, none, or some; a symbol reaches
-            // the top weight only if the tile's base is at most d0 (d16 >= 0)
-            const bool whole = gq + 8 <= V, all_lo = gq + 8 <= (int)tok, none_lo = gq >= (int)tok;
-            const bool top = base <= a.d0;
-            if (packed && whole && (all_lo || none_lo) && !top) {
-                // two symbols per packed u16 add (saturating) and min: d = min(base + d16,
-                // zc + lane % 64), so the symbols of weight 0 (d >= zc) land in the 64 spare bins
-                // past the weighted ones (never read), each lane in its own, and no symbol needs
-                // a test (base < zc <= 16384)
-                const uint32_t inc = all_lo ? 0x10001u : 1u;
+            if (packed && gq + 8 <= V) {
+                // two symbols per packed u16 add and min: d = min(base + d16, zc + lane % 64)
+                // (base + d16 < 2^15), so the symbols of weight 0 (d >= zc) land in the 64 spare
+                // bins past the weighted ones (never read), each lane in its own, and no symbol
+                // needs a test; the count below the Encode token rides in the high half
                 const us2 bb = {(unsigned short)base, (unsigned short)base};
-                const unsigned short zl = (unsigned short)(zc + (tid & 63));
                 const us2 zz = {zl, zl};
                 const uint32_t *wv = (const uint32_t *)&cur[u];
+                us2 v[4];
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
-                    us2 v;
-                    __builtin_memcpy(&v, &wv[p], 4);
-                    v = __builtin_elementwise_min(__builtin_elementwise_add_sat(v, bb), zz);
-                    atomicAdd(&hist[v.x], inc);
-                    atomicAdd(&hist[v.y], inc);
+                    __builtin_memcpy(&v[p], &wv[p], 4);
+                    v[p] = __builtin_elementwise_min(v[p] + bb, zz);
+                }
+                if (!(gq < (int)tok && (int)tok < gq + 8)) {
+                    const uint32_t inc = gq < (int)tok ? 0x10001u : 1u;
+#pragma unroll
+                    for (int p = 0; p < 4; p++) {
+                        atomicAdd(&hist[v[p].x], inc);
+                        atomicAdd(&hist[v[p].y], inc);
+                    }
+                } else {  // the group of the Encode token
+#pragma unroll
+                    for (int p = 0; p < 4; p++) {
+                        atomicAdd(&hist[v[p].x], gq + 2 * p < (int)tok ? 0x10001u : 1u);
+                        atomicAdd(&hist[v[p].y], gq + 2 * p + 1 < (int)tok ? 0x10001u : 1u);
+                    }
+                }
+                if (base <= a.d0) {  // the top weight needs d <= d0, so base <= d0 (d16 >= 0)
+#pragma unroll
+                    for (int q = 0; q < 8; q++)
+                        if (base + (int)dv[q] <= a.d0 && gq + q < first) first = gq + q;
                 }
                 continue;
             }
@@ -3500,15 +3558,43 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
                 }
             }
         }
+    };
+    for (int s0 = 0; s0 < V; s0 += 2 * STEP) {  // uniform trip count; groups past V are skipped
+        const int g0 = s0 + tid * 8;
+        fetch(rb, tb, g0 + STEP);
+        process(ra, ta, g0);
+        if (s0 + STEP >= V) break;
+        fetch(ra, ta, g0 + 2 * STEP);
+        process(rb, tb, g0 + STEP);
     }
     __syncthreads();
-    const int64_t largest = -block_max64w(-first, s_i, tid);
 
-    // The bins of this thread, 8 at a time: the counts from LDS first, then the table entries of
-    // the nonempty bins (up to 8 loads in flight), then the sums.
-    constexpr int BU = 8;
+    // The weighted bins of this thread: d = tid + 256 k. The first KB (zcut up to 8,192) take
+    // their table entries in one batch of loads (the table holds CODER_TABLE_READ entries; a bin
+    // past zcut has count 0), kept in registers for the S pass; bins from 8,192 on go 8 at a
+    // time, loaded in each pass.
+    // c t = c t_lo + 2^32 c t_hi with t <= 2^40: the low parts accumulate in 64 bits (one
+    // multiply-add each), the high parts (c t_hi <= V 2^8 summed over a thread's bins) in 32.
+    constexpr int KB = 32, BU = 8;
+    static_assert(256 * KB <= CODER_TABLE_READ, "the first bins' entries are read without bounds tests");
+    const int kept = zc < 256 * KB ? zc : 256 * KB;
+    uint64_t tk[KB];
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        const int d = tid + 256 * k;
+        tk[k] = a.table[d];
+    }
     uint64_t W = 0;
-    for (int d0 = tid; d0 < zc; d0 += 256 * BU) {
+    uint32_t w_hi = 0;
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        const int d = tid + 256 * k;
+        const uint32_t h = d < kept ? hist[d] : 0;
+        const uint32_t c = packed ? (h & 0xffffu) : h;
+        W += (uint64_t)c * (uint32_t)tk[k];
+        w_hi += c * (uint32_t)(tk[k] >> 32);
+    }
+    for (int d0 = tid + 256 * KB; d0 < zc; d0 += 256 * BU) {
         uint32_t c[BU];
         uint64_t t[BU];
 #pragma unroll
@@ -3519,9 +3605,25 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
 #pragma unroll
         for (int u = 0; u < BU; u++) t[u] = c[u] ? a.table[d0 + 256 * u] : 0;
 #pragma unroll
-        for (int u = 0; u < BU; u++) W += (uint64_t)c[u] * t[u];
+        for (int u = 0; u < BU; u++) {
+            W += (uint64_t)c[u] * (uint32_t)t[u];
+            w_hi += c[u] * (uint32_t)(t[u] >> 32);
+        }
     }
-    W = block_sum64w(W, s_u, tid);
+    W += (uint64_t)w_hi << 32;
+    // W and the largest (the first symbol of weight table[0]) in one round
+    W = (uint64_t)wave_sum64((int64_t)W);
+    first = -wave_max64(-first);
+    if ((tid & 63) == 0) {
+        s_u[tid >> 6] = W;
+        s_i[tid >> 6] = first;
+    }
+    __syncthreads();
+    W = s_u[0] + s_u[1] + s_u[2] + s_u[3];
+    int64_t largest = s_i[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) largest = s_i[w] < largest ? s_i[w] : largest;
+    __syncthreads();
     if (STATS) {  // mixer.rs:278-288 (W >= table[0] >= 1, so top is the largest)
         if (tid == 0) {
             const uint32_t p = a.mix[row].p;
@@ -3538,16 +3640,69 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
         return;
     }
     const uint64_t total = (uint64_t)1 << a.bits, spare = total - (uint64_t)V;
-    if (tid == 0) s_frac = W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0;
-    __syncthreads();
-    const uint64_t frac = s_frac;
-    // q(d) = floor(table[d] spare / W) < 2^32: v = table[d] R with R = spare / W in double takes
-    // three roundings (W to double, the quotient, the product), |v - q| < 2^32 4 2^-53 = 2^-19;
-    // when v lies at least 2^-18 from an integer, floor(v) is q (1.5 2^52 added rounds v to the
-    // nearest integer, the low word of the sum), else the exact quotient.
+    // q(td) = floor(td spare / W) for a weight td <= W, so q < 2^32: v = td R with R = spare / W
+    // in double takes three roundings (W to double, the quotient, the product),
+    // |v - q| < 2^32 4 2^-53 = 2^-19; when v lies at least 2^-18 from an integer, floor(v) is q
+    // (1.5 2^52 added rounds v to the nearest integer, the low word of the sum), else the exact
+    // quotient, whose 64-bit reciprocal floor(spare 2^64 / W) only the thread that needs it forms.
     const double Rq = (double)spare / (double)W;
+    auto q_of = [&](uint64_t td) -> uint64_t {
+        if (!td) return 0;
+        const double v = (double)td * Rq;
+        const double t = v + 6755399441055744.0;
+        const double dl = v - (t - 6755399441055744.0);
+        if (fabs(dl) >= 0x1p-18) {
+            uint64_t bits;
+            __builtin_memcpy(&bits, &t, sizeof bits);
+            return (uint64_t)(uint32_t)bits - (dl < 0.0 ? 1 : 0);
+        }
+        return quotient(td, spare, W, W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0);
+    };
+    // q for a bin from the double estimate; a live bin (count nonzero) whose estimate lies too
+    // close to an integer is marked instead and takes the exact quotient after the pass (its
+    // entry loaded again), which keeps the unrolled pass small. t <= 2^40 goes to double as
+    // 2^32 t_hi + t_lo (exact).
+    auto q_est = [&](uint64_t td, bool &close) -> uint32_t {
+        const double x = (double)(uint32_t)(td >> 32) * 4294967296.0 + (double)(uint32_t)td;
+        const double v = x * Rq;
+        const double t = v + 6755399441055744.0;
+        const double dl = v - (t - 6755399441055744.0);
+        uint64_t bits;
+        __builtin_memcpy(&bits, &t, sizeof bits);
+        close = !(fabs(dl) >= 0x1p-18);
+        return (uint32_t)bits - (dl < 0.0 ? 1u : 0u);
+    };
     uint64_t S = 0, Slo = 0;
-    for (int d0 = tid; d0 < zc; d0 += 256 * BU) {
+    uint32_t exact = 0;  // bit k: bin tid + 256 k needs the exact quotient
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        const int d = tid + 256 * k;
+        const uint32_t h = d < kept ? hist[d] : 0;
+        const uint32_t c = packed ? (h & 0xffffu) : h;
+        const uint32_t clo = packed ? (h >> 16) : (c ? hist[zc + d] : 0);
+        bool close;
+        const uint32_t q = q_est(tk[k], close);
+        if (close && c) {
+            exact |= 1u << k;
+        } else {
+            S += (uint64_t)c * q;
+            Slo += (uint64_t)clo * q;
+        }
+    }
+    auto add_exact = [&](int d) {
+        const uint32_t h = hist[d];
+        const uint32_t c = packed ? (h & 0xffffu) : h;
+        const uint32_t clo = packed ? (h >> 16) : hist[zc + d];
+        const uint64_t q = quotient(a.table[d], spare, W, W >= ((uint64_t)1 << 32) ? coder_frac(spare, W) : 0);
+        S += (uint64_t)c * q;
+        Slo += (uint64_t)clo * q;
+    };
+    while (exact) {
+        const int k = __builtin_ctz(exact);
+        exact &= exact - 1;
+        add_exact(tid + 256 * k);
+    }
+    for (int d0 = tid + 256 * KB; d0 < zc; d0 += 256 * BU) {
         uint32_t c[BU], clo[BU];
         uint64_t td[BU];
 #pragma unroll
@@ -3559,33 +3714,41 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < BU; u++) td[u] = c[u] ? a.table[d0 + 256 * u] : 0;
+        uint32_t ex = 0;
 #pragma unroll
         for (int u = 0; u < BU; u++) {
-            if (!c[u]) continue;
-            const double v = (double)td[u] * Rq;
-            const double t = v + 6755399441055744.0;
-            const double dl = v - (t - 6755399441055744.0);
-            uint64_t q;
-            if (fabs(dl) >= 0x1p-18) {
-                uint64_t bits;
-                __builtin_memcpy(&bits, &t, sizeof bits);
-                q = (uint64_t)(uint32_t)bits - (dl < 0.0 ? 1 : 0);
+            bool close;
+            const uint32_t q = q_est(td[u], close);
+            if (close && c[u]) {
+                ex |= 1u << u;
             } else {
-                q = quotient(td[u], spare, W, frac);
+                S += (uint64_t)c[u] * q;
+                Slo += (uint64_t)clo[u] * q;
             }
-            S += (uint64_t)c[u] * q;
-            Slo += (uint64_t)clo[u] * q;
+        }
+        while (ex) {
+            const int u = __builtin_ctz(ex);
+            ex &= ex - 1;
+            add_exact(d0 + 256 * u);
         }
     }
-    S = block_sum64w(S, s_u, tid);
-    Slo = block_sum64w(Slo, s_u + 8, tid);
+    // S and Slo in one round
+    S = (uint64_t)wave_sum64((int64_t)S);
+    Slo = (uint64_t)wave_sum64((int64_t)Slo);
+    if ((tid & 63) == 0) {
+        s_u[tid >> 6] = S;
+        s_u[4 + (tid >> 6)] = Slo;
+    }
+    __syncthreads();
+    S = s_u[0] + s_u[1] + s_u[2] + s_u[3];
+    Slo = s_u[4] + s_u[5] + s_u[6] + s_u[7];
+    __syncthreads();
     const uint64_t rem = total - ((uint64_t)V + S);
     uint64_t *out = a.intervals ? a.intervals + 3 * (size_t)row : nullptr;
     if (!out) return;
     if (kind == 0) {
-        if (tid == 0) {
-            const int64_t dt = M - tm[tok >> 6] + d16[tok];
-            const uint64_t f = 1 + quotient(a.table[dt < last ? dt : last], spare, W, frac);
+        if (tok_lead) {
+            const uint64_t f = 1 + q_of(tok_w);
             out[0] = tok;
             out[1] = (uint64_t)tok + Slo + ((int64_t)tok > largest ? rem : 0);
             out[2] = f + ((int64_t)tok == largest ? rem : 0);
@@ -3612,26 +3775,13 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
                 if (j < V) {
                     const int64_t dd = base + dv[q];
                     const int d = (int)(dd < last ? dd : last);
-                    f[q] = 1 + quotient(a.table[d], spare, W, frac) + (j == largest ? rem : 0);
+                    f[q] = 1 + q_of(a.table[d]) + (j == largest ? rem : 0);
                     local += f[q];
                 }
             }
         }
-        s_u[tid] = local;
-        __syncthreads();
-        if (tid == 0) {  // exclusive scan of the 256 partial sums, in order
-            uint64_t acc = run;
-            for (int t = 0; t < 256; t++) {
-                const uint64_t v = s_u[t];
-                s_u[t] = acc;
-                acc += v;
-            }
-            s_i[0] = (int64_t)acc;
-        }
-        __syncthreads();
-        uint64_t start = s_u[tid];
-        const uint64_t next_run = (uint64_t)s_i[0];
-        __syncthreads();
+        uint64_t step_total;
+        uint64_t start = run + block_scan64w(local, s_u, tid, step_total);
         if (j0 < V) {
 #pragma unroll
             for (int q = 0; q < 8; q++) {
@@ -3645,9 +3795,9 @@ __global__ __launch_bounds__(256) void k_coder_compact(CompactCoderArgs a) {
                 start += f[q];
             }
         }
-        run = next_run;
+        run += step_total;
     }
-    const int64_t best = block_max64(cand, s_i, tid);
+    const int64_t best = block_max64w(cand, s_i, tid);
     if (cand >= 0 && cand == best) {
         out[0] = (uint64_t)cand;
         out[1] = cstart;
@@ -3893,8 +4043,11 @@ __global__ __launch_bounds__(256) void k_coder_compact_mixed(CompactCoderArgs a)
 template <typename K>
 static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows <= 0) return hipSuccess;
-    // packed counts: zcut bins and 64 spare bins of the weight-0 symbols; else two arrays
-    const size_t lds = sizeof(uint32_t) * (a.vocab < 65536 ? (size_t)a.zcut + 64 : 2 * (size_t)a.zcut);
+    // packed counts: zcut bins and 64 spare bins of the weight-0 symbols; else two arrays;
+    // rounded up to whole 16-byte words (the kernels clear them so)
+    // (k_coder_compact puts 128 bytes of reduction slots after them)
+    const size_t words = a.vocab < 65536 ? (size_t)a.zcut + 64 : 2 * (size_t)a.zcut;
+    const size_t lds = sizeof(uint32_t) * ((words + 3) & ~(size_t)3) + 128;
     {
         const hipError_t e = allow_dynamic_lds((const void *)kernel, lds);
         if (e != hipSuccess) return e;
@@ -3904,12 +4057,14 @@ static hipError_t launch_compact(K kernel, const CompactCoderArgs &a, int n_rows
 }
 
 hipError_t launch_coder_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
-    return launch_compact(k_coder_compact<false>, a, n_rows, stream);
+    return a.vocab < 65536 ? launch_compact(k_coder_compact<false, true>, a, n_rows, stream)
+                           : launch_compact(k_coder_compact<false, false>, a, n_rows, stream);
 }
 
 hipError_t launch_mix_stats_compact(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
     if (!a.mix || !a.stats) return hipErrorInvalidValue;
-    return launch_compact(k_coder_compact<true>, a, n_rows, stream);
+    return a.vocab < 65536 ? launch_compact(k_coder_compact<true, true>, a, n_rows, stream)
+                           : launch_compact(k_coder_compact<true, false>, a, n_rows, stream);
 }
 
 hipError_t launch_coder_compact_mixed(const CompactCoderArgs &a, int n_rows, hipStream_t stream) {
@@ -3960,7 +4115,7 @@ int kernel_resources(KernelResource *out, int cap) {
         {"k_attend_decode_wave<noclamp, 4>", (const void *)k_attend_decode_wave<true, 4>},
         {"k_split_dots<64>", (const void *)k_split_dots<64>},
         {"k_split_pv<noclamp>", (const void *)k_split_pv<true>},
-        {"k_coder_compact", (const void *)k_coder_compact<false>},
+        {"k_coder_compact", (const void *)k_coder_compact<false, true>},
         {"k_coder_compact_mixed", (const void *)k_coder_compact_mixed},
         {"k_read_bw", (const void *)k_read_bw},
     };
