@@ -2452,6 +2452,20 @@ __device__ __forceinline__ void byte_transpose(uint32_t w0, uint32_t w1, uint32_
     out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
+// p = floor(e 2^P / S) for a table entry e <= S (e < 2^31, S < 2^53, P <= 30), exactly and
+// without a branch: n = round(e R) from one fused multiply-add (1.5 2^52 added rounds to the
+// nearest integer, the low word of the sum) with R = 2^P / S rounded once, so
+// |e R - e 2^P / S| <= 2^30 2^-53 and |n - e 2^P / S| < 1/2 + 2^-22; then p = n, or n - 1 when
+// e 2^P < n S (integers: n S <= e 2^P + S < 2^62).
+__device__ __forceinline__ uint32_t softmax_p_of(uint32_t e, double R, uint32_t s_lo, uint32_t s_hi, int P) {
+    const double w = fma((double)e, R, 6755399441055744.0);
+    uint64_t bits;
+    __builtin_memcpy(&bits, &w, sizeof bits);
+    const uint32_t n = (uint32_t)bits;
+    const uint64_t ns = (uint64_t)n * s_lo + ((uint64_t)(n * s_hi) << 32);
+    return n - (((uint64_t)e << P) < ns ? 1u : 0u);
+}
+
 // NOCLAMP: score_s >= 13, so |dot m| < 2^53 keeps every score within +-2^40 (the clamp is a no-op).
 // LDS_TABLE: attn_exp (<= ATTN_LDS_TABLE entries) is read from a copy in LDS.
 // MULTI: some group has more than AT_SB 64 keys (Q K^T is recomputed per pass); without it the
@@ -2645,22 +2659,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    // p = floor(e 2^P / S) (e <= S, P <= 30): v = e R with R = 2^P / S in double takes two
-    // roundings, |v - e 2^P / S| <= 2^-52 2^30; when v lies at least 2^-21 from an integer its
-    // floor is p (1.5 2^52 added rounds v to the nearest integer, the low word of the sum), and
-    // e = 0 gives v = 0 = p. Otherwise the 64-bit reciprocal floor(2^64 / S) and one correction
-    // (S = 1 divides exactly).
+    // p = floor(e 2^P / S) (softmax_p_of)
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
-    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
-    auto p_exact = [&](uint32_t ev) -> uint32_t {
-        const uint64_t num = (uint64_t)ev << a.softmax_p;
-        uint64_t q = num;
-        if (sum >= 2) {
-            q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
-            if (num - q * sum >= sum) q++;
-        }
-        return (uint32_t)q;
-    };
+    const uint32_t s_lo = (uint32_t)sum, s_hi = (uint32_t)(sum >> 32);
     // pass 3: p, its packed digits, and the digit-plane PV products
     v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
 #pragma unroll
@@ -2704,26 +2705,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         for (int b = 0; b < AT_SB; b++) {
             if (b >= nb) break;
             uint32_t dg[4][4];
-            bool fast_all = true;
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint32_t ev = (uint32_t)S[b][t][e];
-                    const double v = (double)ev * R;
-                    const double tt = v + 6755399441055744.0;
-                    const double dl = v - (tt - 6755399441055744.0);
-                    fast_all &= ev == 0 || fabs(dl) >= 0x1p-21;  // e = 0 (a masked key) gives p = 0
-                    uint64_t bits;
-                    __builtin_memcpy(&bits, &tt, sizeof bits);
-                    dg[t][e] = (uint32_t)bits - (dl < 0.0 ? 1u : 0u);
-                }
-            if (!fast_all) {
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) dg[t][e] = p_exact((uint32_t)S[b][t][e]);
-            }
+                for (int e = 0; e < 4; e++) dg[t][e] = softmax_p_of((uint32_t)S[b][t][e], R, s_lo, s_hi, a.softmax_p);
             v4i pf[4];  // [digit plane]: word t holds the digits of keys 16 t + 4 (l / 16) + e
 #pragma unroll
             for (int t = 0; t < 4; t++) {
@@ -2768,11 +2753,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 //    an i32 and its clamp to [0, last] one med3;
 //  - blocks past the group's keys are skipped, and the causal mask is applied only to the
 //    blocks that some row of the wave does not fully see (a wave-uniform test per block);
-//  - p = floor(e 2^P / S) + 0x80808080 (the packed-digit offset) comes from w = e R + 0x80808080
-//    in double precision: R = 2^P / S and the fused multiply-add take one rounding each, so
-//    |w - (t + 0x80808080)| < 2^-21 for t = e 2^P / S <= 2^30; when w lies at least 2^-20 from
-//    an integer its truncation is exact. e = 0 gives w = 0x80808080 exactly (p = 0). Otherwise
-//    the block takes the 64-bit reciprocal with one correction;
+//  - p = floor(e 2^P / S) is the nearest integer of e R (one fused multiply-add) less one where
+//    e 2^P < n S (softmax_p_of: exact, no branch), and tiles of 16 keys that no row of the wave
+//    sees get p = 0 without it;
 //  - the output rescale floor(v m 2^-s + 1/2), clamped to +-127, is one fused multiply-add in
 //    double precision: v = sum of the four digit-plane products is an exact double (|v| <= 2^30
 //    128 < 2^38 and every partial sum stays below 2^47), so y = v m 2^-s + 1/2 carries one
@@ -2878,9 +2861,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
     AttnGroup Gn = G;
     if (more) Gn = groups[tn / a.n_head];
     // key 64 b + 16 t + 4 qg + e is visible to this lane's row iff 16 t + e <= lim - 64 b - 4 qg;
-    // block b is visible to every row of the wave iff 64 b + 63 <= wlim (uniform)
+    // block b is visible to every row of the wave iff 64 b + 63 <= wlim, and its keys
+    // 64 b + 16 t .. +15 to none iff 64 b + 16 t > wmax (both uniform): such a tile has e = 0
+    // and p = 0 for every row, and the passes skip it
     const int lim = mypos < nk - 1 ? mypos : nk - 1;
     const int wlim = G.pos0 + 16 * w < nk - 1 ? G.pos0 + 16 * w : nk - 1;
+    const int wmax = G.pos0 + 16 * w + 15 < nk - 1 ? G.pos0 + 16 * w + 15 : nk - 1;
     // pass 1: the row max, from the largest and the smallest visible dot
     int32_t dmax = INT32_MIN, dmin = INT32_MAX;
 #pragma unroll
@@ -2897,7 +2883,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
         } else {
             const int L = lim - 64 * b - 4 * qg;
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 4; t++) {
+                if (64 * b + 16 * t > wmax) continue;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const bool ok = 16 * t + e <= L;
@@ -2905,6 +2892,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
                     dmax = hiv > dmax ? hiv : dmax;
                     dmin = lov < dmin ? lov : dmin;
                 }
+            }
         }
     }
 #pragma unroll
@@ -2946,6 +2934,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
+    const uint32_t s_lo = (uint32_t)sum, s_hi = (uint32_t)(sum >> 32);
     // The V^T operand comes straight from the V rows: ds_read_b64_tr_b8 gives lane 8 h + j of each
     // 16-lane group byte j of the 8-byte pieces that lanes h, h + 2, .., h + 14 address. Lane i of
     // group qg addresses key 16 t + 4 qg + e (t = 2 r + i / 8, e = (i / 2) % 4 for read r) at
@@ -2971,31 +2960,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
     for (int b = 0; b < NB; b++) {
         if (b >= nkb) break;
         uint32_t dg[4][4];
-        bool fast_all = true;
+        const bool part = 64 * b + 63 > wlim;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < 4; t++) {
+            if (part && 64 * b + 16 * t > wmax) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t ev = (uint32_t)S[b][t][e];
-                const double wv = fma((double)ev, R, 2155905152.0);
-                const double f = __builtin_amdgcn_fract(wv);
-                fast_all &= ev == 0 || fabs(f - 0.5) <= 0.5 - 0x1p-20;
-                dg[t][e] = (uint32_t)wv;
+                for (int e = 0; e < 4; e++) dg[t][e] = 0x80808080u;  // p = 0
+                continue;
             }
-        if (!fast_all) {
-            const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
 #pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint64_t num = (uint64_t)(uint32_t)S[b][t][e] << a.softmax_p;
-                    uint64_t q = num;
-                    if (sum >= 2) {
-                        q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
-                        if (num - q * sum >= sum) q++;
-                    }
-                    dg[t][e] = (uint32_t)q + 0x80808080u;
-                }
+            for (int e = 0; e < 4; e++)
+                dg[t][e] = softmax_p_of((uint32_t)S[b][t][e], R, s_lo, s_hi, a.softmax_p) + 0x80808080u;
         }
         v4i pf[4];  // [digit plane]: word t holds the digits of keys 16 t + 4 (l / 16) + e
 #pragma unroll
