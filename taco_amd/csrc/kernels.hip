@@ -2782,7 +2782,7 @@ __device__ __forceinline__ int32_t clamp0_uniform(int32_t x, int32_t hi) {
 // task r P + i for even r and r P + P - 1 - i for odd r (P workgroups). The host orders the
 // groups by key count, largest first, so the rounds pair long tasks with short ones. The table
 // is copied once per workgroup; the next task's group loads under the current task's softmax,
-// its K rows and Q fragment as soon as every wave has read the current V rows.
+// its K rows as soon as every wave has read the current V rows (under the output rescale).
 template <int NB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3 : 2))) void k_attend_short(AttnArgs a, const AttnGroup *groups, int n_tasks) {
     // the K rows, then the V rows (as loaded)
@@ -2953,10 +2953,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
     // pass 3: p + 0x80808080 (the packed digits), and the digit-plane PV products
     v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) acc[k][c] = v4i{0, 0, 0, 0};
-#pragma unroll
     for (int b = 0; b < NB; b++) {
         if (b >= nkb) break;
         uint32_t dg[4][4];
@@ -2986,10 +2982,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[c], pf[k], acc[k][c], 0, 0, 0);
+            for (int k = 0; k < 4; k++)  // block 0 (every task has it) starts the sums
+                acc[k][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vf[c], pf[k], b == 0 ? v4i{0, 0, 0, 0} : acc[k][c],
+                                                                  0, 0, 0);
     }
-    if (myrow < G.count) {
+    // Every wave has issued its reads of the V rows: after the barrier sKV takes the next task's
+    // K rows, which load while this task's outputs are formed.
+    const int out_count = G.count, out_first = G.first, out_h = h;
+    if (more) {
+        __syncthreads();
+        G = Gn;
+        h = tn % a.n_head;
+        rows_to_lds(a.kc, ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64, key_blocks(G));
+    }
+    if (myrow < out_count) {
         // rescale: s = 0 keeps v m, a shift above 95 gives 0
         const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
         uint32_t packed[4];
@@ -3028,15 +3034,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
                 }
             }
         }
-        int8_t *o = attn_out(a, G.first + myrow, h * 64);
+        int8_t *o = attn_out(a, out_first + myrow, out_h * 64);
 #pragma unroll
         for (int c = 0; c < 4; c++) *(uint32_t *)(o + 16 * c + 4 * qg) = packed[c];
     }
     if (!more) break;
-    __syncthreads();  // every wave read the V rows: sKV takes the next task's K rows
-    G = Gn;
-    h = tn % a.n_head;
-    rows_to_lds(a.kc, ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64, key_blocks(G));
     qf = q_frag(G, h);
     }
 }
