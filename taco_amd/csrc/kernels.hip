@@ -615,6 +615,10 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
             using L = typename std::conditional<NARROW, int32_t, int64_t>::type;
             using U = typename std::conditional<NARROW, uint32_t, int64_t>::type;
             constexpr L LMIN = NARROW ? (L)INT32_MIN : (L)INT64_MIN;
+            // Only the wave tile holding column N (the last) has columns past it: the others take
+            // a form without the per-logit column test (a wave-uniform choice).
+            const bool full = cw + 64 <= g.n;
+            auto rows = [&](auto FULL) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 L l[4][4], mx = LMIN;
@@ -623,7 +627,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int64_t r = rq(acc[i][j][e], 0, mult[j][e]);
-                        const bool ok = cw + 16 * j + 4 * cg + e < g.n;
+                        const bool ok = FULL || cw + 16 * j + 4 * cg + e < g.n;
                         l[j][e] = ok ? (NARROW ? (L)r : (L)clamp64(r, -SCORE_LIMIT, SCORE_LIMIT)) : LMIN;
                         mx = l[j][e] > mx ? l[j][e] : mx;
                     }
@@ -655,6 +659,9 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                     }
                 }
             }
+            };
+            if (full) rows(std::true_type{});
+            else rows(std::false_type{});
             if (!vec) return;
 #pragma unroll
             for (int q = 0; q < 16; q++) {
