@@ -6,7 +6,11 @@ Default workload: a GPT-2-small-shape integer model in .hsm layout (12 layers, d
 a 16,384-token Zipf(1.1) stream as 64 independent 256-token windows (blocks of 1,024 bytes of
 fixed-width 4-byte tokens) batched on one GPU. One step is one whole fold: the integer forward
 pass of all 16,384 rows, the logits -> CDF coder op on the GPU, the host range coder, the block
-payloads and the .taco container.
+payloads and the .taco container. Two batches are in flight by default (--batches): each folds
+whole steps from its own host thread on its own stream, so one batch's host work and kernels
+overlap the other's kernels; every step's container must equal the first one's. `one_batch`
+is the same steps on a single batch (its wall time, the GPU span of its passes, the host's
+share).
 
 Prints one JSON line. `value` is fold tokens per second with the token stream and the model
 already resident (model upload and token staging are outside the timed region; per step the
@@ -35,6 +39,7 @@ import hashlib
 import json
 import os
 import sys
+import threading
 import time
 
 import numpy as np
@@ -331,58 +336,92 @@ def run_fold(args):
     if args.calib_copy_mib:
         calibration_copy(hip, dev, args.calib_copy_mib)
     model = hip.HipModel.load(dev, model_bytes)
-    batch = hip.HipBatch(model, W, W * n)
-    log(f"device {dev.name()}, model {model.weight_bytes() / 1e6:.1f} MB, batch "
+    # Batches in flight: each folds whole steps from its own host thread on its own stream, so
+    # one batch's host work (plan, inputs, range coding, container) and kernels overlap the
+    # other's kernels. The first batch also runs the one-batch, profiled and unfold parts.
+    nb = max(1, args.batches)
+    batches = [hip.HipBatch(model, W, W * n) for _ in range(nb)]
+    batch = batches[0]
+    log(f"device {dev.name()}, model {model.weight_bytes() / 1e6:.1f} MB, {nb} batch(es) of "
         f"{batch.gpu_bytes() / 1e9:.2f} GB")
 
     phase = {"fold": 0.0, "container": 0.0}
 
-    def step():
+    def step(b=None):
         t0 = time.perf_counter()
-        payloads = fold.fold_blocks(batch, blocks, 0)  # every row runs (no early stop)
+        payloads = fold.fold_blocks(b or batch, blocks, 0)  # every row runs (no early stop)
         t1 = time.perf_counter()
         cont = fold.container(model.hash(), original, block_size, 0, payloads)
         phase["fold"] += t1 - t0
         phase["container"] += time.perf_counter() - t1
         return payloads, cont
 
-    for i in range(args.warmup):
+    def steps_in_flight(k):
+        """k steps over the batches, batch t taking steps t, t + nb, ... on its own thread;
+        returns the wall time and every step's container."""
+        conts, errors = [[] for _ in range(nb)], []
+
+        def run(t):
+            try:
+                for _ in range(t, k, nb):
+                    conts[t].append(step(batches[t])[1])
+            except Exception as e:  # surfaced on the main thread
+                errors.append(e)
+
+        threads = [threading.Thread(target=run, args=(t,)) for t in range(nb)]
+        t0 = time.perf_counter()
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        el = time.perf_counter() - t0
+        if errors:
+            raise errors[0]
+        return el, [c for cs in conts for c in cs]
+
+    for i in range(max(args.warmup, nb)):
         ts = time.time()
-        payloads, cont = step()
+        payloads, cont = step(batches[i % nb])
         log(f"warmup {i}: {time.time() - ts:.3f}s, container {len(cont)} B")
     # The timed steps run without per-launch events (an event pair around every launch costs
     # about 10 us of idle GPU between kernels); the per-op times and the roofline come from the
     # same number of profiled steps right after them.
     # The timed steps record one event pair per forward pass (no per-launch events): the GPU
     # span of the passes, so the host's share of a step is the wall time minus the span.
+    # One batch alone first: its wall time, the GPU span of its passes (one event pair per
+    # pass) and so the host's share of a step.
     phase.update(fold=0.0, container=0.0)
     hip._check(hip.lib().hs_batch_set_profiling(batch.h, 2))
     hip.lib().hs_batch_profile(batch.h, None, None, None, None, 0, 1)
     ts = time.perf_counter()
     for i in range(args.steps):
         payloads, cont = step()
-    elapsed = time.perf_counter() - ts
+    one_elapsed = time.perf_counter() - ts
     span = read_profile(hip, batch).get("pass_span", {"ns": 0, "launches": 0})
     hip._check(hip.lib().hs_batch_set_profiling(batch.h, 0))
     span_ms = span["ns"] / 1e6 / max(1, args.steps)
-    host_ms = 1e3 * elapsed / max(1, args.steps) - span_ms
-    log(f"timed steps: GPU span of the passes {span_ms:.3f} ms per step ({span['launches']} passes), "
-        f"host share {host_ms:.3f} ms per step")
+    host_ms = 1e3 * one_elapsed / max(1, args.steps) - span_ms
+    log(f"one batch: {1e3 * one_elapsed / args.steps:.3f} ms per step; GPU span of the passes "
+        f"{span_ms:.3f} ms per step ({span['launches']} passes), host share {host_ms:.3f} ms per step")
     timed_phase = dict(phase)
+    # The timed steps: the batches in flight
+    elapsed, conts = steps_in_flight(args.steps)
+    if any(c != cont for c in conts):
+        log("PARITY FAILURE: a batch in flight gave another container")
+        sys.exit(1)
+    log(f"timed: {args.steps} steps on {nb} batch(es) in flight: {1e3 * elapsed / args.steps:.3f} ms per step")
     # Sustained: fold steps for at least args.sustain_s seconds right after the timed ones (the
     # timed region is short enough to end before the clocks settle under a sustained MFMA load).
     sustained = None
     if args.sustain_s > 0:
-        ss, ts2 = 0, time.perf_counter()
-        while True:
-            spay, scont = step()
-            ss += 1
-            if time.perf_counter() - ts2 >= args.sustain_s:
-                break
-        s_el = time.perf_counter() - ts2
-        if scont != cont:
-            log("PARITY FAILURE: the sustained steps gave another container")
-            sys.exit(1)
+        ss, s_el = 0, 0.0
+        while s_el < args.sustain_s:
+            el, sconts = steps_in_flight(4 * nb)
+            ss += len(sconts)
+            s_el += el
+            if any(c != cont for c in sconts):
+                log("PARITY FAILURE: the sustained steps gave another container")
+                sys.exit(1)
         sustained = {"seconds": round(s_el, 3), "steps": ss,
                      "tokens_per_s": round(W * n * ss / s_el, 1),
                      "ms_per_step": round(1e3 * s_el / ss, 3)}
@@ -513,7 +552,8 @@ def run_fold(args):
                                f"{n} Zipf(1.1) tokens",
                    "layers": dims.n_layer, "d_model": dims.d_model, "heads": dims.n_head,
                    "d_ff": dims.d_ff, "vocab": dims.vocab, "n_ctx": dims.n_ctx,
-                   "tokens_per_step": tokens_per_step, "container_sha256": cont_sha,
+                   "tokens_per_step": tokens_per_step, "batches_in_flight": nb,
+                   "container_sha256": cont_sha,
                    "tokens_sha256": synth.sha256_tokens(tokens)},
         "roofline": {"bound": "mfma", "kernel": "k_gemm (all int8 GEMMs of the pass)",
                      "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS,
@@ -531,6 +571,10 @@ def run_fold(args):
         "ops_ms_per_step": {kk: round(v["ns"] / 1e6 / psteps, 3) for kk, v in prof.items()},
         "profiled_steps": {"steps": psteps, "ms_per_step": round(1e3 * profiled_s / psteps, 3),
                            "kernel_ms_per_step": round(gpu_ms, 3)},
+        "one_batch": {"ms_per_step": round(1e3 * one_elapsed / args.steps, 3),
+                      "tokens_per_s": round(tokens_per_step * args.steps / one_elapsed, 1),
+                      "gpu_span_ms_per_step": round(span_ms, 3),
+                      "host_ms_per_step": round(host_ms, 3)},
         "gpu_span_ms_per_step": round(span_ms, 3),
         "host_ms_per_step": round(host_ms, 3),
         "sustained": sustained,
@@ -886,8 +930,8 @@ def main():
         return main_mfma(sys.argv[2:])
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--workload", default="fold-gpt2-small",
                     choices=sorted(FOLDS) + ["gemm-qkv", "gemm-vendor", "attend-decode", "issue-rates"])
     ap.add_argument("--windows", type=int, default=0)
@@ -899,6 +943,8 @@ def main():
     ap.add_argument("--sustain-s", type=float, default=3.0,
                     help="seconds of fold steps after the timed ones for the sustained figure")
     ap.add_argument("--no-unfold", action="store_true")
+    ap.add_argument("--batches", type=int, default=2,
+                    help="fold batches in flight, each on its own host thread and stream")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (the known-size copy that "
                          "scales FETCH_SIZE / WRITE_SIZE counters)")
