@@ -1847,6 +1847,31 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
 // the score stays within +-2^40 and the clamp is a no-op.
 __host__ __device__ inline bool attn_noclamp(const AttnArgs &a) { return a.score_s >= 13; }
 
+// p = floor(e 2^P / S) for a table entry e <= S (e < 2^31, S < 2^53, P <= 30), exactly and
+// without a branch: n = round(e R) from one fused multiply-add (1.5 2^52 added rounds to the
+// nearest integer, the low word of the sum) with R = 2^P / S rounded once, so
+// |e R - e 2^P / S| <= 2^30 2^-53 and |n - e 2^P / S| < 1/2 + 2^-22; then p = n, or n - 1 when
+// e 2^P < n S (integers: n S <= e 2^P + S < 2^62).
+__device__ __forceinline__ uint32_t softmax_p_of(uint32_t e, double R, uint32_t s_lo, uint32_t s_hi, int P) {
+    const double w = fma((double)e, R, 6755399441055744.0);
+    uint64_t bits;
+    __builtin_memcpy(&bits, &w, sizeof bits);
+    const uint32_t n = (uint32_t)bits;
+    const uint64_t ns = (uint64_t)n * s_lo + ((uint64_t)(n * s_hi) << 32);
+    return n - (((uint64_t)e << P) < ns ? 1u : 0u);
+}
+
+// The attention output byte clamp(rescale(v, m, s), +-127) for an exact |v| < 2^53 (the sum of
+// p v): y = v m 2^-s + 1/2 in double (mo = m 2^-s, exact; v exact; one rounding in the fused
+// multiply-add, relative 2^-53). When |y| >= 256 the clamp decides; when y lies at least 2^-30
+// from an integer floor(y) is exact (|y| < 256: the error is below 2^-45); else the i128 rule.
+__device__ __forceinline__ int32_t attn_out_byte(int64_t v, double mo, int32_t m, int s) {
+    const double y = fma((double)v, mo, 0.5);
+    const double f = __builtin_amdgcn_fract(y);
+    if (fabs(y) >= 256.0 || fabs(f - 0.5) <= 0.5 - 0x1p-30) return (int32_t)fmin(fmax(y - f, -127.0), 127.0);
+    return (int32_t)clamp128(rescale_full(v, m, s), -127, 127);
+}
+
 template <bool NOCLAMP>
 __device__ __forceinline__ int64_t attn_score(const AttnArgs &a, int32_t dot) {
     const int s_eff = a.score_s < 63 ? a.score_s : 63;
@@ -2146,19 +2171,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     if (lane == 0) s_sum[w] = sum;
     __syncthreads();
     sum = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
-    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+    const double R = ldexp(1.0 / (double)sum, a.softmax_p);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int k = tid + 256 * j;
-        if (k < keys) {
-            const uint64_t num = (uint64_t)e[j] << a.softmax_p;
-            uint64_t q = num;
-            if (sum >= 2) {
-                q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
-                if (num - q * sum >= sum) q++;
-            }
-            s_p[k] = (uint32_t)q;  // <= 2^P <= 2^30
-        }
+        if (k < keys) s_p[k] = softmax_p_of(e[j], R, (uint32_t)sum, (uint32_t)(sum >> 32), a.softmax_p);
     }
     __syncthreads();
     // sum p v: thread t takes channels 16 (t % 4) .. +16 of keys t / 4 + 64 i. p = 2^16 ph + pl
@@ -2196,9 +2213,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         for (int i = 0; i < 16; i++) s_acc[w][16 * lane + i] = acc[i];
     }
     __syncthreads();
-    if (tid < 64) {
+    if (tid < 64) {  // |o| <= 1,024 2^30 2^7 < 2^53
         const int64_t o = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
-        *attn_out(a, r, h * 64 + tid) = (int8_t)clamp128(rescale_full(o, a.out_m, a.out_s), -127, 127);
+        const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
+        *attn_out(a, r, h * 64 + tid) = (int8_t)attn_out_byte(o, mo, a.out_m, a.out_s);
     }
 }
 
@@ -2286,18 +2304,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     }
     sum = (uint64_t)wave_sum64((int64_t)sum);
-    const uint64_t frac = sum >= 2 ? div_2p64(sum) : 0;
+    const double R = ldexp(1.0 / (double)sum, a.softmax_p);
     uint32_t p[KB];
 #pragma unroll
-    for (int j = 0; j < KB; j++) {
-        const uint64_t num = (uint64_t)e[j] << a.softmax_p;
-        uint64_t q = num;
-        if (sum >= 2) {
-            q = __umul64hi(num, frac);  // q <= floor(num / S) <= q + 1
-            if (num - q * sum >= sum) q++;
-        }
-        p[j] = (uint32_t)q;  // <= 2^P <= 2^30; 0 for keys past the row
-    }
+    for (int j = 0; j < KB; j++)  // <= 2^P <= 2^30; 0 for keys past the row (e = 0)
+        p[j] = softmax_p_of(e[j], R, (uint32_t)sum, (uint32_t)(sum >> 32), a.softmax_p);
     wait_vmcnt<0>();  // this wave's V rows landed in its LDS region
     int32_t lo[16], hi[16];
 #pragma unroll
@@ -2324,11 +2335,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (int o = 4; o < 64; o <<= 1) acc[c] += __shfl_xor(acc[c], o, 64);
     }
-    if (lane < 4) {  // lane l holds channels 16 l .. 16 l + 15
+    if (lane < 4) {  // lane l holds channels 16 l .. 16 l + 15 (|acc| <= 256 2^30 2^7 < 2^53)
+        const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
         uint32_t w4[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int c = 0; c < 16; c++) {
-            const uint32_t b = (uint32_t)clamp128(rescale_full(acc[c], a.out_m, a.out_s), -127, 127) & 255;
+            const uint32_t b = (uint32_t)attn_out_byte(acc[c], mo, a.out_m, a.out_s) & 255;
             w4[c >> 2] |= b << (8 * (c & 3));
         }
         int8_t *o = attn_out(a, r, h * 64 + 16 * lane);
@@ -2457,20 +2469,6 @@ __device__ __forceinline__ void byte_transpose(uint32_t w0, uint32_t w1, uint32_
     out[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
     out[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
     out[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-}
-
-// p = floor(e 2^P / S) for a table entry e <= S (e < 2^31, S < 2^53, P <= 30), exactly and
-// without a branch: n = round(e R) from one fused multiply-add (1.5 2^52 added rounds to the
-// nearest integer, the low word of the sum) with R = 2^P / S rounded once, so
-// |e R - e 2^P / S| <= 2^30 2^-53 and |n - e 2^P / S| < 1/2 + 2^-22; then p = n, or n - 1 when
-// e 2^P < n S (integers: n S <= e 2^P + S < 2^62).
-__device__ __forceinline__ uint32_t softmax_p_of(uint32_t e, double R, uint32_t s_lo, uint32_t s_hi, int P) {
-    const double w = fma((double)e, R, 6755399441055744.0);
-    uint64_t bits;
-    __builtin_memcpy(&bits, &w, sizeof bits);
-    const uint32_t n = (uint32_t)bits;
-    const uint64_t ns = (uint64_t)n * s_lo + ((uint64_t)(n * s_hi) << 32);
-    return n - (((uint64_t)e << P) < ns ? 1u : 0u);
 }
 
 // NOCLAMP: score_s >= 13, so |dot m| < 2^53 keeps every score within +-2^40 (the clamp is a no-op).
