@@ -2328,29 +2328,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             hi[c] += ph * (int32_t)v[c];
         }
     }
-    int64_t acc[16];
+    // The 16 lanes of channel group g = lane % 4 (lane bits 2..5) hold partial sums of channels
+    // 16 g .. +16 over disjoint keys. A butterfly halves the channels a lane keeps in each round
+    // (bit 2: channels 8..15 or 0..7 of the 16, then bits 3, 4, 5), so lane l ends with the whole
+    // sum of one channel, 16 g + 8 b2 + 4 b3 + 2 b4 + b5. lo and hi stay i32: over at most 256
+    // keys |sum pl v| <= 256 (2^16 - 1) 128 < 2^31 and |sum ph v| <= 256 2^14 128.
+    auto halve = [&](auto n, int o) {  // n channels -> n / 2
+        const bool up = (lane & o) != 0;
 #pragma unroll
-    for (int c = 0; c < 16; c++) {
-        acc[c] = (int64_t)hi[c] * 65536 + lo[c];
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) acc[c] += __shfl_xor(acc[c], o, 64);
-    }
-    if (lane < 4) {  // lane l holds channels 16 l .. 16 l + 15 (|acc| <= 256 2^30 2^7 < 2^53)
-        const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
-        uint32_t w4[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < 16; c++) {
-            const uint32_t b = (uint32_t)attn_out_byte(acc[c], mo, a.out_m, a.out_s) & 255;
-            w4[c >> 2] |= b << (8 * (c & 3));
+        for (int c = 0; c < n / 2; c++) {
+            const int32_t lk = up ? lo[n / 2 + c] : lo[c], ls = up ? lo[c] : lo[n / 2 + c];
+            const int32_t hk = up ? hi[n / 2 + c] : hi[c], hs = up ? hi[c] : hi[n / 2 + c];
+            lo[c] = lk + __shfl_xor(ls, o, 64);
+            hi[c] = hk + __shfl_xor(hs, o, 64);
         }
-        int8_t *o = attn_out(a, r, h * 64 + 16 * lane);
-        if (((uintptr_t)o & 15) == 0) {
-            *(v4i *)o = v4i{(int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]};
-        } else {
-#pragma unroll
-            for (int c = 0; c < 16; c++) o[c] = (int8_t)(w4[c >> 2] >> (8 * (c & 3)));
-        }
-    }
+    };
+    halve(std::integral_constant<int, 16>{}, 4);
+    halve(std::integral_constant<int, 8>{}, 8);
+    halve(std::integral_constant<int, 4>{}, 16);
+    halve(std::integral_constant<int, 2>{}, 32);
+    const int ch = 16 * (lane & 3) + ((lane >> 2) & 1) * 8 + ((lane >> 3) & 1) * 4 + ((lane >> 4) & 1) * 2 +
+                   ((lane >> 5) & 1);
+    // |acc| <= 256 2^30 2^7 < 2^53
+    const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
+    const int64_t acc = (int64_t)hi[0] * 65536 + lo[0];
+    *attn_out(a, r, h * 64 + ch) = (int8_t)attn_out_byte(acc, mo, a.out_m, a.out_s);
 }
 
 template <bool NOCLAMP>
