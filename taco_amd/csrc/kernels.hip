@@ -2201,17 +2201,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int k = DEC_VLDS + (tid >> 2) + 64 * i;
         if (k < keys) pv(k, vr[i]);
     }
-    int64_t acc[16];
+    // Per wave, a butterfly over the 16 lanes of a channel group (lane bits 2..5) halves the
+    // channels a lane keeps in each round, so lane l ends with the wave's sum of one channel,
+    // 16 (l % 4) + 8 b2 + 4 b3 + 2 b4 + b5. lo and hi stay i32: a wave's 256 keys keep
+    // |sum pl v| <= 256 (2^16 - 1) 128 < 2^31 and |sum ph v| <= 256 2^14 128.
+    auto halve = [&](auto n, int o) {  // n channels -> n / 2
+        const bool up = (lane & o) != 0;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        acc[i] = (int64_t)hi[i] * 65536 + lo[i];
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) acc[i] += __shfl_xor(acc[i], o, 64);
-    }
-    if (lane < 4) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) s_acc[w][16 * lane + i] = acc[i];
-    }
+        for (int c = 0; c < n / 2; c++) {
+            const int32_t lk = up ? lo[n / 2 + c] : lo[c], ls = up ? lo[c] : lo[n / 2 + c];
+            const int32_t hk = up ? hi[n / 2 + c] : hi[c], hs = up ? hi[c] : hi[n / 2 + c];
+            lo[c] = lk + __shfl_xor(ls, o, 64);
+            hi[c] = hk + __shfl_xor(hs, o, 64);
+        }
+    };
+    halve(std::integral_constant<int, 16>{}, 4);
+    halve(std::integral_constant<int, 8>{}, 8);
+    halve(std::integral_constant<int, 4>{}, 16);
+    halve(std::integral_constant<int, 2>{}, 32);
+    s_acc[w][16 * (lane & 3) + ((lane >> 2) & 1) * 8 + ((lane >> 3) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 5) & 1)] =
+        (int64_t)hi[0] * 65536 + lo[0];
     __syncthreads();
     if (tid < 64) {  // |o| <= 1,024 2^30 2^7 < 2^53
         const int64_t o = s_acc[0][tid] + s_acc[1][tid] + s_acc[2][tid] + s_acc[3][tid];
