@@ -143,6 +143,16 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// A workgroup barrier for LDS data only: this wave's LDS operations complete (lgkmcnt 0), then
+// s_barrier, without the wait for every outstanding global load that the release fence of
+// __syncthreads brings. Global data read after it must not depend on other waves' stores.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt 63 and expcnt 7 leave those alone
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // A compile-time flag for the steps of an unrolled loop (the first k-step differs).
 template <bool B>
 struct Flag {
@@ -2059,20 +2069,19 @@ __global__ void k_split_out(AttnArgs a, int n_rows, SplitPlan pl, void *scratch)
 }
 
 // Decode attention for head_dim 64 and at most 1,024 keys in one launch: one workgroup (4 waves)
-// per (row, head). The row's K rows go to registers (thread t: keys t + 256 j), the V rows of its
-// first DEC_VLDS keys to LDS (global_load_lds) and those of the later keys to registers in the
-// layout the p v sums read them (thread t: keys DEC_VLDS + t / 4 + 64 i, chunk t % 4), all in one
-// round of loads; the dots, the row max, the table sum, the weights p and the sums p v then come
-// from registers and LDS with the rules of the split kernels above. Dynamic LDS:
-// min(kmax64, DEC_VLDS) V rows of 64 bytes, then kmax64 = 64 ceil(kmax / 64) weights: at most
-// 36 KiB, so four workgroups fit on a CU (a whole 1,024-key V in LDS, 68 KiB, allowed two;
-// measured at 1,024 keys and 768 row-heads: 34.2 -> 31.0 us).
-constexpr int DEC_VLDS = 512;
+// per (row, head). The row's K rows (thread t: keys t + 256 j) and V rows (in the layout the p v
+// sums read them: thread t, keys t / 4 + 64 i, chunk t % 4) go to registers in one round of
+// loads with no branch around them, K first, so the dots wait for K alone (the compiler counts the
+// in-order loads exactly; with part of V going to LDS by global_load_lds it waited for every
+// load); the dots, the row max, the table sum, the weights p and the sums p v then follow the rules
+// of the split kernels above. Dynamic LDS: the kmax64 = 64 ceil(kmax / 64) weights. 155 VGPRs:
+// three workgroups per CU (768 row-heads in one round). Measured at 1,024 keys and 768 row-heads:
+// 34.2 us with all of V in LDS (two workgroups per CU), 31.0 with half, then 29.8 -> 27.9 with
+// the butterfly reduction.
 template <bool NOCLAMP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attend_decode64(AttnArgs a,
                                                                                                   int kmax) {
     extern __shared__ __attribute__((aligned(16))) int8_t s_dyn[];
-    __shared__ __attribute__((aligned(16))) int s_q[16];
     __shared__ int32_t s_mm[2][4];
     __shared__ uint64_t s_sum[4];
     __shared__ int64_t s_acc[4][64];
@@ -2081,40 +2090,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int kmax64 = (kmax + 63) & ~63;
     int keys = split_keys(a, r);
     keys = keys < kmax ? keys : kmax;  // the launch's bound holds every row's count
-    int8_t *sV = s_dyn;
-    const int vl = kmax64 < DEC_VLDS ? kmax64 : DEC_VLDS;  // the V rows in LDS
-    uint32_t *s_p = (uint32_t *)(s_dyn + (size_t)vl * 64);
+    uint32_t *s_p = (uint32_t *)s_dyn;
     const size_t base = ((size_t)split_slot(a, r) * a.n_head + h) * a.ctx_cap * 64;
-    if (tid < 16) s_q[tid] = ((const int *)(a.q + (size_t)r * a.ldq + h * 64))[tid];
-    // K: up to four keys per thread; a round past the row (uniform) issues nothing, a key past the
-    // row in the last round reloads the row's last key
-    v4i kk[4][4] = {};
+    // q straight into every thread's registers (one 64-byte row, the same for all)
+    int qv[16];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const v4i q4 = ((const v4i *)(a.q + (size_t)r * a.ldq + h * 64))[t];
+#pragma unroll
+        for (int e = 0; e < 4; e++) qv[4 * t + e] = q4[e];
+    }
+    // K: four keys per thread, with no branch around the loads (keys past the row reload the
+    // row's last key and are left out of every sum)
+    v4i kk[4][4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        if (256 * j >= keys) break;
         const int k = tid + 256 * j;
         const v4i *k16 = (const v4i *)(a.kc + base + (size_t)(k < keys ? k : keys - 1) * 64);
 #pragma unroll
         for (int t = 0; t < 4; t++) kk[j][t] = k16[t];
     }
-    // V: per round of 64 keys, wave w loads keys 16 w .. 16 w + 15 (lane l: key + l / 4, bytes
-    // 16 (l % 4)); its 1 KiB lands contiguously, so sV is [key][64]
-    for (int k0 = 0; k0 < keys && k0 < DEC_VLDS; k0 += 64) {
-        int key = k0 + 16 * w + (lane >> 2);
-        key = key < keys ? key : keys - 1;
-        __builtin_amdgcn_global_load_lds((const void *)(a.vc + base + (size_t)key * 64 + 16 * (lane & 3)),
-                                         (lds_void *)(sV + (size_t)(k0 + 16 * w) * 64), 16, 0, 0);
-    }
-    // the V rows of keys DEC_VLDS + tid / 4 + 64 i (chunk tid % 4) into registers
-    constexpr int VR = (1024 - DEC_VLDS) / 64;
+    // V after K (keys past the row reload the row's last key; their weight is 0)
+    constexpr int VR = 1024 / 64;
     v4i vr[VR];
 #pragma unroll
     for (int i = 0; i < VR; i++) {
-        const int k = DEC_VLDS + (tid >> 2) + 64 * i;
-        vr[i] = k < keys ? *(const v4i *)(a.vc + base + (size_t)k * 64 + 16 * (tid & 3)) : v4i{0, 0, 0, 0};
+        const int k = (tid >> 2) + 64 * i;
+        vr[i] = *(const v4i *)(a.vc + base + (size_t)(k < keys ? k : keys - 1) * 64 + 16 * (tid & 3));
     }
-    wait_vmcnt<0>();  // this wave's loads landed (the barrier shows the LDS ones to all)
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait
+    // the dots wait for K alone (the compiler's waits on the K registers)
     int32_t d[4];
     int32_t dmin = INT32_MAX, dmax = INT32_MIN;
 #pragma unroll
@@ -2122,10 +2127,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         int32_t x = 0;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            x = __builtin_amdgcn_sdot4(s_q[4 * t], kk[j][t][0], x, false);
-            x = __builtin_amdgcn_sdot4(s_q[4 * t + 1], kk[j][t][1], x, false);
-            x = __builtin_amdgcn_sdot4(s_q[4 * t + 2], kk[j][t][2], x, false);
-            x = __builtin_amdgcn_sdot4(s_q[4 * t + 3], kk[j][t][3], x, false);
+            x = __builtin_amdgcn_sdot4(qv[4 * t], kk[j][t][0], x, false);
+            x = __builtin_amdgcn_sdot4(qv[4 * t + 1], kk[j][t][1], x, false);
+            x = __builtin_amdgcn_sdot4(qv[4 * t + 2], kk[j][t][2], x, false);
+            x = __builtin_amdgcn_sdot4(qv[4 * t + 3], kk[j][t][3], x, false);
         }
         d[j] = x;
         if (tid + 256 * j < keys) {
@@ -2143,7 +2148,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         s_mm[0][w] = dmin;
         s_mm[1][w] = dmax;
     }
-    __syncthreads();
+    lds_barrier();  // not the fence of __syncthreads, which would wait for the V loads too
     // the row max of the scores: the score is monotone in the dot, so it is the score of the
     // smallest or of the largest dot
     int64_t M = INT64_MIN;
@@ -2195,10 +2200,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             hi[i] += ph * (int32_t)v[i];
         }
     };
-    for (int k = tid >> 2; k < keys && k < DEC_VLDS; k += 64) pv(k, *(const v4i *)(sV + (size_t)k * 64 + 16 * g));
 #pragma unroll
     for (int i = 0; i < VR; i++) {
-        const int k = DEC_VLDS + (tid >> 2) + 64 * i;
+        const int k = (tid >> 2) + 64 * i;
         if (k < keys) pv(k, vr[i]);
     }
     // Per wave, a butterfly over the 16 lanes of a channel group (lane bits 2..5) halves the
@@ -2408,20 +2412,21 @@ hipError_t launch_attend_split(const AttnArgs &a, int n_rows, const SplitPlan &p
     if (n_rows <= 0) return hipSuccess;
     if (!attend_split_ok(a.hd) || p.chunk_keys % 64 != 0 || p.chunk_keys > 4096) return hipErrorInvalidValue;
     const int kmax = p.max_keys < a.ctx_cap ? p.max_keys : a.ctx_cap;
-    // a wave per (row, head) when there are enough of them to fill the CUs (measured: 4,096
-    // row-heads of a GPT-2-medium decode pass 42 -> 37 us per launch; 768 at 128 keys 12 -> 18 us,
-    // so those keep a workgroup per row-head)
-    if (a.hd == 64 && kmax >= 1 && kmax <= 256 && n_rows * a.n_head >= 2048)
+    // a wave per (row, head) up to 256 keys (measured, with the butterfly reduction and the
+    // branch-free weights in both kernels: 768 row-heads at 128 keys 10.7 -> 9.6 us per launch
+    // against a workgroup per row-head; 4,096 row-heads of a GPT-2-medium decode pass 42 -> 37 us
+    // before those changes)
+    if (a.hd == 64 && kmax >= 1 && kmax <= 256)
         return attn_noclamp(a) ? launch_decode_wave<true>(a, n_rows, kmax, stream)
                                : launch_decode_wave<false>(a, n_rows, kmax, stream);
     if (attend_split_one_launch(a.hd, a.ctx_cap, p)) {  // one launch, no scratch
         const int kmax64 = (kmax + 63) & ~63;
         if (kmax64 > 1024) return hipErrorInvalidValue;  // the kernel's register rows end at 1,024 keys
-        const size_t dyn = (size_t)(kmax64 < DEC_VLDS ? kmax64 : DEC_VLDS) * 64 + (size_t)kmax64 * 4;
+        const size_t dyn = (size_t)kmax64 * 4;  // the weights p
         const bool nc = attn_noclamp(a);
         const void *fn = nc ? (const void *)k_attend_decode64<true> : (const void *)k_attend_decode64<false>;
         {
-            const hipError_t e = allow_dynamic_lds(fn, DEC_VLDS * 64 + 4096);
+            const hipError_t e = allow_dynamic_lds(fn, 4096);
             if (e != hipSuccess) return e;
         }
         if (nc) launch_k(k_attend_decode64<true>, dim3(n_rows * a.n_head), dim3(256), dyn, stream, a, kmax);
