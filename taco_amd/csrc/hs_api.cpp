@@ -195,6 +195,7 @@ struct hs_model {
     std::vector<DevBlock> blocks;
     DevLn ln_f;
     int32_t *attn_exp = nullptr;
+    int attn_exp_last = 0;  // > 0: attn_exp[i] == 0 for every i >= attn_exp_last (AttnArgs::exp_last)
     uint64_t *logits_exp = nullptr;
     uint64_t weight_bytes = 0;
     bool compact = false;  // the LM head writes compact logits (table_len <= CODER_MAX_TABLE)
@@ -428,6 +429,11 @@ hs_status upload_model(hs_device *dev, std::unique_ptr<hs_model> &m, hs_model **
     if ((st = upload_ln(mem, h.ln_f, m->ln_f)) != HS_OK) return st;
     // padded to a multiple of 256 entries: the prefill attention loads it in 1 KiB chunks
     if ((st = mem.upload(m->attn_exp, h.attn_exp.data(), h.attn_exp.size(), (h.attn_exp.size() + 255) / 256 * 256)) != HS_OK) return st;
+    {  // the zero tail of attn_exp: the short prefill kernel copies only the entries before it
+        size_t z = h.attn_exp.size();
+        while (z > 0 && h.attn_exp[z - 1] == 0) z--;
+        m->attn_exp_last = z < h.attn_exp.size() ? (int)z : 0;
+    }
     // zero-padded to at least CODER_TABLE_READ entries: the compact coder loads its first bins'
     // entries without bounds tests
     if ((st = mem.upload(m->logits_exp, h.logits_exp.data(), h.logits_exp.size(),
@@ -1105,7 +1111,8 @@ hs_status run_pass(hs_batch &b, const std::vector<PassRow> &rows, Out out, const
         at.rows = b.d_rows; at.q = b.d_qkv; at.ldq = 3 * m.d; at.kc = b.kc[l]; at.vc = b.vc[l];
         at.n_head = m.H; at.hd = m.hd; at.ctx_cap = m.C; at.score_m = blk.score_m; at.score_s = blk.score_s;
         at.out_m = blk.out_m; at.out_s = blk.out_s; at.exp_table = m.attn_exp;
-        at.exp_len = (int)m.host.attn_exp.size(); at.softmax_p = m.host.softmax_p;
+        at.exp_len = (int)m.host.attn_exp.size(); at.exp_last = m.attn_exp_last;
+        at.softmax_p = m.host.softmax_p;
         at.out = b.d_att; at.out_rows = RP;
         HIP_TRY(b.launch("attention", 4ull * attn_keys * (uint64_t)m.d, [&] {
             if (mfma_attn) return hs::launch_attend_groups(at, b.d_groups, n_groups, group_keys, st);

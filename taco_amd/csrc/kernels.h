@@ -166,6 +166,9 @@ struct AttnArgs {
     int out_s = 0;
     const int32_t *exp_table = nullptr;
     int exp_len = 0;
+    // > 0: every entry from exp_last on is 0, so table[min(d, exp_last)] = table[min(d, exp_len - 1)]
+    // (the short prefill kernel copies and indexes table[0 .. exp_last] only); 0: not known
+    int exp_last = 0;
     int softmax_p = 0;
     int8_t *out = nullptr;  // row r, head h at out[r * ldo + h * hd] (out_rows 0)
     int ldo = 0;

@@ -2811,7 +2811,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
     extern __shared__ __attribute__((aligned(1024))) int32_t s_exp[];  // attn_exp
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int last = a.exp_len - 1;
+    // the entries up to the zero tail (exp_last) or the whole table
+    const int last = a.exp_last > 0 ? a.exp_last : a.exp_len - 1;
     const int P = gridDim.x, wg = blockIdx.x;
     auto task_at = [&](int r) { return r * P + ((r & 1) ? P - 1 - wg : wg); };
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
@@ -2843,7 +2844,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
     AttnGroup G = groups[t / a.n_head];
     int h = t % a.n_head;
     rows_to_lds(a.kc, ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64, key_blocks(G));
-    for (int ch = w; ch < (a.exp_len + 255) / 256; ch += 4)  // whole 1 KiB chunks
+    for (int ch = w; ch < (last + 256) / 256; ch += 4)  // whole 1 KiB chunks of entries 0 .. last
         __builtin_amdgcn_global_load_lds((const void *)(a.exp_table + ch * 256 + 4 * lane),
                                          (lds_void *)(s_exp + ch * 256), 16, 0, 0);
     v4i qf = q_frag(G, h);
@@ -3092,7 +3093,9 @@ hipError_t launch_attend_groups(const AttnArgs &a, const AttnGroup *groups, int 
         return hipErrorInvalidValue;
     const bool noclamp = a.score_s >= 13, lds_table = a.exp_len <= ATTN_LDS_TABLE;
     if (lds_table && max_keys <= 8 * 64 && a.score_s >= 22 && a.softmax_p <= 30 && a.out_s >= 0) {
-        const size_t lds = ((size_t)a.exp_len + 255) / 256 * 1024;  // whole 1 KiB chunks
+        // whole 1 KiB chunks of the entries up to the zero tail (or the whole table)
+        const int last = a.exp_last > 0 && a.exp_last < a.exp_len ? a.exp_last : a.exp_len - 1;
+        const size_t lds = ((size_t)last + 256) / 256 * 1024;
         const bool four = max_keys <= 4 * 64;
         const void *fn = four ? (const void *)k_attend_short<4> : (const void *)k_attend_short<8>;
         hipError_t e = allow_dynamic_lds(fn, lds);
