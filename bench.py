@@ -119,7 +119,8 @@ ATTEND_CONTEXTS = ((128, 64), (512, 16), (1024, 8))  # (ctx, cache sets): two la
 def attend_traffic_summary(fetch_csv, write_csv, calib_mib, command):
     """HBM bytes per decode-attention launch at each context of the attend-decode workload, from
     two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE), scaled by the calibration copy. The
-    workload launches the kernel 2 * sets times per context, contexts in order."""
+    workload launches 2 * sets decode-attention kernels per context, contexts in order (the wave
+    per row-head form up to 256 keys, the one-launch form above)."""
     import csv
     import collections
 
@@ -133,20 +134,20 @@ def attend_traffic_summary(fetch_csv, write_csv, calib_mib, command):
     copy_kib = calib_mib * 1024.0
     f_scale = copy_kib / max(v for (k, _), v in fetch.items() if "copyBuffer" in k)
     w_scale = copy_kib / max(v for (k, _), v in write.items() if "copyBuffer" in k)
-    names = {k for (k, _) in fetch if "k_attend_decode64" in k or "k_split_pv" in k}
+    def attn(per):  # the decode-attention dispatches in launch order
+        return [(k, v) for (k, d), v in sorted(per.items(), key=lambda kv: kv[0][1])
+                if "k_attend_decode" in k or "k_split_pv" in k]
+
+    fd, wd = attn(fetch), attn(write)
     out = {}
-    for name in sorted(names):
-        fd = [v for (k, d), v in sorted(fetch.items(), key=lambda kv: kv[0][1]) if k == name]
-        wd = [v for (k, d), v in sorted(write.items(), key=lambda kv: kv[0][1]) if k == name]
-        if len(fd) != sum(2 * sets for _, sets in ATTEND_CONTEXTS) or len(wd) != len(fd):
-            continue
+    if len(fd) == sum(2 * sets for _, sets in ATTEND_CONTEXTS) and len(wd) == len(fd):
         i = 0
         for ctx, sets in ATTEND_CONTEXTS:
             n = 2 * sets
-            out[str(ctx)] = {"kernel": name.split("(")[0].replace("void ", ""), "dispatches": n,
+            out[str(ctx)] = {"kernel": fd[i][0].split("(")[0].replace("void ", ""), "dispatches": n,
                              "algorithmic_bytes": 2 * 64 * 12 * ctx * 64 + 2 * 64 * 12 * 64,
-                             "fetch_bytes": round(sum(fd[i:i + n]) / n * f_scale * 1024),
-                             "write_bytes": round(sum(wd[i:i + n]) / n * w_scale * 1024)}
+                             "fetch_bytes": round(sum(v for _, v in fd[i:i + n]) / n * f_scale * 1024),
+                             "write_bytes": round(sum(v for _, v in wd[i:i + n]) / n * w_scale * 1024)}
             i += n
     return {"library": library_version(), "command": command, "calibration_mib": calib_mib,
             "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "contexts": out}
@@ -864,7 +865,7 @@ def run_attend(args):
         "data": "synthetic",
         "config": {"workload": "decode attention, 64 streams x 12 heads x 64, ctx sweep",
                    "contexts": rows},
-        "roofline": {"bound": "hbm", "kernel": "k_attend_decode64", "achieved": big["gbs"],
+        "roofline": {"bound": "hbm", "kernel": "k_attend_decode64 (1,024 keys)", "achieved": big["gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(big["gbs"] / HBM_PEAK_GBS, 4),
                      "stream_read_gbs": round(stream, 1),
@@ -891,7 +892,7 @@ def main_traffic(argv):
     dims_name, W, n, _ = FOLDS[workload]
     tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
     cmd = (f"rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -- python3 bench.py "
-           f"--workload {workload} --steps 1 --warmup 0 --no-cpu --calib-copy-mib {calib}")
+           f"--workload {workload} --steps 1 --warmup 0 --no-cpu --batches 1 --calib-copy-mib {calib}")
     print(json.dumps(traffic_summary(fetch_csv, write_csv, int(calib), tokens_sha, cmd), indent=1))
 
 
@@ -904,7 +905,7 @@ def main_mfma(argv):
     tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
     cmd = ("rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE "
            "SQ_BUSY_CYCLES --output-format csv -- python3 bench.py --workload " + workload +
-           " --steps 1 --warmup 0 --no-cpu --no-unfold --sustain-s 0")
+           " --steps 1 --warmup 0 --no-cpu --no-unfold --sustain-s 0 --batches 1")
     print(json.dumps(mfma_summary(csv_path, tokens_sha, cmd), indent=1))
 
 
@@ -917,7 +918,8 @@ def main_sq(argv):
     dims_name, W, n, _ = FOLDS[workload]
     tokens_sha = synth.sha256_tokens(synth.zipf_tokens(W * n))
     cmd = " ; ".join("rocprofv3 --pmc " + " ".join(p) + " --output-format csv -- python3 bench.py --workload "
-                     + workload + " --steps 1 --warmup 0 --no-cpu --no-unfold --sustain-s 0" for p in SQ_PASSES)
+                     + workload + " --steps 1 --warmup 0 --no-cpu --no-unfold --sustain-s 0 --batches 1"
+                     for p in SQ_PASSES)
     print(json.dumps(sq_summary([a_csv, b_csv], tokens_sha, cmd), indent=1))
 
 
