@@ -820,19 +820,17 @@ def run_attend(args):
             caches.append((kc, vc, _dev_buf(hip, dev, kc), _dev_buf(hip, dev, vc)))
         out = np.zeros((B, H * hd), np.int8)
         dout = _dev_buf(hip, dev, out)
-        total, reps = 0, 0
         ns = C.c_uint64()
-        for r in range(2 * sets):  # one launch per set in turn: every launch reads cold caches
-            kc, vc, dk, dv = caches[r % sets]
-            hip._check(hip.lib().hs_op_attend_decode_gpu_ns(
-                dev.h, dq, dk, dv, dctx, B, H, hd, ctx, score_m, score_s, out_m, out_s, dtab,
-                len(table), 30, dout, 1, C.byref(ns)))
-            if r >= sets:  # the first round warms up
-                total += ns.value
-                reps += 1
+        dks = (C.c_void_p * sets)(*[c[2] for c in caches])
+        dvs = (C.c_void_p * sets)(*[c[3] for c in caches])
+        for r in range(2):  # one launch per set in turn, back to back: every launch reads cold
+            hip._check(hip.lib().hs_op_attend_decode_sets_gpu_ns(  # caches; round 0 warms up
+                dev.h, dq, dks, dvs, sets, dctx, B, H, hd, ctx, score_m, score_s, out_m, out_s,
+                dtab, len(table), 30, dout, C.byref(ns)))
+        total, reps = ns.value, sets
         hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
                                                 out.nbytes))
-        kc, vc = caches[(2 * sets - 1) % sets][:2]
+        kc, vc = caches[sets - 1][:2]  # the last launch wrote out
         ts = time.perf_counter()
         want = O.attend_decode_ref(q, kc, vc, ctxs, score_m, score_s, out_m, out_s, table, 30)
         cpu_s = time.perf_counter() - ts

@@ -338,6 +338,28 @@ unsafe extern "C" {
         reps: usize,
         ns: *mut u64,
     ) -> c_int;
+    /// No counterpart in the reference: one timed launch on each of `sets` cache sets in turn.
+    pub fn hs_op_attend_decode_sets_gpu_ns(
+        dev: *mut hs_device,
+        q: *const i8,
+        k_caches: *const *const i8,
+        v_caches: *const *const i8,
+        sets: usize,
+        ctx: *const u32,
+        b: usize,
+        h: usize,
+        hd: usize,
+        ctx_cap: usize,
+        score_m: i32,
+        score_s: u8,
+        out_m: i32,
+        out_s: u8,
+        attn_exp: *const i32,
+        len: usize,
+        softmax_p: u8,
+        out: *mut i8,
+        ns: *mut u64,
+    ) -> c_int;
     pub fn hs_read_bw(dev: *mut hs_device, bytes: usize, reps: usize, ns: *mut u64) -> c_int;
     /// No counterpart in the reference: the VALU / MFMA issue-rate probe.
     pub fn hs_probe_issue(dev: *mut hs_device, op: u32, waves_per_simd: u32, iters: u32, ns: *mut u64) -> c_int;

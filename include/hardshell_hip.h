@@ -310,6 +310,20 @@ hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q, const int8
                                      uint8_t score_s, int32_t out_m, uint8_t out_s,
                                      const int32_t *attn_exp, size_t len, uint8_t softmax_p,
                                      int8_t *out, size_t reps, uint64_t *ns);
+/* The GPU time of `sets` launches of hs_op_attend_decode_dev, one on each cache set in turn
+ * (k_caches[i], v_caches[i]: device caches of set i, each [b][h][ctx_cap][hd]), back to back on
+ * the device stream between one hipEvent pair. No counterpart in the reference (a measurement
+ * entry, as read_gpu_ns, crates/hardshell-cuda/src/ops.rs:328-335): launches over distinct
+ * caches read HBM rather than the Infinity Cache, and the events' own cost is shared by all the
+ * launches instead of falling on each. */
+hs_status hs_op_attend_decode_sets_gpu_ns(hs_device *dev, const int8_t *q,
+                                          const int8_t *const *k_caches,
+                                          const int8_t *const *v_caches, size_t sets,
+                                          const uint32_t *ctx, size_t b, size_t h, size_t hd,
+                                          size_t ctx_cap, int32_t score_m, uint8_t score_s,
+                                          int32_t out_m, uint8_t out_s, const int32_t *attn_exp,
+                                          size_t len, uint8_t softmax_p, int8_t *out,
+                                          uint64_t *ns);
 
 /* The GPU time of `reps` reads of a device buffer of `bytes` bytes (a multiple of 16) by a
  * streaming kernel (hipEvents on the device stream): the HBM read bandwidth a kernel reaches,

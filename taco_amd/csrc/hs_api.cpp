@@ -1834,6 +1834,49 @@ extern "C" hs_status hs_op_attend_decode_gpu_ns(hs_device *dev, const int8_t *q,
     return time_reps(dev, reps, ns, [&] { return hs::launch_attend(at, (int)b, dev->stream); });
 }
 
+extern "C" hs_status hs_op_attend_decode_sets_gpu_ns(
+    hs_device *dev, const int8_t *q, const int8_t *const *k_caches, const int8_t *const *v_caches,
+    size_t sets, const uint32_t *ctx, size_t b, size_t h, size_t hd, size_t ctx_cap, int32_t score_m,
+    uint8_t score_s, int32_t out_m, uint8_t out_s, const int32_t *attn_exp, size_t len,
+    uint8_t softmax_p, int8_t *out, uint64_t *ns) {
+    hs::clear_error();
+    if (!dev || !q || !k_caches || !v_caches || !ctx || !attn_exp || !out)
+        return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");
+    if (sets == 0) return hs::fail(HS_INVALID_ARGUMENT, 0, "no cache sets");
+    for (size_t i = 0; i < sets; i++)
+        if (!k_caches[i] || !v_caches[i]) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL cache");
+    if (hd == 0 || hd % 4 != 0 || hd > 256 || h == 0 || len == 0 || softmax_p > 30 || ctx_cap == 0 || b == 0)
+        return hs::fail(HS_UNSUPPORTED, 0, "bad attention shape");
+    hs::AttnArgs at;
+    at.rows = nullptr; at.keys = ctx; at.q = q; at.ldq = (int)(h * hd);
+    at.n_head = (int)h; at.hd = (int)hd; at.ctx_cap = (int)ctx_cap; at.score_m = score_m;
+    at.score_s = score_s; at.out_m = out_m; at.out_s = out_s; at.exp_table = attn_exp;
+    at.exp_len = (int)len; at.softmax_p = softmax_p; at.out = out; at.ldo = (int)(h * hd);
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    size_t next = 0;  // the launches take the sets in turn, one each
+    auto use_next = [&] {
+        at.kc = k_caches[next];
+        at.vc = v_caches[next];
+        next++;
+    };
+    if (hs::attend_split_ok((int)hd)) {
+        const hs::SplitPlan plan = hs::attend_split_plan((int)b, (int)h, (int)ctx_cap);
+        const size_t bytes = hs::attend_split_bytes(at, (int)b, plan);
+        void *scratch = nullptr;
+        if (bytes) HIP_TRY(hipMalloc(&scratch, bytes));
+        const hs_status st = time_reps(dev, sets, ns, [&] {
+            use_next();
+            return hs::launch_attend_split(at, (int)b, plan, scratch, dev->stream);
+        });
+        if (scratch) (void)hipFree(scratch);
+        return st;
+    }
+    return time_reps(dev, sets, ns, [&] {
+        use_next();
+        return hs::launch_attend(at, (int)b, dev->stream);
+    });
+}
+
 extern "C" hs_status hs_device_alloc(hs_device *dev, size_t bytes, void **out) {
     hs::clear_error();
     if (!dev || !out) return hs::fail(HS_INVALID_ARGUMENT, 0, "NULL argument");

@@ -175,6 +175,9 @@ def lib() -> C.CDLL:
         L.hs_op_attend_decode_gpu_ns.argtypes = [P, P, P, P, P, S, S, S, S, C.c_int32,
                                                  C.c_uint8, C.c_int32, C.c_uint8, P, S,
                                                  C.c_uint8, P, S, C.POINTER(U64)]
+        L.hs_op_attend_decode_sets_gpu_ns.argtypes = [P, P, P, P, S, P, S, S, S, S, C.c_int32,
+                                                      C.c_uint8, C.c_int32, C.c_uint8, P, S,
+                                                      C.c_uint8, P, C.POINTER(U64)]
         L.hs_batch_set_profiling.argtypes = [P, C.c_int]
         L.hs_batch_profile.restype = S
         L.hs_batch_profile.argtypes = [P, P, P, P, P, S, C.c_int]

@@ -135,6 +135,46 @@ def test_attend_decode_at_the_benchmark_shape(dev, ctx_len):
         assert np.array_equal(out, want)
 
 
+@pytest.mark.parametrize("ctx_len", [128, 1024])
+def test_attend_decode_sets_timing(dev, ctx_len):
+    """hs_op_attend_decode_sets_gpu_ns (the attend-decode bench's timing: one launch per cache set,
+    back to back) launches on every set in turn: the output is the last set's attention, and a
+    call with no sets is refused."""
+    from taco_amd import hip
+    r = np.random.default_rng(7 + ctx_len)
+    B, H, hd, sets = 64, 12, 64, 3
+    q = r.integers(-127, 128, (B, H, hd)).astype(np.int8)
+    ctx = r.integers(1, ctx_len + 1, B).astype(np.uint32)
+    table = np.array([round(2 ** 30 * np.exp(-i / 256)) for i in range(8192)], np.int32)
+    score_m, score_s, out_m, out_s = 1_400_000_000, 34, 1_300_000_000, 53
+    caches = [(r.integers(-127, 128, (B, H, ctx_len, hd)).astype(np.int8),
+               r.integers(-127, 128, (B, H, ctx_len, hd)).astype(np.int8)) for _ in range(sets)]
+    bufs = [_dev_buf(dev, a) for a in (q, ctx, table)]
+    cbufs = [(_dev_buf(dev, k), _dev_buf(dev, v)) for k, v in caches]
+    out = np.zeros((B, H * hd), np.int8)
+    dout = _dev_buf(dev, out)
+    dks = (C.c_void_p * sets)(*[k for k, _ in cbufs])
+    dvs = (C.c_void_p * sets)(*[v for _, v in cbufs])
+    ns = C.c_uint64()
+    try:
+        hip._check(hip.lib().hs_op_attend_decode_sets_gpu_ns(
+            dev.h, bufs[0], dks, dvs, sets, bufs[1], B, H, hd, ctx_len, score_m, score_s, out_m,
+            out_s, bufs[2], len(table), 30, dout, C.byref(ns)))
+        hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                out.nbytes))
+        st = hip.lib().hs_op_attend_decode_sets_gpu_ns(
+            dev.h, bufs[0], dks, dvs, 0, bufs[1], B, H, hd, ctx_len, score_m, score_s, out_m,
+            out_s, bufs[2], len(table), 30, dout, C.byref(ns))
+    finally:
+        for p in bufs + [dout] + [p for kv in cbufs for p in kv]:
+            hip.lib().hs_device_free(dev.h, p)
+    want = O.attend_decode_ref(q, caches[-1][0], caches[-1][1], ctx, score_m, score_s, out_m,
+                               out_s, table, 30)
+    assert np.array_equal(out, want)
+    assert ns.value > 0
+    assert st == hip.HS_INVALID_ARGUMENT
+
+
 @pytest.mark.parametrize("B,H,ctx_len", [(256, 12, 200), (200, 16, 64), (171, 12, 256)])
 def test_attend_decode_wave_per_head(dev, B, H, ctx_len):
     """Decode attention with at least 2,048 row-heads and at most 256 keys (a GPT-2-medium
