@@ -1515,37 +1515,54 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(LnArgs a, int n_rows) {
     }
 }
 
-// Four rows per wave, 16 lanes per row (d % 4 == 0, d <= 64 NG <= 1024): the per-row work (the
-// lane reductions, mean, ln_inv) runs for four rows in one instruction stream, over 4 butterfly
-// steps of 16 lanes. Lane q of a row holds columns 4 (q + 16 t) .. +4 for t < NG. beta and gamma
-// (the same columns for every row) are copied into LDS once per workgroup while x loads.
+// Four rows per wave, 16 lanes per row (d % 4 == 0, d <= 64 NG <= 1024), 64 rows per workgroup
+// of 16 waves. Lane q of a row holds columns 4 (q + 16 t) .. +4 for t < NG. Each row's sums
+// (the 16 lanes' partials over 4 butterfly steps) go to LDS; then wave 0 forms mean, ln_inv and
+// the rule's per-row terms for all 64 rows, one row per lane (not once per four rows in every
+// wave: that per-row work is about 700 instructions of 128-bit integer and double arithmetic), and
+// every wave reads its rows' terms back for the element rule. beta and gamma (the same columns
+// for every row) are copied into LDS once per workgroup.
+// Every load is unconditional, from a clamped address (a row past n_rows reads the last row, a
+// column past d the last group; neither value is used): no branch around the loads.
 // The input is the residual stream (|x| <= RES = 2^30 - 1): every square is below 2^60, so the
 // four of a group sum in i64 without a carry.
 // F32 (8-bit outputs, beta_frac 0, |beta| <= 256): each element takes the single-precision rule
 // (ln_elem_f32, with beta folded into the addend); declined groups take the integer rule, as in
 // the double-precision form.
-// Waves per workgroup of the four-rows-per-wave form: 16 (64 rows) so the beta and gamma staging
-// of a workgroup serves four times the rows of a 4-wave workgroup.
 constexpr int LN_WAVES = 16;
 
 template <int NG, bool F32>
 __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int n_rows) {
+    constexpr int NT = 64 * LN_WAVES, CI = (64 * NG + NT - 1) / NT, RW = 4 * LN_WAVES;
     __shared__ __attribute__((aligned(16))) int32_t s_beta[64 * NG];
     __shared__ __attribute__((aligned(16))) double s_gamma[F32 ? 1 : 64 * NG];
     __shared__ __attribute__((aligned(16))) float s_gammaf[F32 ? 64 * NG : 1];
     __shared__ __attribute__((aligned(16))) float s_betaf[F32 ? 64 * NG : 1];  // 1/2 + beta
+    // per row of the workgroup: the sums, then the rule's terms
+    __shared__ int64_t s_sum[RW];
+    __shared__ uint64_t s_lo[RW], s_hi[RW];
+    __shared__ int32_t s_mx[RW], s_mn[RW];
+    __shared__ int64_t s_mean[RW];
+    __shared__ uint64_t s_inv[RW];
+    __shared__ double s_kr[RW];
+    __shared__ uint32_t s_flags[RW];  // bit 0 small, bit 1 fast
     const int lane = threadIdx.x & 63, q = lane & 15;
-    const int row = (blockIdx.x * LN_WAVES + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const int rw = (threadIdx.x >> 6) * 4 + (lane >> 4);  // the lane's row in the workgroup
+    const int row = blockIdx.x * RW + rw;
     const bool live = row < n_rows;
     const int d = a.d;
-    const int32_t *x = a.x + (size_t)(live ? (a.src ? a.src[row] : row) : 0) * d;
+    const int rc = live ? row : n_rows - 1;
+    const int32_t *x = a.x + (size_t)(a.src ? a.src[rc] : rc) * d;
     v4i xv[NG];
 #pragma unroll
     for (int t = 0; t < NG; t++) {
         const int j = 4 * (q + 16 * t);
-        xv[t] = (live && j < d) ? *(const v4i *)(x + j) : v4i{0, 0, 0, 0};
+        xv[t] = *(const v4i *)(x + (j < d ? j : d - 4));
     }
-    for (int c = threadIdx.x; c < d; c += 64 * LN_WAVES) {  // gamma as doubles or floats (exact)
+#pragma unroll
+    for (int i = 0; i < CI; i++) {  // gamma as doubles or floats (exact)
+        const int c = threadIdx.x + NT * i;
+        if (c >= d) continue;
         s_beta[c] = a.beta[c];
         if (F32) {
             s_gammaf[c] = (float)a.gamma[c];
@@ -1556,47 +1573,69 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
     }
     // squares: the four of a group to an i64 partial (each < 2^60), the partials into a 128-bit
     // lo/hi with carries
-    int64_t sum = 0;
-    uint64_t lo = 0, hi = 0;
-    int32_t mx = INT32_MIN, mn = INT32_MAX;
+    {
+        int64_t sum = 0;
+        uint64_t lo = 0, hi = 0;
+        int32_t mx = INT32_MIN, mn = INT32_MAX;
 #pragma unroll
-    for (int t = 0; t < NG; t++) {
-        const int j = 4 * (q + 16 * t);
-        if (j >= d) continue;
-        int64_t part = 0;
+        for (int t = 0; t < NG; t++) {
+            const int j = 4 * (q + 16 * t);
+            if (j >= d) continue;
+            int64_t part = 0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int32_t v = xv[t][e];
-            sum += v;
-            part += (int64_t)v * v;
-            mx = v > mx ? v : mx;
-            mn = v < mn ? v : mn;
+            for (int e = 0; e < 4; e++) {
+                const int32_t v = xv[t][e];
+                sum += v;
+                part += (int64_t)v * v;
+                mx = v > mx ? v : mx;
+                mn = v < mn ? v : mn;
+            }
+            lo += (uint64_t)part;
+            hi += lo < (uint64_t)part;
         }
-        lo += (uint64_t)part;
-        hi += lo < (uint64_t)part;
-    }
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes of this row
-        sum += __shfl_xor(sum, o, 64);
-        const uint64_t lo2 = __shfl_xor(lo, o, 64), hi2 = __shfl_xor(hi, o, 64);
-        lo += lo2;
-        hi += hi2 + (lo < lo2);
-        const int32_t mx2 = __shfl_xor(mx, o, 64), mn2 = __shfl_xor(mn, o, 64);
-        mx = mx2 > mx ? mx2 : mx;
-        mn = mn2 < mn ? mn2 : mn;
+        for (int o = 1; o < 16; o <<= 1) {  // the 16 lanes of this row
+            sum += __shfl_xor(sum, o, 64);
+            const uint64_t lo2 = __shfl_xor(lo, o, 64), hi2 = __shfl_xor(hi, o, 64);
+            lo += lo2;
+            hi += hi2 + (lo < lo2);
+            const int32_t mx2 = __shfl_xor(mx, o, 64), mn2 = __shfl_xor(mn, o, 64);
+            mx = mx2 > mx ? mx2 : mx;
+            mn = mn2 < mn ? mn2 : mn;
+        }
+        if (q == 0) {
+            s_sum[rw] = sum;
+            s_lo[rw] = lo;
+            s_hi[rw] = hi;
+            s_mx[rw] = mx;
+            s_mn[rw] = mn;
+        }
     }
-    __syncthreads();  // beta and gamma are in LDS
+    lds_barrier();  // the rows' sums, beta and gamma are in LDS
+    const double inv_d = 1.0 / (double)d;  // |sum| <= d RES < 2^52, sq < d 2^62: the estimate forms
+    if (threadIdx.x < RW) {  // wave 0: row threadIdx.x of the workgroup
+        const int r = threadIdx.x;
+        const int64_t sum = s_sum[r];
+        const u128 Q = ((u128)s_hi[r] << 64) | s_lo[r];
+        const int64_t mean = floor_div_est(sum, d, inv_d);
+        const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
+        const uint64_t inv = ln_inv_est(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps, inv_d);
+        const int64_t c1 = (int64_t)s_mx[r] - mean, c2 = mean - (int64_t)s_mn[r];
+        const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
+        const bool small = (u128)cmax * inv < ((u128)1 << 63);
+        const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
+        s_mean[r] = mean;
+        s_inv[r] = inv;
+        s_kr[r] = ldexp((double)inv * (double)a.m, -a.s);
+        s_flags[r] = (small ? 1u : 0u) | (fast ? 2u : 0u);
+    }
+    lds_barrier();  // the rows' terms are in LDS
     if (!live) return;
     const bool wide = a.bits == 16;
-    const u128 Q = ((u128)hi << 64) | lo;
-    const double inv_d = 1.0 / (double)d;  // |sum| <= d RES < 2^52, sq < d 2^62: the estimate forms
-    const int64_t mean = floor_div_est(sum, d, inv_d);
-    const u128 sq = (u128)((i128)Q - 2 * (i128)mean * sum + (i128)d * mean * mean);
-    const uint64_t inv = ln_inv_est(sq, (uint32_t)d, (uint32_t)a.k, (uint32_t)a.j, a.eps, inv_d);
-    const int64_t c1 = (int64_t)mx - mean, c2 = mean - (int64_t)mn;
-    const uint64_t cmax = (uint64_t)(c1 > c2 ? c1 : c2);
-    const bool small = (u128)cmax * inv < ((u128)1 << 63);
-    const bool fast = small && a.beta_frac == 0 && a.s >= 64 && a.s <= 126;
+    const int64_t mean = s_mean[rw];
+    const uint64_t inv = s_inv[rw];
+    const uint32_t flags = s_flags[rw];
+    const bool small = flags & 1, fast = (flags >> 1) & 1;
     // the operand rows of this row (two planes when wide), in panels (panel_off); a wave's four
     // rows are adjacent in every panel, so each store instruction writes 256 contiguous bytes
     const size_t orow = (size_t)row * (wide ? 2 : 1);
@@ -1606,7 +1645,7 @@ __global__ __launch_bounds__(64 * LN_WAVES) void k_layernorm_rows4(LnArgs a, int
     // element are then recomputed by the integer rule and stored again (the same lane rewrites
     // its own bytes, in order).
     const bool fpath = a.beta_frac == 0 && a.s <= 126;
-    const double kr = ldexp((double)inv * (double)a.m, -a.s);
+    const double kr = s_kr[rw];
     const int32_t lim = wide ? 32767 : 127;
     const int32_t mean32 = (int32_t)mean;  // |x|, |mean| < 2^30, so x - mean fits i32
     auto put = [&](int j, const int32_t *y) {
@@ -1700,12 +1739,15 @@ hipError_t launch_layernorm(const LnArgs &a, int n_rows, hipStream_t stream) {
     if (n_rows < 4096 && a.d % 4 == 0 && a.d <= 2048) {
         if (a.d <= 1024) launch_k(k_layernorm_rows<4>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
         else launch_k(k_layernorm_rows<8>, dim3(n_rows), dim3(64), 0, stream, a, n_rows);
-    } else if (a.d % 4 == 0 && a.d <= 768) {
-        if (f32) launch_k((k_layernorm_rows4<12, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
-        else launch_k((k_layernorm_rows4<12, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
     } else if (a.d % 4 == 0 && a.d <= 1024) {
-        if (f32) launch_k((k_layernorm_rows4<16, true>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
-        else launch_k((k_layernorm_rows4<16, false>), dim3((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), dim3(64 * LN_WAVES), 0, stream, a, n_rows);
+        const dim3 g4((n_rows + 4 * LN_WAVES - 1) / (4 * LN_WAVES)), b4(64 * LN_WAVES);
+        if (a.d <= 768) {
+            if (f32) launch_k((k_layernorm_rows4<12, true>), g4, b4, 0, stream, a, n_rows);
+            else launch_k((k_layernorm_rows4<12, false>), g4, b4, 0, stream, a, n_rows);
+        } else {
+            if (f32) launch_k((k_layernorm_rows4<16, true>), g4, b4, 0, stream, a, n_rows);
+            else launch_k((k_layernorm_rows4<16, false>), g4, b4, 0, stream, a, n_rows);
+        }
     } else if (a.d % 4 == 0 && a.d <= 2048) {
         launch_k(k_layernorm_rows<8>, grid, dim3(256), 0, stream, a, n_rows);
     } else {
