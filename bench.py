@@ -6,9 +6,9 @@ Default workload: a GPT-2-small-shape integer model in .hsm layout (12 layers, d
 a 16,384-token Zipf(1.1) stream as 64 independent 256-token windows (blocks of 1,024 bytes of
 fixed-width 4-byte tokens) batched on one GPU. One step is one whole fold: the integer forward
 pass of all 16,384 rows, the logits -> CDF coder op on the GPU, the host range coder, the block
-payloads and the .taco container. Two batches are in flight by default (--batches): each folds
+payloads and the .taco container. Four batches are in flight by default (--batches): each folds
 whole steps from its own host thread on its own stream, so one batch's host work and kernels
-overlap the other's kernels; every step's container must equal the first one's. `one_batch`
+overlap the others' kernels; every step's container must equal the first one's. `one_batch`
 is the same steps on a single batch (its wall time, the GPU span of its passes, the host's
 share).
 
@@ -943,7 +943,7 @@ def main():
     ap.add_argument("--sustain-s", type=float, default=3.0,
                     help="seconds of fold steps after the timed ones for the sustained figure")
     ap.add_argument("--no-unfold", action="store_true")
-    ap.add_argument("--batches", type=int, default=2,
+    ap.add_argument("--batches", type=int, default=4,
                     help="fold batches in flight, each on its own host thread and stream")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (the known-size copy that "
