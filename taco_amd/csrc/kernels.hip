@@ -711,6 +711,29 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         constexpr int RS8 = 16 * TJ + 16, Q8 = TI * TJ / 4;
         static_assert(16 * TI * RS8 <= 10240 && Q8 * 64 == 16 * TI * TJ, "i8 staging");
         int8_t *wr = gemm_lds + toff + wave * 10240;
+        // Act with the caches: when TJ divides 64, the lane's 16-column piece of every row it
+        // stores, cw + 16 (lane % TJ), is the same for each of its Q8 rows, so whether it goes to
+        // K or V, its head and the offset in the head are found once; the rows' slots and
+        // positions load before the staging (their latency under the packing). Other TJ (the
+        // 128 x 192 tiles) find them per row.
+        constexpr bool KV_LANE = 64 % TJ == 0;
+        const int n_l = cw + 16 * (lane % TJ);
+        const bool to_kv = KV_LANE && EPI == (int)Epi::Act && vec && g.kv_rows && n_l >= g.kv_d;
+        int8_t *kv_base = nullptr;
+        int kv_slot[Q8], kv_pos[Q8];
+        if (to_kv) {
+            const int part = n_l >= 2 * g.kv_d, c = n_l - (part + 1) * g.kv_d;
+            const int hh = c / g.kv_hd, cc = c - hh * g.kv_hd;
+            kv_base = (part ? g.vc : g.kc) + (size_t)hh * g.kv_ctx * g.kv_hd + cc;
+#pragma unroll
+            for (int q = 0; q < Q8; q++) {
+                const int m = rw + (q * 64 + lane) / TJ;
+                const RowInfo ri = g.kv_rows[m < g.m ? m : g.m - 1];
+                kv_slot[q] = ri.slot;
+                kv_pos[q] = ri.pos;
+            }
+        }
+        const size_t kv_slot_stride = (size_t)g.kv_h * g.kv_ctx * g.kv_hd;
         // GeluWide: the hi plane of every row, then the lo plane (this wave's region is rewritten
         // only after its own reads: LDS operations of a wave stay in order)
         constexpr int PLANES = EPI == (int)Epi::GeluWide ? 2 : 1;
@@ -765,9 +788,14 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                 const v4i v = *(const v4i *)(wr + rl2 * RS8 + cl);
                 const int m = rw + rl2, n = cw + cl;
                 if (m >= g.m) continue;
-                if (EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
+                if (to_kv) {
                     // K or V of the row straight into the cache (kv_d, kv_hd multiples of 16);
                     // the columns past N = 3 kv_d are padding and go nowhere
+                    if (n + 16 > g.n) continue;
+                    *(v4i *)(kv_base + (size_t)kv_slot[q] * kv_slot_stride + (size_t)kv_pos[q] * g.kv_hd) = v;
+                    continue;
+                }
+                if (!KV_LANE && EPI == (int)Epi::Act && g.kv_rows && n >= g.kv_d) {
                     if (n + 16 > g.n) continue;
                     const RowInfo ri = g.kv_rows[m];
                     const int part = n >= 2 * g.kv_d, c = n - (part + 1) * g.kv_d;
