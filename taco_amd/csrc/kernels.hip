@@ -741,7 +741,7 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         for (int pl = 0; pl < PLANES; pl++) {
             auto byte_of = [&](int32_t v) -> uint32_t {
                 if (EPI == (int)Epi::GeluWide) return (uint32_t)(pl == 0 ? v >> 8 : (v & 255) - 128) & 255;
-                return (uint32_t)v & 255;
+                return (uint32_t)v;  // the low byte is packed
             };
             if (!vec) {  // unaligned output rows: one byte store per output
 #pragma unroll
@@ -779,7 +779,11 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                     for (int e = 0; e < 4; e++)
                         b[e] = EPI == (int)Epi::Gelu ? (uint32_t)(uint8_t)(GELU_LDS ? gemm_lds[acc[i][j][e]] : gspan[acc[i][j][e]])
                                                      : byte_of(acc[i][j][e]);
-                    *(uint32_t *)(wr + (16 * i + rl) * RS8 + 16 * j + 4 * cg) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+                    // the low bytes of b[0..3] packed by three byte permutes: [b0 b1 0 0],
+                    // [b2 b3 0 0], then their low halves side by side
+                    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u);
+                    const uint32_t hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+                    *(uint32_t *)(wr + (16 * i + rl) * RS8 + 16 * j + 4 * cg) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
                     if (EPI == (int)Epi::Gelu && j == TJ - 1) asm volatile("" ::: "memory");  // 4 TJ lookups in flight at most
                 }
 #pragma unroll
