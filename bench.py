@@ -6,7 +6,8 @@ Default workload: a GPT-2-small-shape integer model in .hsm layout (12 layers, d
 a 16,384-token Zipf(1.1) stream as 64 independent 256-token windows (blocks of 1,024 bytes of
 fixed-width 4-byte tokens) batched on one GPU. One step is one whole fold: the integer forward
 pass of all 16,384 rows, the logits -> CDF coder op on the GPU, the host range coder, the block
-payloads and the .taco container. Four batches are in flight by default (--batches): each folds
+payloads and the .taco container. Four batches are in flight by default (--batches; fewer when
+they would not fit in three quarters of the device memory): each folds
 whole steps from its own host thread on its own stream, so one batch's host work and kernels
 overlap the others' kernels; every step's container must equal the first one's. `one_batch`
 is the same steps on a single batch (its wall time, the GPU span of its passes, the host's
@@ -340,8 +341,13 @@ def run_fold(args):
     # Batches in flight: each folds whole steps from its own host thread on its own stream, so
     # one batch's host work (plan, inputs, range coding, container) and kernels overlap the
     # other's kernels. The first batch also runs the one-batch, profiled and unfold parts.
-    nb = max(1, args.batches)
-    batches = [hip.HipBatch(model, W, W * n) for _ in range(nb)]
+    # The batches beyond the first are made while they fit in three quarters of the device
+    # memory left (the GPT-2-XL workload's caches take about 80 GB per batch).
+    batches = [hip.HipBatch(model, W, W * n)]
+    per_batch = batches[0].gpu_bytes()
+    while len(batches) < max(1, args.batches) and per_batch <= 0.75 * dev.memory()[0]:
+        batches.append(hip.HipBatch(model, W, W * n))
+    nb = len(batches)
     batch = batches[0]
     log(f"device {dev.name()}, model {model.weight_bytes() / 1e6:.1f} MB, {nb} batch(es) of "
         f"{batch.gpu_bytes() / 1e9:.2f} GB")
