@@ -425,9 +425,23 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         // basic block and no wait for them lands before the MFMAs; the empty asm keeps the
         // compiler from sinking them into the next step (where they would wait at its barrier)
         read_frags(more ? kt + 1 : kt, na, nb);
-        asm volatile("" ::: "memory");
         if constexpr (decltype(first_tag)::value) mfma_first(ca, cb);
         else mfma_step(ca, cb);
+        // The step's order: two MFMAs, then one fragment read of the next step, repeated, then
+        // the remaining MFMAs. Opening with MFMAs keeps the wait that precedes the first of them
+        // from landing after a read; spreading the reads keeps the LDS busy under the MFMAs (the
+        // compiler left them after 24 of 32 MFMAs, or all before with a wait on the first).
+        constexpr int NR = TI + TJ;
+        if constexpr (2 * NR <= TI * TJ) {
+#pragma unroll
+            for (int z = 0; z < NR; z++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ - 2 * NR, 0);
+        } else {
+            asm volatile("" ::: "memory");
+        }
     };
     v4i fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     read_frags(0, fa0, fb0);
