@@ -3588,6 +3588,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 
     int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0 < zcut)
     const unsigned short zl = (unsigned short)(zc + (tid & 63));
+    // the packed path forms bin byte addresses in 16 bits: 4 (zc + 63) < 2^16 (other tables
+    // take the per-symbol path)
+    const bool addr16 = zc <= 16320;
     auto process = [&](const uint4 (&cur)[4], const int64_t (&tmv)[4], int g0) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -3597,7 +3600,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             if (b64 >= zc) continue;
             const int base = (int)b64;
             const uint16_t *dv = (const uint16_t *)&cur[u];
-            if (packed && gq + 8 <= V) {
+            if (packed && addr16 && gq + 8 <= V) {
                 // two symbols per packed u16 add and min: d = min(base + d16, zc + lane % 64)
                 // (base + d16 < 2^15), so the symbols of weight 0 (d >= zc) land in the 64 spare
                 // bins past the weighted ones (never read), each lane in its own, and no symbol
@@ -3605,24 +3608,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
                 const us2 bb = {(unsigned short)base, (unsigned short)base};
                 const us2 zz = {zl, zl};
                 const uint32_t *wv = (const uint32_t *)&cur[u];
+                // then both bins' byte addresses in one packed shift (4 d <= 4 (zc + 63) < 2^16)
                 us2 v[4];
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     __builtin_memcpy(&v[p], &wv[p], 4);
-                    v[p] = __builtin_elementwise_min(v[p] + bb, zz);
+                    v[p] = __builtin_elementwise_min(v[p] + bb, zz) << (unsigned short)2;
                 }
+                uint8_t *hb = (uint8_t *)hist;
+                auto bin = [&](unsigned short byte) { return (uint32_t *)(hb + byte); };
                 if (!(gq < (int)tok && (int)tok < gq + 8)) {
                     const uint32_t inc = gq < (int)tok ? 0x10001u : 1u;
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
-                        atomicAdd(&hist[v[p].x], inc);
-                        atomicAdd(&hist[v[p].y], inc);
+                        atomicAdd(bin(v[p].x), inc);
+                        atomicAdd(bin(v[p].y), inc);
                     }
                 } else {  // the group of the Encode token
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
-                        atomicAdd(&hist[v[p].x], gq + 2 * p < (int)tok ? 0x10001u : 1u);
-                        atomicAdd(&hist[v[p].y], gq + 2 * p + 1 < (int)tok ? 0x10001u : 1u);
+                        atomicAdd(bin(v[p].x), gq + 2 * p < (int)tok ? 0x10001u : 1u);
+                        atomicAdd(bin(v[p].y), gq + 2 * p + 1 < (int)tok ? 0x10001u : 1u);
                     }
                 }
                 if (base <= a.d0) {  // the top weight needs d <= d0, so base <= d0 (d16 >= 0)
