@@ -1361,9 +1361,44 @@ __global__ void k_embed(const RowInfo *rows, const int8_t *wte, int wte_rows, co
     x[(size_t)r * d + j] = (int32_t)clamp64(v, -RES, RES);
 }
 
+// d % 4 == 0: one wave per row, each lane four consecutive columns at a time (one 4-byte load
+// of each table: the four lie in one panel of wte; one 16-byte store). |w m| < 2^38, so the
+// rescale is one i64 multiply-add and shift, exactly shift_round64's result.
+__global__ __launch_bounds__(256) void k_embed4(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_rows,
+                                                const int8_t *wpe, const int32_t *embed_m, int embed_s,
+                                                const int32_t *pos_m, int pos_s, int d, int32_t *x) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= n_rows) return;
+    const RowInfo ri = rows[r];
+    const int64_t em = embed_m[ri.token], pm = pos_m[ri.pos];
+    auto rs = [](int64_t p, int s) -> int64_t {  // shift_round64 for |p| < 2^62
+        if (s == 0) return p;
+        if (s >= 64) return 0;
+        return (p + ((int64_t)1 << (s - 1))) >> s;
+    };
+    for (int j = 4 * lane; j < d; j += 256) {
+        const uint32_t tw = *(const uint32_t *)(wte + panel_off(ri.token, j, wte_rows));
+        const uint32_t pw = *(const uint32_t *)(wpe + (size_t)ri.pos * d + j);
+        v4i o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int64_t v = rs((int64_t)(int8_t)(tw >> (8 * e)) * em, embed_s) +
+                              rs((int64_t)(int8_t)(pw >> (8 * e)) * pm, pos_s);
+            o[e] = (int32_t)clamp64(v, -RES, RES);
+        }
+        *(v4i *)(x + (size_t)r * d + j) = o;
+    }
+}
+
 hipError_t launch_embed(const RowInfo *rows, int n_rows, const int8_t *wte, int wte_rows,
                         const int8_t *wpe, const int32_t *embed_m, int embed_s,
                         const int32_t *pos_m, int pos_s, int d, int32_t *x, hipStream_t stream) {
+    if (n_rows <= 0) return hipSuccess;
+    if (d % 4 == 0) {
+        launch_k(k_embed4, dim3((n_rows + 3) / 4), dim3(256), 0, stream, rows, n_rows, wte, wte_rows, wpe,
+                 embed_m, embed_s, pos_m, pos_s, d, x);
+        return hipGetLastError();
+    }
     dim3 grid(n_rows, (d + 255) / 256);
     launch_k(k_embed, grid, dim3(256), 0, stream, rows, wte, wte_rows, wpe, embed_m,
                        embed_s, pos_m, pos_s, d, x);
@@ -4196,6 +4231,7 @@ int kernel_resources(KernelResource *out, int cap) {
         {"k_split_epi<Act>", (const void *)k_split_epi<1>},
         {"k_split_epi<Residual>", (const void *)k_split_epi<2>},
         {"k_embed", (const void *)k_embed},
+        {"k_embed4", (const void *)k_embed4},
         {"k_layernorm", (const void *)k_layernorm},
         {"k_layernorm_rows<4>", (const void *)k_layernorm_rows<4>},
         {"k_layernorm_rows<8>", (const void *)k_layernorm_rows<8>},
