@@ -3541,9 +3541,10 @@ __device__ __forceinline__ uint64_t block_scan64w(uint64_t v, uint64_t *s4, int 
 }
 
 // One row per workgroup. The histogram counts the symbols of each table index d < zcut (the
-// bins with a nonzero weight); with V < 2^16 the count and the count below the Encode token
-// share one u32 (low and high half), else they are two arrays. Symbols with d >= zcut have
-// weight 0, f = 1 and no share of the spare, and need no count.
+// bins with a nonzero weight; a symbol's index is min(d, len - 1)); with V < 2^16 the count and
+// the count below the Encode token share one u32 (low and high half), else they are two arrays.
+// When the table ends in zeros (zcut < len), symbols with d >= zcut have weight 0, f = 1 and no
+// share of the spare, and need no count; else (zcut = len) every symbol has a bin.
 // STATS: the mixer statistics of the row (sum w, w[p] for the record's p, the top token = the
 // largest) instead of the coder interval.
 // PACKED: V < 2^16 (the launch picks the form). The histogram is the only sizeable LDS of the
@@ -3621,25 +3622,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         }
     }
 
-    int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0 < zcut)
-    const unsigned short zl = (unsigned short)(zc + (tid & 63));
-    // the packed path forms bin byte addresses in 16 bits: 4 (zc + 63) < 2^16 (other tables
-    // take the per-symbol path)
-    const bool addr16 = zc <= 16320;
+    int64_t first = INT64_MAX;  // the first symbol with weight table[0] (d <= d0)
+    // A symbol's index is min(d, last) (logits.rs:62-72). tail0: the table ends in zeros, so
+    // every d >= zcut weighs 0 (no count needed); else (zcut = len) every d >= last weighs
+    // table[last] and counts in the last bin, and no group can be skipped.
+    const bool tail0 = zc < len;
+    const unsigned short zl = (unsigned short)(tail0 ? zc + (tid & 63) : last);
+    // the packed path forms bin byte addresses in 16 bits: 4 zl < 2^16 (other tables take the
+    // per-symbol path)
+    const bool addr16 = tail0 ? zc <= 16320 : last <= 16383;
     auto process = [&](const uint4 (&cur)[4], const int64_t (&tmv)[4], int g0) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int gq = g0 + u * 256 * 8;
-            // a group whose tile max is zcut or more below M has only weight-0 symbols
-            const int64_t b64 = gq < V ? M - tmv[u] : (int64_t)zc;
-            if (b64 >= zc) continue;
-            const int base = (int)b64;
+            // with tail0, a group whose tile max is zcut or more below M has only weight-0
+            // symbols; else its symbols' indexes start at min(M - tile max, last)
+            if (gq >= V) continue;
+            const int64_t b64 = M - tmv[u];
+            if (tail0 && b64 >= zc) continue;
+            const int base = (int)(b64 < last ? b64 : last);
             const uint16_t *dv = (const uint16_t *)&cur[u];
             if (packed && addr16 && gq + 8 <= V) {
-                // two symbols per packed u16 add and min: d = min(base + d16, zc + lane % 64)
-                // (base + d16 < 2^15), so the symbols of weight 0 (d >= zc) land in the 64 spare
-                // bins past the weighted ones (never read), each lane in its own, and no symbol
-                // needs a test; the count below the Encode token rides in the high half
+                // two symbols per packed u16 add and min: d = min(base + d16, zl) (base + d16 <
+                // 2^15): with tail0 the symbols of weight 0 (d >= zc) land in the 64 spare bins
+                // past the weighted ones (never read), each lane in its own, else d >= last lands
+                // in the last bin, and no symbol needs a test; the count below the Encode token
+                // rides in the high half
                 const us2 bb = {(unsigned short)base, (unsigned short)base};
                 const us2 zz = {zl, zl};
                 const uint32_t *wv = (const uint32_t *)&cur[u];
@@ -3666,18 +3674,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
                         atomicAdd(bin(v[p].y), gq + 2 * p + 1 < (int)tok ? 0x10001u : 1u);
                     }
                 }
-                if (base <= a.d0) {  // the top weight needs d <= d0, so base <= d0 (d16 >= 0)
+                if (base <= a.d0) {  // the top weight needs min(d, last) <= d0, so base <= d0
 #pragma unroll
-                    for (int q = 0; q < 8; q++)
-                        if (base + (int)dv[q] <= a.d0 && gq + q < first) first = gq + q;
+                    for (int q = 0; q < 8; q++) {
+                        const int dq = base + (int)dv[q];
+                        if ((dq < last ? dq : last) <= a.d0 && gq + q < first) first = gq + q;
+                    }
                 }
                 continue;
             }
 #pragma unroll
             for (int q = 0; q < 8; q++) {
                 const int j = gq + q;
-                const int dd = base + (int)dv[q];
-                if (j < V && dd < zc) {  // then dd <= last: d = dd
+                const int dd = base + (int)dv[q] < last ? base + (int)dv[q] : last;
+                if (j < V && dd < zc) {
                     if (packed) {
                         atomicAdd(&hist[dd], (uint32_t)j < tok ? 0x10001u : 1u);
                     } else {
@@ -3938,8 +3948,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // The mixed coder op over compact logits: k_coder_compact with the weights of each row's mix
 // record (mixer.rs:256-292, 491-516). The histogram leaves out the predicted token p; the
 // weight of bin d is g(d) = max(1, (table[d] m) >> k) (max(1, table[d]) without a prediction,
-// table[d] for a plain row), non-increasing in d, and every symbol with d >= zcut (table 0)
-// weighs g_rest = 1 (0 for a plain row), counted as V - (p) - the binned symbols. Then
+// table[d] for a plain row), non-increasing in d, and every symbol with d >= zcut (table 0; a
+// symbol's index is min(d, len - 1), so with zcut = len there are none) weighs g_rest = 1 (0
+// for a plain row), counted as V - (p) - the binned symbols. Then
 //   W' = sum_d cnt[d] g(d) + n_rest g_rest + w'[p],
 //   sum_{j<tok} f = tok + sum_d cnt_lo[d] q(g(d)) + rest_lo q(g_rest) + [p < tok] q(w'[p]).
 // The largest weight of the others is g of their smallest bin; the first symbol other than p
@@ -3979,24 +3990,29 @@ __global__ __launch_bounds__(256) void k_coder_compact_mixed(CompactCoderArgs a)
     for (int d = tid; d < (packed ? zc : 2 * zc); d += 256) hist[d] = 0;
     __syncthreads();
     int64_t first = INT64_MAX;  // plain rows: the first symbol with weight table[0]
+    // A symbol's index is min(d, last) (logits.rs:62-72): with a zero tail (zcut < len) every
+    // d >= zcut is in the rest; else every d >= last counts in the last bin and no group skips.
+    const bool tail0 = zc < len;
     for (int g0 = tid * 8; g0 < V; g0 += 4 * 256 * 8) {
         uint4 raw[4];
         int64_t b64[4];
+        bool live[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int gq = g0 + u * 256 * 8;
             b64[u] = gq < V ? M - tm[gq >> 6] : (int64_t)zc;
-            if (b64[u] < zc) raw[u] = *(const uint4 *)(d16 + gq);
+            live[u] = gq < V && !(tail0 && b64[u] >= zc);
+            if (live[u]) raw[u] = *(const uint4 *)(d16 + gq);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            if (b64[u] >= zc) continue;
-            const int gq = g0 + u * 256 * 8, base = (int)b64[u];
+            if (!live[u]) continue;
+            const int gq = g0 + u * 256 * 8, base = (int)(b64[u] < last ? b64[u] : last);
             const uint16_t *dv = (const uint16_t *)&raw[u];
 #pragma unroll
             for (int q = 0; q < 8; q++) {
                 const int j = gq + q;
-                const int dd = base + (int)dv[q];
+                const int dd = base + (int)dv[q] < last ? base + (int)dv[q] : last;
                 if (j < V && dd < zc && (uint32_t)j != p) {
                     if (packed) {
                         atomicAdd(&hist[dd], (uint32_t)j < tok ? 0x10001u : 1u);

@@ -240,6 +240,8 @@ def _table(kind):
         t = [1 << 40] * 5 + [round(2 ** 40 * np.exp(-i / 64)) for i in range(1, 3000)]
     elif kind == "short":  # 40 entries, the last ones 0 (zcut < len)
         t = [max(0, (1 << 36) - i * (1 << 31)) for i in range(40)]
+    elif kind == "notail":  # no zero tail: every d >= len - 1 weighs the last entry
+        t = [round(2 ** 40 * np.exp(-i / 1024)) for i in range(4096)]
     elif kind == "long":  # longer than the compact form: the i64 kernels
         t = [round(2 ** 40 * np.exp(-i / 256)) for i in range(20000)]
     else:
@@ -248,7 +250,8 @@ def _table(kind):
 
 
 @pytest.mark.parametrize("vocab,kind", [(300, "exp"), (50257, "exp"), (1000, "flat"), (257, "short"),
-                                        (1000, "long"), (70000, "exp")])
+                                        (1000, "long"), (70000, "exp"), (1000, "notail"),
+                                        (50257, "notail")])
 def test_mixed_op_on_logits_equals_the_cpu_table(dev, vocab, kind):
     # The compact (d16) and i64 sources of the statistics and mixed kernels on rows built to
     # reach their corners: the prediction as the unique argmax (the best other weight then comes

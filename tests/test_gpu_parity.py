@@ -417,6 +417,13 @@ def _coder_cases():
     # a short table and a table with a flat start (ties among weights for different logits)
     t2 = np.array([1 << 40, 1 << 40, 1 << 39, 5, 1], np.uint64)
     cases.append((700, r.integers(-8, 8, (4, 700)).astype(np.int64), t2))
+    # tables of 16,300 and 16,384 weighted entries: the packed histogram forms its bins' byte
+    # addresses in 16 bits up to 16,320 weighted bins, and takes the per-symbol path above
+    for L in (16300, 16384):
+        t4 = np.array([round(2 ** 40 * np.exp(-i / 4096)) for i in range(L)], np.uint64)
+        l4 = r.integers(-20000, 20000, (4, 50257)).astype(np.int64)
+        l4[2, [7, 50000]] = 30000  # a tie at the maximum
+        cases.append((50257, l4, t4))
     # a table longer than the compact form allows (the i64 logits kernel)
     t3 = np.array([round(2 ** 40 * np.exp(-i / 2048)) for i in range(20000)], np.uint64)
     l3 = r.integers(-30000, 30000, (6, 3000)).astype(np.int64)
