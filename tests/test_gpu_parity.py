@@ -395,6 +395,38 @@ def test_attend_decode_op(dev, ctx_cap, hd, score_s):
     assert np.array_equal(out, want)
 
 
+@pytest.mark.parametrize("ctx_cap,hd", [(200, 64), (1024, 64), (512, 128), (320, 48)])
+def test_attend_decode_table_without_zero_tail(dev, ctx_cap, hd):
+    """A 300-entry table whose last entry is nonzero: every key past the table weighs the last
+    entry (the index is min(M - score, len - 1), softmax.rs:78-104), through the wave-per-row-head,
+    one-launch, split-key and row kernels."""
+    import ctypes as C
+    from taco_amd import hip
+    r = np.random.default_rng(17 + hd)
+    B, H = 8, 12
+    q = r.integers(-127, 128, (B, H, hd)).astype(np.int8)
+    kc = r.integers(-127, 128, (B, H, ctx_cap, hd)).astype(np.int8)
+    vc = r.integers(-127, 128, (B, H, ctx_cap, hd)).astype(np.int8)
+    ctx = np.array([1, 2, 63, 64, 65, 128, ctx_cap - 20, ctx_cap], np.uint32)
+    table = np.array([round(2 ** 30 * np.exp(-i / 64)) for i in range(300)], np.int32)
+    assert table[-1] > 0
+    score_m, score_s, out_m, out_s = 1_400_000_000, 36, 1_300_000_000, 53
+    want = O.attend_decode_ref(q, kc, vc, ctx, score_m, score_s, out_m, out_s, table, 30)
+    bufs = [_dev_buf(dev, a) for a in (q, kc, vc, ctx, table)]
+    out = np.zeros((B, H * hd), np.int8)
+    dout = _dev_buf(dev, out)
+    try:
+        hip._check(hip.lib().hs_op_attend_decode_dev(
+            dev.h, bufs[0], bufs[1], bufs[2], bufs[3], B, H, hd, ctx_cap, score_m, score_s,
+            out_m, out_s, bufs[4], len(table), 30, dout, None))
+        hip._check(hip.lib().hs_device_download(dev.h, out.ctypes.data_as(C.c_void_p), dout,
+                                                out.nbytes))
+    finally:
+        for p in bufs + [dout]:
+            hip.lib().hs_device_free(dev.h, p)
+    assert np.array_equal(out, want)
+
+
 def _coder_cases():
     r = np.random.default_rng(11)
     cases = []
