@@ -251,7 +251,7 @@ def _table(kind):
 
 @pytest.mark.parametrize("vocab,kind", [(300, "exp"), (50257, "exp"), (1000, "flat"), (257, "short"),
                                         (1000, "long"), (70000, "exp"), (1000, "notail"),
-                                        (50257, "notail")])
+                                        (50257, "notail"), (70000, "notail")])
 def test_mixed_op_on_logits_equals_the_cpu_table(dev, vocab, kind):
     # The compact (d16) and i64 sources of the statistics and mixed kernels on rows built to
     # reach their corners: the prediction as the unique argmax (the best other weight then comes

@@ -456,6 +456,9 @@ def _coder_cases():
         l4 = r.integers(-20000, 20000, (4, 50257)).astype(np.int64)
         l4[2, [7, 50000]] = 30000  # a tie at the maximum
         cases.append((50257, l4, t4))
+    # the unpacked compact form (V >= 2^16) on a table without a zero tail
+    t5 = np.array([round(2 ** 40 * np.exp(-i / 1024)) for i in range(4096)], np.uint64)
+    cases.append((70000, r.integers(-9000, 9000, (3, 70000)).astype(np.int64), t5))
     # a table longer than the compact form allows (the i64 logits kernel)
     t3 = np.array([round(2 ** 40 * np.exp(-i / 2048)) for i in range(20000)], np.uint64)
     l3 = r.integers(-30000, 30000, (6, 3000)).astype(np.int64)
