@@ -223,13 +223,14 @@ LN_MODELS = {
 
 
 @pytest.mark.parametrize("name", sorted(LN_MODELS))
-@pytest.mark.parametrize("windows", [8, 32])
-def test_layernorm_forms_equal_the_cpu(dev, name, windows):
-    """`windows` x 128-token windows in one pass: 1,024 rows (the decode-size form) or 4,096
-    rows (the prefill forms), every interval against the CPU fast path's."""
+@pytest.mark.parametrize("windows,n", [(8, 128), (32, 128), (33, 127)])
+def test_layernorm_forms_equal_the_cpu(dev, name, windows, n):
+    """`windows` x `n`-token windows in one pass: 1,024 rows (the decode-size form), 4,096 rows
+    (the prefill forms) or 4,191 (their last workgroup partial), every interval against the CPU
+    fast path's."""
     from taco_amd import hip, synth
     L, H, d, f = LN_MODELS[name]["dims"]
-    V, n = 512, 128
+    V = 512
     mb = synth.build_model(synth.Dims(L, H, d, f, vocab=V, n_ctx=256), seed=0x1F00 + d,
                            **LN_MODELS[name]["kw"])
     hm, om = hip.HipModel.load(dev, mb), O.Model(mb)
