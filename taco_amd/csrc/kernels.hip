@@ -428,9 +428,10 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         if constexpr (decltype(first_tag)::value) mfma_first(ca, cb);
         else mfma_step(ca, cb);
         // The step's order: two MFMAs, then one fragment read of the next step, repeated, then
-        // the remaining MFMAs. Opening with MFMAs keeps the wait that precedes the first of them
-        // from landing after a read; spreading the reads keeps the LDS busy under the MFMAs (the
-        // compiler left them after 24 of 32 MFMAs, or all before with a wait on the first).
+        // the remaining MFMAs (one MFMA per read for the 64 x 64 tiles, 8 MFMAs and 6 reads).
+        // Opening with MFMAs keeps the wait that precedes the first of them from landing after a
+        // read; spreading the reads keeps the LDS busy under the MFMAs (the compiler left them
+        // after 24 of 32 MFMAs, or all before with a wait on the first).
         constexpr int NR = TI + TJ;
         if constexpr (2 * NR <= TI * TJ) {
 #pragma unroll
@@ -439,6 +440,13 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
             }
             __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ - 2 * NR, 0);
+        } else if constexpr (NR <= TI * TJ) {
+#pragma unroll
+            for (int z = 0; z < NR; z++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TI * TJ - NR, 0);
         } else {
             asm volatile("" ::: "memory");
         }
