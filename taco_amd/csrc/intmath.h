@@ -262,4 +262,23 @@ HS_HD uint64_t ln_inv_est(u128 sq, uint32_t n, uint32_t k, uint32_t j, uint64_t 
     return pow2_div_est(k, r > 0 ? r : 1);
 }
 
+// The softmax weight p = floor(e 2^P / S) (softmax.rs:78-104) of a table entry e <= S, e < 2^31,
+// S < 2^53, P <= 30, exactly and without a branch. The row gives R = 2^P / S rounded once and
+// sp = -S 2^-P (exact). n = round(e R) comes from one fused multiply-add (adding 1.5 2^52 rounds
+// to an integer, the low word of the sum); |e R - e 2^P / S| <= 2^P 2^-53, so
+// |n - e 2^P / S| < 1/2 + 2^-23 and n is p or p + 1. p = n - 1 exactly when e 2^P < n S: the sign
+// of fma(n, sp, e) = (e 2^P - n S) 2^-P rounded once, since every operand is exact (n is
+// w - 1.5 2^52 exactly, S < 2^53, e < 2^31), a rounding keeps the sign of a nonzero value and an
+// exact zero gives +0. The sign word shifted arithmetically is -1 or 0.
+HS_HD double softmax_sp(uint64_t S, int P) { return -ldexp((double)S, -P); }
+HS_HD uint32_t softmax_p_of(uint32_t e, double R, double sp) {
+    const double ed = (double)e;
+    const double w = fma(ed, R, 6755399441055744.0);
+    const double r = fma(w - 6755399441055744.0, sp, ed);
+    uint64_t wb, rb;
+    memcpy(&wb, &w, sizeof wb);
+    memcpy(&rb, &r, sizeof rb);
+    return (uint32_t)wb + (uint32_t)((int32_t)(rb >> 32) >> 31);
+}
+
 }  // namespace hs

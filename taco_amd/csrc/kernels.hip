@@ -1988,20 +1988,6 @@ hipError_t launch_attend(const AttnArgs &a, int n_rows, hipStream_t stream) {
 // the score stays within +-2^40 and the clamp is a no-op.
 __host__ __device__ inline bool attn_noclamp(const AttnArgs &a) { return a.score_s >= 13; }
 
-// p = floor(e 2^P / S) for a table entry e <= S (e < 2^31, S < 2^53, P <= 30), exactly and
-// without a branch: n = round(e R) from one fused multiply-add (1.5 2^52 added rounds to the
-// nearest integer, the low word of the sum) with R = 2^P / S rounded once, so
-// |e R - e 2^P / S| <= 2^30 2^-53 and |n - e 2^P / S| < 1/2 + 2^-22; then p = n, or n - 1 when
-// e 2^P < n S (integers: n S <= e 2^P + S < 2^62).
-__device__ __forceinline__ uint32_t softmax_p_of(uint32_t e, double R, uint32_t s_lo, uint32_t s_hi, int P) {
-    const double w = fma((double)e, R, 6755399441055744.0);
-    uint64_t bits;
-    __builtin_memcpy(&bits, &w, sizeof bits);
-    const uint32_t n = (uint32_t)bits;
-    const uint64_t ns = (uint64_t)n * s_lo + ((uint64_t)(n * s_hi) << 32);
-    return n - (((uint64_t)e << P) < ns ? 1u : 0u);
-}
-
 // The attention output byte clamp(rescale(v, m, s), +-127) for an exact |v| < 2^53 (the sum of
 // p v): y = v m 2^-s + 1/2 in double (mo = m 2^-s, exact; v exact; one rounding in the fused
 // multiply-add, relative 2^-53). When |y| >= 256 the clamp decides; when y lies at least 2^-30
@@ -2308,10 +2294,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     __syncthreads();
     sum = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
+    const double sp = softmax_sp(sum, a.softmax_p);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int k = tid + 256 * j;
-        if (k < keys) s_p[k] = softmax_p_of(e[j], R, (uint32_t)sum, (uint32_t)(sum >> 32), a.softmax_p);
+        if (k < keys) s_p[k] = softmax_p_of(e[j], R, sp);
     }
     __syncthreads();
     // sum p v: thread t takes channels 16 (t % 4) .. +16 of keys t / 4 + 64 i. p = 2^16 ph + pl
@@ -2449,10 +2436,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     }
     sum = (uint64_t)wave_sum64((int64_t)sum);
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
+    const double sp = softmax_sp(sum, a.softmax_p);
     uint32_t p[KB];
 #pragma unroll
     for (int j = 0; j < KB; j++)  // <= 2^P <= 2^30; 0 for keys past the row (e = 0)
-        p[j] = softmax_p_of(e[j], R, (uint32_t)sum, (uint32_t)(sum >> 32), a.softmax_p);
+        p[j] = softmax_p_of(e[j], R, sp);
     wait_vmcnt<0>();  // this wave's V rows landed in its LDS region
     int32_t lo[16], hi[16];
 #pragma unroll
@@ -2813,7 +2801,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
     // p = floor(e 2^P / S) (softmax_p_of)
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
-    const uint32_t s_lo = (uint32_t)sum, s_hi = (uint32_t)(sum >> 32);
+    const double sp = softmax_sp(sum, a.softmax_p);
     // pass 3: p, its packed digits, and the digit-plane PV products
     v4i acc[4][4];  // [digit plane][channel tile]: channel 16 c + 4 (l / 16) + e of row l % 16
 #pragma unroll
@@ -2860,7 +2848,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) dg[t][e] = softmax_p_of((uint32_t)S[b][t][e], R, s_lo, s_hi, a.softmax_p);
+                for (int e = 0; e < 4; e++) dg[t][e] = softmax_p_of((uint32_t)S[b][t][e], R, sp);
             v4i pf[4];  // [digit plane]: word t holds the digits of keys 16 t + 4 (l / 16) + e
 #pragma unroll
             for (int t = 0; t < 4; t++) {
@@ -3087,7 +3075,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
 #pragma unroll
     for (int o = 16; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
     const double R = ldexp(1.0 / (double)sum, a.softmax_p);
-    const uint32_t s_lo = (uint32_t)sum, s_hi = (uint32_t)(sum >> 32);
+    const double sp = softmax_sp(sum, a.softmax_p);
     // The V^T operand comes straight from the V rows: ds_read_b64_tr_b8 gives lane 8 h + j of each
     // 16-lane group byte j of the 8-byte pieces that lanes h, h + 2, .., h + 14 address. Lane i of
     // group qg addresses key 16 t + 4 qg + e (t = 2 r + i / 8, e = (i / 2) % 4 for read r) at
@@ -3119,7 +3107,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
             }
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                dg[t][e] = softmax_p_of((uint32_t)S[b][t][e], R, s_lo, s_hi, a.softmax_p) + 0x80808080u;
+                dg[t][e] = softmax_p_of((uint32_t)S[b][t][e], R, sp) + 0x80808080u;
         }
         v4i pf[4];  // [digit plane]: word t holds the digits of keys 16 t + 4 (l / 16) + e
 #pragma unroll

@@ -281,6 +281,43 @@ int main(int argc, char **argv) {
                 }
             }
     CHECK(taken32 > n / 2, "ln_elem_f32 declined too often (%ld of %ld)", declined32, declined32 + taken32);
+    // softmax_p_of: floor(e 2^P / S) for e <= S, e < 2^31, S < 2^53, P <= 30; random rows and
+    // entries on, just below and just above the multiples of S / 2^P
+    auto check_p = [&](uint32_t e, uint64_t S, int P) -> bool {
+        const double R = ldexp(1.0 / (double)S, P);
+        const uint64_t want = (uint64_t)(((u128)e << P) / S);
+        return hs::softmax_p_of(e, R, hs::softmax_sp(S, P)) == (uint32_t)want;
+    };
+    for (long i = 0; i < 4 * n; i++) {
+        const int bits = 1 + (int)(next() % 52);
+        uint64_t S = next() & ((1ull << bits) - 1);
+        if (S == 0) S = 1;
+        const int P = (int)(next() % 31);
+        const uint64_t emax = S < 0x7FFFFFFFull ? S : 0x7FFFFFFFull;
+        uint32_t e;
+        if (i % 2) {
+            e = (uint32_t)(next() % (emax + 1));
+        } else {  // near the first e with floor(e 2^P / S) >= q
+            const uint64_t q = next() % (((u128)emax << P) / S + 1);
+            const u128 e0 = ((u128)q * S + ((u128)1 << P) - 1) >> P;
+            const int delta = (int)(next() % 3) - 1;
+            const i128 ev = (i128)e0 + delta;
+            e = (uint32_t)(ev < 0 ? 0 : (ev > (i128)emax ? emax : (uint64_t)ev));
+        }
+        CHECK(check_p(e, S, P), "softmax_p_of e %u S %llu P %d", e, (unsigned long long)S, P);
+        count++;
+    }
+    for (int P = 0; P <= 30; P++)
+        for (uint64_t S : {1ull, 2ull, 3ull, 0x7FFFFFFFull, 0x80000000ull, 0xFFFFFFFFull, 0x100000001ull,
+                           255ull * 0x7FFFFFFFull, (1ull << 53) - 1}) {
+            const uint64_t emax = S < 0x7FFFFFFFull ? S : 0x7FFFFFFFull;
+            for (uint64_t e : {(uint64_t)0, (uint64_t)1, emax / 2, emax - 1, emax}) {
+                if (e > emax) continue;
+                CHECK(check_p((uint32_t)e, S, P), "softmax_p_of edge e %llu S %llu P %d", (unsigned long long)e,
+                      (unsigned long long)S, P);
+                count++;
+            }
+        }
     std::printf("ok %ld\n", count);
     return 0;
 }
