@@ -11,7 +11,8 @@ they would not fit in three quarters of the device memory): each folds
 whole steps from its own host thread on its own stream, so one batch's host work and kernels
 overlap the others' kernels; every step's container must equal the first one's. `one_batch`
 is the same steps on a single batch (its wall time, the GPU span of its passes, the host's
-share).
+share). The warmup steps run one batch at a time (each batch's first use), then again with the
+batches in flight right before the timed ones.
 
 Prints one JSON line. `value` is fold tokens per second with the token stream and the model
 already resident (model upload and token staging are outside the timed region; per step the
@@ -411,6 +412,9 @@ def run_fold(args):
     log(f"one batch: {1e3 * one_elapsed / args.steps:.3f} ms per step; GPU span of the passes "
         f"{span_ms:.3f} ms per step ({span['launches']} passes), host share {host_ms:.3f} ms per step")
     timed_phase = dict(phase)
+    # The warmup steps again, now with the batches in flight (the steps above ran one batch
+    # alone), so the timed region starts with every batch's thread and stream already busy.
+    steps_in_flight(max(args.warmup, nb))
     # The timed steps: the batches in flight
     elapsed, conts = steps_in_flight(args.steps)
     if any(c != cont for c in conts):
@@ -936,7 +940,7 @@ def main():
         return main_mfma(sys.argv[2:])
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--steps", type=int, default=80)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--workload", default="fold-gpt2-small",
                     choices=sorted(FOLDS) + ["gemm-qkv", "gemm-vendor", "attend-decode", "issue-rates"])
