@@ -350,23 +350,38 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
     // bank groups.
     auto sw = [](int r) { return ((r >> 1) ^ (r >> 3)) & 3; };
     const size_t pa = (size_t)g.a_rows * 64, pw = (size_t)g.w_rows * 64;  // bytes per panel
-    // A load's address is a wave-uniform fragment base (scalar registers, advanced by scalar
-    // adds each k-step) plus the lane's 32-bit offset inside the fragment, the same for every
-    // load: the loads take the scalar-base form and the loop forms no vector addresses.
+    // A load's address is a wave-uniform fragment base (scalar registers, recomputed by scalar
+    // instructions each k-step) plus the lane's 32-bit offset inside the fragment, the same for
+    // every load (one vector add per load). The 64 x 64 tiles of decode passes, whose k-steps hold
+    // 8 MFMAs per wave, keep a per-lane pointer per load instead: their loop is too short to hide
+    // the scalar work (GPT-2-medium unfold GEMMs 2-4% slower with the shared form).
     const uint32_t lane_off = (uint32_t)((lane >> 2) * 64 + (((lane & 3) ^ sw(lane >> 2)) * 16));
     auto frag_base = [&](int i) -> const int8_t * {
         const int f = wave * LOADS + i;
         return f < BM / 16 ? g.a + (size_t)(kb0 / GEMM_BK) * pa + (size_t)(m0 + 16 * f) * 64
                            : g.w + (size_t)(kb0 / GEMM_BK) * pw + (size_t)(n0 + 16 * (f - BM / 16)) * 64;
     };
+    constexpr bool LANE_PTRS = BM == 64;
+    const int8_t *src[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; i++) {
+        src[i] = nullptr;
+        if constexpr (LANE_PTRS) {
+            const int f = wave * LOADS + i;
+            const int r = lane >> 2, c = (lane & 3) ^ sw(r);
+            const int row = (f < BM / 16 ? f : f - BM / 16) * 16 + r;
+            src[i] = (f < BM / 16 ? g.a + (size_t)(kb0 / GEMM_BK) * pa + (size_t)(m0 + row) * 64
+                                  : g.w + (size_t)(kb0 / GEMM_BK) * pw + (size_t)(n0 + row) * 64) + c * 16;
+        }
+    }
     const int rd_slot = 4 * (lane & 15) + ((lane >> 4) ^ sw(lane & 15));
     auto issue = [&](int kt, int stage) {
         int8_t *base = gemm_lds + stage * (FRAGS * 1024) + wave * LOADS * 1024;
 #pragma unroll
         for (int i = 0; i < LOADS; i++) {
             const size_t step = wave * LOADS + i < BM / 16 ? pa : pw;
-            __builtin_amdgcn_global_load_lds((const void *)(frag_base(i) + (size_t)kt * step + lane_off),
-                                             (lds_void *)(base + i * 1024), 16, 0, 0);
+            const int8_t *p = LANE_PTRS ? src[i] + (size_t)kt * step : frag_base(i) + (size_t)kt * step + lane_off;
+            __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)(base + i * 1024), 16, 0, 0);
         }
     };
 
