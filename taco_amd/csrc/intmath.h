@@ -270,6 +270,20 @@ HS_HD uint64_t ln_inv_est(u128 sq, uint32_t n, uint32_t k, uint32_t j, uint64_t 
 // of fma(n, sp, e) = (e 2^P - n S) 2^-P rounded once, since every operand is exact (n is
 // w - 1.5 2^52 exactly, S < 2^53, e < 2^31), a rounding keeps the sign of a nonzero value and an
 // exact zero gives +0. The sign word shifted arithmetically is -1 or 0.
+// The attention output byte clamp(rescale_full(v, m, s), +-127) (attention.rs:36-46, int.rs:63-67)
+// of v = hi 2^16 + lo, the pairwise sums of the four digit-plane products, for
+// |hi|, |lo| <= 2^30 + 2^22 and 48 <= s <= 63, in i64: with A = hi m and B = lo m + 2^(s-1)
+// (|A| < 2^61.01, |B| < 2^63), v m + 2^(s-1) = A 2^16 + B, and
+// floor((A 2^16 + B) / 2^s) = floor((A + floor(B / 2^16)) / 2^(s-16)) (A is an integer, and
+// floor(floor(z) / n) = floor(z / n)); C = A + (B >> 16) stays below 2^61.02, so its high word
+// shifted by s - 48 is the quotient, an i32.
+HS_HD int32_t attn_out_planes(int32_t hi, int32_t lo, int32_t m, uint32_t s) {
+    const int64_t b = (int64_t)lo * m + ((int64_t)1 << (s - 1));
+    const int64_t c = (int64_t)hi * m + (b >> 16);
+    const int32_t r = (int32_t)(c >> 32) >> (s - 48);
+    return r < -127 ? -127 : (r > 127 ? 127 : r);
+}
+
 HS_HD double softmax_sp(uint64_t S, int P) { return -ldexp((double)S, -P); }
 HS_HD uint32_t softmax_p_of(uint32_t e, double R, double sp) {
     const double ed = (double)e;

@@ -3151,7 +3151,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NB <= 4 ? 3
         h = tn % a.n_head;
         rows_to_lds(a.kc, ((size_t)G.slot * a.n_head + h) * a.ctx_cap * 64, key_blocks(G));
     }
-    if (myrow < out_count) {
+    // Shifts 48..63 with at most 4 blocks (|plane| <= 2^22): the exact rescale in i64 from the two
+    // pairwise plane sums (attn_out_planes: two multiply-adds and two shifts per output)
+    if (NB <= 4 && a.out_s >= 48 && a.out_s <= 63 && myrow < out_count) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            packed[c] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int32_t hi = (int32_t)((uint32_t)acc[3][c][e] << 8) + acc[2][c][e];
+                const int32_t lo = (int32_t)((uint32_t)acc[1][c][e] << 8) + acc[0][c][e];
+                const int32_t r = attn_out_planes(hi, lo, a.out_m, (uint32_t)a.out_s);
+                packed[c] |= (uint32_t)(uint8_t)(int8_t)r << (8 * e);
+            }
+        }
+        int8_t *o = attn_out(a, out_first + myrow, out_h * 64);
+#pragma unroll
+        for (int c = 0; c < 4; c++) *(uint32_t *)(o + 16 * c + 4 * qg) = packed[c];
+    } else if (myrow < out_count) {
         // rescale: s = 0 keeps v m, a shift above 95 gives 0
         const double mo = a.out_s > 95 ? 0.0 : ldexp((double)a.out_m, -a.out_s);
         uint32_t packed[4];

@@ -318,6 +318,40 @@ int main(int argc, char **argv) {
                 count++;
             }
         }
+    // attn_out_planes: clamp(rescale_full(hi 2^16 + lo, m, s), +-127) for |hi|, |lo| <= 2^30 + 2^22,
+    // 48 <= s <= 63; random planes and values on, just below and just above the rounding steps
+    const int64_t PL = (1ll << 30) + (1ll << 22);
+    auto check_out = [&](int64_t v, int32_t m, uint32_t s) -> bool {
+        const int64_t hi = v >> 16, lo = v - (hi << 16);  // lo in [0, 2^16)
+        if (hi > PL || hi < -PL) return true;           // outside the domain
+        const int64_t want = hs::clamp128(hs::rescale_full(v, m, s), -127, 127);
+        return hs::attn_out_planes((int32_t)hi, (int32_t)lo, m, s) == (int32_t)want;
+    };
+    for (long i = 0; i < 2 * n; i++) {
+        const uint32_t s = 48 + (uint32_t)(next() % 16);
+        const int32_t m = (int32_t)(uint32_t)next();
+        const int64_t hi = (int64_t)(next() % (2 * PL + 1)) - PL, lo = (int64_t)(next() % (2 * PL + 1)) - PL;
+        const int64_t want = hs::clamp128(hs::rescale_full(hi * 65536 + lo, m, s), -127, 127);
+        CHECK(hs::attn_out_planes((int32_t)hi, (int32_t)lo, m, s) == (int32_t)want, "attn_out_planes %lld %lld %d %u",
+              (long long)hi, (long long)lo, m, s);
+        count++;
+    }
+    for (long i = 0; i < n; i++) {  // v m + 2^(s-1) beside a multiple of 2^s, |q| <= 200
+        const uint32_t s = 48 + (uint32_t)(next() % 16);
+        int32_t m = (int32_t)(uint32_t)(next() >> (next() % 32));
+        if (m == 0) m = 1;
+        if (next() & 1) m = -m;
+        const i128 q = (i128)(int64_t)(next() % 401) - 200;
+        const i128 num = q * ((i128)1 << s) - ((i128)1 << (s - 1));  // v m = num at the step
+        const i128 am = m < 0 ? -(i128)m : (i128)m;
+        const i128 v0 = (num >= 0 ? (num + am - 1) / am : -((-num) / am)) * (m < 0 ? -1 : 1);
+        for (int d = -2; d <= 2; d++) {
+            const i128 v = v0 + d;
+            if (v > ((i128)1 << 46) || v < -((i128)1 << 46)) continue;
+            CHECK(check_out((int64_t)v, m, s), "attn_out_planes step v %lld m %d s %u", (long long)v, m, s);
+            count++;
+        }
+    }
     std::printf("ok %ld\n", count);
     return 0;
 }
