@@ -2021,7 +2021,7 @@ hs_status coder_on_logits(hs_device *dev, const int64_t *logits, size_t rows, si
     hs::CoderArgs ca;
     if (len <= (size_t)hs::CODER_MAX_TABLE) {
         // the compact form the LM head writes: the max of each 64-column tile and
-        // min(tilemax - l, len - 1) as u16
+        // min(tilemax - l, 65535) as u16 (its narrow form; every index min(d, len - 1) follows)
         const size_t nt = (vocab + 63) / 64, ld16 = round_up(vocab, 64);
         std::vector<int64_t> tm(rows * nt, INT64_MIN);
         std::vector<uint16_t> dd(rows * ld16, 0);
@@ -2031,7 +2031,7 @@ hs_status coder_on_logits(hs_device *dev, const int64_t *logits, size_t rows, si
         for (size_t r = 0; r < rows; r++)
             for (size_t j = 0; j < vocab; j++) {
                 const int64_t d = tm[r * nt + j / 64] - logits[r * vocab + j];
-                dd[r * ld16 + j] = (uint16_t)std::min<int64_t>(d, (int64_t)len - 1);
+                dd[r * ld16 + j] = (uint16_t)std::min<int64_t>(d, 65535);
             }
         uint16_t *d16;
         int64_t *dtm;

@@ -56,8 +56,9 @@ struct GemmArgs {
     // gelu_lo. gelu_copy 0: the whole table (the launcher fills the fields).
     int gelu_lo = 0, gelu_clo = 0, gelu_chi = 0, gelu_shift = 0, gelu_copy = 0;
     const int32_t *wsum = nullptr;    // the wide epilogues: sum_k w[n][k] per output column
-    // LogitsCompact: out is u16 [m, ldo] = min(tilemax - logit, cap16) and tmax [m, tmax_ld] is
-    // the largest logit of each 64-column tile.
+    // LogitsCompact: out is u16 [m, ldo] = tilemax - logit capped at 65535 (NARROW) or cap16
+    // (at least min(tilemax - logit, cap16) either way, all the readers need) and tmax
+    // [m, tmax_ld] is the largest logit of each 64-column tile.
     int64_t *tmax = nullptr;
     int tmax_ld = 0;
     int cap16 = 0;

@@ -645,9 +645,10 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
         if constexpr (EPI == (int)Epi::LogitsCompact) {
             static_assert(TI == 8 && TJ == 4, "the compact logits keep 64-column tiles");
             // logit = clamp(rescale(acc, m[n], s), +-2^40) (ops.rs:229-234), stored as the
-            // largest logit of this wave's 64 columns (per row) and min(tilemax - logit, cap16)
-            // per logit; the table index min(max - l, len - 1) follows exactly from them, because
-            // max - l = (max - tilemax) + (tilemax - l) and cap16 >= len - 1. Each row's 64
+            // largest logit of this wave's 64 columns (per row) and per logit the distance
+            // tilemax - logit capped at c: c = 65535 (NARROW: a saturating pack) or cap16; the
+            // table index min(max - l, len - 1) follows exactly from them, because
+            // max - l = (max - tilemax) + (tilemax - l) and c >= cap16 >= len - 1. Each row's 64
             // columns are 16 in each of the 4 lanes lane % 16 + 16 c.
             int32_t mult[4][4];
 #pragma unroll
@@ -692,9 +693,16 @@ __global__ __launch_bounds__(64 * gemm_waves(BN)) __attribute__((amdgpu_waves_pe
 #pragma unroll
                     for (int p = 0; p < 2; p++) {
                         const U d0 = (U)mx - (U)l[j][2 * p], d1 = (U)mx - (U)l[j][2 * p + 1];
-                        const uint32_t u0 = (uint32_t)(d0 < cap ? d0 : cap);
-                        const uint32_t u1 = (uint32_t)(d1 < cap ? d1 : cap);
-                        w2[p] = (u0 & 0xFFFF) | (u1 << 16);
+                        if constexpr (NARROW) {
+                            // two u32 distances to a u16 pair, each min(d, 65535), in one
+                            // instruction: every distance of cap16 or more stays at least cap16
+                            const us2 pk = __builtin_amdgcn_cvt_pk_u16((uint32_t)d0, (uint32_t)d1);
+                            __builtin_memcpy(&w2[p], &pk, 4);
+                        } else {
+                            const uint32_t u0 = (uint32_t)(d0 < cap ? d0 : cap);
+                            const uint32_t u1 = (uint32_t)(d1 < cap ? d1 : cap);
+                            w2[p] = (u0 & 0xFFFF) | (u1 << 16);
+                        }
                     }
                     if (vec) {
                         *(uint2 *)(wr + (16 * i + rl) * 144 + (16 * j + 4 * cg) * 2) = make_uint2(w2[0], w2[1]);
@@ -3672,8 +3680,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             const int base = (int)(b64 < last ? b64 : last);
             const uint16_t *dv = (const uint16_t *)&cur[u];
             if (packed && addr16 && gq + 8 <= V) {
-                // two symbols per packed u16 add and min: d = min(base + d16, zl) (base + d16 <
-                // 2^15): with tail0 the symbols of weight 0 (d >= zc) land in the 64 spare bins
+                // two symbols per packed u16 add and min: d = min(base + d16, zl), the add
+                // saturating at 65535 (> zl; a d16 may be up to 65535, base <= last < 2^14):
+                // with tail0 the symbols of weight 0 (d >= zc) land in the 64 spare bins
                 // past the weighted ones (never read), each lane in its own, else d >= last lands
                 // in the last bin, and no symbol needs a test; the count below the Encode token
                 // rides in the high half
@@ -3685,7 +3694,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     __builtin_memcpy(&v[p], &wv[p], 4);
-                    v[p] = __builtin_elementwise_min(v[p] + bb, zz) << (unsigned short)2;
+                    v[p] = __builtin_elementwise_min(__builtin_elementwise_add_sat(v[p], bb), zz) << (unsigned short)2;
                 }
                 uint8_t *hb = (uint8_t *)hist;
                 auto bin = [&](unsigned short byte) { return (uint32_t *)(hb + byte); };
