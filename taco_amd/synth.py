@@ -197,14 +197,17 @@ SIGMA_ACT_SQ = Fraction(1600 * 1600)       # i8 model activations times weights
 
 
 def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_len: int = 8192,
-                score_target: int = 768, beta_max: int = 16, residual_target: int = 1 << 14) -> bytes:
+                score_target: int = 768, beta_max: int = 16, residual_target: int = 1 << 14,
+                score_mult: int = 0) -> bytes:
     """The synthetic model. wide=True makes a model-file version 2 model: an i16 GELU table
     (output unit 1/10240), a 16-bit ln_f (target 10240) and ln_beta_frac = 8 (beta in units of
     2^-8, uniform in [-4096, 4096]); the shifts that read those activations are 8 larger.
     table_len sets the length of both exponent tables; score_target the typical attention score
     (larger targets give smaller score shifts); beta_max the LayerNorm beta range [-beta_max,
     beta_max] in output units; residual_target the typical residual update (larger targets give
-    the residual products shifts below 31, the general rescale form)."""
+    the residual products shifts below 31, the general rescale form); score_mult, when nonzero,
+    replaces every layer's attention score multiplier (after drawing it, so the rest of the model
+    stays the same), e.g. a negative one."""
     d, f, V, C, L, H = dims.d_model, dims.d_ff, dims.vocab, dims.n_ctx, dims.n_layer, dims.n_head
     hd = d // H
     s = Stream(seed)
@@ -246,7 +249,10 @@ def build_model(dims: Dims, seed: int = 0x7AC0_5EED, wide: bool = False, table_l
         p = f"h.{l}"
         layernorm(p + ".ln_1")
         linear(p + ".attn.c_attn", 3 * d, d, 40)
-        w.add_tensor(p + ".attn.score.rescale", mult(1), shift_for(SIGMA_ACT_SQ * hd, score_target))
+        sm = mult(1)
+        if score_mult:
+            sm = np.array([score_mult], np.int32)
+        w.add_tensor(p + ".attn.score.rescale", sm, shift_for(SIGMA_ACT_SQ * hd, score_target))
         w.add_tensor(p + ".attn.out.rescale", mult(1), shift_for(Fraction(2) ** 60 * 1600, 40))
         linear(p + ".attn.c_proj", d, d, residual_target)
         layernorm(p + ".ln_2")

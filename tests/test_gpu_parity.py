@@ -530,6 +530,27 @@ def test_head_dim_64_prefill_score_shifts(dev, score_target, shift):
         assert got[i] == O.encode_block(om, blk, overlap=0), i
 
 
+@pytest.mark.parametrize("score_mult", [-1_400_000_000, -(1 << 31)])
+def test_head_dim_64_prefill_negative_score_multiplier(dev, score_mult):
+    """A negative attention score multiplier: the short prefill kernel negates the Q bytes, so
+    every score grows with its dot and the row max comes from the largest one; INT32_MIN, whose
+    magnitude is not an i32, takes the general kernel. Ragged groups (windows of 1 to 300
+    tokens, n_ctx 256)."""
+    from taco_amd import fold, hip, synth
+    from tests.test_oracle import read_hsm
+    b = synth.build_model(synth.Dims(2, 4, 256, 512, 1000, 256), seed=0x5C0E, score_mult=score_mult)
+    _, ts = read_hsm(b)
+    assert int(ts["h.0.attn.score.rescale"][0][0]) == score_mult
+    om, hm = O.Model(b), hip.HipModel.load(dev, b)
+    lens = [1, 40, 64, 100, 256, 300]
+    blocks = [np.array(splitmix_tokens(150 + i, n, 999), np.uint32) for i, n in enumerate(lens)]
+    batch = hip.HipBatch(hm, 4, 512)
+    got = fold.fold_blocks(batch, blocks, 0)
+    for i, blk in enumerate(blocks):
+        print(f"score multiplier {score_mult}: block {i} ({len(blk)} tokens)", flush=True)
+        assert got[i] == O.encode_block(om, blk, overlap=0), i
+
+
 @pytest.mark.parametrize("score_target", [768, 1 << 23])
 def test_head_dim_64_prefill_up_to_512_keys(dev, score_target):
     """Groups of 257 to 512 keys: the 8-block form of the short prefill kernel (score shift 34)
