@@ -1064,7 +1064,17 @@ int gemm_split_plan(Epi epi, int m, int n, int k_pad, int wanted) {
     if (!ok || m <= 0 || n <= 0 || k_pad < 2 * GEMM_BK) return 1;
     const int nks = k_pad / GEMM_BK;
     if (wanted >= 1) return wanted > nks ? nks : wanted;
-    if (gemm_decode_tiles(m, k_pad)) return 1;  // the 64 x 64 tiles take the whole of K
+    if (gemm_decode_tiles(m, k_pad)) {
+        // 64 x 64 tiles over the whole of K, unless they are too few for the GPU and K is long:
+        // then 64 x 64 partials over slices of at least 16 k-steps (GPT-2 medium's mlp.c_proj in
+        // a 256-row pass: 256 workgroups of 16 k-steps instead of 64 of 64)
+        const int tiles64 = ((m + 63) / 64) * ((n + 63) / 64);
+        if (tiles64 >= 128 || k_pad < 2048) return 1;
+        int sp = (256 + tiles64 - 1) / tiles64;
+        sp = sp < nks / 16 ? sp : nks / 16;
+        sp = sp > 16 ? 16 : sp;
+        return sp < 2 ? 1 : sp;
+    }
     const int gm = (m + GEMM_BM - 1) / GEMM_BM, tiles128 = gm * ((n + 127) / 128);
     // enough workgroups without a split, or K too short for the partials to pay (measured: the
     // c_attn product at M 256, K 768 takes 12.3 us whole and 13.5 us in three slices; at K 1,024
@@ -1177,14 +1187,31 @@ static hipError_t launch_gemm_split(Epi epi, const GemmArgs &ga, int splits, hip
     p.out = ga.partials;
     p.ldo = ldp;
     constexpr int EPI_RAW = (int)Epi::Raw;
-    constexpr size_t lds = (size_t)GEMM_STAGES * (GEMM_BM / 16 + SPLIT_BN / 16) * 1024;
-    {
-        const hipError_t e = allow_dynamic_lds((const void *)k_gemm<EPI_RAW, false, SPLIT_BN, true>, lds);
+    if (gemm_decode_tiles(ga.m, ga.k_pad)) {
+        // decode-shaped: the partials in 64 x 64 tiles (two waves), with the 6-stage ring for
+        // slices of 1,024 or more (as the whole-K 64 x 64 tiles)
+        const int gm = (ga.m + 63) / 64, gn = (ga.n + 63) / 64;
+        p.group = 4 * ga.group < gm ? 4 * ga.group : gm;
+        auto run = [&](auto kernel, int stages) -> hipError_t {
+            const size_t lds = (size_t)stages * 8 * 1024;
+            const hipError_t e = allow_dynamic_lds((const void *)kernel, lds);
+            if (e != hipSuccess) return e;
+            launch_k(kernel, dim3(gm * gn, splits), dim3(64 * gemm_waves(64)), lds, stream, p);
+            return hipGetLastError();
+        };
+        const hipError_t e = p.kslice >= 1024 ? run(k_gemm<EPI_RAW, false, 64, true, 64, true>, gemm_stages(64, true))
+                                              : run(k_gemm<EPI_RAW, false, 64, true, 64>, gemm_stages(64, false));
         if (e != hipSuccess) return e;
+    } else {
+        constexpr size_t lds = (size_t)GEMM_STAGES * (GEMM_BM / 16 + SPLIT_BN / 16) * 1024;
+        {
+            const hipError_t e = allow_dynamic_lds((const void *)k_gemm<EPI_RAW, false, SPLIT_BN, true>, lds);
+            if (e != hipSuccess) return e;
+        }
+        const int gm = (ga.m + GEMM_BM - 1) / GEMM_BM, gn = (ga.n + SPLIT_BN - 1) / SPLIT_BN;
+        launch_k((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(64 * gemm_waves(SPLIT_BN)),
+                 lds, stream, p);
     }
-    const int gm = (ga.m + GEMM_BM - 1) / GEMM_BM, gn = (ga.n + SPLIT_BN - 1) / SPLIT_BN;
-    launch_k((k_gemm<EPI_RAW, false, SPLIT_BN, true>), dim3(gm * gn, splits), dim3(64 * gemm_waves(SPLIT_BN)), lds,
-                       stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     switch (epi) {
