@@ -972,7 +972,9 @@ static hipError_t launch_gemm_t(const GemmArgs &ga, hipStream_t stream) {
 }
 
 // Decode-shaped products (at most two 256-row tiles of rows, K at most 4,096) take 64 x 64 tiles
-// over the whole of K (more workgroups than 128 x 192 tiles, no partials); longer K splits.
+// over the whole of K (more workgroups than 128 x 192 tiles, no partials), or, when those tiles
+// are fewer than 128 and K is 2,048 or more, 64 x 64 partial tiles over slices of K
+// (gemm_split_plan); longer K splits in 256 x 64 partial tiles.
 static bool gemm_decode_tiles(int m, int k_pad) { return m <= 2 * GEMM_BM && k_pad <= 4096; }
 
 // 256 x 128 tiles (two workgroups per CU, so one's epilogue overlaps the other's main loop),
