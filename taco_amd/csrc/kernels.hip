@@ -1102,8 +1102,17 @@ __global__ __launch_bounds__(256) void k_split_epi(GemmArgs g, int splits, int l
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const int m = (int)(idx / groups), n4 = (int)(idx % groups) * 4;
     if (m >= g.m || n4 >= g.n) return;
+    // four slices' loads in flight at a time (i32 sums of the partials are exact in any order)
+    const int32_t *src = g.partials + (size_t)m * ldp + n4;
+    const size_t slice = (size_t)g.m * ldp;
     v4i acc = {0, 0, 0, 0};
-    for (int sl = 0; sl < splits; sl++) acc += *(const v4i *)(g.partials + ((size_t)sl * g.m + m) * ldp + n4);
+    int sl = 0;
+    for (; sl + 4 <= splits; sl += 4) {
+        const v4i p0 = *(const v4i *)(src + sl * slice), p1 = *(const v4i *)(src + (sl + 1) * slice);
+        const v4i p2 = *(const v4i *)(src + (sl + 2) * slice), p3 = *(const v4i *)(src + (sl + 3) * slice);
+        acc += (p0 + p1) + (p2 + p3);
+    }
+    for (; sl < splits; sl++) acc += *(const v4i *)(src + sl * slice);
     const int cnt = g.n - n4 < 4 ? g.n - n4 : 4;
     if (EPI == (int)Epi::Raw) {
         int32_t *o = (int32_t *)g.out + (size_t)m * g.ldo + n4;
